@@ -1,0 +1,148 @@
+/* mx_sampler.h -- C ABI of the MI355X (gfx950) token sampler, libmx_sampler.so.
+ *
+ * The drop-in boundary for metallix's device pick.  Each entry point names
+ * the reference interface it replaces (paths relative to the
+ * arclabs561/metallix tree):
+ *
+ *   mxs_create / mxs_destroy  <- mlx_kernels::MetalKernel::new + Drop
+ *                                (crates/metal/mlx-kernels/src/lib.rs:203-215, 444-450):
+ *                                one handle owns the compiled kernels and scratch.
+ *   mxs_sample                <- Qwen3TokenPicks::start_with(rows, binding, rule)
+ *                                (crates/models/qwen/src/forward/picks.rs:279-381) with
+ *                                Qwen3Selection::{Greedy, TopKNucleus}; the arithmetic is
+ *                                TokenPicker::pick -> SamplingPolicy::sample_nucleus ->
+ *                                nucleus_mask + sample_categorical
+ *                                (crates/app/cli/src/qwen_forward.rs:264-278, 474-549;
+ *                                crates/core/engine/src/sampling.rs:56-158), greedy_token
+ *                                (crates/app/cli/src/chat_generation.rs:2213-2231) and the
+ *                                grammar-mask consumption of
+ *                                crates/core/engine/src/constraint.rs:793-806, 895-932.
+ *   mxs_logsoftmax_topn       <- token_logprob (crates/app/cli/src/chat_turn.rs:506-563) and
+ *                                Qwen3RowCandidates (picks.rs:97-129).
+ *   mxs_spec_verify           <- engine::speculative::accept_or_resample
+ *                                (crates/core/engine/src/speculative.rs:369-444) applied
+ *                                position by position as in speculative_step (:202-227).
+ *   mxs_sync                  <- Qwen3TokenPicks::wait (picks.rs:390-401).
+ *   mxs_last_error            <- KernelError's message (mlx-kernels/src/lib.rs:444-450).
+ *
+ * Conventions.  Every buffer is caller-owned device memory unless stated.
+ * Calls are asynchronous on the context's stream and never synchronise the
+ * host (except mxs_sync).  Return codes: 0 = accepted, negative = rejected
+ * before launch (see mxs_last_error).  Per-row results carry a status:
+ * 0 = ok, 1 = ok but uncertified (a decision margin fell below the device's
+ * rigorous floating-point error bound; the token is the device's best
+ * decision and a caller that owes bit-exact parity re-derives the row on the
+ * host, as TokenPicker does when candidates cannot settle a pick,
+ * chat_turn.rs:348-358), negative = the row's error (MXS_ROW_* below, the
+ * first seven mirroring engine::sampling::SamplingError,
+ * sampling.rs:19-43).  One context belongs to one host thread at a time.
+ */
+#ifndef MX_SAMPLER_H
+#define MX_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXS_ABI_VERSION 1
+
+/* Call return codes. */
+enum {
+  MXS_OK = 0,
+  MXS_EINVAL = -1,     /* bad argument: null pointer, size over the context limits, misalignment */
+  MXS_EHIP = -2,       /* a HIP runtime call failed */
+  MXS_ENOMEM = -3,     /* device allocation failed */
+  MXS_ENODEV = -4      /* no gfx950 device */
+};
+
+/* Per-row status codes (mxs_out.status). */
+enum {
+  MXS_ROW_OK = 0,
+  MXS_ROW_UNCERTIFIED = 1,
+  MXS_ROW_EMPTY_LOGITS = -1,
+  MXS_ROW_MASK_LENGTH_MISMATCH = -2,
+  MXS_ROW_EMPTY_SUPPORT = -3,
+  MXS_ROW_INVALID_TEMPERATURE = -4,
+  MXS_ROW_INVALID_UNIFORM = -5,
+  MXS_ROW_NON_FINITE_LOGIT = -6,
+  MXS_ROW_VOCABULARY_TOO_LARGE = -7,
+  MXS_ROW_INVALID_TOP_P = -8,
+  MXS_ROW_INVALID_MIN_P = -9,
+  MXS_ROW_INVALID_PENALTY = -10,
+  MXS_ROW_INVALID_HISTORY = -11,
+  MXS_ROW_INVALID_BIAS = -12,
+  MXS_ROW_TOKEN_OUT_OF_RANGE = -13,
+  MXS_ROW_PROBABILITIES = -14
+};
+
+typedef enum { MXS_F32 = 0, MXS_BF16 = 1 } mxs_dtype;
+
+typedef struct mxs_ctx mxs_ctx;
+
+/* One batch of logit rows and the per-row sampling rule.  Per-row arrays
+ * are device arrays of `rows` entries; NULL selects the default shown.
+ * These fields are Qwen3Selection::TopKNucleus's (temperature, top_p,
+ * top_k, uniforms; picks.rs:20-40) plus the stages the reference rejects
+ * at its HTTP layer and this sampler defines (penalties, logit bias,
+ * min_p) and the grammar mask (constraint.rs:793-806). */
+typedef struct {
+  const void* logits;             /* rows x row_stride elements of `dtype` */
+  int32_t dtype;                  /* mxs_dtype */
+  uint32_t rows;
+  uint32_t vocab;
+  uint64_t row_stride;            /* elements between row starts; multiple of 4 */
+  const double* temperature;      /* required; 0 => greedy */
+  const uint32_t* top_k;          /* NULL => 0 (off) */
+  const double* top_p;            /* NULL => 1 (off) */
+  const double* min_p;            /* NULL => 0 (off) */
+  const float* repetition;        /* NULL => 1 (off) */
+  const float* presence;          /* NULL => 0 */
+  const float* frequency;         /* NULL => 0 */
+  const double* uniform;          /* required unless every row is greedy; [0, 1) */
+  const uint32_t* history_offsets;/* rows + 1 offsets into history_ids (CSR); NULL => none */
+  const uint32_t* history_ids;
+  const uint32_t* bias_offsets;   /* rows + 1 offsets into bias_ids/bias_values; NULL => none */
+  const uint32_t* bias_ids;       /* strictly increasing within a row */
+  const float* bias_values;
+  const uint32_t* mask_words;     /* rows x mask_stride u32 words, bit b of word w <-> token 32w+b; NULL => none */
+  uint64_t mask_stride;           /* words between row masks; >= ceil(vocab / 32) */
+  uint32_t tokenizer_vocab;       /* with a mask: tokens at or past it are never legal */
+  uint32_t reserved;
+} mxs_batch;
+
+/* Outputs of mxs_sample: device arrays of `rows` entries; the debug
+ * outputs may be NULL. */
+typedef struct {
+  int32_t* token;                 /* required */
+  double* sampling_logprob;       /* NULL => not written */
+  int32_t* status;                /* required */
+  uint32_t* kept_count;           /* NULL => not written */
+  float* adjusted;                /* debug: rows x vocab penalised, biased logits */
+  uint32_t* kept_bits;            /* debug: rows x ceil(vocab / 32) final kept set */
+} mxs_out;
+
+int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, mxs_ctx** out);
+int mxs_destroy(mxs_ctx* ctx);
+int mxs_set_stream(mxs_ctx* ctx, void* stream);
+int mxs_sample(mxs_ctx* ctx, const mxs_batch* batch, const mxs_out* out);
+int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dtype, uint32_t rows,
+                        uint32_t vocab, uint64_t row_stride, uint32_t n, int32_t* ids,
+                        double* logprobs, double* maximum, double* log_normalizer, int32_t* status);
+int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const float* draft_logits,
+                    uint32_t rows, uint32_t draft_len, uint32_t vocab,
+                    const int32_t* draft_tokens, const double* temperature,
+                    const double* accept_uniform, const double* resample_uniform,
+                    const double* bonus_uniform, int32_t* out_tokens, int32_t* out_count,
+                    int32_t* out_accepted, int32_t* status);
+int mxs_sync(mxs_ctx* ctx);
+const char* mxs_last_error(const mxs_ctx* ctx);
+const char* mxs_status_string(int32_t status);
+int mxs_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,213 @@
+"""ctypes binding of libmx_sampler.so (include/mx_sampler.h).
+
+`Sampler` mirrors the reference's device-pick plugin: one handle owns the
+kernels and scratch (mlx_kernels::MetalKernel, crates/metal/mlx-kernels/src/
+lib.rs:203-215); `sample` queues a batched pick on the stream like
+Qwen3TokenPicks::start_with (crates/models/qwen/src/forward/picks.rs:279-381)
+and returns device tensors the caller reads back after synchronising, the
+Qwen3TokenPicks::wait step (picks.rs:390-401).  Per-row statuses mirror
+engine::sampling::SamplingError (crates/core/engine/src/sampling.rs:19-43).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional, Sequence
+
+LIB_PATH = Path(__file__).resolve().parent / "_build" / "libmx_sampler.so"
+
+MXS_F32 = 0
+MXS_BF16 = 1
+
+ROW_STATUS = {
+    0: "ok",
+    1: "uncertified",
+    -1: "EmptyLogits",
+    -2: "MaskLengthMismatch",
+    -3: "EmptySupport",
+    -4: "InvalidTemperature",
+    -5: "InvalidUniform",
+    -6: "NonFiniteLogit",
+    -7: "VocabularyTooLarge",
+    -8: "InvalidTopP",
+    -9: "InvalidMinP",
+    -10: "InvalidPenalty",
+    -11: "InvalidHistory",
+    -12: "InvalidBias",
+    -13: "TokenOutOfRange",
+    -14: "Probabilities",
+}
+
+_vp = ctypes.c_void_p
+
+
+class MxsBatch(ctypes.Structure):
+    _fields_ = [
+        ("logits", _vp), ("dtype", ctypes.c_int32), ("rows", ctypes.c_uint32),
+        ("vocab", ctypes.c_uint32), ("row_stride", ctypes.c_uint64),
+        ("temperature", _vp), ("top_k", _vp), ("top_p", _vp), ("min_p", _vp),
+        ("repetition", _vp), ("presence", _vp), ("frequency", _vp), ("uniform", _vp),
+        ("history_offsets", _vp), ("history_ids", _vp),
+        ("bias_offsets", _vp), ("bias_ids", _vp), ("bias_values", _vp),
+        ("mask_words", _vp), ("mask_stride", ctypes.c_uint64),
+        ("tokenizer_vocab", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+    ]
+
+
+class MxsOut(ctypes.Structure):
+    _fields_ = [
+        ("token", _vp), ("sampling_logprob", _vp), ("status", _vp),
+        ("kept_count", _vp), ("adjusted", _vp), ("kept_bits", _vp),
+    ]
+
+
+# Exported symbols and their prototypes, as declared in include/mx_sampler.h.
+PROTOTYPES = {
+    "mxs_abi_version": (ctypes.c_int, []),
+    "mxs_status_string": (ctypes.c_char_p, [ctypes.c_int32]),
+    "mxs_create": (ctypes.c_int, [ctypes.c_int, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_vp)]),
+    "mxs_destroy": (ctypes.c_int, [_vp]),
+    "mxs_set_stream": (ctypes.c_int, [_vp, _vp]),
+    "mxs_sample": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), ctypes.POINTER(MxsOut)]),
+    "mxs_logsoftmax_topn": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_uint64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _vp]),
+    "mxs_spec_verify": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                       _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mxs_sync": (ctypes.c_int, [_vp]),
+    "mxs_last_error": (ctypes.c_char_p, [_vp]),
+}
+
+_LIB = None
+
+
+class SamplerError(RuntimeError):
+    pass
+
+
+def load_library(path: Optional[Path] = None):
+    """Loads the built library; raises when it is missing (no fallback)."""
+    global _LIB
+    if _LIB is not None and path is None:
+        return _LIB
+    p = Path(path) if path else LIB_PATH
+    if not p.exists():
+        raise SamplerError(f"{p} is not built: run `python -m metallix_amd.build` (hipcc, gfx950)")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if path is None:
+        _LIB = lib
+    return lib
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+@dataclass
+class SampleResult:
+    token: "object"
+    sampling_logprob: "object"
+    status: "object"
+    kept_count: "object"
+    adjusted: "object" = None
+    kept_bits: "object" = None
+
+
+class Sampler:
+    """One sampler context on one GPU and stream (not thread-safe)."""
+
+    def __init__(self, max_rows: int, max_vocab: int, device: int = 0, stream=None):
+        import torch
+
+        if not torch.cuda.is_available():
+            raise SamplerError("no GPU visible: the HIP sampler has no CPU path")
+        self.torch = torch
+        self.lib = load_library()
+        self.device = device
+        self.stream = stream if stream is not None else torch.cuda.current_stream(device)
+        ctx = _vp()
+        rc = self.lib.mxs_create(device, _vp(self.stream.cuda_stream), max_rows, max_vocab, ctypes.byref(ctx))
+        if rc != 0:
+            raise SamplerError(f"mxs_create failed: {rc}")
+        self.ctx = ctx
+        self.max_rows = max_rows
+        self.max_vocab = max_vocab
+
+    def close(self):
+        if getattr(self, "ctx", None):
+            self.lib.mxs_destroy(self.ctx)
+            self.ctx = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc: int, what: str):
+        if rc != 0:
+            msg = self.lib.mxs_last_error(self.ctx)
+            raise SamplerError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")
+
+    def sample(self, logits, temperature, *, top_k=None, top_p=None, min_p=None, repetition=None,
+               presence=None, frequency=None, uniform=None, history=None, bias=None, mask=None,
+               tokenizer_vocab=None, debug: bool = False, out: Optional[SampleResult] = None,
+               vocab: Optional[int] = None) -> SampleResult:
+        """Queues one batched pick.  All tensor arguments live on the GPU.
+
+        history: (offsets u32[rows+1], ids u32) CSR; bias: (offsets, ids, values f32);
+        mask: u32[rows, mask_stride].
+        """
+        torch = self.torch
+        rows = logits.shape[0]
+        V = vocab if vocab is not None else logits.shape[1]
+        dev = logits.device
+        if out is None:
+            out = SampleResult(
+                token=torch.empty(rows, dtype=torch.int32, device=dev),
+                sampling_logprob=torch.empty(rows, dtype=torch.float64, device=dev),
+                status=torch.empty(rows, dtype=torch.int32, device=dev),
+                kept_count=torch.empty(rows, dtype=torch.int32, device=dev),
+            )
+            if debug:
+                out.adjusted = torch.empty((rows, V), dtype=torch.float32, device=dev)
+                out.kept_bits = torch.empty((rows, (V + 31) // 32), dtype=torch.int32, device=dev)
+        b = MxsBatch()
+        b.logits = logits.data_ptr()
+        b.dtype = MXS_BF16 if logits.dtype == torch.bfloat16 else MXS_F32
+        b.rows = rows
+        b.vocab = V
+        b.row_stride = logits.stride(0)
+        b.temperature = _ptr(temperature)
+        b.top_k = _ptr(top_k)
+        b.top_p = _ptr(top_p)
+        b.min_p = _ptr(min_p)
+        b.repetition = _ptr(repetition)
+        b.presence = _ptr(presence)
+        b.frequency = _ptr(frequency)
+        b.uniform = _ptr(uniform)
+        if history is not None:
+            b.history_offsets, b.history_ids = _ptr(history[0]), _ptr(history[1])
+        if bias is not None:
+            b.bias_offsets, b.bias_ids, b.bias_values = _ptr(bias[0]), _ptr(bias[1]), _ptr(bias[2])
+        if mask is not None:
+            b.mask_words = mask.data_ptr()
+            b.mask_stride = mask.stride(0)
+            b.tokenizer_vocab = V if tokenizer_vocab is None else tokenizer_vocab
+        o = MxsOut()
+        o.token = out.token.data_ptr()
+        o.sampling_logprob = _ptr(out.sampling_logprob)
+        o.status = out.status.data_ptr()
+        o.kept_count = _ptr(out.kept_count)
+        o.adjusted = _ptr(out.adjusted)
+        o.kept_bits = _ptr(out.kept_bits)
+        self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
+        self._keep = (b, o)
+        return out
+
+    def sync(self):
+        self._check(self.lib.mxs_sync(self.ctx), "mxs_sync")
