@@ -1,0 +1,191 @@
+"""Benchmark: sampled rows/s of the HIP token sampler on one MI355X.
+
+Workload (the metric's configuration): B=64 rows x
+V=151936 f32 logits drawn N(0, 2^2) with 1-50 peaks per row, per-row
+temperature U[0.3, 1.5], top_k in {0, 20, 50, 1000}, top_p U[0.5, 1),
+min_p 0.05, presence 0.5 / frequency 0.3 / repetition 1.1 over 2048-token
+Zipf(1.1) histories, one seeded uniform per row.  One step = one full
+pipeline pass (penalties + top-k + top-p + min-p + draw) over the batch.
+
+Inputs are resident in HBM before timing starts.  The logits rotate over 8
+copies (311 MB, more than the 256 MB Infinity Cache) so every step streams
+its logits from HBM rather than from the cache.  The CPU baseline is the C
+restatement of the reference sampler (oracle/) timed on this host on a
+bounded sample of the same rows.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "sampled rows/s at B=64,V=151936 fp32; achieved HBM GB/s vs MI355X peak"
+HBM_PEAK_GBS = 8000.0
+NBUF = 8
+
+
+def algorithmic_bytes(b) -> int:
+    """Compulsory bytes of one pass: inputs read once, required outputs written once."""
+    n = b.logits.nbytes                                  # 38,895,616
+    n += b.history_ids.nbytes + b.history_offsets.nbytes  # 524,288 + 260
+    n += b.rows * (8 + 4 + 8 + 8 + 4 + 4 + 4 + 8)        # T, top_k, top_p, min_p, rep, pres, freq, u
+    n += b.rows * (4 + 8 + 4)                            # token, sampling_logprob, status
+    return n
+
+
+def cpu_baseline(b, seconds: float):
+    """Times the oracle (the reference sampler restated in C) on this host."""
+    import numpy as np
+    from oracle import oracle
+
+    oracle.lib()
+    rows_done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        oracle.sample_batch(b)
+        rows_done += b.rows
+    single = rows_done / (time.perf_counter() - t0)
+    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+    rows_mt, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        oracle.sample_batch_threads(b, threads)
+        rows_mt += b.rows
+    multi = rows_mt / (time.perf_counter() - t0)
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(single, 2), "unit": "rows/s", "cores": 1, "kind": "port",
+        "sample": f"{rows_done} rows of the same cfg2 batch (1 thread, rows serial, {seconds:.0f} s)",
+        "multi_thread": {"value": round(multi, 2), "cores": threads, "sample": f"{rows_mt} rows"},
+        "cpu": cpu,
+    }
+
+
+def committed_traffic():
+    p = ROOT / "profiles" / "sample_kernel_cfg2_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from metallix_amd import Sampler, synth
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import to_device
+
+    assert torch.cuda.is_available(), "bench.py needs the GPU"
+    b = synth.config2()
+    logits, kw = to_device(torch, b)
+    bufs = [logits] + [logits.clone() for _ in range(NBUF - 1)]
+    stream = torch.cuda.Stream()
+    s = Sampler(max_rows=b.rows, max_vocab=b.vocab, stream=stream)
+    with torch.cuda.stream(stream):
+        launch = s.launcher(bufs[0], **kw)
+        out = launch.out
+        for i in range(args.warmup):
+            launch(bufs[i % NBUF])
+    torch.cuda.synchronize()
+    # Timed region: K back-to-back steps on the sampler's stream, bracketed by
+    # events on that stream; a second pair per launch gives kernel durations.
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    t_begin = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        t_begin.record(stream)
+        for i in range(args.steps):
+            launch(bufs[i % NBUF])
+        t_end.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t_begin.elapsed_time(t_end)
+    # kernel durations: a separate pass with an event pair around each launch
+    with torch.cuda.stream(stream):
+        for i in range(args.steps):
+            starts[i].record(stream)
+            launch(bufs[i % NBUF])
+            ends[i].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
+    kern_ms = float(np.mean(per))
+    status = out.status.cpu().numpy()
+    assert (status >= 0).all(), f"row errors in the benchmark batch: {status}"
+
+    ms_per_step = total_ms / args.steps
+    rows_per_s = b.rows / (ms_per_step / 1e3)
+    bytes_ = algorithmic_bytes(b)
+    achieved = bytes_ / (kern_ms / 1e3) / 1e9
+    step_gbs = bytes_ / (ms_per_step / 1e3) / 1e9
+    props = torch.cuda.get_device_properties(0)
+    res = {
+        "metric": METRIC,
+        "value": round(rows_per_s, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32 logits, f64 sampling math",
+        "data": "synthetic (seeded SplitMix64, BASELINE config 2)",
+        "config": {
+            "workload": "cfg2: B=64 x V=151936 f32, penalties + top-k {0,20,50,1000} + top-p U[.5,1) + "
+                        "min-p .05 + inverse-CDF draw; logits rotated over 8 HBM copies",
+            "rows": b.rows, "vocab": b.vocab, "history": 2048,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": committed_traffic(),
+            "kernel": "sample_kernel<float>",
+            "algorithmic_bytes": bytes_,
+            "kernel_ms_mean": round(kern_ms, 6),
+            "kernel_ms_median": round(per[len(per) // 2], 6),
+            "step_gbs": round(step_gbs, 1),
+            "device": props.name,
+        },
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(b, args.cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -138,6 +138,12 @@ int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const float* draft
                     const double* bonus_uniform, int32_t* out_tokens, int32_t* out_count,
                     int32_t* out_accepted, int32_t* status);
 int mxs_sync(mxs_ctx* ctx);
+/* Diagnostics (no reference counterpart): when `device_buffer` is non-null,
+ * mxs_sample records 100 MHz wall-clock stamps at fixed phase boundaries:
+ * u64 [rows][MXS_DEBUG_TIMING_SLOTS][8], chunk workgroups at slot = chunk,
+ * the row finisher at slot MXS_DEBUG_TIMING_SLOTS - 1.  NULL disables. */
+#define MXS_DEBUG_TIMING_SLOTS 65
+int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer);
 const char* mxs_last_error(const mxs_ctx* ctx);
 const char* mxs_status_string(int32_t status);
 int mxs_abi_version(void);

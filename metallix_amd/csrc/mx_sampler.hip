@@ -30,6 +30,7 @@
 #include <string.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/mx_sampler.h"
 #include "mxs_math.h"
@@ -42,11 +43,15 @@ constexpr int PER_MAX = 10;               // 4-token quads per thread per chunk
 constexpr int SLICE = NT * 4;             // tokens per slice (one quad per thread)
 constexpr int CHUNK_MAX = SLICE * PER_MAX;
 constexpr int MAXC = 64;                  // chunks per row (vocab <= MAXC * CHUNK_MAX)
-constexpr int ECAP = 4096;                // finisher's LDS set capacity
+constexpr int CCAP = 8192;                // candidates the finisher caches in LDS
+constexpr int ECAP = 4096;                // finisher's exact working-set capacity
 constexpr int KCAND_MAX = ECAP;           // top_k served from per-chunk candidates
 constexpr int NB = 2048;                  // radix-select bins (11 bits)
 constexpr int HB = 1024;                  // chunk top-k histogram bins
 constexpr float HRANGE = 32.0f;           // logit units covered by HB bins
+constexpr int HCAP = 4 * NT;              // history ids staged in LDS
+constexpr int BCAP = 2 * NT;              // bias entries staged in LDS
+constexpr int MCAP = CHUNK_MAX / 32 + 2;  // mask words of one chunk
 constexpr uint32_t NONE = 0xffffffffu;
 constexpr double U = 1.1102230246251565e-16;  // 2^-53
 
@@ -81,7 +86,18 @@ struct SampleArgs {
   uint32_t C;          // chunks per row
   uint32_t per;        // quads per thread per chunk (<= PER_MAX)
   uint32_t CH;         // tokens per chunk (multiple of 4)
+  uint64_t* timing;    // optional phase timestamps (diagnostics), see mxs_debug_set_timing
+  uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
 };
+
+// Phase timestamps for diagnostics: wall clock (100 MHz) at fixed points of
+// each chunk workgroup and each row finisher.
+// Every lane stores the same value (a uniform branch only): a lane-0
+// condition would make the compiler move uniform values into vector
+// registers.
+__device__ __forceinline__ void stamp(const SampleArgs& A, uint32_t row, uint32_t chunk, uint32_t k) {
+  if (A.timing) A.timing[((uint64_t)row * (MAXC + 1) + chunk) * 8 + k] = wall_clock64();
+}
 
 // ---------------------------------------------------------------------------
 // Device-scope (coherent across workgroups and XCDs) loads and stores.  Data
@@ -179,8 +195,12 @@ __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t
 // ---------------------------------------------------------------------------
 // Shared memory: one static pool, carved per phase.
 struct ChunkSmem {
-  uint32_t tab[SLICE];                 // per-slice history counts
-  uint32_t btab[SLICE];                // per-slice bias slot (index + 1)
+  uint32_t tab[2][SLICE];              // per-slice history counts (double-buffered)
+  uint32_t btab[2][SLICE];             // per-slice bias slot, index + 1 (double-buffered)
+  uint32_t hids[HCAP];                 // the row's history ids (when at most HCAP)
+  uint32_t bids[BCAP];                 // the row's bias ids and values (when at most BCAP)
+  float bvals[BCAP];
+  uint32_t mask[MCAP];                 // the chunk's grammar-mask words
   uint32_t hist[HB];                   // top-k threshold histogram
   uint32_t wcnt[PER_MAX * NW];         // candidates per (slice, wave)
   uint32_t woff[PER_MAX * NW];
@@ -193,13 +213,20 @@ struct ChunkSmem {
   uint32_t s_last;
 };
 struct FinSmem {
-  float e_l[ECAP];
-  uint32_t e_id[ECAP];
-  double e_w[ECAP];
-  unsigned long long skey[ECAP];       // sort keys: (key << 32) | ~id, descending
-  uint32_t sidx[ECAP];                 // sort payload: index into e_*
-  uint32_t hcnt[NB];
-  double hmass[NB];
+  float cl[CCAP];                      // candidates cached in LDS, token-ID order
+  uint32_t cid[CCAP];
+  uint32_t eidx[ECAP];                 // working set E: indices into the candidates
+  union {
+    struct {
+      double ew[ECAP];                 // weights of E
+      unsigned long long skey[ECAP];   // sort keys: (key << 32) | ~E-index, descending
+    } e;
+    struct {
+      uint32_t hcnt[NB];               // radix-select histograms
+      double hmass[NB];
+    } h;
+  } u;
+  uint8_t kflag[ECAP];                 // kept flags by E index
   ChunkStat st[MAXC];
   double cscale[MAXC];
   uint32_t coff[MAXC + 1];
@@ -207,7 +234,7 @@ struct FinSmem {
   double red_d[NW];
   float red_f[NW];
   uint32_t red_i[NW];
-  uint32_t s_u[8];
+  uint32_t s_u[16];
   double s_d[8];
 };
 constexpr size_t SMEM_BYTES = sizeof(FinSmem) > sizeof(ChunkSmem) ? sizeof(FinSmem) : sizeof(ChunkSmem);
@@ -223,19 +250,41 @@ struct RowCfg {
   bool greedy;
 };
 
-__device__ RowCfg load_cfg(const mxs_batch& b, uint32_t row) {
+// Per-row parameter arrays, passed as separate read-only kernel arguments so
+// the compiler reads them with scalar loads (uniform per workgroup).  The
+// host substitutes default arrays for the ABI's NULLs, so none is null here.
+struct RowParams {
+  const double* __restrict__ temperature;
+  const uint32_t* __restrict__ top_k;
+  const double* __restrict__ top_p;
+  const double* __restrict__ min_p;
+  const float* __restrict__ repetition;
+  const float* __restrict__ presence;
+  const float* __restrict__ frequency;
+  const double* __restrict__ uniform;
+  const uint32_t* __restrict__ history_offsets;
+  const uint32_t* __restrict__ bias_offsets;
+};
+
+__device__ __forceinline__ RowCfg load_cfg(const double* __restrict__ temperature, const uint32_t* __restrict__ top_k,
+                                           const double* __restrict__ top_p, const double* __restrict__ min_p,
+                                           const float* __restrict__ repetition, const float* __restrict__ presence,
+                                           const float* __restrict__ frequency, const double* __restrict__ uniform,
+                                           const uint32_t* __restrict__ hoff, const uint32_t* __restrict__ boff,
+                                           uint32_t row) {
   RowCfg c;
-  c.T = b.temperature[row];
-  c.top_p = b.top_p ? b.top_p[row] : 1.0;
-  c.min_p = b.min_p ? b.min_p[row] : 0.0;
-  c.u = b.uniform ? b.uniform[row] : 0.0;
-  c.k = b.top_k ? b.top_k[row] : 0u;
-  c.rep = b.repetition ? b.repetition[row] : 1.0f;
-  c.pres = b.presence ? b.presence[row] : 0.0f;
-  c.freq = b.frequency ? b.frequency[row] : 0.0f;
-  c.hb = c.he = c.bb = c.be = 0;
-  if (b.history_offsets) { c.hb = b.history_offsets[row]; c.he = b.history_offsets[row + 1]; }
-  if (b.bias_offsets) { c.bb = b.bias_offsets[row]; c.be = b.bias_offsets[row + 1]; }
+  c.T = temperature[row];
+  c.top_p = top_p[row];
+  c.min_p = min_p[row];
+  c.u = uniform[row];
+  c.k = top_k[row];
+  c.rep = repetition[row];
+  c.pres = presence[row];
+  c.freq = frequency[row];
+  c.hb = hoff[row];
+  c.he = hoff[row + 1];
+  c.bb = boff[row];
+  c.be = boff[row + 1];
   c.err = 0;
   c.greedy = c.T == 0.0;
   if (!(c.T >= 0.0) || !isfinite(c.T)) c.err = MXS_ROW_INVALID_TEMPERATURE;
@@ -270,9 +319,8 @@ __device__ __forceinline__ uint32_t chunk_mode(const RowCfg& c, uint32_t V) {
 
 // Logit-bias and penalty stage for one token (BUILD-DEFINED semantics, f32,
 // every operation rounded separately).
-__device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, const RowCfg& c,
-                                       const float* bias_values) {
-  if (slot) l = l + bias_values[c.bb + slot - 1];
+__device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, float bias, const RowCfg& c) {
+  if (slot) l = l + bias;
   if (cnt) {
     l = l < 0.0f ? l * c.rep : l / c.rep;
     const float cf = (float)cnt * c.freq;
@@ -317,23 +365,19 @@ __device__ void rederive_token(const SampleArgs& A, const RowCfg& c, uint32_t ro
   for (uint32_t h = c.hb; h < c.he; ++h) cnt += b.history_ids[h] == id;
   for (uint32_t j = c.bb; j < c.be; ++j)
     if (b.bias_ids[j] == id) slot = j - c.bb + 1;
-  *l_out = adjust(l, cnt, slot, c, b.bias_values);
-  bool legal = true;
-  if (b.mask_words) {
-    const uint32_t w = b.mask_words[(uint64_t)row * b.mask_stride + (id >> 5)];
-    legal = ((w >> (id & 31)) & 1u) && id < b.tokenizer_vocab;
-  }
-  *legal_out = legal;
+  *l_out = adjust(l, cnt, slot, slot ? b.bias_values[c.bb + slot - 1] : 0.0f, c);
+  const uint32_t w = b.mask_words[(uint64_t)row * b.mask_stride + (id >> 5)];
+  *legal_out = ((w >> (id & 31)) & 1u) && id < b.tokenizer_vocab;
 }
 
 // ---------------------------------------------------------------------------
 // Finisher helpers.
 
-// Bitonic sort of n (<= ECAP) descending keys with payload, in LDS.
-__device__ void bitonic_sort_desc(unsigned long long* key, uint32_t* idx, uint32_t n) {
+// Bitonic sort of n (<= ECAP) keys into descending order, in LDS.
+__device__ void bitonic_sort_desc(unsigned long long* key, uint32_t n) {
   uint32_t np = 1;
   while (np < n) np <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < np; i += NT) { key[i] = 0ull; idx[i] = NONE; }
+  for (uint32_t i = n + threadIdx.x; i < np; i += NT) key[i] = 0ull;
   __syncthreads();
   for (uint32_t size = 2; size <= np; size <<= 1) {
     for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
@@ -341,11 +385,8 @@ __device__ void bitonic_sort_desc(unsigned long long* key, uint32_t* idx, uint32
         const uint32_t i = 2 * stride * (t / stride) + (t % stride);
         const uint32_t j = i + stride;
         const bool desc = ((i & size) == 0);
-        unsigned long long a = key[i], bb = key[j];
-        if ((a < bb) == desc) {
-          key[i] = bb; key[j] = a;
-          uint32_t ti = idx[i]; idx[i] = idx[j]; idx[j] = ti;
-        }
+        const unsigned long long a = key[i], bb = key[j];
+        if ((a < bb) == desc) { key[i] = bb; key[j] = a; }
       }
       __syncthreads();
     }
@@ -363,19 +404,19 @@ __device__ __forceinline__ double sum_bound(double s, uint32_t n, double term_ul
 }
 
 // ---------------------------------------------------------------------------
-// Finisher path for a working set E larger than the LDS capacity: E stays in
-// the candidate arrays (global memory, token-ID order) and is filtered by a
-// predicate on every pass; the nucleus cut comes from a mass-weighted radix
-// select (three 11/11/10-bit passes with LDS count and f64 mass histograms)
-// whose bin decisions are certified against the same error bounds.
-struct LargeCtx {
+// Finisher state shared by its phases.
+struct FinCtx {
   const SampleArgs* A;
   const RowCfg* c;
-  uint32_t row, mode, C, ncand, ne, nlegal;
+  uint32_t row, mode, C, V, ncand, nlegal;
+  uint64_t rbase;
+  bool lds_c;          // candidates cached in LDS
   bool k_path;
   uint32_t kappa, id_tie;
   double M, L, Lclose, total, total_err;
   bool have_total;
+  uint32_t* kbits;
+  uint32_t nwords;
 };
 
 __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, uint64_t rbase, uint32_t CH, uint32_t j) {
@@ -384,66 +425,73 @@ __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, ui
   return rbase + (uint64_t)q * CH + (j - F.coff[q]);
 }
 
-__device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint32_t* kbits, uint32_t nwords) {
-  const SampleArgs& A = *X.A;
+// Candidate j (token-ID order): from LDS when cached, else from the
+// device-scope candidate arrays.
+__device__ __forceinline__ float cand_l(const FinCtx& X, const FinSmem& F, uint32_t j) {
+  return X.lds_c ? F.cl[j] : ld_dev(&X.A->w.cand_l[cand_pos_of(F, X.C, X.rbase, X.A->CH, j)]);
+}
+__device__ __forceinline__ uint32_t cand_id(const FinCtx& X, const FinSmem& F, uint32_t j) {
+  return X.lds_c ? F.cid[j] : ld_dev(&X.A->w.cand_id[cand_pos_of(F, X.C, X.rbase, X.A->CH, j)]);
+}
+__device__ __forceinline__ bool member(const FinCtx& X, float l, uint32_t id) {
+  if (X.k_path) {
+    const uint32_t key = okey(l);
+    return key > X.kappa || (key == X.kappa && id <= X.id_tie);
+  }
+  if (X.mode == M_MINP) return (((double)l - X.M) / X.c->T) >= X.L;
+  return true;
+}
+
+__device__ __forceinline__ void write_result(const FinCtx& X, int32_t status, int32_t token, double lp, uint32_t kept) {
+  if (threadIdx.x == 0) {
+    const mxs_out& o = X.A->o;
+    o.token[X.row] = token;
+    o.status[X.row] = status;
+    if (o.sampling_logprob) o.sampling_logprob[X.row] = lp;
+    if (o.kept_count) o.kept_count[X.row] = kept;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Large working set (E beyond the LDS capacity): E is the predicate `member`
+// over the candidates; the nucleus cut comes from a mass-weighted radix
+// select (11/11/10-bit passes, LDS count and f64 mass histograms) whose bin
+// decisions are certified with the same bounds as the exact path.
+__device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   const RowCfg& c = *X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
-  auto member = [&](float l, uint32_t id) -> bool {
-    if (X.k_path) {
-      const uint32_t key = okey(l);
-      return key > X.kappa || (key == X.kappa && id <= X.id_tie);
-    }
-    if (X.mode == M_MINP) return (((double)l - X.M) / c.T) >= X.L;
-    return true;
-  };
-  auto finish = [&](int32_t status, int32_t token, double lp, uint32_t kept) {
-    if (tid == 0) {
-      A.o.token[X.row] = token;
-      A.o.status[X.row] = status;
-      if (A.o.sampling_logprob) A.o.sampling_logprob[X.row] = lp;
-      if (A.o.kept_count) A.o.kept_count[X.row] = kept;
-    }
-  };
+  auto weight = [&](float l) { return exp_neg(((double)l - X.M) / c.T); };
   bool uncert = false;
-  // P1: exact weights of E into cand_w (0 for non-members), their sum and minimum.
   double wpart = 0.0, wmin = INFINITY;
-  uint32_t bad = 0;
   for (uint32_t j = tid; j < n; j += NT) {
-    const uint64_t pos = cand_pos_of(F, X.C, rbase, A.CH, j);
-    const float l = ld_dev(&A.w.cand_l[pos]);
-    const uint32_t id = ld_dev(&A.w.cand_id[pos]);
-    double w = 0.0;
-    if (member(l, id)) {
-      w = exp_neg(((double)l - X.M) / c.T);
+    const float l = cand_l(X, F, j);
+    if (member(X, l, cand_id(X, F, j))) {
+      const double w = weight(l);
+      wpart += w;
       wmin = fmin(wmin, w);
     }
-    st_dev(&A.w.cand_w[pos], w);
-    wpart += w;
   }
   const double esum = block_sum<double>(wpart, F.red_d);
   wmin = -block_max<double>(-wmin, F.red_d);
   double total = X.total, total_err = X.total_err;
-  if (!X.have_total) { total = esum; total_err = sum_bound(esum, X.ne, 8.0); }
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
 
-  // P2: nucleus threshold (tau, id_cut): member kept iff key > tau or (key == tau and id <= id_cut).
-  uint32_t tau = 0, id_cut = NONE;   // default: every member
+  uint32_t tau = 0, id_cut = NONE;
   bool cut = false;
   double theta = 0.0, theta_err = 0.0;
   if (X.k_path) {
     if (c.top_p >= 1.0) {
-      // covered reaches kept only at the last head token when every weight
-      // is large enough to change the running f64 sum.
       if (!(wmin > 2.3e-16 * esum)) uncert = true;
     } else {
       cut = true;
       theta = c.top_p * esum;
-      theta_err = c.top_p * sum_bound(esum, X.ne, 8.0) + U * theta;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
     }
   } else if (c.top_p < 1.0) {
     theta = c.top_p * total;
     theta_err = c.top_p * total_err + U * theta;
-    cut = !(esum + sum_bound(esum, X.ne, 8.0) < theta - theta_err);
+    cut = !(esum + sum_bound(esum, ne, 8.0) < theta - theta_err);
   }
   if (cut) {
     uint32_t prefix = 0, pmask = 0, above_n = 0;
@@ -451,23 +499,21 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
     const int shifts[3] = {21, 10, 0};
     for (int pass = 0; pass < 3; ++pass) {
       const int sh = shifts[pass];
-      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) { F.hcnt[t] = 0u; F.hmass[t] = 0.0; }
+      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
       __syncthreads();
       for (uint32_t j = tid; j < n; j += NT) {
-        const uint64_t pos = cand_pos_of(F, X.C, rbase, A.CH, j);
-        const float l = ld_dev(&A.w.cand_l[pos]);
-        const uint32_t id = ld_dev(&A.w.cand_id[pos]);
+        const float l = cand_l(X, F, j);
         const uint32_t key = okey(l);
-        if ((key & pmask) == prefix && member(l, id)) {
+        if ((key & pmask) == prefix && member(X, l, cand_id(X, F, j))) {
           const uint32_t bin = (key >> sh) & (NB - 1);
-          atomicAdd(&F.hcnt[bin], 1u);
-          atomicAdd(&F.hmass[bin], ld_dev(&A.w.cand_w[pos]));
+          atomicAdd(&F.u.h.hcnt[bin], 1u);
+          atomicAdd(&F.u.h.hmass[bin], weight(l));
         }
       }
       __syncthreads();
       const uint32_t b_hi = NB - 1 - 2 * tid, b_lo = b_hi - 1;
-      const double mh = F.hmass[b_hi], ml = F.hmass[b_lo];
-      const uint32_t nh = F.hcnt[b_hi], nl = F.hcnt[b_lo];
+      const double mh = F.u.h.hmass[b_hi], ml = F.u.h.hmass[b_lo];
+      const uint32_t nh = F.u.h.hcnt[b_hi], nl = F.u.h.hcnt[b_lo];
       double mtot;
       uint32_t ntot;
       const double minc = above + block_scan_incl<double>(mh + ml, F.red_d, &mtot);
@@ -476,7 +522,6 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
       const uint32_t nexc = ninc - nh - nl;
       if (tid == 0) { F.s_u[4] = NONE; F.s_u[6] = 0u; }
       __syncthreads();
-      // the bin where the descending cumulative mass first reaches theta
       const double e1 = sum_bound(mexc + mh, nexc + nh + 64u, 8.0);
       if (nh && mexc < theta && theta <= mexc + mh) {
         F.s_u[4] = b_hi; F.s_u[5] = nexc; F.s_d[4] = mexc;
@@ -488,29 +533,26 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
         if (!(mexc + mh + e1 < theta - theta_err) || !(minc - e2 >= theta + theta_err)) F.s_u[6] = 1u;
       }
       __syncthreads();
-      if (F.s_u[4] == NONE) {
-        // theta beyond the accumulated mass (rounding): keep every member
-        cut = false;
-        uncert = true;
-        __syncthreads();
-        break;
-      }
-      if (F.s_u[6]) uncert = true;
-      prefix |= F.s_u[4] << sh;
-      pmask |= (uint32_t)(NB - 1) << sh;
-      above = F.s_d[4];
-      above_n = F.s_u[5];
+      const uint32_t bin = F.s_u[4];
+      const uint32_t amb = F.s_u[6];
+      const uint32_t an = F.s_u[5];
+      const double am = F.s_d[4];
       __syncthreads();
+      if (bin == NONE) { cut = false; uncert = true; break; }
+      if (amb) uncert = true;
+      prefix |= bin << sh;
+      pmask |= (uint32_t)(NB - 1) << sh;
+      above = am;
+      above_n = an;
     }
     if (cut) {
       tau = prefix;
-      // ties at tau share one weight; the reference adds them one by one
-      const double wt = exp_neg(((double)okey_value(tau) - X.M) / c.T);
+      const double wt = weight(okey_value(tau));
       if (tid == 0) {
         uint32_t jn = 0;
         double cov = above;
         bool close = false;
-        for (uint32_t q = 0; q < 1000000u; ++q) {
+        for (uint32_t q = 0; q < (uint32_t)NB * 64u; ++q) {
           cov += wt;
           ++jn;
           const double e = sum_bound(cov, above_n + jn + 64u, 8.0);
@@ -519,24 +561,20 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
         }
         F.s_u[6] = jn;
         F.s_u[7] = close ? 1u : 0u;
+        F.s_u[3] = NONE;
       }
       __syncthreads();
       const uint32_t jneed = F.s_u[6];
       if (F.s_u[7]) uncert = true;
-      __syncthreads();
-      // id of the jneed-th member with key == tau, in ID order
       uint32_t seen = 0;
-      if (tid == 0) F.s_u[3] = NONE;
-      __syncthreads();
       for (uint32_t base = 0; base < n; base += NT) {
         const uint32_t j = base + tid;
         bool tie = false;
         uint32_t id = 0;
         if (j < n) {
-          const uint64_t pos = cand_pos_of(F, X.C, rbase, A.CH, j);
-          const float l = ld_dev(&A.w.cand_l[pos]);
-          id = ld_dev(&A.w.cand_id[pos]);
-          tie = okey(l) == tau && member(l, id);
+          const float l = cand_l(X, F, j);
+          id = cand_id(X, F, j);
+          tie = okey(l) == tau && member(X, l, id);
         }
         uint32_t tt;
         const uint32_t ti = block_scan_incl<uint32_t>(tie ? 1u : 0u, F.red_u, &tt);
@@ -550,33 +588,28 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
     }
   }
 
-  // P3: kept = member, inside the nucleus cut, and (unless E is already the
-  // min-p set) at or above ln(min_p).  Draw in token-ID order.
+  // kept = member, inside the cut, and (unless E is the min-p set already)
+  // at or above ln(min_p); the draw walks kept tokens in ID order.
   const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
-  auto kept_w = [&](uint32_t j, uint32_t* id_out, double* s_out) -> double {
-    const uint64_t pos = cand_pos_of(F, X.C, rbase, A.CH, j);
-    const float l = ld_dev(&A.w.cand_l[pos]);
-    const uint32_t id = ld_dev(&A.w.cand_id[pos]);
-    *id_out = id;
-    *s_out = ((double)l - X.M) / c.T;
-    if (!member(l, id)) return -1.0;
+  auto kept = [&](float l, uint32_t id, double* s) -> bool {
+    *s = ((double)l - X.M) / c.T;
+    if (!member(X, l, id)) return false;
     if (cut) {
       const uint32_t key = okey(l);
-      if (!(key > tau || (key == tau && id <= id_cut))) return -1.0;
+      if (!(key > tau || (key == tau && id <= id_cut))) return false;
     }
-    if (apply_minp && !(*s_out >= X.L)) return -1.0;
-    return ld_dev(&A.w.cand_w[pos]);
+    return !(apply_minp && !(*s >= X.L));
   };
   double kpart = 0.0;
-  uint32_t kn = 0, close = 0;
+  uint32_t kn = 0, close = 0, bad = 0;
   for (uint32_t j = tid; j < n; j += NT) {
-    uint32_t id;
+    const float l = cand_l(X, F, j);
     double s;
-    const double w = kept_w(j, &id, &s);
+    const bool k = kept(l, cand_id(X, F, j), &s);
     if (apply_minp && fabs(s - X.L) < X.Lclose) close = 1;
-    if (w >= 0.0) { kpart += w; ++kn; if (!isfinite(s)) bad = 1; }
+    if (k) { kpart += exp_neg(s); ++kn; if (!isfinite(s)) bad = 1; }
   }
-  if (block_max<uint32_t>(bad, F.red_u)) { finish(MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+  if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
   if (block_max<uint32_t>(close, F.red_u)) uncert = true;
   const double S = block_sum<double>(kpart, F.red_d);
   const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
@@ -587,11 +620,12 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
   double run = 0.0;
   for (uint32_t base = 0; base < n; base += NT) {
     const uint32_t j = base + tid;
-    uint32_t id = 0;
     double s = 0.0, w = 0.0;
+    uint32_t id = 0;
     if (j < n) {
-      const double kw = kept_w(j, &id, &s);
-      w = kw > 0.0 ? kw : 0.0;
+      const float l = cand_l(X, F, j);
+      id = cand_id(X, F, j);
+      if (kept(l, id, &s)) w = exp_neg(s);
     }
     double tot;
     const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
@@ -599,8 +633,204 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
     if (w > 0.0) {
       atomicMax(&F.s_u[1], j + 1u);
       if (target < inc && !(target < exc)) {
-        F.s_u[0] = j;
+        F.s_u[0] = id;
         F.s_d[0] = s;
+        if (fabs(target - exc) <= derr || fabs(inc - target) <= derr) F.s_u[2] = 1u;
+      }
+    }
+    run += tot;
+  }
+  __syncthreads();
+  uint32_t tok = F.s_u[0];
+  double shifted = F.s_d[0];
+  if (F.s_u[2]) uncert = true;
+  if (tok == NONE && F.s_u[1]) {
+    // rounding left the variate past the accumulated mass: last positive kept token
+    const uint32_t j = F.s_u[1] - 1u;
+    tok = cand_id(X, F, j);
+    shifted = ((double)cand_l(X, F, j) - X.M) / c.T;
+    uncert = true;
+  }
+  __syncthreads();
+  if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, shifted - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = tid; q < X.nwords; q += NT) X.kbits[q] = 0u;
+    __syncthreads();
+    for (uint32_t j = tid; j < n; j += NT) {
+      const float l = cand_l(X, F, j);
+      const uint32_t id = cand_id(X, F, j);
+      double s;
+      if (kept(l, id, &s)) atomicOr(&X.kbits[id >> 5], 1u << (id & 31u));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exact path: E (token-ID order) fits in LDS as indices into the cached
+// candidates.  P = E's min-p prefix.  The nucleus is a prefix of E in
+// descending order; when P's mass certainly stays below the nucleus target
+// the final set is P with no sort, otherwise the crossing lies inside P and
+// only P is sorted.  An uncertain crossing replays the reference's
+// sequential f64 sums over E sorted.
+__device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_close_in) {
+  const RowCfg& c = *X.c;
+  const uint32_t tid = threadIdx.x;
+  auto el = [&](uint32_t t) { return F.cl[F.eidx[t]]; };
+  auto eid = [&](uint32_t t) { return F.cid[F.eidx[t]]; };
+  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
+  bool uncert = mp_close_in;
+  double epart = 0.0, ppart = 0.0, wmin = INFINITY;
+  uint32_t pn = 0, close = 0;
+  for (uint32_t t = tid; t < ne; t += NT) {
+    const double s = ((double)el(t) - X.M) / c.T;
+    const double w = exp_neg(s);
+    F.u.e.ew[t] = w;
+    epart += w;
+    wmin = fmin(wmin, w);
+    bool inp = true;
+    if (apply_minp) {
+      inp = s >= X.L;
+      if (fabs(s - X.L) < X.Lclose) close = 1;
+    }
+    F.kflag[t] = inp ? 1 : 0;   // provisional: in P
+    if (inp) { ppart += w; ++pn; }
+  }
+  const double esum = block_sum<double>(epart, F.red_d);
+  const double psum = block_sum<double>(ppart, F.red_d);
+  const uint32_t np_ = block_sum<uint32_t>(pn, F.red_u);
+  wmin = -block_max<double>(-wmin, F.red_d);
+  if (block_max<uint32_t>(close, F.red_u)) uncert = true;
+  double total = X.total, total_err = X.total_err;
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
+
+  // The nucleus over E in descending order, intersected with P.
+  bool theta_set = false, replay = false;
+  double theta = 0.0, theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      // covered reaches kept only at E's last token when every weight is
+      // large enough to change the running f64 sum; otherwise replay.
+      replay = !(wmin > 2.3e-16 * esum);
+    } else {
+      theta_set = true;
+      theta = c.top_p * esum;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
+    }
+  } else if (c.top_p < 1.0) {
+    theta_set = true;
+    theta = c.top_p * total;
+    theta_err = c.top_p * total_err + U * theta;
+  }
+  if (theta_set && !(psum + sum_bound(psum, np_, 8.0) < theta - theta_err)) {
+    // The crossing lies inside P: sort P and find the first prefix reaching theta.
+    if (tid == 0) F.s_u[8] = 0u;
+    __syncthreads();
+    for (uint32_t t = tid; t < ne; t += NT) {
+      if (F.kflag[t]) {
+        const uint32_t at = atomicAdd(&F.s_u[8], 1u);
+        F.u.e.skey[at] = ((unsigned long long)okey(el(t)) << 32) | (unsigned long long)(0xffffffffu - t);
+      }
+    }
+    __syncthreads();
+    bitonic_sort_desc(F.u.e.skey, np_);
+    if (tid == 0) { F.s_u[6] = NONE; F.s_u[7] = 0u; }
+    __syncthreads();
+    double run = 0.0;
+    for (uint32_t base = 0; base < np_; base += NT) {
+      const uint32_t p = base + tid;
+      const double w = p < np_ ? F.u.e.ew[0xffffffffu - (uint32_t)F.u.e.skey[p]] : 0.0;
+      double tot;
+      const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
+      const double exc = inc - w;
+      if (p < np_) {
+        const double e_inc = sum_bound(inc, p + 65u, 8.0);
+        const double e_exc = sum_bound(exc, p + 64u, 8.0);
+        const bool lt = inc + e_inc < theta - theta_err;
+        if (!lt) {
+          const bool prev_lt = p == 0 || exc + e_exc < theta - theta_err;
+          if (prev_lt) {
+            F.s_u[6] = p;   // the first position not certainly below theta
+            if (!(inc - e_inc >= theta + theta_err)) F.s_u[7] = 1u;
+          }
+        }
+      }
+      run += tot;
+    }
+    __syncthreads();
+    const uint32_t first = F.s_u[6];
+    if (first == NONE || F.s_u[7]) {
+      replay = true;
+    } else {
+      // kept = the first `first + 1` sorted positions of P
+      for (uint32_t t = tid; t < ne; t += NT) F.kflag[t] = 0;
+      __syncthreads();
+      for (uint32_t p = tid; p <= first; p += NT) F.kflag[0xffffffffu - (uint32_t)F.u.e.skey[p]] = 1;
+    }
+    __syncthreads();
+  }
+  if (replay) {
+    // Sort all of E and replay the reference's sequential f64 sums.
+    for (uint32_t t = tid; t < ne; t += NT)
+      F.u.e.skey[t] = ((unsigned long long)okey(el(t)) << 32) | (unsigned long long)(0xffffffffu - t);
+    __syncthreads();
+    bitonic_sort_desc(F.u.e.skey, ne);
+    if (tid == 0) {
+      double th = theta;
+      if (X.k_path) {
+        double keptsum = 0.0;
+        for (uint32_t q = 0; q < ne; ++q) keptsum += F.u.e.ew[0xffffffffu - (uint32_t)F.u.e.skey[q]];
+        th = c.top_p * keptsum;
+      }
+      double cov = 0.0;
+      uint32_t nk = ne, cl = 0;
+      for (uint32_t q = 0; q < ne; ++q) {
+        cov += F.u.e.ew[0xffffffffu - (uint32_t)F.u.e.skey[q]];
+        if (!X.k_path && fabs(cov - th) <= theta_err + sum_bound(cov, q + 1, 8.0)) cl = 1;
+        if (cov >= th) { nk = q + 1; break; }
+      }
+      F.s_u[6] = nk;
+      F.s_u[7] = cl;
+    }
+    __syncthreads();
+    const uint32_t nk = F.s_u[6];
+    if (F.s_u[7]) uncert = true;
+    // kept = sorted positions < nk, intersected with P
+    for (uint32_t p = tid; p < ne; p += NT) {
+      const uint32_t t = 0xffffffffu - (uint32_t)F.u.e.skey[p];
+      if (p >= nk) F.kflag[t] = 0;
+    }
+    __syncthreads();
+  }
+
+  // sample_categorical rejects a kept token whose shifted logit overflows.
+  uint32_t bad = 0;
+  for (uint32_t t = tid; t < ne; t += NT)
+    if (F.kflag[t] && !isfinite(((double)el(t) - X.M) / c.T)) bad = 1;
+  if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+
+  // Inverse-CDF draw over the kept set in token-ID order.
+  double kpart = 0.0;
+  uint32_t kn = 0;
+  for (uint32_t t = tid; t < ne; t += NT)
+    if (F.kflag[t]) { kpart += F.u.e.ew[t]; ++kn; }
+  const double S = block_sum<double>(kpart, F.red_d);
+  const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
+  __syncthreads();
+  double run = 0.0;
+  for (uint32_t base = 0; base < ne; base += NT) {
+    const uint32_t t = base + tid;
+    const double w = (t < ne && F.kflag[t]) ? F.u.e.ew[t] : 0.0;
+    double tot;
+    const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
+    const double exc = inc - w;
+    if (w > 0.0) {
+      atomicMax(&F.s_u[1], t + 1u);
+      if (target < inc && !(target < exc)) {
+        F.s_u[0] = t;
         if (fabs(target - exc) <= derr || fabs(inc - target) <= derr) F.s_u[2] = 1u;
       }
     }
@@ -609,29 +839,18 @@ __device__ void finish_large(const LargeCtx& X, FinSmem& F, uint64_t rbase, uint
   __syncthreads();
   uint32_t pick = F.s_u[0];
   if (F.s_u[2]) uncert = true;
-  double shifted = F.s_d[0];
   if (pick == NONE) {
-    uncert = true;
     pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
-    if (pick != NONE) {
-      uint32_t id;
-      kept_w(pick, &id, &shifted);
-    }
+    uncert = true;
   }
-  __syncthreads();
-  if (pick == NONE) { finish(MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
-  uint32_t tok;
-  double sh2;
-  kept_w(pick, &tok, &sh2);
-  finish(uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, shifted - log(S), nkept);
-  if (kbits) {
-    for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = 0u;
+  if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+  const double shifted = ((double)el(pick) - X.M) / c.T;
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)eid(pick), shifted - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = tid; q < X.nwords; q += NT) X.kbits[q] = 0u;
     __syncthreads();
-    for (uint32_t j = tid; j < n; j += NT) {
-      uint32_t id;
-      double s;
-      if (kept_w(j, &id, &s) >= 0.0) atomicOr(&kbits[id >> 5], 1u << (id & 31u));
-    }
+    for (uint32_t t = tid; t < ne; t += NT)
+      if (F.kflag[t]) atomicOr(&X.kbits[eid(t) >> 5], 1u << (eid(t) & 31u));
   }
 }
 
@@ -684,22 +903,17 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   const int32_t err = combine_errors(c, flags, nlegal);
   const uint32_t nwords = (V + 31u) / 32u;
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
-  auto finish = [&](int32_t status, int32_t token, double lp, uint32_t kept) {
-    if (tid == 0) {
-      A.o.token[row] = token;
-      A.o.status[row] = status;
-      if (A.o.sampling_logprob) A.o.sampling_logprob[row] = lp;
-      if (A.o.kept_count) A.o.kept_count[row] = kept;
-    }
-  };
+  FinCtx X;
+  X.A = &A; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
+  X.kbits = kbits; X.nwords = nwords; X.M = M;
   if (err) {
-    finish(err, -1, 0.0, 0u);
+    write_result(X, err, -1, 0.0, 0u);
     if (kbits)
       for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = 0u;
     return;
   }
   if (mode == M_GREEDY) {
-    finish(0, (int32_t)bi, 0.0, 1u);
+    write_result(X, 0, (int32_t)bi, 0.0, 1u);
     if (kbits)
       for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = (q == (bi >> 5)) ? (1u << (bi & 31u)) : 0u;
     return;
@@ -711,10 +925,9 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     uint32_t mink = NONE;
     for (uint32_t q = 0; q < C; ++q)
       if (F.st[q].nlegal && F.st[q].minkey < mink) mink = F.st[q].minkey;
-    if (!isfinite(((double)okey_value(mink) - M) / c.T)) { finish(MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+    if (!isfinite(((double)okey_value(mink) - M) / c.T)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
     const uint32_t segs_per_chunk = A.per * NW;
     const uint32_t nseg = C * segs_per_chunk;
-    // total mass
     double part = 0.0;
     for (uint32_t s = tid; s < nseg; s += NT) {
       const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
@@ -722,7 +935,7 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     }
     const double total = block_sum<double>(part, F.red_d);
     const double target = c.u * total;
-    // Bound: each segment mass carries the x = (l - m) / T product rounding
+    // Each segment mass carries the x = (l - m) / T product rounding
     // (x e^x <= 1/e per token) and 8 ulp per weight; plus the scale factors.
     const double err_b = sum_bound(total, nlegal + nseg, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
     if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
@@ -753,19 +966,17 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     bool near = F.s_u[2] != 0u;
     double before = F.s_d[0];
     if (seg == NONE) {
-      // rounding left the variate past the accumulated mass
       seg = F.s_u[1] ? F.s_u[1] - 1u : NONE;
       near = true;
       before = -INFINITY;   // forces the last positive token of the segment
     }
-    if (seg == NONE) { finish(MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+    if (seg == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
     if (wave() == 0) {
       const uint32_t q = seg / segs_per_chunk, r = seg % segs_per_chunk;
       const uint32_t i = r / NW, w = r % NW;
       const uint32_t q1 = min(V, q * A.CH + A.CH);
       const uint32_t id0 = q * A.CH + i * SLICE + w * 256u + lane() * 4u;
-      double wl[4];
-      double sh[4];
+      double wl[4], sh[4];
       double lsum = 0.0;
       for (int e = 0; e < 4; ++e) {
         const uint32_t id = id0 + (uint32_t)e;
@@ -820,14 +1031,14 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     }
     __syncthreads();
     const uint32_t tok = F.s_u[3];
-    if (tok == NONE) { finish(MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+    if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
     near = near || F.s_u[4] != 0u;
-    finish(near ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, F.s_d[1] - log(total), nlegal);
+    write_result(X, near ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, F.s_d[1] - log(total), nlegal);
     if (kbits) {
       for (uint32_t q = tid; q < nwords; q += NT) {
         uint32_t wv = 0xffffffffu;
         if (q == nwords - 1 && (V & 31u)) wv = (1u << (V & 31u)) - 1u;
-        if (b.mask_words) {
+        if (A.masked) {
           wv &= b.mask_words[(uint64_t)row * b.mask_stride + q];
           const uint32_t tv = b.tokenizer_vocab;
           if (q * 32u >= tv) wv = 0u;
@@ -840,45 +1051,84 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   }
 
   // =================== candidate paths ====================================
-  const uint32_t ncand_total = F.coff[C];
-  auto cand_pos = [&](uint32_t j) -> uint64_t {
-    uint32_t q = 0;
-    while (q + 1 < C && F.coff[q + 1] <= j) ++q;
-    return rbase + (uint64_t)q * A.CH + (j - F.coff[q]);
-  };
+  const uint32_t ncand = F.coff[C];
+  X.ncand = ncand;
+  X.lds_c = ncand <= (uint32_t)CCAP;
+  // One bulk load of every candidate into LDS: all loads in flight at once.
+  if (X.lds_c) {
+    for (uint32_t j0 = 0; j0 < ncand; j0 += NT * 4u) {
+      float lv8[4];
+      uint32_t iv8[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t j = j0 + (uint32_t)u * NT + tid;
+        if (j < ncand) {
+          const uint64_t pos = cand_pos_of(F, C, rbase, A.CH, j);
+          lv8[u] = ld_dev(&A.w.cand_l[pos]);
+          iv8[u] = ld_dev(&A.w.cand_id[pos]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t j = j0 + (uint32_t)u * NT + tid;
+        if (j < ncand) { F.cl[j] = lv8[u]; F.cid[j] = iv8[u]; }
+      }
+    }
+    __syncthreads();
+  }
+  stamp(A, row, MAXC, 1);
   const double L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
   // ln(min_p) is exact for min_p = 1 (and -inf for 0); otherwise device and
   // host logs may differ in the last ulps, so a shifted logit within 4 ulp is
   // an uncertain cut.
-  const double Lclose = (c.min_p > 0.0 && c.min_p < 1.0) ? 4.0 * U * fabs(L) : 0.0;
+  X.L = L;
+  X.Lclose = (c.min_p > 0.0 && c.min_p < 1.0) ? 4.0 * U * fabs(L) : 0.0;
 
   // total = sum over every legal token of exp((l - M) / T), from chunk masses
-  double total = 0.0, total_err = 0.0;
-  bool have_total = false;
-  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && b.mask_words))) {
-    for (uint32_t q = 0; q < C; ++q) total += F.st[q].mass * F.cscale[q];
-    total_err = sum_bound(total, nlegal + C, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
-    have_total = true;
+  X.total = 0.0;
+  X.total_err = 0.0;
+  X.have_total = false;
+  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
+    double t = 0.0;
+    for (uint32_t q = 0; q < C; ++q) t += F.st[q].mass * F.cscale[q];
+    X.total = t;
+    X.total_err = sum_bound(t, nlegal + C, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
+    X.have_total = true;
   }
 
-  // top-k head: kappa = the k-th largest key, ties_needed = how many
-  // candidates with key == kappa join it, lowest IDs first.
-  uint32_t kappa = 0, ties_needed = 0;
-  const bool k_path = k_act && (mode == M_TOPK || mode == M_ALL);
-  if (k_path) {
-    uint32_t prefix = 0, pmask = 0, above = 0;
-    const int shifts[3] = {21, 10, 0};
-    for (int pass = 0; pass < 3; ++pass) {
-      const int sh = shifts[pass];
-      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) F.hcnt[t] = 0u;
+  // top-k head: kappa = the k-th largest key; the head takes every candidate
+  // above it and the lowest-ID ties at it.
+  X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
+  X.kappa = 0;
+  X.id_tie = NONE;
+  uint32_t ties_needed = 0;
+  if (X.k_path) {
+    // Radix select from the first bit where the candidates' keys differ:
+    // the shared high bits would put every candidate in one bin.
+    uint32_t kmin_p = NONE, kmax_p = 0;
+    for (uint32_t j = tid; j < ncand; j += NT) {
+      const uint32_t key = okey(cand_l(X, F, j));
+      kmin_p = min(kmin_p, key);
+      kmax_p = max(kmax_p, key);
+    }
+    const uint32_t kmax = block_max<uint32_t>(kmax_p, F.red_u);
+    const uint32_t kmin = ~block_max<uint32_t>(~kmin_p, F.red_u);
+    const uint32_t diff = kmin ^ kmax;
+    int hb = diff ? 31 - __clz((int)diff) : -1;   // highest differing bit
+    uint32_t pmask = hb >= 0 ? (uint32_t)(~0ull << (hb + 1)) : 0xffffffffu;
+    uint32_t prefix = kmin & pmask, above = 0;
+    while (hb >= 0) {
+      const int sh = hb >= 10 ? hb - 10 : 0;
+      const uint32_t dmask = (uint32_t)((1ull << (hb - sh + 1)) - 1ull);
+      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) F.u.h.hcnt[t] = 0u;
       __syncthreads();
-      for (uint32_t j = tid; j < ncand_total; j += NT) {
-        const uint32_t key = okey(ld_dev(&A.w.cand_l[cand_pos(j)]));
-        if ((key & pmask) == prefix) atomicAdd(&F.hcnt[(key >> sh) & (NB - 1)], 1u);
+      for (uint32_t j = tid; j < ncand; j += NT) {
+        const uint32_t key = okey(cand_l(X, F, j));
+        if ((key & pmask) == prefix) atomicAdd(&F.u.h.hcnt[(key >> sh) & dmask], 1u);
       }
       __syncthreads();
       const uint32_t b_hi = NB - 1 - 2 * tid, b_lo = b_hi - 1;
-      const uint32_t ch = F.hcnt[b_hi], cl = F.hcnt[b_lo];
+      const uint32_t ch = F.u.h.hcnt[b_hi], cl = F.u.h.hcnt[b_lo];
       uint32_t tot;
       const uint32_t inc = block_scan_incl<uint32_t>(ch + cl, F.red_u, &tot);
       const uint32_t exc = inc - ch - cl;
@@ -887,37 +1137,37 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
       else if (exc + ch < need && need <= inc) { F.s_u[4] = b_lo; F.s_u[5] = above + exc + ch; }
       __syncthreads();
       prefix |= F.s_u[4] << sh;
-      pmask |= (uint32_t)(NB - 1) << sh;
+      pmask |= dmask << sh;
       above = F.s_u[5];
       __syncthreads();
+      hb = sh - 1;
     }
-    kappa = prefix;
+    X.kappa = prefix;
     ties_needed = c.k - above;
   }
+  stamp(A, row, MAXC, 2);
 
-  // ---- working set E in LDS, token-ID order -------------------------------
-  // E = the head (k path), the exact min-p set (MINP), or every candidate.
+  // ---- working set E: the head (k path), the exact min-p set (MINP) or
+  // every candidate; token-ID order.
   uint32_t ne = 0, tie_seen = 0;
   bool mp_close = false;
   if (tid == 0) F.s_u[7] = NONE;
   __syncthreads();
-  for (uint32_t base = 0; base < ncand_total; base += NT) {
+  for (uint32_t base = 0; base < ncand; base += NT) {
     const uint32_t j = base + tid;
-    float l = 0.0f;
-    uint32_t id = 0;
     bool in = false, tie = false;
-    if (j < ncand_total) {
-      const uint64_t pos = cand_pos(j);
-      l = ld_dev(&A.w.cand_l[pos]);
-      id = ld_dev(&A.w.cand_id[pos]);
-      if (k_path) {
+    uint32_t id = 0;
+    if (j < ncand) {
+      const float l = cand_l(X, F, j);
+      id = cand_id(X, F, j);
+      if (X.k_path) {
         const uint32_t key = okey(l);
-        in = key > kappa;
-        tie = key == kappa;
+        in = key > X.kappa;
+        tie = key == X.kappa;
       } else if (mode == M_MINP) {
         const double s = ((double)l - M) / c.T;
         in = s >= L;
-        if (fabs(s - L) < Lclose) mp_close = true;
+        if (fabs(s - L) < X.Lclose) mp_close = true;
       } else {
         in = true;
       }
@@ -929,249 +1179,135 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     tie_seen += ttot;
     uint32_t etot;
     const uint32_t einc = block_scan_incl<uint32_t>(in ? 1u : 0u, F.red_u, &etot);
-    if (in && ne + einc - 1u < (uint32_t)ECAP) {
-      F.e_l[ne + einc - 1u] = l;
-      F.e_id[ne + einc - 1u] = id;
-    }
+    if (in && ne + einc - 1u < (uint32_t)ECAP) F.eidx[ne + einc - 1u] = j;
     ne += etot;
   }
   __syncthreads();
-  if (block_max<uint32_t>(mp_close ? 1u : 0u, F.red_u)) mp_close = true;
-  if (ne > (uint32_t)ECAP) {
-    LargeCtx X;
-    X.A = &A; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.ncand = ncand_total; X.ne = ne;
-    X.nlegal = nlegal; X.k_path = k_path; X.kappa = kappa; X.id_tie = F.s_u[7];
-    X.M = M; X.L = L; X.Lclose = Lclose; X.total = total; X.total_err = total_err; X.have_total = have_total;
-    __syncthreads();
-    finish_large(X, F, rbase, kbits, nwords);
-    if (mp_close && tid == 0 && A.o.status[row] == 0) A.o.status[row] = MXS_ROW_UNCERTIFIED;
-    return;
-  }
-
-  // weights
-  double wpart = 0.0;
-  for (uint32_t t = tid; t < ne; t += NT) {
-    const double s = ((double)F.e_l[t] - M) / c.T;
-    const double w = exp_neg(s);
-    F.e_w[t] = w;
-    wpart += w;
-  }
-  const double esum = block_sum<double>(wpart, F.red_d);
-  if (!have_total && !k_path && mode != M_MINP) {
-    total = esum;   // E holds every legal token
-    total_err = sum_bound(total, ne, 8.0);
-    have_total = true;
-  }
-
-  // ---- nucleus over E in (key desc, ID asc) order -------------------------
-  bool uncert = false;
-  uint32_t n_keep = ne;
-  bool walk = false;
-  double theta = 0.0, theta_err = 0.0;
-  if (k_path) {
-    walk = true;
-    theta = c.top_p * esum;
-    theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
-  } else if (c.top_p < 1.0) {
-    theta = c.top_p * total;
-    theta_err = c.top_p * total_err + U * theta;
-    walk = !(esum + sum_bound(esum, ne, 8.0) < theta - theta_err);   // else the nucleus covers E
-  }
-  if (walk) {
-    for (uint32_t t = tid; t < ne; t += NT) { F.skey[t] = sort_key(F.e_l[t], F.e_id[t]); F.sidx[t] = t; }
-    __syncthreads();
-    bitonic_sort_desc(F.skey, F.sidx, ne);
-    bool replay = false;
-    if (k_path && c.top_p >= 1.0) {
-      // covered reaches kept only at the last head token when every weight
-      // is large enough to change the running f64 sum; otherwise replay.
-      double wmin_part = INFINITY;
-      for (uint32_t t = tid; t < ne; t += NT) wmin_part = fmin(wmin_part, F.e_w[t]);
-      const double wmin = -block_max<double>(-wmin_part, F.red_d);
-      if (wmin > 2.3e-16 * esum) n_keep = ne;
-      else replay = true;
-    }
-    const bool freeze_done = k_path && c.top_p >= 1.0 && !replay;
-    if (!replay && !freeze_done) {
-      // first sorted position not certainly below theta
-      if (tid == 0) { F.s_u[6] = NONE; F.s_u[7] = 0u; }
-      __syncthreads();
-      double run = 0.0;
-      for (uint32_t base = 0; base < ne; base += NT) {
-        const uint32_t t = base + tid;
-        const double w = t < ne ? F.e_w[F.sidx[t]] : 0.0;
-        double tot;
-        const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
-        const double exc = inc - w;
-        if (t < ne) {
-          const double e_inc = sum_bound(inc, t + 65u, 8.0);
-          const double e_exc = sum_bound(exc, t + 64u, 8.0);
-          const bool lt = inc + e_inc < theta - theta_err;
-          if (!lt) {
-            const bool prev_lt = t == 0 || exc + e_exc < theta - theta_err;
-            if (prev_lt) {
-              F.s_u[6] = t;   // unique: the first position not certainly below
-              if (!(inc - e_inc >= theta + theta_err)) F.s_u[7] = 1u;
-            } else if (t == 0 || !(exc - e_exc >= theta + theta_err)) {
-              // previous position is ambiguous as well
-              atomicOr(&F.s_u[7], 2u);
-            }
-          }
-        }
-        run += tot;
-      }
-      __syncthreads();
-      if (F.s_u[6] == NONE || F.s_u[7]) replay = true;
-      else n_keep = F.s_u[6] + 1u;
-      __syncthreads();
-    }
-    if (replay) {
-      // The reference's sequential f64 sums in descending order, one lane.
-      if (tid == 0) {
-        double th = theta;
-        if (k_path) {
-          double kept = 0.0;
-          for (uint32_t q = 0; q < ne; ++q) kept += F.e_w[F.sidx[q]];
-          th = c.top_p * kept;
-        }
-        double cov = 0.0;
-        uint32_t nk = ne;
-        uint32_t close = 0;
-        for (uint32_t q = 0; q < ne; ++q) {
-          cov += F.e_w[F.sidx[q]];
-          if (!k_path && fabs(cov - th) <= theta_err + sum_bound(cov, q + 1, 8.0)) close = 1;
-          if (cov >= th) { nk = q + 1; break; }
-        }
-        F.s_u[6] = nk;
-        F.s_u[7] = close;
-      }
-      __syncthreads();
-      n_keep = F.s_u[6];
-      if (F.s_u[7]) uncert = true;
-      __syncthreads();
-    }
-    // flags by E index: kept iff sorted position < n_keep
-    for (uint32_t t = tid; t < ne; t += NT) F.skey[t] = 0ull;
-    __syncthreads();
-    for (uint32_t t = tid; t < n_keep; t += NT) F.skey[F.sidx[t]] = 1ull;
-    __syncthreads();
+  X.id_tie = F.s_u[7];
+  mp_close = block_max<uint32_t>(mp_close ? 1u : 0u, F.red_u) != 0u;
+  stamp(A, row, MAXC, 3);
+  if (ne <= (uint32_t)ECAP && X.lds_c) {
+    finish_exact(X, F, ne, mp_close);
   } else {
-    for (uint32_t t = tid; t < ne; t += NT) F.skey[t] = 1ull;
-    __syncthreads();
-  }
-
-  // ---- min-p after the nucleus (E is already the min-p set under MINP) ----
-  if (c.min_p > 0.0 && mode != M_MINP) {
-    for (uint32_t t = tid; t < ne; t += NT) {
-      const double s = ((double)F.e_l[t] - M) / c.T;
-      if (fabs(s - L) < Lclose) mp_close = true;
-      if (F.skey[t] && !(s >= L)) F.skey[t] = 0ull;
-    }
-    __syncthreads();
-  }
-  if (block_max<uint32_t>(mp_close ? 1u : 0u, F.red_u)) uncert = true;
-  {
-    // sample_categorical rejects a kept token whose shifted logit overflows
-    uint32_t bad = 0;
-    for (uint32_t t = tid; t < ne; t += NT)
-      if (F.skey[t] && !isfinite(((double)F.e_l[t] - M) / c.T)) bad = 1;
-    if (block_max<uint32_t>(bad, F.red_u)) { finish(MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
-  }
-
-  // ---- inverse-CDF draw over the kept set, token-ID order -----------------
-  double kpart = 0.0;
-  uint32_t kn = 0;
-  for (uint32_t t = tid; t < ne; t += NT)
-    if (F.skey[t]) { kpart += F.e_w[t]; ++kn; }
-  const double S = block_sum<double>(kpart, F.red_d);
-  const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
-  const double target = c.u * S;
-  const double derr = sum_bound(S, nkept + 64u, 8.0);
-  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
-  __syncthreads();
-  double run = 0.0;
-  for (uint32_t base = 0; base < ne; base += NT) {
-    const uint32_t t = base + tid;
-    const bool kept = t < ne && F.skey[t] != 0ull;
-    const double w = kept ? F.e_w[t] : 0.0;
-    double tot;
-    const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
-    const double exc = inc - w;
-    if (w > 0.0) {
-      atomicMax(&F.s_u[1], t + 1u);
-      if (target < inc && !(target < exc)) {
-        F.s_u[0] = t;
-        if (fabs(target - exc) <= derr || fabs(inc - target) <= derr) F.s_u[2] = 1u;
-      }
-    }
-    run += tot;
-  }
-  __syncthreads();
-  uint32_t pick = F.s_u[0];
-  if (F.s_u[2]) uncert = true;
-  if (pick == NONE) {
-    pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;   // last positive-weight kept token
-    uncert = true;
-  }
-  if (pick == NONE) { finish(MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
-  const double shifted = ((double)F.e_l[pick] - M) / c.T;
-  finish(uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.e_id[pick], shifted - log(S), nkept);
-  if (kbits) {
-    for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = 0u;
-    __syncthreads();
-    for (uint32_t t = tid; t < ne; t += NT)
-      if (F.skey[t]) atomicOr(&kbits[F.e_id[t] >> 5], 1u << (F.e_id[t] & 31u));
+    finish_large(X, F, ne);
+    if (mp_close && tid == 0 && A.o.status[row] == 0) A.o.status[row] = MXS_ROW_UNCERTIFIED;
   }
 }
 
 // ---------------------------------------------------------------------------
 // The sampling kernel.
 template <typename In>
-__global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
+__global__ __launch_bounds__(NT) void sample_kernel(
+    SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
+    const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
+    const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
+    const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
   __shared__ __align__(16) unsigned char smem_raw[SMEM_BYTES];
   ChunkSmem& S = *reinterpret_cast<ChunkSmem*>(smem_raw);
   FinSmem& F = *reinterpret_cast<FinSmem*>(smem_raw);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
 
-  // Workgroup -> (row, chunk): the chunks of one row share an XCD (workgroup
-  // IDs are dealt to the 8 XCDs round robin), so their exchange stays local.
-  const uint32_t bid = blockIdx.x;
-  const uint32_t xcd = bid & 7u, j8 = bid >> 3;
-  const uint32_t row = (j8 / A.C) * 8u + xcd;
-  const uint32_t chunk = j8 % A.C;
+  // Workgroup -> (row, chunk): grid (8 * C, ceil(rows / 8)); x = chunk * 8 +
+  // xcd.  Workgroups are dealt to the 8 XCDs round robin in linear order and
+  // 8 * C is a multiple of 8, so the C chunks of a row share an XCD and their
+  // exchange stays in one L2.
+  const uint32_t xcd = blockIdx.x & 7u;
+  const uint32_t chunk = blockIdx.x >> 3;
+  const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= b.rows) return;
 
   const uint32_t V = b.vocab;
-  const RowCfg c = load_cfg(b, row);
-  const uint32_t mode = chunk_mode(c, V);
+  stamp(A, row, chunk, 0);
   const uint32_t c0 = chunk * A.CH;
   const uint32_t c1 = min(V, c0 + A.CH);
   const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
-  const double invT = c.greedy ? 0.0 : 1.0 / c.T;
-  const bool has_tab = (c.he > c.hb) || (c.be > c.bb);
 
-  // ---- stream the chunk: every load issued before any use ----------------
+  // ---- stream the chunk ---------------------------------------------------
+  // Vector loads complete in issue order, so the issue order below is the
+  // order data becomes usable: the first two slices, then the row's history
+  // and bias lists and the chunk's mask words (loaded straight into LDS, no
+  // registers), then the rest of the chunk.  A quad starting below the chunk
+  // end lies inside the row stride (a multiple of 4); past the end, the
+  // chunk's first quad is re-read and ignored.
   typename Quad<In>::Raw raw[PER_MAX];
 #pragma unroll
-  for (int i = 0; i < PER_MAX; ++i) {
-    if (i < (int)A.per && !c.err) {
-      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-      // A quad starting below the chunk end lies inside the row stride (a
-      // multiple of 4); past the end, re-read the chunk's first quad.
-      raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
-    }
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+    raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
   }
+  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
+                            p_boff, row);
+  const uint32_t mode = chunk_mode(c, V);
+  const double invT = c.greedy ? 0.0 : 1.0 / c.T;
+  const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
+  const bool has_tab = hn || bn;
+  const bool h_lds = hn <= (uint32_t)HCAP, b_lds = bn <= (uint32_t)BCAP;
+  const uint32_t w0 = c0 >> 5, nmw = ((c1 - 1u) >> 5) - w0 + 1u;
+  {
+    using gp = const void __attribute__((address_space(1)))*;
+    using lp = void __attribute__((address_space(3)))*;
+    const uint32_t wb = wave() * 64u;
+    __asm__ volatile("" ::: "memory");
+    if (hn && h_lds) {
+      const uint32_t* hp = b.history_ids + c.hb;
+#pragma unroll
+      for (int r = 0; r < HCAP / NT; ++r)
+        if ((uint32_t)r * NT < hn)
+          __builtin_amdgcn_global_load_lds((gp)(hp + min((uint32_t)r * NT + tid, hn - 1u)),
+                                           (lp)(&S.hids[r * NT + wb]), 4, 0, 0);
+    }
+    if (bn && b_lds) {
+      const uint32_t* ip = b.bias_ids + c.bb;
+      const float* vp = b.bias_values + c.bb;
+#pragma unroll
+      for (int r = 0; r < BCAP / NT; ++r)
+        if ((uint32_t)r * NT < bn) {
+          __builtin_amdgcn_global_load_lds((gp)(ip + min((uint32_t)r * NT + tid, bn - 1u)),
+                                           (lp)(&S.bids[r * NT + wb]), 4, 0, 0);
+          __builtin_amdgcn_global_load_lds((gp)(vp + min((uint32_t)r * NT + tid, bn - 1u)),
+                                           (lp)(&S.bvals[r * NT + wb]), 4, 0, 0);
+        }
+    }
+    const uint32_t* mp = b.mask_words + (uint64_t)row * b.mask_stride + w0;
+#pragma unroll
+    for (int r = 0; r < (MCAP + NT - 1) / NT; ++r)
+      if ((uint32_t)r * NT < nmw)
+        __builtin_amdgcn_global_load_lds((gp)(mp + min((uint32_t)r * NT + tid, nmw - 1u)),
+                                         (lp)(&S.mask[r * NT + wb]), 4, 0, 0);
+    __asm__ volatile("" ::: "memory");
+  }
+#pragma unroll
+  for (int i = 2; i < PER_MAX; ++i) {
+    const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+    raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
+  }
+  // Everything issued before the last PER_MAX - 2 loads has landed.
+  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_MAX - 2) : "memory");
   if (tid == 0) S.s_flags = 0;
   if (has_tab) {
-    for (uint32_t t = tid; t < (uint32_t)SLICE; t += NT) { S.tab[t] = 0u; S.btab[t] = 0u; }
+    for (uint32_t t = tid; t < (uint32_t)(2 * SLICE); t += NT) { (&S.tab[0][0])[t] = 0u; (&S.btab[0][0])[t] = 0u; }
   }
   __syncthreads();
+  uint32_t my_flags = 0;
+  if (has_tab && !c.err) {
+    // validation: history ids below the vocabulary; bias ids strictly
+    // increasing, below the vocabulary, with finite values
+    for (uint32_t j = tid; j < hn; j += NT) {
+      const uint32_t id = h_lds ? S.hids[j] : b.history_ids[c.hb + j];
+      if (id >= V) my_flags |= F_HIST;
+    }
+    for (uint32_t j = tid; j < bn; j += NT) {
+      const uint32_t id = b_lds ? S.bids[j] : b.bias_ids[c.bb + j];
+      const float bvv = b_lds ? S.bvals[j] : b.bias_values[c.bb + j];
+      const uint32_t prev = j == 0 ? 0u : (b_lds ? S.bids[j - 1] : b.bias_ids[c.bb + j - 1]);
+      if (id >= V || !isfinite(bvv) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+    }
+  }
 
   // ---- bias, penalties, mask, finite check, chunk statistics -------------
   float lv[PER_MAX][4];
   uint64_t lbits = 0;                 // bit 4i+e: token (i, e) is legal
-  uint32_t my_flags = 0;
   uint32_t maxkey = 0, nleg = 0;
   float gv = 0.0f;
   uint32_t gi = NONE;
@@ -1179,48 +1315,48 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
   uint32_t tminkey = NONE;            // and smallest
 #pragma unroll
   for (int i = 0; i < PER_MAX; ++i) {
-    if (i < (int)A.per && !c.err) {
+    if (i < (int)A.per) {
       const uint32_t sbase = c0 + (uint32_t)i * SLICE;
       const uint32_t send = min(c1, sbase + (uint32_t)SLICE);
       uint4 tv = make_uint4(0u, 0u, 0u, 0u), bv4 = make_uint4(0u, 0u, 0u, 0u);
       if (has_tab) {
-        for (uint32_t h = c.hb + tid; h < c.he; h += NT) {
-          const uint32_t id = b.history_ids[h];
-          if (i == 0 && id >= V) my_flags |= F_HIST;
-          if (id >= sbase && id < send) atomicAdd(&S.tab[id - sbase], 1u);
+        const int buf = i & 1;
+        // Scatter this slice's history ids (counts) and bias ids (slot) into
+        // the LDS table; a buffer is rewritten two slices later, after the
+        // next slice's barrier, so one barrier per slice suffices.
+        for (uint32_t j = tid; j < hn; j += NT) {
+          const uint32_t id = h_lds ? S.hids[j] : b.history_ids[c.hb + j];
+          if (id >= sbase && id < send) atomicAdd(&S.tab[buf][id - sbase], 1u);
         }
-        for (uint32_t jb = c.bb + tid; jb < c.be; jb += NT) {
-          const uint32_t id = b.bias_ids[jb];
-          if (i == 0) {
-            if (id >= V || !isfinite(b.bias_values[jb]) || (jb > c.bb && b.bias_ids[jb - 1] >= id)) my_flags |= F_BIAS;
-          }
-          if (id >= sbase && id < send) S.btab[id - sbase] = jb - c.bb + 1u;
+        for (uint32_t j = tid; j < bn; j += NT) {
+          const uint32_t id = b_lds ? S.bids[j] : b.bias_ids[c.bb + j];
+          if (id >= sbase && id < send) S.btab[buf][id - sbase] = j + 1u;
         }
         __syncthreads();
-        tv = *reinterpret_cast<uint4*>(&S.tab[tid * 4u]);
-        bv4 = *reinterpret_cast<uint4*>(&S.btab[tid * 4u]);
-        *reinterpret_cast<uint4*>(&S.tab[tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&S.btab[tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
-        __syncthreads();
+        tv = *reinterpret_cast<uint4*>(&S.tab[buf][tid * 4u]);
+        bv4 = *reinterpret_cast<uint4*>(&S.btab[buf][tid * 4u]);
+        *reinterpret_cast<uint4*>(&S.tab[buf][tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(&S.btab[buf][tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
       }
       const uint32_t e0 = sbase + tid * 4u;
       float x[4];
       Quad<In>::unpack(raw[i], x);
-      uint32_t mword = NONE;
-      if (b.mask_words && e0 < c1) mword = b.mask_words[(uint64_t)row * b.mask_stride + (e0 >> 5)];
+      const uint32_t mword = e0 < c1 ? S.mask[(e0 >> 5) - w0] : 0u;
       const uint32_t tva[4] = {tv.x, tv.y, tv.z, tv.w};
       const uint32_t bva[4] = {bv4.x, bv4.y, bv4.z, bv4.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t id = e0 + (uint32_t)e;
         float l = x[e];
-        if (tva[e] | bva[e]) l = adjust(l, tva[e], bva[e], c, b.bias_values);
+        if (tva[e] | bva[e]) {
+          const float bias = bva[e] ? (b_lds ? S.bvals[bva[e] - 1u] : b.bias_values[c.bb + bva[e] - 1u]) : 0.0f;
+          l = adjust(l, tva[e], bva[e], bias, c);
+        }
         lv[i][e] = l;
         if (id < c1) {
           if (!isfinite(l)) my_flags |= F_NONFINITE;
           if (A.o.adjusted) A.o.adjusted[(uint64_t)row * V + id] = l;
-          bool legal = true;
-          if (b.mask_words) legal = ((mword >> (id & 31u)) & 1u) && id < b.tokenizer_vocab;
+          const bool legal = ((mword >> (id & 31u)) & 1u) && id < b.tokenizer_vocab;
           if (legal) {
             lbits |= 1ull << (i * 4 + e);
             ++nleg;
@@ -1254,6 +1390,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
     __syncthreads();
   }
   const uint32_t cflags = S.s_flags;
+  stamp(A, row, chunk, 1);
   const float m = nleg ? okey_value(maxkey) : 0.0f;   // chunk's largest legal logit
   const double md = (double)m;
   const bool row_ok = !c.err && !(cflags & (F_HIST | F_BIAS | F_NONFINITE));
@@ -1319,7 +1456,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
     }
 
     const bool need_mass = (mode == M_MINP && c.top_p < 1.0) || mode == M_ALL || mode == M_KEEPALL ||
-                           (mode == M_TOPK && b.mask_words != nullptr);
+                           (mode == M_TOPK && A.masked);
     const float scale = (float)HB / HRANGE;
     // Pass 1: per (slice, wave) counts and the chunk mass.
     double mloc = 0.0;
@@ -1354,12 +1491,30 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
     if (emit_kind) {
       __syncthreads();
       // exclusive offsets in (slice, wave) order == token-ID order
-      if (tid < 64) {
-        uint32_t run = 0;
-        if (tid == 0) {
-          for (int q = 0; q < PER_MAX * NW; ++q) { S.woff[q] = run; run += S.wcnt[q]; }
-          S.s_thresh_bin = run;
+      if (wave() == 0) {
+        // exclusive prefix over the PER_MAX * NW (slice, wave) counts; each
+        // lane owns 3 consecutive entries (160 <= 3 * 64)
+        constexpr int PERL = (PER_MAX * NW + 63) / 64;
+        uint32_t v[PERL], sum = 0;
+#pragma unroll
+        for (int k = 0; k < PERL; ++k) {
+          const uint32_t q = lane() * PERL + (uint32_t)k;
+          v[k] = q < (uint32_t)(PER_MAX * NW) ? S.wcnt[q] : 0u;
+          sum += v[k];
         }
+        uint32_t inc = sum;
+        for (int o = 1; o < 64; o <<= 1) {
+          const uint32_t t = __shfl_up(inc, o);
+          if (lane() >= (uint32_t)o) inc += t;
+        }
+        uint32_t run = inc - sum;
+#pragma unroll
+        for (int k = 0; k < PERL; ++k) {
+          const uint32_t q = lane() * PERL + (uint32_t)k;
+          if (q < (uint32_t)(PER_MAX * NW)) S.woff[q] = run;
+          run += v[k];
+        }
+        if (lane() == 63) S.s_thresh_bin = inc;
       }
       __syncthreads();
       ncand = S.s_thresh_bin;
@@ -1403,6 +1558,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
   }
 
   // ---- publish the chunk's statistics, then count arrivals ---------------
+  stamp(A, row, chunk, 2);
   if (tid == 0) {
     ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + chunk];
     st_dev(&st->maxkey, nleg ? maxkey : 0u);
@@ -1426,7 +1582,9 @@ __global__ __launch_bounds__(NT) void sample_kernel(SampleArgs A) {
   // =========================================================================
   // Finisher: the last chunk workgroup of the row.
   // =========================================================================
+  stamp(A, row, MAXC, 0);
   finish_row<In>(A, F, c, row, mode, rbase, invT);
+  stamp(A, row, MAXC, 7);
 }
 
 }  // namespace mxs
@@ -1439,6 +1597,16 @@ struct mxs_ctx {
   hipStream_t stream = nullptr;
   uint32_t max_rows = 0, max_vocab = 0;
   mxs::Work work{};
+  // Defaults standing in for the ABI's NULL arrays, so the kernel never tests
+  // a pointer: zeros (u32, max_rows + 1), ones/zeros (f64), ones/zeros (f32),
+  // and one all-ones mask row.
+  uint32_t* d_zero_u32 = nullptr;
+  double* d_one_f64 = nullptr;
+  double* d_zero_f64 = nullptr;
+  float* d_one_f32 = nullptr;
+  float* d_zero_f32 = nullptr;
+  uint32_t* d_mask_ones = nullptr;
+  uint64_t* timing = nullptr;
   std::string last_error;
 };
 
@@ -1507,6 +1675,23 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.cand_w, rv * sizeof(double));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;
+  e = e ? e : hipMalloc(&ctx->d_zero_u32, nr * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->d_one_f64, nr * sizeof(double));
+  e = e ? e : hipMalloc(&ctx->d_zero_f64, nr * sizeof(double));
+  e = e ? e : hipMalloc(&ctx->d_one_f32, nr * sizeof(float));
+  e = e ? e : hipMalloc(&ctx->d_zero_f32, nr * sizeof(float));
+  e = e ? e : hipMalloc(&ctx->d_mask_ones, nwords * sizeof(uint32_t));
+  if (e == hipSuccess) {
+    std::vector<double> one64(nr, 1.0);
+    std::vector<float> one32(nr, 1.0f);
+    e = hipMemset(ctx->d_zero_u32, 0, nr * sizeof(uint32_t));
+    e = e ? e : hipMemset(ctx->d_zero_f64, 0, nr * sizeof(double));
+    e = e ? e : hipMemset(ctx->d_zero_f32, 0, nr * sizeof(float));
+    e = e ? e : hipMemset(ctx->d_mask_ones, 0xff, nwords * sizeof(uint32_t));
+    e = e ? e : hipMemcpy(ctx->d_one_f64, one64.data(), nr * sizeof(double), hipMemcpyHostToDevice);
+    e = e ? e : hipMemcpy(ctx->d_one_f32, one32.data(), nr * sizeof(float), hipMemcpyHostToDevice);
+  }
   e = e ? e : hipDeviceSynchronize();
   hipSetDevice(prev);
   if (e != hipSuccess) {
@@ -1529,6 +1714,12 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->work.cand_id);
   hipFree(ctx->work.cand_w);
   hipFree(ctx->work.seg);
+  hipFree(ctx->d_zero_u32);
+  hipFree(ctx->d_one_f64);
+  hipFree(ctx->d_zero_f64);
+  hipFree(ctx->d_one_f32);
+  hipFree(ctx->d_zero_f32);
+  hipFree(ctx->d_mask_ones);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;
@@ -1537,6 +1728,12 @@ int mxs_destroy(mxs_ctx* ctx) {
 int mxs_set_stream(mxs_ctx* ctx, void* stream) {
   if (!ctx) return MXS_EINVAL;
   ctx->stream = (hipStream_t)stream;
+  return MXS_OK;
+}
+
+int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer) {
+  if (!ctx) return MXS_EINVAL;
+  ctx->timing = (uint64_t*)device_buffer;
   return MXS_OK;
 }
 
@@ -1566,6 +1763,22 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   A.b = *b;
   A.o = *o;
   A.w = ctx->work;
+  A.timing = ctx->timing;
+  A.masked = b->mask_words != nullptr;
+  if (!A.masked) {
+    A.b.mask_words = ctx->d_mask_ones;
+    A.b.mask_stride = 0;
+    A.b.tokenizer_vocab = b->vocab;
+  }
+  if (!b->history_offsets) { A.b.history_offsets = ctx->d_zero_u32; A.b.history_ids = ctx->d_zero_u32; }
+  if (!b->bias_offsets) { A.b.bias_offsets = ctx->d_zero_u32; A.b.bias_ids = ctx->d_zero_u32; A.b.bias_values = ctx->d_zero_f32; }
+  const double* p_tp = b->top_p ? b->top_p : ctx->d_one_f64;
+  const double* p_mp = b->min_p ? b->min_p : ctx->d_zero_f64;
+  const double* p_u = b->uniform ? b->uniform : ctx->d_zero_f64;
+  const uint32_t* p_k = b->top_k ? b->top_k : ctx->d_zero_u32;
+  const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
+  const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
+  const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
   const uint32_t V = b->vocab;
   const uint32_t quads = (V + 3u) / 4u;
   uint32_t C = (quads + (uint32_t)(mxs::NT * mxs::PER_MAX) - 1u) / (uint32_t)(mxs::NT * mxs::PER_MAX);
@@ -1575,14 +1788,16 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   A.CH = ch;
   A.per = (ch / 4u + (uint32_t)mxs::NT - 1u) / (uint32_t)mxs::NT;
   if (A.per > (uint32_t)mxs::PER_MAX || C > (uint32_t)mxs::MAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
-  const uint32_t groups = ((b->rows + 7u) / 8u) * 8u * C;
+  const dim3 grid(8u * C, (b->rows + 7u) / 8u);
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
   if (b->dtype == MXS_F32)
-    hipLaunchKernelGGL(mxs::sample_kernel<float>, dim3(groups), dim3(mxs::NT), 0, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::sample_kernel<float>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
+                       p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
   else
-    hipLaunchKernelGGL(mxs::sample_kernel<uint16_t>, dim3(groups), dim3(mxs::NT), 0, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::sample_kernel<uint16_t>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
+                       p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");

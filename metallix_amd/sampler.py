@@ -75,6 +75,7 @@ PROTOTYPES = {
     "mxs_spec_verify": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mxs_sync": (ctypes.c_int, [_vp]),
+    "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
     "mxs_last_error": (ctypes.c_char_p, [_vp]),
 }
 
@@ -208,6 +209,23 @@ class Sampler:
         self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
         self._keep = (b, o)
         return out
+
+    def launcher(self, logits, **kw):
+        """Pre-built launch for repeated picks with the same parameters and
+        outputs: returns f(logits) that only swaps the logits pointer."""
+        out = self.sample(logits, **kw)
+        b, o = self._keep
+        bp, op = ctypes.byref(b), ctypes.byref(o)
+        fn, ctx = self.lib.mxs_sample, self.ctx
+
+        def launch(t):
+            b.logits = t.data_ptr()
+            rc = fn(ctx, bp, op)
+            if rc != 0:
+                self._check(rc, "mxs_sample")
+
+        launch.out = out
+        return launch
 
     def sync(self):
         self._check(self.lib.mxs_sync(self.ctx), "mxs_sync")
