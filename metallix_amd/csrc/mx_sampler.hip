@@ -47,11 +47,18 @@ constexpr int CCAP = 8192;                // candidates the finisher caches in L
 constexpr int ECAP = 4096;                // finisher's exact working-set capacity
 constexpr int KCAND_MAX = ECAP;           // top_k served from per-chunk candidates
 constexpr int NB = 2048;                  // radix-select bins (11 bits)
-constexpr int HB = 1024;                  // chunk top-k histogram bins
+constexpr int HB = 1024;                  // chunk top-k histogram bins (== NT)
+constexpr uint32_t TOP1_MAX = 256;        // top_k served by per-thread maxima; above, top-2 maxima
+constexpr uint32_t CT_MAXH = 32767;       // longest history the u16 chunk count table takes
 constexpr float HRANGE = 32.0f;           // logit units covered by HB bins
 constexpr int HCAP = 4 * NT;              // history ids staged in LDS
 constexpr int BCAP = 2 * NT;              // bias entries staged in LDS
-constexpr int MCAP = CHUNK_MAX / 32 + 2;  // mask words of one chunk
+// mask words of one chunk (CHUNK_MAX / 32 + 2), rounded up to whole
+// 1024-word rounds of the LDS staging, which writes every lane's slot
+constexpr int MCAP = ((CHUNK_MAX / 32 + 2 + NT - 1) / NT) * NT;
+static_assert(HCAP % NT == 0 && BCAP % NT == 0 && MCAP % NT == 0,
+              "LDS staging copies whole 1024-entry rounds");
+static_assert(HB == NT, "one histogram bin per thread");
 constexpr uint32_t NONE = 0xffffffffu;
 constexpr double U = 1.1102230246251565e-16;  // 2^-53
 
@@ -65,9 +72,10 @@ struct ChunkStat {
   uint32_t nlegal;
   uint32_t ncand;
   uint32_t flags;
-  double mass;         // sum of exp((l - chunk max) / T) over legal tokens, when computed
   uint32_t minkey;     // total-order key of the smallest legal logit
-  uint32_t pad;
+  float thr;           // candidate threshold used (diagnostics)
+  double mass;         // sum of exp((l - chunk max) / T) over legal tokens, when computed
+  double mass_err;     // bound on |mass - exact sum| from the f32 path (0 for the f64 path)
 };
 
 struct Work {
@@ -123,6 +131,11 @@ __device__ __forceinline__ double ld_dev(const double* p) {
 }
 // Waits until this lane's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
+// operations only.  __syncthreads() also drains every outstanding global
+// load and store first, which would stall the chunk phase until its whole
+// stream has landed; the chunk phase tracks its global loads itself.
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t lane() { return threadIdx.x & 63; }
 __device__ __forceinline__ uint32_t wave() { return threadIdx.x >> 6; }
@@ -184,6 +197,79 @@ __device__ T block_scan_incl(T v, T* red, T* total) {
   return before + v;
 }
 
+// ---------------------------------------------------------------------------
+// Wave primitives on DPP lane moves (no LDS round trip).  A row is 16 lanes;
+// row_shr:n shifts within a row, row_bcast:15 / row_bcast:31 carry a row's
+// last lane into the following rows.  Lanes with no source receive `old`
+// (the operation's identity), so the scans below are Hillis-Steele scans
+// within rows followed by the two cross-row carries.
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, RM, 0xf, false);
+}
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
+constexpr int DPP_BC15 = 0x142, DPP_BC31 = 0x143;
+
+// Inclusive sum scan in lane order.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp<DPP_SHR1>(0u, v);
+  v += dpp<DPP_SHR2>(0u, v);
+  v += dpp<DPP_SHR4>(0u, v);
+  v += dpp<DPP_SHR8>(0u, v);
+  v += dpp<DPP_BC15, 0xa>(0u, v);
+  v += dpp<DPP_BC31, 0xc>(0u, v);
+  return v;
+}
+__device__ __forceinline__ uint32_t bcast63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return bcast63(wave_scan_u32(v)); }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp<DPP_SHR1>(0u, v));
+  v = max(v, dpp<DPP_SHR2>(0u, v));
+  v = max(v, dpp<DPP_SHR4>(0u, v));
+  v = max(v, dpp<DPP_SHR8>(0u, v));
+  v = max(v, dpp<DPP_BC15, 0xa>(0u, v));
+  v = max(v, dpp<DPP_BC31, 0xc>(0u, v));
+  return bcast63(v);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  v |= dpp<DPP_SHR1>(0u, v);
+  v |= dpp<DPP_SHR2>(0u, v);
+  v |= dpp<DPP_SHR4>(0u, v);
+  v |= dpp<DPP_SHR8>(0u, v);
+  v |= dpp<DPP_BC15, 0xa>(0u, v);
+  v |= dpp<DPP_BC31, 0xc>(0u, v);
+  return bcast63(v);
+}
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ unsigned long long dpp64(unsigned long long v) {
+  const uint32_t lo = dpp<CTRL, RM>(0u, (uint32_t)v), hi = dpp<CTRL, RM>(0u, (uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  unsigned long long t;
+  t = dpp64<DPP_SHR1>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR2>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR4>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR8>(v); v = t > v ? t : v;
+  t = dpp64<DPP_BC15, 0xa>(v); v = t > v ? t : v;
+  t = dpp64<DPP_BC31, 0xc>(v); v = t > v ? t : v;
+  const uint32_t lo = bcast63((uint32_t)v), hi = bcast63((uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+// Sum over the wave (identity +0.0; addition order fixed by the lane tree).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  unsigned long long b;
+  b = dpp64<DPP_SHR1>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR2>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR4>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR8>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC15, 0xa>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC31, 0xc>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  const unsigned long long r = __builtin_bit_cast(unsigned long long, v);
+  const uint32_t lo = bcast63((uint32_t)r), hi = bcast63((uint32_t)(r >> 32));
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
 // IEEE argmax with the lowest index on ties (-0.0 ties 0.0): greedy_token's
 // and masked_argmax's rule.
 __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t bi) {
@@ -194,25 +280,32 @@ __device__ __forceinline__ bool better(float av, uint32_t ai, float bv, uint32_t
 
 // ---------------------------------------------------------------------------
 // Shared memory: one static pool, carved per phase.
-struct ChunkSmem {
-  uint32_t tab[2][SLICE];              // per-slice history counts (double-buffered)
-  uint32_t btab[2][SLICE];             // per-slice bias slot, index + 1 (double-buffered)
-  uint32_t hids[HCAP];                 // the row's history ids (when at most HCAP)
-  uint32_t bids[BCAP];                 // the row's bias ids and values (when at most BCAP)
-  float bvals[BCAP];
-  uint32_t mask[MCAP];                 // the chunk's grammar-mask words
-  uint32_t hist[HB];                   // top-k threshold histogram
-  uint32_t wcnt[PER_MAX * NW];         // candidates per (slice, wave)
-  uint32_t woff[PER_MAX * NW];
-  uint32_t red_u[NW];
-  double red_d[NW];
-  float red_f[NW];
-  uint32_t red_i[NW];
-  uint32_t s_flags;
-  uint32_t s_thresh_bin;
+struct WavePart {                     // one wave's share of the chunk statistics
+  uint32_t kmax, kmin, nleg, flags;
+  unsigned long long arg;              // (okey(value) << 32) | ~id of the wave's argmax
+  double m0, m1;                       // mass and its error weight
+};
+struct alignas(16) ChunkSmem {
+  // members read as 16-byte vectors are 16-byte aligned
+  union {
+    // whole-chunk table: per token a u16, count in bits 0-14, bias flag in bit 15
+    alignas(16) uint32_t ct[CHUNK_MAX / 2];
+    struct {                           // per-slice tables (histories longer than CT_MAXH)
+      alignas(16) uint32_t tab[2][SLICE];   // count | bias flag << 31 (double-buffered)
+      alignas(16) float btab[2][SLICE];     // bias value (double-buffered)
+    } sl;
+  } t;
+  alignas(16) uint32_t hids[HCAP];     // the row's history ids (when at most HCAP)
+  alignas(16) uint32_t bids[BCAP];     // the row's bias ids and values (when at most BCAP)
+  alignas(16) float bvals[BCAP];
+  alignas(16) uint32_t mask[MCAP];     // the chunk's grammar-mask words
+  alignas(16) uint32_t hist[HB];       // top-k threshold histogram
+  alignas(16) uint32_t wcnt[PER_MAX * NW + 32];   // candidates per (slice, wave), padded for the scan
+  WavePart wp[NW];
+  WavePart wq[NW];
   uint32_t s_last;
 };
-struct FinSmem {
+struct alignas(16) FinSmem {
   float cl[CCAP];                      // candidates cached in LDS, token-ID order
   uint32_t cid[CCAP];
   uint32_t eidx[ECAP];                 // working set E: indices into the candidates
@@ -875,6 +968,7 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     v.ncand = ld_dev(&st->ncand);
     v.flags = ld_dev(&st->flags);
     v.mass = ld_dev(&st->mass);
+    v.mass_err = ld_dev(&st->mass_err);
     v.minkey = ld_dev(&st->minkey);
     F.st[q] = v;
   }
@@ -1090,9 +1184,12 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   X.have_total = false;
   if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
     double t = 0.0;
-    for (uint32_t q = 0; q < C; ++q) t += F.st[q].mass * F.cscale[q];
+    double te = 0.0;
+    for (uint32_t q = 0; q < C; ++q) { t += F.st[q].mass * F.cscale[q]; te += F.st[q].mass_err * F.cscale[q]; }
     X.total = t;
-    X.total_err = sum_bound(t, nlegal + C, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
+    // chunk error bounds (f32 weights), scaled; plus both sides' f64
+    // rounding of weights and sums, and the x e^x <= 1/e product term
+    X.total_err = te * 1.000001 + sum_bound(t, nlegal + C, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
     X.have_total = true;
   }
 
@@ -1244,313 +1341,461 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const bool has_tab = hn || bn;
   const bool h_lds = hn <= (uint32_t)HCAP, b_lds = bn <= (uint32_t)BCAP;
   const uint32_t w0 = c0 >> 5, nmw = ((c1 - 1u) >> 5) - w0 + 1u;
-  {
-    using gp = const void __attribute__((address_space(1)))*;
-    using lp = void __attribute__((address_space(3)))*;
-    const uint32_t wb = wave() * 64u;
-    __asm__ volatile("" ::: "memory");
-    if (hn && h_lds) {
-      const uint32_t* hp = b.history_ids + c.hb;
+  // The row's history and bias lists (when they fit in LDS) and, for masked
+  // rows, the chunk's mask words go through registers into LDS.  They are
+  // issued before the bulk of the logits, so they land first (vector loads
+  // complete in issue order); each lane loads whole 1024-entry rounds,
+  // repeating the last entry past the list's end.
+  const bool stage_h = hn && h_lds, stage_b = bn && b_lds, stage_m = A.masked != 0u;
+  uint32_t hreg[HCAP / NT], breg[BCAP / NT], mreg[MCAP / NT];
+  float vreg[BCAP / NT];
+  if (stage_h) {
+    const uint32_t* hp = b.history_ids + c.hb;
 #pragma unroll
-      for (int r = 0; r < HCAP / NT; ++r)
-        if ((uint32_t)r * NT < hn)
-          __builtin_amdgcn_global_load_lds((gp)(hp + min((uint32_t)r * NT + tid, hn - 1u)),
-                                           (lp)(&S.hids[r * NT + wb]), 4, 0, 0);
-    }
-    if (bn && b_lds) {
-      const uint32_t* ip = b.bias_ids + c.bb;
-      const float* vp = b.bias_values + c.bb;
+    for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
+  }
+  if (stage_b) {
+    const uint32_t* ip = b.bias_ids + c.bb;
+    const float* vp = b.bias_values + c.bb;
 #pragma unroll
-      for (int r = 0; r < BCAP / NT; ++r)
-        if ((uint32_t)r * NT < bn) {
-          __builtin_amdgcn_global_load_lds((gp)(ip + min((uint32_t)r * NT + tid, bn - 1u)),
-                                           (lp)(&S.bids[r * NT + wb]), 4, 0, 0);
-          __builtin_amdgcn_global_load_lds((gp)(vp + min((uint32_t)r * NT + tid, bn - 1u)),
-                                           (lp)(&S.bvals[r * NT + wb]), 4, 0, 0);
-        }
+    for (int r = 0; r < BCAP / NT; ++r) {
+      breg[r] = ip[min((uint32_t)r * NT + tid, bn - 1u)];
+      vreg[r] = vp[min((uint32_t)r * NT + tid, bn - 1u)];
     }
+  }
+  if (stage_m) {
     const uint32_t* mp = b.mask_words + (uint64_t)row * b.mask_stride + w0;
 #pragma unroll
-    for (int r = 0; r < (MCAP + NT - 1) / NT; ++r)
-      if ((uint32_t)r * NT < nmw)
-        __builtin_amdgcn_global_load_lds((gp)(mp + min((uint32_t)r * NT + tid, nmw - 1u)),
-                                         (lp)(&S.mask[r * NT + wb]), 4, 0, 0);
-    __asm__ volatile("" ::: "memory");
+    for (int r = 0; r < MCAP / NT; ++r) mreg[r] = mp[min((uint32_t)r * NT + tid, nmw - 1u)];
   }
 #pragma unroll
   for (int i = 2; i < PER_MAX; ++i) {
     const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
     raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
   }
-  // Everything issued before the last PER_MAX - 2 loads has landed.
-  __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_MAX - 2) : "memory");
-  if (tid == 0) S.s_flags = 0;
-  if (has_tab) {
-    for (uint32_t t = tid; t < (uint32_t)(2 * SLICE); t += NT) { (&S.tab[0][0])[t] = 0u; (&S.btab[0][0])[t] = 0u; }
+  if (stage_h) {
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) S.hids[r * NT + tid] = hreg[r];
   }
-  __syncthreads();
+  if (stage_b) {
+#pragma unroll
+    for (int r = 0; r < BCAP / NT; ++r) { S.bids[r * NT + tid] = breg[r]; S.bvals[r * NT + tid] = vreg[r]; }
+  }
+  if (stage_m) {
+#pragma unroll
+    for (int r = 0; r < MCAP / NT; ++r) S.mask[r * NT + tid] = mreg[r];
+  }
+  // History counts and bias flags: one table for the whole chunk, built
+  // once, when no count can pass 15 bits and the bias list is in LDS (its
+  // values are found by binary search there); otherwise per-slice u32 tables.
+  const bool tab_chunk = has_tab && hn <= CT_MAXH && b_lds;
+  const bool tab_slices = has_tab && !tab_chunk;
+  if (tab_chunk) {
+    const uint32_t n4 = A.per * (SLICE / 8);   // uint4 words covering per slices
+    for (uint32_t t = tid; t < n4; t += NT) reinterpret_cast<uint4*>(S.t.ct)[t] = make_uint4(0u, 0u, 0u, 0u);
+  } else if (tab_slices) {
+    for (uint32_t t = tid; t < (uint32_t)(2 * SLICE); t += NT) (&S.t.sl.tab[0][0])[t] = 0u;
+  }
+  if (mode == M_TOPK) S.hist[tid] = 0u;   // HB == NT
+  lds_barrier();
   uint32_t my_flags = 0;
   if (has_tab && !c.err) {
     // validation: history ids below the vocabulary; bias ids strictly
     // increasing, below the vocabulary, with finite values
-    for (uint32_t j = tid; j < hn; j += NT) {
-      const uint32_t id = h_lds ? S.hids[j] : b.history_ids[c.hb + j];
-      if (id >= V) my_flags |= F_HIST;
+    // (LDS and global copies in separate loops: a pointer select between
+    // them would compile to flat loads, which wait on every global load)
+    if (h_lds) {
+      for (uint32_t j = tid; j < hn; j += NT)
+        if (S.hids[j] >= V) my_flags |= F_HIST;
+    } else {
+      for (uint32_t j = tid; j < hn; j += NT)
+        if (b.history_ids[c.hb + j] >= V) my_flags |= F_HIST;
     }
-    for (uint32_t j = tid; j < bn; j += NT) {
-      const uint32_t id = b_lds ? S.bids[j] : b.bias_ids[c.bb + j];
-      const float bvv = b_lds ? S.bvals[j] : b.bias_values[c.bb + j];
-      const uint32_t prev = j == 0 ? 0u : (b_lds ? S.bids[j - 1] : b.bias_ids[c.bb + j - 1]);
-      if (id >= V || !isfinite(bvv) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+    if (b_lds) {
+      for (uint32_t j = tid; j < bn; j += NT) {
+        const uint32_t id = S.bids[j];
+        const uint32_t prev = j == 0 ? 0u : S.bids[j - 1];
+        if (id >= V || !isfinite(S.bvals[j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+      }
+    } else {
+      for (uint32_t j = tid; j < bn; j += NT) {
+        const uint32_t id = b.bias_ids[c.bb + j];
+        const uint32_t prev = j == 0 ? 0u : b.bias_ids[c.bb + j - 1];
+        if (id >= V || !isfinite(b.bias_values[c.bb + j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+      }
     }
   }
+  const uint32_t clen = c1 - c0;
+  if (tab_chunk) {
+    if (h_lds) {
+      for (uint32_t j = tid; j < hn; j += NT) {
+        const uint32_t t = S.hids[j] - c0;
+        if (t < clen) atomicAdd(&S.t.ct[t >> 1], 1u << ((t & 1u) * 16u));
+      }
+    } else {
+      for (uint32_t j = tid; j < hn; j += NT) {
+        const uint32_t t = b.history_ids[c.hb + j] - c0;
+        if (t < clen) atomicAdd(&S.t.ct[t >> 1], 1u << ((t & 1u) * 16u));
+      }
+    }
+    for (uint32_t j = tid; j < bn; j += NT) {
+      const uint32_t t = S.bids[j] - c0;
+      if (t < clen) atomicOr(&S.t.ct[t >> 1], 0x8000u << ((t & 1u) * 16u));
+    }
+    lds_barrier();
+  }
 
-  // ---- bias, penalties, mask, finite check, chunk statistics -------------
+  stamp(A, row, chunk, 3);
+  // ---- pass 1: bias, penalties, mask, finite check, chunk statistics ------
+  // Full slices of unmasked rows take a path with no per-token legality
+  // work; partial slices and masked rows carry 4 legal bits per slice.
+  // Penalised tokens are rare: each of the quad's 4 lanes enters the
+  // penalty arithmetic only when some lane of the wave needs it.
+  const bool masked_row = A.masked != 0u;
+  const uint32_t lim = masked_row ? min(c1, b.tokenizer_vocab) : c1;   // no legal token at or past lim
+  const bool want_top2 = mode == M_TOPK && c.k > (uint32_t)TOP1_MAX;
+  const bool want_min = mode == M_KEEPALL;
+  const bool want_arg = mode == M_GREEDY;
+  const double inv_rep = 1.0 / (double)c.rep;
   float lv[PER_MAX][4];
-  uint64_t lbits = 0;                 // bit 4i+e: token (i, e) is legal
-  uint32_t maxkey = 0, nleg = 0;
-  float gv = 0.0f;
-  uint32_t gi = NONE;
-  uint32_t tmaxkey = 0;               // this thread's largest legal key
-  uint32_t tminkey = NONE;            // and smallest
+  uint64_t lq = 0;                    // legal bits of partial / masked slices, 4 per slice
+  float t1 = -INFINITY, t2 = -INFINITY, tmin = INFINITY, gv = -INFINITY;
+  uint32_t gi = NONE, nleg = 0;
+  uint64_t nf = 0;                    // wave-uniform: a lane saw a non-finite logit
 #pragma unroll
   for (int i = 0; i < PER_MAX; ++i) {
     if (i < (int)A.per) {
       const uint32_t sbase = c0 + (uint32_t)i * SLICE;
       const uint32_t send = min(c1, sbase + (uint32_t)SLICE);
-      uint4 tv = make_uint4(0u, 0u, 0u, 0u), bv4 = make_uint4(0u, 0u, 0u, 0u);
-      if (has_tab) {
+      uint32_t tva[4] = {0u, 0u, 0u, 0u};   // count | bias flag << 31
+      float bva[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (tab_chunk) {
+        const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
+        const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tva[e] = (h[e] & 0x7fffu) | ((h[e] & 0x8000u) << 16);
+      } else if (tab_slices) {
         const int buf = i & 1;
-        // Scatter this slice's history ids (counts) and bias ids (slot) into
-        // the LDS table; a buffer is rewritten two slices later, after the
-        // next slice's barrier, so one barrier per slice suffices.
+        // Scatter this slice's history ids (counts) and bias ids (flag and
+        // value) into the LDS table; a buffer is rewritten two slices later,
+        // after the next slice's barrier, so one barrier per slice suffices.
         for (uint32_t j = tid; j < hn; j += NT) {
-          const uint32_t id = h_lds ? S.hids[j] : b.history_ids[c.hb + j];
-          if (id >= sbase && id < send) atomicAdd(&S.tab[buf][id - sbase], 1u);
+          const uint32_t id = b.history_ids[c.hb + j];
+          if (id >= sbase && id < send) atomicAdd(&S.t.sl.tab[buf][id - sbase], 1u);
         }
-        for (uint32_t j = tid; j < bn; j += NT) {
-          const uint32_t id = b_lds ? S.bids[j] : b.bias_ids[c.bb + j];
-          if (id >= sbase && id < send) S.btab[buf][id - sbase] = j + 1u;
+        if (b_lds) {
+          for (uint32_t j = tid; j < bn; j += NT) {
+            const uint32_t id = S.bids[j];
+            if (id >= sbase && id < send) {
+              atomicOr(&S.t.sl.tab[buf][id - sbase], 0x80000000u);
+              S.t.sl.btab[buf][id - sbase] = S.bvals[j];
+            }
+          }
+        } else {
+          for (uint32_t j = tid; j < bn; j += NT) {
+            const uint32_t id = b.bias_ids[c.bb + j];
+            if (id >= sbase && id < send) {
+              atomicOr(&S.t.sl.tab[buf][id - sbase], 0x80000000u);
+              S.t.sl.btab[buf][id - sbase] = b.bias_values[c.bb + j];
+            }
+          }
         }
-        __syncthreads();
-        tv = *reinterpret_cast<uint4*>(&S.tab[buf][tid * 4u]);
-        bv4 = *reinterpret_cast<uint4*>(&S.btab[buf][tid * 4u]);
-        *reinterpret_cast<uint4*>(&S.tab[buf][tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(&S.btab[buf][tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
+        lds_barrier();
+        const uint4 tv = *reinterpret_cast<uint4*>(&S.t.sl.tab[buf][tid * 4u]);
+        const float4 bv4 = *reinterpret_cast<float4*>(&S.t.sl.btab[buf][tid * 4u]);
+        *reinterpret_cast<uint4*>(&S.t.sl.tab[buf][tid * 4u]) = make_uint4(0u, 0u, 0u, 0u);
+        tva[0] = tv.x; tva[1] = tv.y; tva[2] = tv.z; tva[3] = tv.w;
+        bva[0] = bv4.x; bva[1] = bv4.y; bva[2] = bv4.z; bva[3] = bv4.w;
       }
-      const uint32_t e0 = sbase + tid * 4u;
       float x[4];
       Quad<In>::unpack(raw[i], x);
-      const uint32_t mword = e0 < c1 ? S.mask[(e0 >> 5) - w0] : 0u;
-      const uint32_t tva[4] = {tv.x, tv.y, tv.z, tv.w};
-      const uint32_t bva[4] = {bv4.x, bv4.y, bv4.z, bv4.w};
+      if (has_tab) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t id = e0 + (uint32_t)e;
-        float l = x[e];
-        if (tva[e] | bva[e]) {
-          const float bias = bva[e] ? (b_lds ? S.bvals[bva[e] - 1u] : b.bias_values[c.bb + bva[e] - 1u]) : 0.0f;
-          l = adjust(l, tva[e], bva[e], bias, c);
-        }
-        lv[i][e] = l;
-        if (id < c1) {
-          if (!isfinite(l)) my_flags |= F_NONFINITE;
-          if (A.o.adjusted) A.o.adjusted[(uint64_t)row * V + id] = l;
-          const bool legal = ((mword >> (id & 31u)) & 1u) && id < b.tokenizer_vocab;
-          if (legal) {
-            lbits |= 1ull << (i * 4 + e);
-            ++nleg;
-            const uint32_t k = okey(l);
-            tmaxkey = k > tmaxkey ? k : tmaxkey;
-            tminkey = k < tminkey ? k : tminkey;
-            if (better(l, id, gv, gi)) { gv = l; gi = id; }
+        for (int e = 0; e < 4; ++e) {
+          const bool hit = tva[e] != 0u;
+          if (__builtin_amdgcn_ballot_w64(hit)) {
+            float bias = bva[e];
+            if (tab_chunk && (tva[e] >> 31)) {
+              // the bias value: binary search over the strictly increasing ids
+              const uint32_t id = sbase + tid * 4u + (uint32_t)e;
+              uint32_t lo = 0, hi = bn;
+              while (lo < hi) { const uint32_t md2 = (lo + hi) >> 1; if (S.bids[md2] < id) lo = md2 + 1u; else hi = md2; }
+              bias = S.bvals[min(lo, bn - 1u)];
+            }
+            x[e] = hit ? bias_and_penalize(x[e], tva[e], bias, c.rep, inv_rep, c.freq, c.pres) : x[e];
           }
         }
       }
+      const uint32_t e0 = sbase + tid * 4u;
+      const bool full = !masked_row && send - sbase == (uint32_t)SLICE;   // uniform
+      uint32_t qb = 0xfu, rb = 0xfu;  // legal bits, in-range bits of the quad
+      if (!full) {
+        rb = e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u;
+        const uint32_t lb = e0 < lim ? (lim - e0 >= 4u ? 0xfu : (1u << (lim - e0)) - 1u) : 0u;
+        const uint32_t mw = (masked_row && e0 < c1) ? (S.mask[(e0 >> 5) - w0] >> (e0 & 31u)) & 0xfu : 0xfu;
+        qb = lb & mw;
+        lq |= (uint64_t)qb << (4 * i);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lv[i][e] = x[e];
+      if (full) {
+        // every token of the quad is in range and legal
+#pragma unroll
+        for (int e = 0; e < 4; ++e) nf |= __builtin_amdgcn_ballot_w64(!__builtin_isfinite(x[e]));
+        if (want_arg) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool g = x[e] > gv;
+            gv = g ? x[e] : gv;
+            gi = g ? e0 + (uint32_t)e : gi;
+          }
+        } else if (want_top2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { t2 = fmaxf(t2, fminf(t1, x[e])); t1 = fmaxf(t1, x[e]); }
+        } else if (want_min) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { t1 = fmaxf(t1, x[e]); tmin = fminf(tmin, x[e]); }
+        } else {
+          t1 = fmaxf(fmaxf(t1, x[0]), fmaxf(fmaxf(x[1], x[2]), x[3]));
+        }
+      } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool inr = (rb >> e) & 1u;
+        nf |= __builtin_amdgcn_ballot_w64(inr && !__builtin_isfinite(x[e]));
+        const bool lg = (qb >> e) & 1u;
+        const float lm = lg ? x[e] : -INFINITY;
+        if (want_top2) t2 = fmaxf(t2, fminf(t1, lm));
+        t1 = fmaxf(t1, lm);
+        if (want_min) tmin = fminf(tmin, lg ? x[e] : INFINITY);
+        if (want_arg) {
+          const bool g = lm > gv;
+          gv = g ? lm : gv;
+          gi = g ? e0 + (uint32_t)e : gi;
+        }
+      }
+      }
+      if (A.o.adjusted) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((rb >> e) & 1u) A.o.adjusted[(uint64_t)row * V + e0 + (uint32_t)e] = x[e];
+      }
+      nleg += full ? 4u : (uint32_t)__builtin_popcount(qb);
     }
   }
+  stamp(A, row, chunk, 6);
 
-  // Block reductions.
-  if (my_flags) atomicOr(&S.s_flags, my_flags);
-  maxkey = block_max<uint32_t>(tmaxkey, S.red_u);
-  const uint32_t minkey = ~block_max<uint32_t>(~tminkey, S.red_u);
-  nleg = block_sum<uint32_t>(nleg, S.red_u);
+  // ---- chunk statistics: one block reduction ------------------------------
   {
-    // argmax: reduce within the wave, then across waves
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(gv, o);
-      const uint32_t oi = __shfl_xor(gi, o);
-      if (better(ov, oi, gv, gi)) { gv = ov; gi = oi; }
+    const uint32_t kmax = wave_max_u32(okey(t1));
+    const uint32_t kmin = want_min ? ~wave_max_u32(~okey(tmin)) : 0u;
+    const uint32_t wn = wave_sum_u32(nleg);
+    const uint32_t wf = wave_or_u32(my_flags) | (nf ? (uint32_t)F_NONFINITE : 0u);
+    unsigned long long arg = 0ull;
+    if (want_arg) {
+      // -0.0 ties +0.0 under IEEE >: key both as +0.0 so the lower ID wins
+      arg = gi == NONE ? 0ull : ((unsigned long long)okey(gv + 0.0f) << 32) | (unsigned long long)(~gi);
+      arg = wave_max_u64(arg);
     }
-    if (lane() == 0) { S.red_f[wave()] = gv; S.red_i[wave()] = gi; }
-    __syncthreads();
-    gv = S.red_f[0]; gi = S.red_i[0];
-    for (int w = 1; w < NW; ++w)
-      if (better(S.red_f[w], S.red_i[w], gv, gi)) { gv = S.red_f[w]; gi = S.red_i[w]; }
-    __syncthreads();
+    if (lane() == 0) {
+      WavePart& p = S.wp[wave()];
+      p.kmax = kmax; p.kmin = kmin; p.nleg = wn; p.flags = wf; p.arg = arg;
+    }
   }
-  const uint32_t cflags = S.s_flags;
+  lds_barrier();
+  uint32_t maxkey = 0u, minkey = NONE, cflags = 0u;
+  nleg = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const WavePart& p = S.wp[w];
+    maxkey = max(maxkey, p.kmax);
+    minkey = min(minkey, p.kmin);
+    nleg += p.nleg;
+    cflags |= p.flags;
+  }
   stamp(A, row, chunk, 1);
   const float m = nleg ? okey_value(maxkey) : 0.0f;   // chunk's largest legal logit
   const double md = (double)m;
   const bool row_ok = !c.err && !(cflags & (F_HIST | F_BIAS | F_NONFINITE));
 
-  // ---- mode-specific chunk output ----------------------------------------
+  // ---- pass 2: candidate threshold, counts, chunk mass --------------------
+  // Candidates are emitted in token-ID order: per (slice, wave) counts, an
+  // exclusive scan, then the writes.  A token is a candidate when it is
+  // legal and its logit is at least `thr`.
   uint32_t ncand = 0;
-  double mass = 0.0;
+  double mass = 0.0, mass_err = 0.0;
   const uint64_t rbase = (uint64_t)row * V;
-  if (row_ok && mode != M_GREEDY && nleg > 0) {
-    // Emission predicate per token: which tokens become candidates.
-    uint32_t emit_kind = 0;      // 0 none, 1 all legal, 2 bin <= thresh, 3 min-p superset
-    uint32_t thresh_bin = 0;
-    float minp_pre = 0.0f;
-    double L = 0.0;
+  bool emit = false;
+  float thr = -INFINITY;
+  if (row_ok && nleg > 0) {
     if (mode == M_TOPK) {
+      emit = true;
       const uint32_t need = min(c.k, nleg);
-      if (need >= nleg) {
-        emit_kind = 1;
-      } else {
-        // Histogram over d = (m - l) * HB / HRANGE, bins 0..HB-2 (HB-1 = beyond range).
-        for (uint32_t t = tid; t < (uint32_t)HB; t += NT) S.hist[t] = 0u;
-        __syncthreads();
+      if (need < nleg) {
+        // The need-th largest of the per-thread maxima (top-2 maxima for
+        // large k) is at most the chunk's need-th largest legal logit.
+        // Histogram them on a 1/32-logit grid below m, find the bin where
+        // the count reaches need, and emit down to one bin below it.
         const float scale = (float)HB / HRANGE;
-        if (need <= 128u) {
-          // The need-th largest per-thread maximum bounds the chunk's need-th
-          // largest logit from below: histogram the NT thread maxima only.
-          if (tmaxkey) {
-            const float d = (m - okey_value(tmaxkey)) * scale;
-            const uint32_t bin = d < (float)(HB - 1) ? (uint32_t)d : (uint32_t)(HB - 1);
-            if (bin < (uint32_t)(HB - 1)) atomicAdd(&S.hist[bin], 1u);
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < PER_MAX; ++i) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              if ((lbits >> (i * 4 + e)) & 1ull) {
-                const float d = (m - lv[i][e]) * scale;
-                if (d < (float)(HB - 1)) atomicAdd(&S.hist[(uint32_t)d], 1u);
-              }
-            }
+        {
+          const float d1 = (m - t1) * scale;
+          if (d1 < (float)(HB - 1)) atomicAdd(&S.hist[(uint32_t)d1], 1u);
+          if (want_top2) {
+            const float d2 = (m - t2) * scale;
+            if (d2 < (float)(HB - 1)) atomicAdd(&S.hist[(uint32_t)d2], 1u);
           }
         }
-        __syncthreads();
-        // first bin whose cumulative count reaches `need`
-        uint32_t cnt = S.hist[tid];
-        uint32_t tot;
-        const uint32_t inc = block_scan_incl<uint32_t>(cnt, S.red_u, &tot);
-        if (tid == 0) S.s_thresh_bin = NONE;
-        __syncthreads();
-        if (inc >= need && inc - cnt < need) S.s_thresh_bin = tid;
-        __syncthreads();
-        thresh_bin = S.s_thresh_bin;
-        emit_kind = thresh_bin == NONE ? 1u : 2u;
+        lds_barrier();
+        // Every wave finds the bin itself: lane j sums bins [16j, 16j + 16).
+        uint32_t hv[16];
+        uint32_t s = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint4 h4 = *reinterpret_cast<const uint4*>(&S.hist[lane() * 16u + (uint32_t)q * 4u]);
+          hv[q * 4 + 0] = h4.x; hv[q * 4 + 1] = h4.y; hv[q * 4 + 2] = h4.z; hv[q * 4 + 3] = h4.w;
+          s += h4.x + h4.y + h4.z + h4.w;
+        }
+        const uint32_t inc = wave_scan_u32(s);
+        const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+        if (reach) {
+          const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+          uint32_t run = inc - s, bin = 16u * lane() + 15u;
+          bool found = false;
+#pragma unroll
+          for (int q = 0; q < 16; ++q) {
+            run += hv[q];
+            if (!found && run >= need) { found = true; bin = 16u * lane() + (uint32_t)q; }
+          }
+          const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
+          thr = m - (float)(tb + 2u) / scale;
+        }
       }
     } else if (mode == M_MINP) {
-      L = log(c.min_p);
-      const double lim = md + c.T * L;
-      minp_pre = (float)lim - (fabsf((float)lim) + fabsf(m)) * 1e-5f - 1e-30f;
-      emit_kind = 3;
+      // Superset of the min-p set: the row maximum is at least m.
+      emit = true;
+      const double lim_d = md + c.T * log(c.min_p);
+      thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(m)) * 1e-5f - 1e-30f;
     } else if (mode == M_ALL) {
-      emit_kind = 1;
+      emit = true;
     }
-
-    const bool need_mass = (mode == M_MINP && c.top_p < 1.0) || mode == M_ALL || mode == M_KEEPALL ||
-                           (mode == M_TOPK && A.masked);
-    const float scale = (float)HB / HRANGE;
-    // Pass 1: per (slice, wave) counts and the chunk mass.
-    double mloc = 0.0;
+  }
+  stamp(A, row, chunk, 4);
+  const bool mass32 = row_ok && nleg > 0 &&
+                      ((mode == M_MINP && c.top_p < 1.0) || (mode == M_TOPK && masked_row));
+  const bool mass64 = row_ok && nleg > 0 && (mode == M_ALL || mode == M_KEEPALL);
+  uint32_t cnt_i[PER_MAX];
+  double m0 = 0.0, m1 = 0.0;
+  {
+    // f32 weights 2^((l - m) * c2) with c2 = log2(e) / T; see the chunk
+    // error bound below.  f64 weights (exp_neg) for the modes whose draw
+    // walks the full row.
+    const float c2 = (float)(invT * 1.4426950408889634);
 #pragma unroll
     for (int i = 0; i < PER_MAX; ++i) {
-      uint32_t cnt_i = 0;
-      double seg_mass = 0.0;
+      cnt_i[i] = 0u;
+      if (i < (int)A.per) {
+        const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+        const bool full = !masked_row && min(c1, sbase + (uint32_t)SLICE) - sbase == (uint32_t)SLICE;
+        const uint32_t qb = full ? 0xfu : (uint32_t)(lq >> (4 * i)) & 0xfu;
+        if (emit) {
+          uint32_t cnt = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool legal = (lbits >> (i * 4 + e)) & 1ull;
-        bool emit = false;
-        if (legal) {
-          const float l = lv[i][e];
-          if (emit_kind == 1) emit = true;
-          else if (emit_kind == 2) { const float d = (m - l) * scale; emit = d < (float)(HB - 1) && (uint32_t)d <= thresh_bin; }
-          else if (emit_kind == 3) emit = l >= minp_pre && (((double)l - md) / c.T) >= L;
-          if (need_mass) seg_mass += exp_neg(((double)l - md) * invT);
+          for (int e = 0; e < 4; ++e)
+            cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((qb >> e) & 1u) && lv[i][e] >= thr));
+          cnt_i[i] = cnt;
+          if (lane() == 0) S.wcnt[i * NW + wave()] = cnt;
         }
-        cnt_i += emit;
-      }
-      if (need_mass) mloc += seg_mass;
-      if (mode == M_KEEPALL && i < (int)A.per) {
-        const double ws = wave_sum(seg_mass);
-        if (lane() == 0) st_dev(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
-      }
-      if (emit_kind) {
-        const uint32_t wc = wave_sum(cnt_i);
-        if (lane() == 0) S.wcnt[i * NW + wave()] = wc;
-      }
-    }
-    if (need_mass) mass = block_sum<double>(mloc, S.red_d);
-    if (emit_kind) {
-      __syncthreads();
-      // exclusive offsets in (slice, wave) order == token-ID order
-      if (wave() == 0) {
-        // exclusive prefix over the PER_MAX * NW (slice, wave) counts; each
-        // lane owns 3 consecutive entries (160 <= 3 * 64)
-        constexpr int PERL = (PER_MAX * NW + 63) / 64;
-        uint32_t v[PERL], sum = 0;
-#pragma unroll
-        for (int k = 0; k < PERL; ++k) {
-          const uint32_t q = lane() * PERL + (uint32_t)k;
-          v[k] = q < (uint32_t)(PER_MAX * NW) ? S.wcnt[q] : 0u;
-          sum += v[k];
-        }
-        uint32_t inc = sum;
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t t = __shfl_up(inc, o);
-          if (lane() >= (uint32_t)o) inc += t;
-        }
-        uint32_t run = inc - sum;
-#pragma unroll
-        for (int k = 0; k < PERL; ++k) {
-          const uint32_t q = lane() * PERL + (uint32_t)k;
-          if (q < (uint32_t)(PER_MAX * NW)) S.woff[q] = run;
-          run += v[k];
-        }
-        if (lane() == 63) S.s_thresh_bin = inc;
-      }
-      __syncthreads();
-      ncand = S.s_thresh_bin;
-      // Pass 2: write candidates in token-ID order.
-      const uint64_t cbase = rbase + c0;
-#pragma unroll
-      for (int i = 0; i < PER_MAX; ++i) {
-        uint32_t base = S.woff[i * NW + wave()];
-        bool em[4];
-        uint32_t before_me = 0, mine = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const bool legal = (lbits >> (i * 4 + e)) & 1ull;
-          bool emit = false;
-          if (legal) {
-            const float l = lv[i][e];
-            if (emit_kind == 1) emit = true;
-            else if (emit_kind == 2) { const float d = (m - l) * scale; emit = d < (float)(HB - 1) && (uint32_t)d <= thresh_bin; }
-            else if (emit_kind == 3) emit = l >= minp_pre && (((double)l - md) / c.T) >= L;
-          }
-          em[e] = emit;
-          const uint64_t bal = __ballot(emit);
-          before_me += lanes_below(bal);
-        }
-        if (i < (int)A.per) {
-          uint32_t off = base + before_me;
+        if (mass32) {
+          float sw = 0.0f, ew = 0.0f;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if (em[e]) {
-              const uint32_t id = c0 + (uint32_t)i * SLICE + tid * 4u + (uint32_t)e;
-              const uint64_t pos = cbase + off + mine;
-              st_dev(&A.w.cand_l[pos], lv[i][e]);
-              st_dev(&A.w.cand_id[pos], id);
-              if (mode == M_ALL) st_dev(&A.w.cand_w[pos], exp_neg(((double)lv[i][e] - md) * invT));
-              ++mine;
-            }
+            const float y = (lv[i][e] - m) * c2;
+            const float w = __builtin_amdgcn_exp2f(y);
+            const bool lg = (qb >> e) & 1u;
+            sw += lg ? w : 0.0f;
+            ew += lg ? w * -y : 0.0f;
+          }
+          m0 += (double)sw;
+          m1 += (double)ew;
+        } else if (mass64) {
+          double sw = 0.0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sw += ((qb >> e) & 1u) ? exp_neg(((double)lv[i][e] - md) * invT) : 0.0;
+          m0 += sw;
+          if (mode == M_KEEPALL) {
+            const double ws = wave_sum_f64(sw);
+            if (lane() == 0) st_dev(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
+          }
+        }
+      } else if (lane() == 0 && emit) {
+        S.wcnt[i * NW + wave()] = 0u;
+      }
+    }
+    if (mass32 || mass64) {
+      const double w0s = wave_sum_f64(m0), w1s = wave_sum_f64(m1);
+      if (lane() == 0) { S.wq[wave()].m0 = w0s; S.wq[wave()].m1 = w1s; }
+    }
+  }
+  stamp(A, row, chunk, 5);
+  if (emit || mass32 || mass64) lds_barrier();
+  if (mass32 || mass64) {
+    double s0 = 0.0, s1 = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) { s0 += S.wq[w].m0; s1 += S.wq[w].m1; }
+    mass = s0;
+    if (mass32) {
+      // |mass - sum of exact weights| <= 1.01 (2^-22 S + 3 2^-24 S) for the
+      // f32 exp (2 ulp) and the 4-term f32 slice sums, + 1.01 ln2 3 2^-24
+      // sum w |y| for the rounding of y (three f32 roundings, relative),
+      // + n 2^-124 for weights below 2^-126, + 2^-40 S for the f64 sums.
+      const double S0 = s0, E0 = s1;
+      mass_err = 1.01 * (0x1p-22 * S0 + 3.0 * 0x1p-24 * S0 + 0.6931471805599453 * 3.0001 * 0x1p-24 * E0) +
+                 (double)nleg * 0x1p-124 + 0x1p-40 * S0;
+    }
+  }
+  if (emit) {
+    // exclusive offsets in (slice, wave) order == token-ID order; every wave
+    // scans the PER_MAX * NW counts itself (lane j holds j, j + 64, j + 128)
+    const uint32_t nent = A.per * NW;
+    const uint32_t v0 = lane() < nent ? S.wcnt[lane()] : 0u;
+    const uint32_t v1 = lane() + 64u < nent ? S.wcnt[lane() + 64u] : 0u;
+    const uint32_t v2 = lane() + 128u < nent ? S.wcnt[lane() + 128u] : 0u;
+    const uint32_t i0 = wave_scan_u32(v0), i1 = wave_scan_u32(v1), i2 = wave_scan_u32(v2);
+    const uint32_t t0 = (uint32_t)__builtin_amdgcn_readlane((int)i0, 63);
+    const uint32_t t1s = (uint32_t)__builtin_amdgcn_readlane((int)i1, 63);
+    const uint32_t t2s = (uint32_t)__builtin_amdgcn_readlane((int)i2, 63);
+    ncand = t0 + t1s + t2s;
+    const uint32_t x0 = i0 - v0, x1 = i1 - v1 + t0, x2 = i2 - v2 + t0 + t1s;
+    const uint64_t cbase = rbase + c0;
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i) {
+      if (i < (int)A.per && cnt_i[i]) {
+        const uint32_t idx = (uint32_t)i * NW + wave();
+        const uint32_t src = idx & 63u;
+        const uint32_t reg = idx >> 6;
+        const uint32_t xv = reg == 0 ? x0 : (reg == 1 ? x1 : x2);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)src);
+        const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+        const bool full = !masked_row && min(c1, sbase + (uint32_t)SLICE) - sbase == (uint32_t)SLICE;
+        const uint32_t qb = full ? 0xfu : (uint32_t)(lq >> (4 * i)) & 0xfu;
+        bool em[4];
+        uint32_t before_me = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          em[e] = ((qb >> e) & 1u) && lv[i][e] >= thr;
+          before_me += lanes_below(__builtin_amdgcn_ballot_w64(em[e]));
+        }
+        uint32_t off = base + before_me;
+        const uint32_t e0 = sbase + tid * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (em[e]) {
+            const uint64_t pos = cbase + off;
+            st_dev(&A.w.cand_l[pos], lv[i][e]);
+            st_dev(&A.w.cand_id[pos], e0 + (uint32_t)e);
+            if (mode == M_ALL) st_dev(&A.w.cand_w[pos], exp_neg(((double)lv[i][e] - md) * invT));
+            ++off;
           }
         }
       }
@@ -1558,20 +1803,27 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   }
 
   // ---- publish the chunk's statistics, then count arrivals ---------------
-  stamp(A, row, chunk, 2);
+  stamp(A, row, chunk, 7);
   if (tid == 0) {
+    // the greedy argmax: the largest (value key, ~id) of the waves' argmaxes
+    unsigned long long garg = 0ull;
+    if (want_arg)
+      for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
     ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + chunk];
     st_dev(&st->maxkey, nleg ? maxkey : 0u);
-    st_dev(&st->gbest_id, gi);
-    st_dev(&st->gbest_val, gv);
+    st_dev(&st->gbest_id, garg ? ~(uint32_t)garg : NONE);
+    st_dev(&st->gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
     st_dev(&st->nlegal, nleg);
     st_dev(&st->ncand, ncand);
     st_dev(&st->flags, cflags);
     st_dev(&st->mass, mass);
+    st_dev(&st->mass_err, mass_err);
     st_dev(&st->minkey, minkey);
+    st_dev(&st->thr, thr);
   }
   wait_mem();
   __syncthreads();
+  stamp(A, row, chunk, 2);
   if (tid == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     S.s_last = (prev == A.C - 1u) ? 1u : 0u;

@@ -39,6 +39,30 @@ MXS_HD float okey_value(uint32_t k) {
   return f;
 }
 
+// l / r rounded to f32, for finite r > 0, without an f32 division: the f64
+// product l * (1/r) carries at most 2^-52 relative error, while the exact
+// quotient of two f32 values (24-bit significands) is either exact in f64
+// arithmetic here (r a power of two) or at least 2^-49 (relative) away from
+// every f32 rounding midpoint, normal or subnormal.  So the single f64->f32
+// rounding lands where the IEEE f32 division rounds.  Checked against the
+// f32 division on the host over random and edge-case operands.
+MXS_HD float div_by_recip(float l, double inv_r) { return (float)((double)l * inv_r); }
+
+// Logit bias and penalties for one token, every step rounded to f32 in this
+// order: l + bias (when the token has a bias entry), then for a token seen
+// `cnt` > 0 times in the history: repetition (l < 0 ? l * rep : l / rep),
+// minus cnt * frequency, minus presence.  `tv` packs cnt in bits 0-30 and
+// "has a bias entry" in bit 31.
+MXS_HD float bias_and_penalize(float l, uint32_t tv, float bias, float rep, double inv_rep, float freq,
+                               float pres) {
+  const uint32_t cnt = tv & 0x7fffffffu;
+  const float a = (tv >> 31) ? l + bias : l;
+  const float r = a < 0.0f ? a * rep : div_by_recip(a, inv_rep);
+  const float cf = (float)cnt * freq;
+  const float p = (r - cf) - pres;
+  return cnt ? p : a;
+}
+
 // exp(x) for x <= 0 in f64: x = n ln2/64 + r, |r| <= ln2/128, degree-6 Taylor
 // polynomial for e^r - 1 (truncation below 3e-20 relative), 2^(n mod 64 / 64)
 // as a two-part table so one final rounding dominates, scaled by
