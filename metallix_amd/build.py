@@ -23,7 +23,6 @@ HIPCC_FLAGS = [
     "--offload-arch=gfx950",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-fno-gpu-flush-denormals-to-zero",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
@@ -38,16 +37,32 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build_library(verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), "-o", str(tmp),
-           str(CSRC / "mx_sampler.hip")]
+def _compile(src: Path, obj: Path, verbose: bool) -> None:
+    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), "-c", "-o", str(obj), str(src)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+        raise RuntimeError(f"hipcc failed on {src.name} ({res.returncode}):\n{res.stderr[-4000:]}")
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compiles every csrc/*.hip for gfx950 (in parallel) and links the library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    BUILD.mkdir(exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    objs = [BUILD / (s.stem + ".o") for s in srcs]
+    with ThreadPoolExecutor(max_workers=min(4, len(srcs))) as ex:
+        for f in [ex.submit(_compile, s, o, verbose) for s, o in zip(srcs, objs)]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-4000:]}")
     os.replace(tmp, LIB)
     return LIB
 

@@ -33,16 +33,12 @@
 #include <vector>
 
 #include "../../include/mx_sampler.h"
+#include "mxs_ctx.h"
+#include "mxs_device.h"
 #include "mxs_math.h"
 
 namespace mxs {
 
-constexpr int NT = 1024;                  // threads per workgroup
-constexpr int NW = NT / 64;               // waves per workgroup
-constexpr int PER_MAX = 10;               // 4-token quads per thread per chunk
-constexpr int SLICE = NT * 4;             // tokens per slice (one quad per thread)
-constexpr int CHUNK_MAX = SLICE * PER_MAX;
-constexpr int MAXC = 64;                  // chunks per row (vocab <= MAXC * CHUNK_MAX)
 constexpr int CCAP = 8192;                // candidates the finisher caches in LDS
 constexpr int ECAP = 4096;                // finisher's exact working-set capacity
 constexpr int KCAND_MAX = ECAP;           // top_k served from per-chunk candidates
@@ -59,8 +55,6 @@ constexpr int MCAP = ((CHUNK_MAX / 32 + 2 + NT - 1) / NT) * NT;
 static_assert(HCAP % NT == 0 && BCAP % NT == 0 && MCAP % NT == 0,
               "LDS staging copies whole 1024-entry rounds");
 static_assert(HB == NT, "one histogram bin per thread");
-constexpr uint32_t NONE = 0xffffffffu;
-constexpr double U = 1.1102230246251565e-16;  // 2^-53
 
 enum Mode : uint32_t { M_GREEDY = 0, M_TOPK = 1, M_MINP = 2, M_ALL = 3, M_KEEPALL = 4 };
 enum Flag : uint32_t { F_NONFINITE = 1, F_HIST = 2, F_BIAS = 4 };
@@ -78,14 +72,6 @@ struct ChunkStat {
   double mass_err;     // bound on |mass - exact sum| from the f32 path (0 for the f64 path)
 };
 
-struct Work {
-  uint32_t* ctr;       // [max_rows] arrival counters (reset by each finisher)
-  ChunkStat* stat;     // [max_rows * MAXC]
-  float* cand_l;       // [max_rows * max_vocab]
-  uint32_t* cand_id;   // [max_rows * max_vocab]
-  double* cand_w;      // [max_rows * max_vocab]
-  double* seg;         // [max_rows * MAXC * PER_MAX * NW]
-};
 
 struct SampleArgs {
   mxs_batch b;
@@ -105,169 +91,6 @@ struct SampleArgs {
 // registers.
 __device__ __forceinline__ void stamp(const SampleArgs& A, uint32_t row, uint32_t chunk, uint32_t k) {
   if (A.timing) A.timing[((uint64_t)row * (MAXC + 1) + chunk) * 8 + k] = wall_clock64();
-}
-
-// ---------------------------------------------------------------------------
-// Device-scope (coherent across workgroups and XCDs) loads and stores.  Data
-// exchanged between a row's workgroups goes through these: they bypass the
-// non-coherent caches, so no L2 writeback/invalidate is needed.
-__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(double* p, double v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
-  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ double ld_dev(const double* p) {
-  return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Waits until this lane's outstanding memory operations have completed.
-__device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
-// operations only.  __syncthreads() also drains every outstanding global
-// load and store first, which would stall the chunk phase until its whole
-// stream has landed; the chunk phase tracks its global loads itself.
-__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-__device__ __forceinline__ uint32_t lane() { return threadIdx.x & 63; }
-__device__ __forceinline__ uint32_t wave() { return threadIdx.x >> 6; }
-__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
-  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
-// ---------------------------------------------------------------------------
-// Block-wide reductions and scans (all threads participate and receive the
-// result).  `red` is LDS scratch of at least NW elements of the type.
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-template <typename T>
-__device__ __forceinline__ T wave_max(T v) {
-  for (int o = 32; o > 0; o >>= 1) { T t = __shfl_xor(v, o); v = t > v ? t : v; }
-  return v;
-}
-template <typename T>
-__device__ T block_sum(T v, T* red) {
-  v = wave_sum(v);
-  if (lane() == 0) red[wave()] = v;
-  __syncthreads();
-  T s = red[0];
-  for (int i = 1; i < NW; ++i) s += red[i];
-  __syncthreads();
-  return s;
-}
-template <typename T>
-__device__ T block_max(T v, T* red) {
-  v = wave_max(v);
-  if (lane() == 0) red[wave()] = v;
-  __syncthreads();
-  T s = red[0];
-  for (int i = 1; i < NW; ++i) s = red[i] > s ? red[i] : s;
-  __syncthreads();
-  return s;
-}
-// Inclusive scan in thread order; *total receives the block total.
-template <typename T>
-__device__ T block_scan_incl(T v, T* red, T* total) {
-  const uint32_t l = lane();
-  for (int o = 1; o < 64; o <<= 1) {
-    T t = __shfl_up(v, o);
-    if (l >= (uint32_t)o) v += t;
-  }
-  if (l == 63) red[wave()] = v;
-  __syncthreads();
-  T before = T(0), all = T(0);
-  for (int i = 0; i < NW; ++i) {
-    T r = red[i];
-    if (i < (int)wave()) before += r;
-    all += r;
-  }
-  __syncthreads();
-  *total = all;
-  return before + v;
-}
-
-// ---------------------------------------------------------------------------
-// Wave primitives on DPP lane moves (no LDS round trip).  A row is 16 lanes;
-// row_shr:n shifts within a row, row_bcast:15 / row_bcast:31 carry a row's
-// last lane into the following rows.  Lanes with no source receive `old`
-// (the operation's identity), so the scans below are Hillis-Steele scans
-// within rows followed by the two cross-row carries.
-template <int CTRL, int RM = 0xf>
-__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, RM, 0xf, false);
-}
-constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
-constexpr int DPP_BC15 = 0x142, DPP_BC31 = 0x143;
-
-// Inclusive sum scan in lane order.
-__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
-  v += dpp<DPP_SHR1>(0u, v);
-  v += dpp<DPP_SHR2>(0u, v);
-  v += dpp<DPP_SHR4>(0u, v);
-  v += dpp<DPP_SHR8>(0u, v);
-  v += dpp<DPP_BC15, 0xa>(0u, v);
-  v += dpp<DPP_BC31, 0xc>(0u, v);
-  return v;
-}
-__device__ __forceinline__ uint32_t bcast63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return bcast63(wave_scan_u32(v)); }
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, dpp<DPP_SHR1>(0u, v));
-  v = max(v, dpp<DPP_SHR2>(0u, v));
-  v = max(v, dpp<DPP_SHR4>(0u, v));
-  v = max(v, dpp<DPP_SHR8>(0u, v));
-  v = max(v, dpp<DPP_BC15, 0xa>(0u, v));
-  v = max(v, dpp<DPP_BC31, 0xc>(0u, v));
-  return bcast63(v);
-}
-__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-  v |= dpp<DPP_SHR1>(0u, v);
-  v |= dpp<DPP_SHR2>(0u, v);
-  v |= dpp<DPP_SHR4>(0u, v);
-  v |= dpp<DPP_SHR8>(0u, v);
-  v |= dpp<DPP_BC15, 0xa>(0u, v);
-  v |= dpp<DPP_BC31, 0xc>(0u, v);
-  return bcast63(v);
-}
-template <int CTRL, int RM = 0xf>
-__device__ __forceinline__ unsigned long long dpp64(unsigned long long v) {
-  const uint32_t lo = dpp<CTRL, RM>(0u, (uint32_t)v), hi = dpp<CTRL, RM>(0u, (uint32_t)(v >> 32));
-  return ((unsigned long long)hi << 32) | lo;
-}
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-  unsigned long long t;
-  t = dpp64<DPP_SHR1>(v); v = t > v ? t : v;
-  t = dpp64<DPP_SHR2>(v); v = t > v ? t : v;
-  t = dpp64<DPP_SHR4>(v); v = t > v ? t : v;
-  t = dpp64<DPP_SHR8>(v); v = t > v ? t : v;
-  t = dpp64<DPP_BC15, 0xa>(v); v = t > v ? t : v;
-  t = dpp64<DPP_BC31, 0xc>(v); v = t > v ? t : v;
-  const uint32_t lo = bcast63((uint32_t)v), hi = bcast63((uint32_t)(v >> 32));
-  return ((unsigned long long)hi << 32) | lo;
-}
-// Sum over the wave (identity +0.0; addition order fixed by the lane tree).
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  unsigned long long b;
-  b = dpp64<DPP_SHR1>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  b = dpp64<DPP_SHR2>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  b = dpp64<DPP_SHR4>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  b = dpp64<DPP_SHR8>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  b = dpp64<DPP_BC15, 0xa>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  b = dpp64<DPP_BC31, 0xc>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
-  const unsigned long long r = __builtin_bit_cast(unsigned long long, v);
-  const uint32_t lo = bcast63((uint32_t)r), hi = bcast63((uint32_t)(r >> 32));
-  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
 }
 
 // IEEE argmax with the lowest index on ties (-0.0 ties 0.0): greedy_token's
@@ -422,28 +245,6 @@ __device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, fl
   }
   return l;
 }
-
-__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
-
-template <typename In>
-struct Quad;
-template <>
-struct Quad<float> {
-  using Raw = float4;
-  __device__ static Raw load(const float* p) { return *reinterpret_cast<const float4*>(p); }
-  __device__ static void unpack(const Raw& r, float x[4]) { x[0] = r.x; x[1] = r.y; x[2] = r.z; x[3] = r.w; }
-  __device__ static float one(const float* p) { return *p; }
-};
-template <>
-struct Quad<uint16_t> {
-  using Raw = uint2;
-  __device__ static Raw load(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
-  __device__ static void unpack(const Raw& r, float x[4]) {
-    x[0] = bf16_to_f32((uint16_t)(r.x & 0xffffu)); x[1] = bf16_to_f32((uint16_t)(r.x >> 16));
-    x[2] = bf16_to_f32((uint16_t)(r.y & 0xffffu)); x[3] = bf16_to_f32((uint16_t)(r.y >> 16));
-  }
-  __device__ static float one(const uint16_t* p) { return bf16_to_f32(*p); }
-};
 
 // Re-derives adjusted logits and legality for `cnt` tokens starting at `id0`
 // (one lane per token, cnt <= 64, one wave).  Used by the finisher to locate
@@ -1844,36 +1645,6 @@ __global__ __launch_bounds__(NT) void sample_kernel(
 // ===========================================================================
 // Host side: context, validation, launch.
 // ===========================================================================
-struct mxs_ctx {
-  int device = 0;
-  hipStream_t stream = nullptr;
-  uint32_t max_rows = 0, max_vocab = 0;
-  mxs::Work work{};
-  // Defaults standing in for the ABI's NULL arrays, so the kernel never tests
-  // a pointer: zeros (u32, max_rows + 1), ones/zeros (f64), ones/zeros (f32),
-  // and one all-ones mask row.
-  uint32_t* d_zero_u32 = nullptr;
-  double* d_one_f64 = nullptr;
-  double* d_zero_f64 = nullptr;
-  float* d_one_f32 = nullptr;
-  float* d_zero_f32 = nullptr;
-  uint32_t* d_mask_ones = nullptr;
-  uint64_t* timing = nullptr;
-  std::string last_error;
-};
-
-namespace {
-
-int fail(mxs_ctx* ctx, int code, const std::string& msg) {
-  if (ctx) ctx->last_error = msg;
-  return code;
-}
-
-int hip_fail(mxs_ctx* ctx, hipError_t e, const char* what) {
-  return fail(ctx, MXS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-}  // namespace
 
 extern "C" {
 
@@ -1927,6 +1698,9 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.cand_w, rv * sizeof(double));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
   const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;
   e = e ? e : hipMalloc(&ctx->d_zero_u32, nr * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->d_one_f64, nr * sizeof(double));
@@ -1972,6 +1746,10 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->d_one_f32);
   hipFree(ctx->d_zero_f32);
   hipFree(ctx->d_mask_ones);
+  hipFree(ctx->topn_ctr);
+  hipFree(ctx->topn_scratch);
+  hipFree(ctx->spec_ctr);
+  hipFree(ctx->spec_scratch);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;
@@ -2031,14 +1809,11 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
   const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
   const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
-  const uint32_t V = b->vocab;
-  const uint32_t quads = (V + 3u) / 4u;
-  uint32_t C = (quads + (uint32_t)(mxs::NT * mxs::PER_MAX) - 1u) / (uint32_t)(mxs::NT * mxs::PER_MAX);
-  if (C < 1) C = 1;
-  uint32_t ch = ((V + C - 1u) / C + 3u) & ~3u;
-  A.C = C;
-  A.CH = ch;
-  A.per = (ch / 4u + (uint32_t)mxs::NT - 1u) / (uint32_t)mxs::NT;
+  const mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
+  const uint32_t C = L.C;
+  A.C = L.C;
+  A.CH = L.CH;
+  A.per = L.per;
   if (A.per > (uint32_t)mxs::PER_MAX || C > (uint32_t)mxs::MAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
   const dim3 grid(8u * C, (b->rows + 7u) / 8u);
   int prev = 0;
@@ -2054,17 +1829,6 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");
   return MXS_OK;
-}
-
-int mxs_logsoftmax_topn(mxs_ctx* ctx, const void*, int32_t, uint32_t, uint32_t, uint64_t, uint32_t, int32_t*,
-                        double*, double*, double*, int32_t*) {
-  return fail(ctx, MXS_EINVAL, "mxs_logsoftmax_topn: not built yet");
-}
-
-int mxs_spec_verify(mxs_ctx* ctx, const float*, const float*, uint32_t, uint32_t, uint32_t, const int32_t*,
-                    const double*, const double*, const double*, const double*, int32_t*, int32_t*, int32_t*,
-                    int32_t*) {
-  return fail(ctx, MXS_EINVAL, "mxs_spec_verify: not built yet");
 }
 
 }  // extern "C"

@@ -1,0 +1,67 @@
+// mxs_ctx.h -- the host-side context behind the C ABI's mxs_ctx handle,
+// shared by the entry points of the sampler, log-softmax and speculative
+// verification kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/mx_sampler.h"
+
+namespace mxs {
+
+struct ChunkStat;
+
+// Scratch sizes of the entry points other than mxs_sample (defined beside
+// their kernels).
+size_t topn_scratch_bytes(uint32_t max_rows);
+
+// Device scratch of mxs_sample, sized for the context's limits.
+struct Work {
+  uint32_t* ctr;       // [max_rows] arrival counters (reset by each finisher)
+  ChunkStat* stat;     // [max_rows * MAXC]
+  float* cand_l;       // [max_rows * max_vocab]
+  uint32_t* cand_id;   // [max_rows * max_vocab]
+  double* cand_w;      // [max_rows * max_vocab]
+  double* seg;         // [max_rows * MAXC * PER_MAX * NW]
+};
+
+}  // namespace mxs
+
+struct mxs_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint32_t max_rows = 0, max_vocab = 0;
+  mxs::Work work{};
+  // Defaults standing in for the ABI's NULL arrays, so the kernel never tests
+  // a pointer: zeros (u32, max_rows + 1), ones/zeros (f64), ones/zeros (f32),
+  // and one all-ones mask row.
+  uint32_t* d_zero_u32 = nullptr;
+  double* d_one_f64 = nullptr;
+  double* d_zero_f64 = nullptr;
+  float* d_one_f32 = nullptr;
+  float* d_zero_f32 = nullptr;
+  uint32_t* d_mask_ones = nullptr;
+  uint64_t* timing = nullptr;
+  // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
+  uint32_t* topn_ctr = nullptr;
+  void* topn_scratch = nullptr;
+  // mxs_spec_verify: per-position arrival counters and per-chunk results
+  uint32_t* spec_ctr = nullptr;
+  void* spec_scratch = nullptr;
+  std::string last_error;
+};
+
+namespace {
+
+inline int fail(mxs_ctx* ctx, int code, const std::string& msg) {
+  if (ctx) ctx->last_error = msg;
+  return code;
+}
+
+inline int hip_fail(mxs_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, MXS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+}  // namespace

@@ -1,0 +1,221 @@
+// mxs_device.h -- device building blocks shared by the sampler kernels:
+// the chunk layout, coherent cross-workgroup loads and stores, barriers,
+// DPP wave reductions and scans, block reductions, and the logit loaders.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mxs_math.h"
+
+namespace mxs {
+
+constexpr int NT = 1024;                  // threads per workgroup
+constexpr int NW = NT / 64;               // waves per workgroup
+constexpr int PER_MAX = 10;               // 4-token quads per thread per chunk
+constexpr int SLICE = NT * 4;             // tokens per slice (one quad per thread)
+constexpr int CHUNK_MAX = SLICE * PER_MAX;
+constexpr int MAXC = 64;                  // chunks per row (vocab <= MAXC * CHUNK_MAX)
+constexpr uint32_t NONE = 0xffffffffu;
+constexpr double U = 1.1102230246251565e-16;  // 2^-53
+
+// Chunk layout of a row of V tokens: C chunks of CH tokens (a multiple of
+// 4), each streamed by one workgroup as `per` quads per thread.
+struct ChunkLayout {
+  uint32_t C, CH, per;
+};
+inline ChunkLayout chunk_layout(uint32_t V, uint32_t per_max = PER_MAX) {
+  const uint32_t quads = (V + 3u) / 4u;
+  uint32_t C = (quads + (uint32_t)NT * per_max - 1u) / ((uint32_t)NT * per_max);
+  if (C < 1) C = 1;
+  const uint32_t ch = ((V + C - 1u) / C + 3u) & ~3u;
+  return {C, ch, (ch / 4u + (uint32_t)NT - 1u) / (uint32_t)NT};
+}
+
+// ---------------------------------------------------------------------------
+// Device-scope (coherent across workgroups and XCDs) loads and stores.  Data
+// exchanged between a row's workgroups goes through these: they bypass the
+// non-coherent caches, so no L2 writeback/invalidate is needed.
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(double* p, double v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ double ld_dev(const double* p) {
+  return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this lane's outstanding memory operations have completed.
+__device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
+// operations only.  __syncthreads() also drains every outstanding global
+// load and store first, which would stall the chunk phase until its whole
+// stream has landed; the chunk phase tracks its global loads itself.
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t lane() { return threadIdx.x & 63; }
+__device__ __forceinline__ uint32_t wave() { return threadIdx.x >> 6; }
+__device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+// ---------------------------------------------------------------------------
+// Block-wide reductions and scans (all threads participate and receive the
+// result).  `red` is LDS scratch of at least NW elements of the type.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ T wave_max(T v) {
+  for (int o = 32; o > 0; o >>= 1) { T t = __shfl_xor(v, o); v = t > v ? t : v; }
+  return v;
+}
+template <typename T>
+__device__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  T s = red[0];
+  for (int i = 1; i < NW; ++i) s += red[i];
+  __syncthreads();
+  return s;
+}
+template <typename T>
+__device__ T block_max(T v, T* red) {
+  v = wave_max(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  T s = red[0];
+  for (int i = 1; i < NW; ++i) s = red[i] > s ? red[i] : s;
+  __syncthreads();
+  return s;
+}
+// Inclusive scan in thread order; *total receives the block total.
+template <typename T>
+__device__ T block_scan_incl(T v, T* red, T* total) {
+  const uint32_t l = lane();
+  for (int o = 1; o < 64; o <<= 1) {
+    T t = __shfl_up(v, o);
+    if (l >= (uint32_t)o) v += t;
+  }
+  if (l == 63) red[wave()] = v;
+  __syncthreads();
+  T before = T(0), all = T(0);
+  for (int i = 0; i < NW; ++i) {
+    T r = red[i];
+    if (i < (int)wave()) before += r;
+    all += r;
+  }
+  __syncthreads();
+  *total = all;
+  return before + v;
+}
+
+// ---------------------------------------------------------------------------
+// Wave primitives on DPP lane moves (no LDS round trip).  A row is 16 lanes;
+// row_shr:n shifts within a row, row_bcast:15 / row_bcast:31 carry a row's
+// last lane into the following rows.  Lanes with no source receive `old`
+// (the operation's identity), so the scans below are Hillis-Steele scans
+// within rows followed by the two cross-row carries.
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ uint32_t dpp(uint32_t old, uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, RM, 0xf, false);
+}
+constexpr int DPP_SHR1 = 0x111, DPP_SHR2 = 0x112, DPP_SHR4 = 0x114, DPP_SHR8 = 0x118;
+constexpr int DPP_BC15 = 0x142, DPP_BC31 = 0x143;
+
+// Inclusive sum scan in lane order.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+  v += dpp<DPP_SHR1>(0u, v);
+  v += dpp<DPP_SHR2>(0u, v);
+  v += dpp<DPP_SHR4>(0u, v);
+  v += dpp<DPP_SHR8>(0u, v);
+  v += dpp<DPP_BC15, 0xa>(0u, v);
+  v += dpp<DPP_BC31, 0xc>(0u, v);
+  return v;
+}
+__device__ __forceinline__ uint32_t bcast63(uint32_t v) { return (uint32_t)__builtin_amdgcn_readlane((int)v, 63); }
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) { return bcast63(wave_scan_u32(v)); }
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp<DPP_SHR1>(0u, v));
+  v = max(v, dpp<DPP_SHR2>(0u, v));
+  v = max(v, dpp<DPP_SHR4>(0u, v));
+  v = max(v, dpp<DPP_SHR8>(0u, v));
+  v = max(v, dpp<DPP_BC15, 0xa>(0u, v));
+  v = max(v, dpp<DPP_BC31, 0xc>(0u, v));
+  return bcast63(v);
+}
+__device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
+  v |= dpp<DPP_SHR1>(0u, v);
+  v |= dpp<DPP_SHR2>(0u, v);
+  v |= dpp<DPP_SHR4>(0u, v);
+  v |= dpp<DPP_SHR8>(0u, v);
+  v |= dpp<DPP_BC15, 0xa>(0u, v);
+  v |= dpp<DPP_BC31, 0xc>(0u, v);
+  return bcast63(v);
+}
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ unsigned long long dpp64(unsigned long long v) {
+  const uint32_t lo = dpp<CTRL, RM>(0u, (uint32_t)v), hi = dpp<CTRL, RM>(0u, (uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  unsigned long long t;
+  t = dpp64<DPP_SHR1>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR2>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR4>(v); v = t > v ? t : v;
+  t = dpp64<DPP_SHR8>(v); v = t > v ? t : v;
+  t = dpp64<DPP_BC15, 0xa>(v); v = t > v ? t : v;
+  t = dpp64<DPP_BC31, 0xc>(v); v = t > v ? t : v;
+  const uint32_t lo = bcast63((uint32_t)v), hi = bcast63((uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+// Sum over the wave (identity +0.0; addition order fixed by the lane tree).
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  unsigned long long b;
+  b = dpp64<DPP_SHR1>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR2>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR4>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR8>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC15, 0xa>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC31, 0xc>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  const unsigned long long r = __builtin_bit_cast(unsigned long long, v);
+  const uint32_t lo = bcast63((uint32_t)r), hi = bcast63((uint32_t)(r >> 32));
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+template <typename In>
+struct Quad;
+template <>
+struct Quad<float> {
+  using Raw = float4;
+  __device__ static Raw load(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  __device__ static void unpack(const Raw& r, float x[4]) { x[0] = r.x; x[1] = r.y; x[2] = r.z; x[3] = r.w; }
+  __device__ static float one(const float* p) { return *p; }
+};
+template <>
+struct Quad<uint16_t> {
+  using Raw = uint2;
+  __device__ static Raw load(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+  __device__ static void unpack(const Raw& r, float x[4]) {
+    x[0] = bf16_to_f32((uint16_t)(r.x & 0xffffu)); x[1] = bf16_to_f32((uint16_t)(r.x >> 16));
+    x[2] = bf16_to_f32((uint16_t)(r.y & 0xffffu)); x[3] = bf16_to_f32((uint16_t)(r.y >> 16));
+  }
+  __device__ static float one(const uint16_t* p) { return bf16_to_f32(*p); }
+};
+
+
+}  // namespace mxs

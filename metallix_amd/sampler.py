@@ -227,5 +227,26 @@ class Sampler:
         launch.out = out
         return launch
 
+    def logsoftmax_topn(self, logits, n: int, *, vocab: Optional[int] = None):
+        """Queues the T=1 log-softmax of every row with its n most likely IDs
+        (token_logprob, crates/app/cli/src/chat_turn.rs:506-563).  Returns
+        device tensors (ids i32[rows, n], logprobs f64[rows, n], maximum
+        f64[rows], log_normalizer f64[rows], status i32[rows])."""
+        torch = self.torch
+        rows = logits.shape[0]
+        V = vocab if vocab is not None else logits.shape[1]
+        dev = logits.device
+        ids = torch.empty((rows, max(n, 1)), dtype=torch.int32, device=dev)
+        lps = torch.empty((rows, max(n, 1)), dtype=torch.float64, device=dev)
+        mx = torch.empty(rows, dtype=torch.float64, device=dev)
+        ln = torch.empty(rows, dtype=torch.float64, device=dev)
+        st = torch.empty(rows, dtype=torch.int32, device=dev)
+        dtype = MXS_BF16 if logits.dtype == torch.bfloat16 else MXS_F32
+        rc = self.lib.mxs_logsoftmax_topn(self.ctx, logits.data_ptr(), dtype, rows, V, logits.stride(0), n,
+                                          ids.data_ptr(), lps.data_ptr(), mx.data_ptr(), ln.data_ptr(),
+                                          st.data_ptr())
+        self._check(rc, "mxs_logsoftmax_topn")
+        return ids[:, :n], lps[:, :n], mx, ln, st
+
     def sync(self):
         self._check(self.lib.mxs_sync(self.ctx), "mxs_sync")
