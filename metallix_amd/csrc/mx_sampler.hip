@@ -1701,6 +1701,9 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
+  e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->spec_scratch, mxs::spec_scratch_bytes(max_rows));
   const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;
   e = e ? e : hipMalloc(&ctx->d_zero_u32, nr * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->d_one_f64, nr * sizeof(double));

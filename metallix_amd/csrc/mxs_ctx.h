@@ -16,6 +16,8 @@ struct ChunkStat;
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);
+size_t spec_scratch_bytes(uint32_t max_rows);
+constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8), one per row
 
 // Device scratch of mxs_sample, sized for the context's limits.
 struct Work {

@@ -248,5 +248,29 @@ class Sampler:
         self._check(rc, "mxs_logsoftmax_topn")
         return ids[:, :n], lps[:, :n], mx, ln, st
 
+    def spec_verify(self, target, draft, draft_tokens, temperature, accept_uniform, resample_uniform,
+                    bonus_uniform):
+        """Queues speculative verification (accept_or_resample position by
+        position, crates/core/engine/src/speculative.rs:369-444; the bonus
+        draw past an accepted draft).  target f32[rows, K+1, V], draft
+        f32[rows, K, V], draft_tokens i32[rows, K], temperature f64[rows],
+        accept/resample f64[rows, K], bonus f64[rows].  Returns device tensors
+        (out_tokens i32[rows, K+1], count, accepted, status i32[rows])."""
+        torch = self.torch
+        rows, k1, V = target.shape
+        K = k1 - 1
+        dev = target.device
+        out = torch.empty((rows, k1), dtype=torch.int32, device=dev)
+        cnt = torch.empty(rows, dtype=torch.int32, device=dev)
+        acc = torch.empty(rows, dtype=torch.int32, device=dev)
+        st = torch.empty(rows, dtype=torch.int32, device=dev)
+        rc = self.lib.mxs_spec_verify(self.ctx, target.data_ptr(), _ptr(draft) if K else None, rows, K, V,
+                                      _ptr(draft_tokens) if K else None, temperature.data_ptr(),
+                                      _ptr(accept_uniform) if K else None, _ptr(resample_uniform) if K else None,
+                                      bonus_uniform.data_ptr(), out.data_ptr(), cnt.data_ptr(), acc.data_ptr(),
+                                      st.data_ptr())
+        self._check(rc, "mxs_spec_verify")
+        return out, cnt, acc, st
+
     def sync(self):
         self._check(self.lib.mxs_sync(self.ctx), "mxs_sync")
