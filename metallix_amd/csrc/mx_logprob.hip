@@ -29,7 +29,6 @@
 namespace mxs {
 
 constexpr uint32_t TOPN_MAX = 64;         // largest n served
-constexpr int NBR = 2048;                 // radix-select bins (11 bits)
 constexpr int TP = 5;                     // quads per thread per chunk (registers hold the chunk)
 constexpr int TMAXC = 128;                // chunks per row
 
@@ -69,56 +68,6 @@ struct alignas(16) TopnSmem {
   double red_d[NW];
   uint32_t s_cnt, s_last;
 };
-
-// The k-th largest (k >= 1) of the active 32-bit keys the workgroup's
-// threads hold (up to R each; bit r of `act` marks key[r] active), by three
-// radix passes (11, 11 and 10 bits) over LDS histograms; *above receives how
-// many active keys are larger.  Needs at least k active keys and three
-// zeroed NBR-word histograms, which it leaves dirty.
-template <int R>
-__device__ uint32_t block_kth_largest(const uint32_t (&key)[R], uint64_t act, uint32_t k, uint32_t* hist,
-                                      uint32_t* above) {
-  uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
-    const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
-    uint32_t* h = hist + p * NBR;
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (((act >> r) & 1ull) && (key[r] & pmask) == prefix) atomicAdd(&h[(key[r] >> sh) & dmask], 1u);
-    lds_barrier();
-    // Every wave finds the bin itself.  Lane j owns bins
-    // [NBR - 32 (j + 1), NBR - 32 j), visited from the highest.
-    const uint32_t hi = (uint32_t)NBR - 32u * lane();
-    uint32_t s = 0;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 4u * (uint32_t)(q + 1)]);
-      s += v.x + v.y + v.z + v.w;
-    }
-    const uint32_t inc = wave_scan_u32(s);
-    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
-    if (!reach) break;   // fewer than k active keys: the caller's contract is broken
-    const uint32_t L = (uint32_t)__builtin_ctzll(reach);
-    // the crossing bin inside lane L's range (every lane walks its own)
-    uint32_t run = inc - s, bin = hi - 1u, before = run;
-    bool found = false;
-    for (int q = 0; q < 32; ++q) {
-      const uint32_t c = h[hi - 1u - (uint32_t)q];
-      if (!found && run + c >= need) { found = true; bin = hi - 1u - (uint32_t)q; before = run; }
-      run += c;
-    }
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
-    const uint32_t cnt_above = (uint32_t)__builtin_amdgcn_readlane((int)before, (int)L);
-    need -= cnt_above;
-    abv += cnt_above;
-    prefix |= b << sh;
-    pmask |= dmask << sh;
-  }
-  *above = abv;
-  return prefix;
-}
 
 __device__ __forceinline__ unsigned long long entry_key(uint32_t k, uint32_t id) {
   return ((unsigned long long)k << 32) | (unsigned long long)(~id);

@@ -126,8 +126,12 @@ struct alignas(16) ChunkSmem {
   alignas(16) uint32_t wcnt[PER_MAX * NW + 32];   // candidates per (slice, wave), padded for the scan
   WavePart wp[NW];
   WavePart wq[NW];
-  uint32_t s_last;
 };
+// The row finisher runs 256 threads (4 waves, one per SIMD): its decision
+// logic is serial in places and wants registers more than lanes.
+constexpr int FT = 1024;
+constexpr int FW = FT / 64;
+constexpr uint32_t BPT = NB / FT;          // radix bins per finisher thread
 struct alignas(16) FinSmem {
   float cl[CCAP];                      // candidates cached in LDS, token-ID order
   uint32_t cid[CCAP];
@@ -141,19 +145,25 @@ struct alignas(16) FinSmem {
       uint32_t hcnt[NB];               // radix-select histograms
       double hmass[NB];
     } h;
+    uint32_t hist3[3][NBR];            // finish_small's radix select
   } u;
+  uint32_t kbit[CCAP / 32];            // finish_small: kept candidates after a nucleus cut
+  uint32_t sc_u[2][FW];                // single-barrier scan slots
+  double sc_d[2][FW];
+  double rd[FW][2];                    // multi-value reduction
+  uint32_t ru[FW][4];
+  unsigned long long rm[FW];
   uint8_t kflag[ECAP];                 // kept flags by E index
   ChunkStat st[MAXC];
   double cscale[MAXC];
   uint32_t coff[MAXC + 1];
-  uint32_t red_u[NW];
-  double red_d[NW];
-  float red_f[NW];
-  uint32_t red_i[NW];
+  uint32_t red_u[FW];
+  double red_d[FW];
+  float red_f[FW];
+  uint32_t red_i[FW];
   uint32_t s_u[16];
   double s_d[8];
 };
-constexpr size_t SMEM_BYTES = sizeof(FinSmem) > sizeof(ChunkSmem) ? sizeof(FinSmem) : sizeof(ChunkSmem);
 
 // ---------------------------------------------------------------------------
 // Per-row parameters and their validation (uniform across the workgroup).
@@ -214,7 +224,7 @@ __device__ __forceinline__ RowCfg load_cfg(const double* __restrict__ temperatur
 
 // Error precedence after the parameter checks: history ids, bias entries,
 // uniform, non-finite adjusted logit, empty support.
-__device__ int32_t combine_errors(const RowCfg& c, uint32_t flags, uint32_t nlegal) {
+__device__ __forceinline__ int32_t combine_errors(const RowCfg& c, uint32_t flags, uint32_t nlegal) {
   if (c.err) return c.err;
   if (flags & F_HIST) return MXS_ROW_INVALID_HISTORY;
   if (flags & F_BIAS) return MXS_ROW_INVALID_BIAS;
@@ -250,7 +260,7 @@ __device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, fl
 // (one lane per token, cnt <= 64, one wave).  Used by the finisher to locate
 // a draw inside a 256-token segment without the chunk's registers.
 template <typename In>
-__device__ void rederive_token(const SampleArgs& A, const RowCfg& c, uint32_t row, uint32_t id,
+__device__ __forceinline__ void rederive_token(const SampleArgs& A, const RowCfg& c, uint32_t row, uint32_t id,
                                float* l_out, bool* legal_out) {
   const mxs_batch& b = A.b;
   const In* p = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
@@ -268,14 +278,14 @@ __device__ void rederive_token(const SampleArgs& A, const RowCfg& c, uint32_t ro
 // Finisher helpers.
 
 // Bitonic sort of n (<= ECAP) keys into descending order, in LDS.
-__device__ void bitonic_sort_desc(unsigned long long* key, uint32_t n) {
+__device__ __forceinline__ void bitonic_sort_desc(unsigned long long* key, uint32_t n) {
   uint32_t np = 1;
   while (np < n) np <<= 1;
-  for (uint32_t i = n + threadIdx.x; i < np; i += NT) key[i] = 0ull;
+  for (uint32_t i = n + threadIdx.x; i < np; i += FT) key[i] = 0ull;
   __syncthreads();
   for (uint32_t size = 2; size <= np; size <<= 1) {
     for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
-      for (uint32_t t = threadIdx.x; t < np / 2; t += NT) {
+      for (uint32_t t = threadIdx.x; t < np / 2; t += FT) {
         const uint32_t i = 2 * stride * (t / stride) + (t % stride);
         const uint32_t j = i + stride;
         const bool desc = ((i & size) == 0);
@@ -300,7 +310,12 @@ __device__ __forceinline__ double sum_bound(double s, uint32_t n, double term_ul
 // ---------------------------------------------------------------------------
 // Finisher state shared by its phases.
 struct FinCtx {
-  const SampleArgs* A;
+  // copies of the launch arguments the decisions need (taking the address
+  // of the by-value kernel argument would force it into private memory)
+  const float* cand_l;
+  const uint32_t* cand_id;
+  uint32_t CH;
+  mxs_out o;
   const RowCfg* c;
   uint32_t row, mode, C, V, ncand, nlegal;
   uint64_t rbase;
@@ -311,7 +326,13 @@ struct FinCtx {
   bool have_total;
   uint32_t* kbits;
   uint32_t nwords;
+  uint64_t* timing;    // phase timestamps (diagnostics), null when off
 };
+
+// Finisher phase timestamp k (slot MAXC of the row's timing record).
+__device__ __forceinline__ void fstamp(const FinCtx& X, uint32_t k) {
+  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + k] = wall_clock64();
+}
 
 __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, uint64_t rbase, uint32_t CH, uint32_t j) {
   uint32_t q = 0;
@@ -322,10 +343,10 @@ __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, ui
 // Candidate j (token-ID order): from LDS when cached, else from the
 // device-scope candidate arrays.
 __device__ __forceinline__ float cand_l(const FinCtx& X, const FinSmem& F, uint32_t j) {
-  return X.lds_c ? F.cl[j] : ld_dev(&X.A->w.cand_l[cand_pos_of(F, X.C, X.rbase, X.A->CH, j)]);
+  return X.lds_c ? F.cl[j] : X.cand_l[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
 }
 __device__ __forceinline__ uint32_t cand_id(const FinCtx& X, const FinSmem& F, uint32_t j) {
-  return X.lds_c ? F.cid[j] : ld_dev(&X.A->w.cand_id[cand_pos_of(F, X.C, X.rbase, X.A->CH, j)]);
+  return X.lds_c ? F.cid[j] : X.cand_id[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
 }
 __device__ __forceinline__ bool member(const FinCtx& X, float l, uint32_t id) {
   if (X.k_path) {
@@ -338,7 +359,7 @@ __device__ __forceinline__ bool member(const FinCtx& X, float l, uint32_t id) {
 
 __device__ __forceinline__ void write_result(const FinCtx& X, int32_t status, int32_t token, double lp, uint32_t kept) {
   if (threadIdx.x == 0) {
-    const mxs_out& o = X.A->o;
+    const mxs_out& o = X.o;
     o.token[X.row] = token;
     o.status[X.row] = status;
     if (o.sampling_logprob) o.sampling_logprob[X.row] = lp;
@@ -351,14 +372,14 @@ __device__ __forceinline__ void write_result(const FinCtx& X, int32_t status, in
 // over the candidates; the nucleus cut comes from a mass-weighted radix
 // select (11/11/10-bit passes, LDS count and f64 mass histograms) whose bin
 // decisions are certified with the same bounds as the exact path.
-__device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
+__device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   const RowCfg& c = *X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
   auto weight = [&](float l) { return exp_neg(((double)l - X.M) / c.T); };
   bool uncert = false;
   double wpart = 0.0, wmin = INFINITY;
-  for (uint32_t j = tid; j < n; j += NT) {
+  for (uint32_t j = tid; j < n; j += FT) {
     const float l = cand_l(X, F, j);
     if (member(X, l, cand_id(X, F, j))) {
       const double w = weight(l);
@@ -390,12 +411,11 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   if (cut) {
     uint32_t prefix = 0, pmask = 0, above_n = 0;
     double above = 0.0;
-    const int shifts[3] = {21, 10, 0};
     for (int pass = 0; pass < 3; ++pass) {
-      const int sh = shifts[pass];
-      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
+      const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      for (uint32_t t = tid; t < (uint32_t)NB; t += FT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
       __syncthreads();
-      for (uint32_t j = tid; j < n; j += NT) {
+      for (uint32_t j = tid; j < n; j += FT) {
         const float l = cand_l(X, F, j);
         const uint32_t key = okey(l);
         if ((key & pmask) == prefix && member(X, l, cand_id(X, F, j))) {
@@ -405,26 +425,38 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
         }
       }
       __syncthreads();
-      const uint32_t b_hi = NB - 1 - 2 * tid, b_lo = b_hi - 1;
-      const double mh = F.u.h.hmass[b_hi], ml = F.u.h.hmass[b_lo];
-      const uint32_t nh = F.u.h.hcnt[b_hi], nl = F.u.h.hcnt[b_lo];
-      double mtot;
-      uint32_t ntot;
-      const double minc = above + block_scan_incl<double>(mh + ml, F.red_d, &mtot);
-      const uint32_t ninc = above_n + block_scan_incl<uint32_t>(nh + nl, F.red_u, &ntot);
-      const double mexc = minc - mh - ml;
-      const uint32_t nexc = ninc - nh - nl;
+      // Each thread owns BPT consecutive bins in descending key order; the
+      // per-thread intervals (mexc, minc] tile the mass exactly (the
+      // exclusive prefix is the previous thread's inclusive value), and so
+      // do the per-bin intervals inside a thread, so at most one bin claims
+      // theta.
+      const uint32_t b0 = NB - 1 - BPT * tid;
+      double msum = 0.0;
+      uint32_t nsum = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) { msum += F.u.h.hmass[b0 - i]; nsum += F.u.h.hcnt[b0 - i]; }
+      double mtot, mexc;
+      uint32_t ntot, nexc;
+      const double minc = above + block_scan_pair<double>(msum, F.red_d, &mexc, &mtot);
+      mexc += above;
+      nexc = above_n + block_scan_incl<uint32_t>(nsum, F.red_u, &ntot) - nsum;
       if (tid == 0) { F.s_u[4] = NONE; F.s_u[6] = 0u; }
       __syncthreads();
-      const double e1 = sum_bound(mexc + mh, nexc + nh + 64u, 8.0);
-      if (nh && mexc < theta && theta <= mexc + mh) {
-        F.s_u[4] = b_hi; F.s_u[5] = nexc; F.s_d[4] = mexc;
-        const double e0 = sum_bound(mexc, nexc + 64u, 8.0);
-        if (!(mexc + e0 < theta - theta_err) || !(mexc + mh - e1 >= theta + theta_err)) F.s_u[6] = 1u;
-      } else if (nl && mexc + mh < theta && theta <= minc) {
-        F.s_u[4] = b_lo; F.s_u[5] = nexc + nh; F.s_d[4] = mexc + mh;
-        const double e2 = sum_bound(minc, ninc + 64u, 8.0);
-        if (!(mexc + mh + e1 < theta - theta_err) || !(minc - e2 >= theta + theta_err)) F.s_u[6] = 1u;
+      double lo = mexc;
+      uint32_t nlo = nexc;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) {
+        const double mh = F.u.h.hmass[b0 - i];
+        const uint32_t nh = F.u.h.hcnt[b0 - i];
+        const double hi = i + 1 == BPT ? minc : lo + mh;
+        if (nh && lo < theta && theta <= hi) {
+          F.s_u[4] = b0 - i; F.s_u[5] = nlo; F.s_d[4] = lo;
+          const double e0 = sum_bound(lo, nlo + 64u, 8.0);
+          const double e1 = sum_bound(hi, nlo + nh + 64u, 8.0);
+          if (!(lo + e0 < theta - theta_err) || !(hi - e1 >= theta + theta_err)) F.s_u[6] = 1u;
+        }
+        lo = hi;
+        nlo += nh;
       }
       __syncthreads();
       const uint32_t bin = F.s_u[4];
@@ -461,7 +493,7 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
       const uint32_t jneed = F.s_u[6];
       if (F.s_u[7]) uncert = true;
       uint32_t seen = 0;
-      for (uint32_t base = 0; base < n; base += NT) {
+      for (uint32_t base = 0; base < n; base += FT) {
         const uint32_t j = base + tid;
         bool tie = false;
         uint32_t id = 0;
@@ -496,7 +528,7 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   };
   double kpart = 0.0;
   uint32_t kn = 0, close = 0, bad = 0;
-  for (uint32_t j = tid; j < n; j += NT) {
+  for (uint32_t j = tid; j < n; j += FT) {
     const float l = cand_l(X, F, j);
     double s;
     const bool k = kept(l, cand_id(X, F, j), &s);
@@ -512,7 +544,7 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
   __syncthreads();
   double run = 0.0;
-  for (uint32_t base = 0; base < n; base += NT) {
+  for (uint32_t base = 0; base < n; base += FT) {
     const uint32_t j = base + tid;
     double s = 0.0, w = 0.0;
     uint32_t id = 0;
@@ -549,9 +581,9 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
   if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
   write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, shifted - log(S), nkept);
   if (X.kbits) {
-    for (uint32_t q = tid; q < X.nwords; q += NT) X.kbits[q] = 0u;
+    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
     __syncthreads();
-    for (uint32_t j = tid; j < n; j += NT) {
+    for (uint32_t j = tid; j < n; j += FT) {
       const float l = cand_l(X, F, j);
       const uint32_t id = cand_id(X, F, j);
       double s;
@@ -567,7 +599,7 @@ __device__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
 // the final set is P with no sort, otherwise the crossing lies inside P and
 // only P is sorted.  An uncertain crossing replays the reference's
 // sequential f64 sums over E sorted.
-__device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_close_in) {
+__device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_close_in) {
   const RowCfg& c = *X.c;
   const uint32_t tid = threadIdx.x;
   auto el = [&](uint32_t t) { return F.cl[F.eidx[t]]; };
@@ -576,7 +608,7 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
   bool uncert = mp_close_in;
   double epart = 0.0, ppart = 0.0, wmin = INFINITY;
   uint32_t pn = 0, close = 0;
-  for (uint32_t t = tid; t < ne; t += NT) {
+  for (uint32_t t = tid; t < ne; t += FT) {
     const double s = ((double)el(t) - X.M) / c.T;
     const double w = exp_neg(s);
     F.u.e.ew[t] = w;
@@ -620,7 +652,7 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
     // The crossing lies inside P: sort P and find the first prefix reaching theta.
     if (tid == 0) F.s_u[8] = 0u;
     __syncthreads();
-    for (uint32_t t = tid; t < ne; t += NT) {
+    for (uint32_t t = tid; t < ne; t += FT) {
       if (F.kflag[t]) {
         const uint32_t at = atomicAdd(&F.s_u[8], 1u);
         F.u.e.skey[at] = ((unsigned long long)okey(el(t)) << 32) | (unsigned long long)(0xffffffffu - t);
@@ -631,7 +663,7 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
     if (tid == 0) { F.s_u[6] = NONE; F.s_u[7] = 0u; }
     __syncthreads();
     double run = 0.0;
-    for (uint32_t base = 0; base < np_; base += NT) {
+    for (uint32_t base = 0; base < np_; base += FT) {
       const uint32_t p = base + tid;
       const double w = p < np_ ? F.u.e.ew[0xffffffffu - (uint32_t)F.u.e.skey[p]] : 0.0;
       double tot;
@@ -657,15 +689,15 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
       replay = true;
     } else {
       // kept = the first `first + 1` sorted positions of P
-      for (uint32_t t = tid; t < ne; t += NT) F.kflag[t] = 0;
+      for (uint32_t t = tid; t < ne; t += FT) F.kflag[t] = 0;
       __syncthreads();
-      for (uint32_t p = tid; p <= first; p += NT) F.kflag[0xffffffffu - (uint32_t)F.u.e.skey[p]] = 1;
+      for (uint32_t p = tid; p <= first; p += FT) F.kflag[0xffffffffu - (uint32_t)F.u.e.skey[p]] = 1;
     }
     __syncthreads();
   }
   if (replay) {
     // Sort all of E and replay the reference's sequential f64 sums.
-    for (uint32_t t = tid; t < ne; t += NT)
+    for (uint32_t t = tid; t < ne; t += FT)
       F.u.e.skey[t] = ((unsigned long long)okey(el(t)) << 32) | (unsigned long long)(0xffffffffu - t);
     __syncthreads();
     bitonic_sort_desc(F.u.e.skey, ne);
@@ -690,7 +722,7 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
     const uint32_t nk = F.s_u[6];
     if (F.s_u[7]) uncert = true;
     // kept = sorted positions < nk, intersected with P
-    for (uint32_t p = tid; p < ne; p += NT) {
+    for (uint32_t p = tid; p < ne; p += FT) {
       const uint32_t t = 0xffffffffu - (uint32_t)F.u.e.skey[p];
       if (p >= nk) F.kflag[t] = 0;
     }
@@ -699,14 +731,14 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
 
   // sample_categorical rejects a kept token whose shifted logit overflows.
   uint32_t bad = 0;
-  for (uint32_t t = tid; t < ne; t += NT)
+  for (uint32_t t = tid; t < ne; t += FT)
     if (F.kflag[t] && !isfinite(((double)el(t) - X.M) / c.T)) bad = 1;
   if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
 
   // Inverse-CDF draw over the kept set in token-ID order.
   double kpart = 0.0;
   uint32_t kn = 0;
-  for (uint32_t t = tid; t < ne; t += NT)
+  for (uint32_t t = tid; t < ne; t += FT)
     if (F.kflag[t]) { kpart += F.u.e.ew[t]; ++kn; }
   const double S = block_sum<double>(kpart, F.red_d);
   const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
@@ -715,7 +747,7 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
   if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
   __syncthreads();
   double run = 0.0;
-  for (uint32_t base = 0; base < ne; base += NT) {
+  for (uint32_t base = 0; base < ne; base += FT) {
     const uint32_t t = base + tid;
     const double w = (t < ne && F.kflag[t]) ? F.u.e.ew[t] : 0.0;
     double tot;
@@ -741,36 +773,274 @@ __device__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_c
   const double shifted = ((double)el(pick) - X.M) / c.T;
   write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)eid(pick), shifted - log(S), nkept);
   if (X.kbits) {
-    for (uint32_t q = tid; q < X.nwords; q += NT) X.kbits[q] = 0u;
+    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
     __syncthreads();
-    for (uint32_t t = tid; t < ne; t += NT)
+    for (uint32_t t = tid; t < ne; t += FT)
       if (F.kflag[t]) atomicOr(&X.kbits[eid(t) >> 5], 1u << (eid(t) & 31u));
   }
+}
+
+// ---------------------------------------------------------------------------
+// Lean finisher for candidate sets cached in LDS: every thread holds up to
+// FR contiguous candidates (token-ID order), the top-k head comes from one
+// three-pass radix select with ties ranked in ID order, sums come from one
+// multi-value reduction, and a sort happens only when the nucleus cut falls
+// inside the min-p set.  Returns false, having written nothing, for a row
+// the general path must decide (uncertain cuts, the top_p = 1 freeze rule,
+// large sorts); the general path then recomputes from the LDS candidates.
+constexpr int FR = CCAP / FT;   // at most 32 candidates per thread (bit masks)
+
+__device__ __forceinline__ bool finish_small(const FinCtx& X, FinSmem& F) {
+  const RowCfg& c = *X.c;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n = X.ncand;
+  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + 3] = n;   // candidate count (diagnostics)
+  if (n == 0 || n > (uint32_t)CCAP || !X.lds_c) return false;
+  const uint32_t R = (n + FT - 1u) / FT;
+  if (R > (uint32_t)FR) return false;
+  // this thread's candidates are j = tid * R + r, r < R (token-ID order);
+  // their weights live in LDS (wl[j]), their flags in bit masks
+  auto cj = [&](uint32_t r) { return tid * R + r; };
+  double* wl = F.u.e.ew;   // CCAP doubles: ew and skey are contiguous
+  uint64_t act = 0;
+  for (uint32_t r = 0; r < R; ++r)
+    if (cj(r) < n) act |= 1ull << r;
+  // ---- the working set E: the top-k head, the exact min-p set, or all ----
+  uint64_t inE = 0;
+  uint32_t unc = 0;
+  if (X.k_path) {
+    for (uint32_t t = tid; t < 3u * NBR; t += FT) (&F.u.hist3[0][0])[t] = 0u;
+    lds_barrier();
+    uint32_t above = 0;
+    const uint32_t kappa = block_kth_largest_fn([&](uint32_t r) { return okey(F.cl[cj(r)]); }, R, act, c.k,
+                                                &F.u.hist3[0][0], &above);
+    uint32_t nt = 0;
+    for (uint32_t r = 0; r < R; ++r)
+      if (((act >> r) & 1ull) && okey(F.cl[cj(r)]) == kappa) ++nt;
+    uint32_t ttot;
+    uint32_t tr = block_excl_scan_u32(nt, F.sc_u[0], &ttot);
+    const uint32_t need_t = c.k - above;
+    for (uint32_t r = 0; r < R; ++r) {
+      if (!((act >> r) & 1ull)) continue;
+      const uint32_t key = okey(F.cl[cj(r)]);
+      if (key > kappa) inE |= 1ull << r;
+      else if (key == kappa) { if (tr < need_t) inE |= 1ull << r; ++tr; }
+    }
+    lds_barrier();   // the histograms share LDS with the weights below
+  } else if (X.mode == M_MINP) {
+    for (uint32_t r = 0; r < R; ++r) {
+      if (!((act >> r) & 1ull)) continue;
+      const double sh = ((double)F.cl[cj(r)] - X.M) / c.T;
+      if (sh >= X.L) inE |= 1ull << r;
+      if (fabs(sh - X.L) < X.Lclose) unc = 1;
+    }
+  } else {
+    inE = act;
+  }
+  fstamp(X, 4);
+  // ---- weights, the min-p subset P, sums ----------------------------------
+  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
+  uint64_t inP = 0;
+  double epart = 0.0, ppart = 0.0;
+  unsigned long long wmin_key = ~0ull;   // smallest weight (non-negative doubles order as u64)
+  uint32_t ne = 0, pn = 0;
+  for (uint32_t r = 0; r < R; ++r) {
+    if (!((inE >> r) & 1ull)) continue;
+    const double sh = ((double)F.cl[cj(r)] - X.M) / c.T;
+    const double w = exp_neg(sh);
+    wl[cj(r)] = w;
+    epart += w;
+    ++ne;
+    const unsigned long long wk = __builtin_bit_cast(unsigned long long, w);
+    wmin_key = wk < wmin_key ? wk : wmin_key;
+    bool p = true;
+    if (apply_minp) {
+      p = sh >= X.L;
+      if (fabs(sh - X.L) < X.Lclose) unc = 1;
+    }
+    if (p) { inP |= 1ull << r; ppart += w; ++pn; }
+  }
+  {
+    const double a = wave_sum_f64(epart), b = wave_sum_f64(ppart);
+    const uint32_t e1 = wave_sum_u32(ne), e2 = wave_sum_u32(pn), e3 = wave_or_u32(unc);
+    const unsigned long long mk = ~wave_max_u64(~wmin_key);
+    if (lane() == 0) {
+      F.rd[wave()][0] = a; F.rd[wave()][1] = b;
+      F.ru[wave()][0] = e1; F.ru[wave()][1] = e2; F.ru[wave()][2] = e3;
+      F.rm[wave()] = mk;
+    }
+  }
+  lds_barrier();
+  double esum = 0.0, psum = 0.0;
+  uint32_t NE = 0, NP = 0;
+  unsigned long long wmk = ~0ull;
+#pragma unroll
+  for (int q = 0; q < FW; ++q) {
+    esum += F.rd[q][0]; psum += F.rd[q][1];
+    NE += F.ru[q][0]; NP += F.ru[q][1]; unc |= F.ru[q][2];
+    wmk = F.rm[q] < wmk ? F.rm[q] : wmk;
+  }
+  const double wmin = __builtin_bit_cast(double, wmk);
+  fstamp(X, 5);
+  // ---- the nucleus cut ------------------------------------------------------
+  double total = X.total, total_err = X.total_err;
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, NE, 8.0); }
+  bool theta_set = false;
+  double theta = 0.0, theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      if (!(wmin > 2.3e-16 * esum)) return false;   // the running sum may stall: replay
+    } else {
+      theta_set = true;
+      theta = c.top_p * esum;
+      theta_err = c.top_p * sum_bound(esum, NE, 8.0) + U * theta;
+    }
+  } else if (c.top_p < 1.0) {
+    theta_set = true;
+    theta = c.top_p * total;
+    theta_err = c.top_p * total_err + U * theta;
+  }
+  uint64_t kept = inP;
+  if (theta_set && !(psum + sum_bound(psum, NP, 8.0) < theta - theta_err)) {
+    // The cut falls inside P: order P by (value desc, ID asc) and find the
+    // first prefix reaching theta.
+    constexpr uint32_t PCAP = 1024;
+    if (NP > PCAP) return false;
+    unsigned long long* pkey = reinterpret_cast<unsigned long long*>(F.eidx);   // PCAP keys
+    double* sw = reinterpret_cast<double*>(F.eidx) + PCAP;                       // PCAP sorted weights
+    uint16_t* prank = reinterpret_cast<uint16_t*>(F.kflag);                      // PCAP ranks
+    uint32_t ptot;
+    uint32_t pos = block_excl_scan_u32((uint32_t)__builtin_popcountll(inP), F.sc_u[1], &ptot);
+    for (uint32_t r = 0; r < R; ++r) {
+      if (!((inP >> r) & 1ull)) continue;
+      const uint32_t j = cj(r);
+      pkey[pos] = ((unsigned long long)okey(F.cl[j]) << 32) | (unsigned long long)(~j);
+      ++pos;
+    }
+    for (uint32_t t = tid; t < CCAP / 32; t += FT) F.kbit[t] = 0u;
+    lds_barrier();
+    for (uint32_t e = tid; e < NP; e += FT) {
+      const unsigned long long mine = pkey[e];
+      uint32_t rank = 0;
+      for (uint32_t q = 0; q < NP; ++q) rank += pkey[q] > mine ? 1u : 0u;
+      sw[rank] = wl[~(uint32_t)mine];
+      prank[e] = (uint16_t)rank;
+    }
+    if (tid == 0) { F.s_u[6] = NONE; F.s_u[7] = 0u; }
+    lds_barrier();
+    double run = 0.0;
+    for (uint32_t base = 0; base < NP; base += FT) {
+      const uint32_t p = base + tid;
+      double tot;
+      const double vv = p < NP ? sw[p] : 0.0;
+      const double inc = run + block_incl_scan_f64(vv, F.sc_d[(base / FT) & 1u], &tot);
+      const double exc = inc - vv;
+      if (p < NP) {
+        const double e_inc = sum_bound(inc, p + 65u, 8.0);
+        const double e_exc = sum_bound(exc, p + 64u, 8.0);
+        if (!(inc + e_inc < theta - theta_err) && (p == 0 || exc + e_exc < theta - theta_err)) {
+          F.s_u[6] = p;
+          if (!(inc - e_inc >= theta + theta_err)) F.s_u[7] = 1u;
+        }
+      }
+      run += tot;
+    }
+    lds_barrier();
+    const uint32_t first = F.s_u[6];
+    if (first == NONE || F.s_u[7]) return false;   // uncertain cut: replay
+    for (uint32_t e = tid; e < NP; e += FT) {
+      if (prank[e] <= first) {
+        const uint32_t j = ~(uint32_t)pkey[e];
+        atomicOr(&F.kbit[j >> 5], 1u << (j & 31u));
+      }
+    }
+    lds_barrier();
+    kept = 0;
+    for (uint32_t r = 0; r < R; ++r) {
+      const uint32_t j = cj(r);
+      if (((inP >> r) & 1ull) && ((F.kbit[j >> 5] >> (j & 31u)) & 1u)) kept |= 1ull << r;
+    }
+  }
+  fstamp(X, 6);
+  // ---- overflow check and the inverse-CDF draw in token-ID order ----------
+  double kpart = 0.0;
+  uint32_t kn = 0;
+  bool bad = false;
+  for (uint32_t r = 0; r < R; ++r) {
+    if (!((kept >> r) & 1ull)) continue;
+    kpart += wl[cj(r)];
+    ++kn;
+    if (!isfinite(((double)F.cl[cj(r)] - X.M) / c.T)) bad = true;
+  }
+  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; F.s_u[3] = 0u; F.s_u[4] = unc; }
+  uint32_t nkept;
+  (void)block_excl_scan_u32(kn, F.sc_u[0], &nkept);
+  if (bad) F.s_u[3] = 1u;
+  double S;
+  const double kinc = block_incl_scan_f64(kpart, F.sc_d[1], &S);
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  double cum = kinc - kpart;
+  for (uint32_t r = 0; r < R; ++r) {
+    if (!((kept >> r) & 1ull)) continue;
+    const uint32_t j = cj(r);
+    const double w = wl[j];
+    const double prev = cum;
+    cum += w;
+    if (w > 0.0) {
+      atomicMax(&F.s_u[1], j + 1u);
+      if (target < cum && !(target < prev)) {
+        F.s_u[0] = j;
+        if (fabs(target - prev) <= derr || fabs(cum - target) <= derr) F.s_u[2] = 1u;
+      }
+    }
+  }
+  lds_barrier();
+  if (F.s_u[3]) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
+  bool uncert = F.s_u[4] != 0u || F.s_u[2] != 0u;
+  uint32_t pick = F.s_u[0];
+  if (pick == NONE) {
+    // rounding left the variate past the accumulated mass: last positive kept token
+    pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
+    uncert = true;
+  }
+  if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
+  const double shifted = ((double)F.cl[pick] - X.M) / c.T;
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.cid[pick], shifted - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
+    __syncthreads();
+    for (uint32_t r = 0; r < R; ++r) {
+      if (!((kept >> r) & 1ull)) continue;
+      const uint32_t tok = F.cid[cj(r)];
+      atomicOr(&X.kbits[tok >> 5], 1u << (tok & 31u));
+    }
+  }
+  return true;
 }
 
 // ---------------------------------------------------------------------------
 // The row finisher.  Runs in the last chunk workgroup of a row, after every
 // chunk published its statistics and candidates.
 template <typename In>
-__device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
+__device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
                            uint64_t rbase, double invT) {
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
   const uint32_t C = A.C;
-  if (tid == 0) st_dev(&A.w.ctr[row], 0u);   // ready for the next launch
-  for (uint32_t q = tid; q < C; q += NT) {
+  for (uint32_t q = tid; q < C; q += FT) {
     const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + q];
     ChunkStat v;
-    v.maxkey = ld_dev(&st->maxkey);
-    v.gbest_id = ld_dev(&st->gbest_id);
-    v.gbest_val = ld_dev(&st->gbest_val);
-    v.nlegal = ld_dev(&st->nlegal);
-    v.ncand = ld_dev(&st->ncand);
-    v.flags = ld_dev(&st->flags);
-    v.mass = ld_dev(&st->mass);
-    v.mass_err = ld_dev(&st->mass_err);
-    v.minkey = ld_dev(&st->minkey);
+    v.maxkey = *(&st->maxkey);
+    v.gbest_id = *(&st->gbest_id);
+    v.gbest_val = *(&st->gbest_val);
+    v.nlegal = *(&st->nlegal);
+    v.ncand = *(&st->ncand);
+    v.flags = *(&st->flags);
+    v.mass = *(&st->mass);
+    v.mass_err = *(&st->mass_err);
+    v.minkey = *(&st->minkey);
     F.st[q] = v;
   }
   __syncthreads();
@@ -799,18 +1069,18 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   const uint32_t nwords = (V + 31u) / 32u;
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
-  X.A = &A; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
-  X.kbits = kbits; X.nwords = nwords; X.M = M;
+  X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
+  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing;
   if (err) {
     write_result(X, err, -1, 0.0, 0u);
     if (kbits)
-      for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = 0u;
+      for (uint32_t q = tid; q < nwords; q += FT) kbits[q] = 0u;
     return;
   }
   if (mode == M_GREEDY) {
     write_result(X, 0, (int32_t)bi, 0.0, 1u);
     if (kbits)
-      for (uint32_t q = tid; q < nwords; q += NT) kbits[q] = (q == (bi >> 5)) ? (1u << (bi & 31u)) : 0u;
+      for (uint32_t q = tid; q < nwords; q += FT) kbits[q] = (q == (bi >> 5)) ? (1u << (bi & 31u)) : 0u;
     return;
   }
   const bool k_act = c.k > 0 && c.k < nlegal;
@@ -821,12 +1091,12 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     for (uint32_t q = 0; q < C; ++q)
       if (F.st[q].nlegal && F.st[q].minkey < mink) mink = F.st[q].minkey;
     if (!isfinite(((double)okey_value(mink) - M) / c.T)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
-    const uint32_t segs_per_chunk = A.per * NW;
+    const uint32_t segs_per_chunk = A.per * NW;   // the chunk kernel's 256-token (slice, wave) segments
     const uint32_t nseg = C * segs_per_chunk;
     double part = 0.0;
-    for (uint32_t s = tid; s < nseg; s += NT) {
+    for (uint32_t s = tid; s < nseg; s += FT) {
       const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-      if (F.st[q].nlegal) part += ld_dev(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
+      if (F.st[q].nlegal) part += A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r] * F.cscale[q];
     }
     const double total = block_sum<double>(part, F.red_d);
     const double target = c.u * total;
@@ -836,12 +1106,12 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
     __syncthreads();
     double run = 0.0;
-    for (uint32_t base = 0; base < nseg; base += NT) {
+    for (uint32_t base = 0; base < nseg; base += FT) {
       const uint32_t s = base + tid;
       double w = 0.0;
       if (s < nseg) {
         const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-        if (F.st[q].nlegal) w = ld_dev(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
+        if (F.st[q].nlegal) w = A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r] * F.cscale[q];
       }
       double tot;
       const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
@@ -930,7 +1200,7 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     near = near || F.s_u[4] != 0u;
     write_result(X, near ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, F.s_d[1] - log(total), nlegal);
     if (kbits) {
-      for (uint32_t q = tid; q < nwords; q += NT) {
+      for (uint32_t q = tid; q < nwords; q += FT) {
         uint32_t wv = 0xffffffffu;
         if (q == nwords - 1 && (V & 31u)) wv = (1u << (V & 31u)) - 1u;
         if (A.masked) {
@@ -951,21 +1221,21 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   X.lds_c = ncand <= (uint32_t)CCAP;
   // One bulk load of every candidate into LDS: all loads in flight at once.
   if (X.lds_c) {
-    for (uint32_t j0 = 0; j0 < ncand; j0 += NT * 4u) {
+    for (uint32_t j0 = 0; j0 < ncand; j0 += FT * 4u) {
       float lv8[4];
       uint32_t iv8[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t j = j0 + (uint32_t)u * NT + tid;
+        const uint32_t j = j0 + (uint32_t)u * FT + tid;
         if (j < ncand) {
           const uint64_t pos = cand_pos_of(F, C, rbase, A.CH, j);
-          lv8[u] = ld_dev(&A.w.cand_l[pos]);
-          iv8[u] = ld_dev(&A.w.cand_id[pos]);
+          lv8[u] = *(&A.w.cand_l[pos]);
+          iv8[u] = *(&A.w.cand_id[pos]);
         }
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t j = j0 + (uint32_t)u * NT + tid;
+        const uint32_t j = j0 + (uint32_t)u * FT + tid;
         if (j < ncand) { F.cl[j] = lv8[u]; F.cid[j] = iv8[u]; }
       }
     }
@@ -999,12 +1269,17 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
   X.kappa = 0;
   X.id_tie = NONE;
+  if (mode != M_KEEPALL && finish_small(X, F)) {
+    stamp(A, row, MAXC, 2);
+    return;
+  }
+  __syncthreads();   // the general path below reuses LDS the lean finisher touched
   uint32_t ties_needed = 0;
   if (X.k_path) {
     // Radix select from the first bit where the candidates' keys differ:
     // the shared high bits would put every candidate in one bin.
     uint32_t kmin_p = NONE, kmax_p = 0;
-    for (uint32_t j = tid; j < ncand; j += NT) {
+    for (uint32_t j = tid; j < ncand; j += FT) {
       const uint32_t key = okey(cand_l(X, F, j));
       kmin_p = min(kmin_p, key);
       kmax_p = max(kmax_p, key);
@@ -1018,21 +1293,26 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
     while (hb >= 0) {
       const int sh = hb >= 10 ? hb - 10 : 0;
       const uint32_t dmask = (uint32_t)((1ull << (hb - sh + 1)) - 1ull);
-      for (uint32_t t = tid; t < (uint32_t)NB; t += NT) F.u.h.hcnt[t] = 0u;
+      for (uint32_t t = tid; t < (uint32_t)NB; t += FT) F.u.h.hcnt[t] = 0u;
       __syncthreads();
-      for (uint32_t j = tid; j < ncand; j += NT) {
+      for (uint32_t j = tid; j < ncand; j += FT) {
         const uint32_t key = okey(cand_l(X, F, j));
         if ((key & pmask) == prefix) atomicAdd(&F.u.h.hcnt[(key >> sh) & dmask], 1u);
       }
       __syncthreads();
-      const uint32_t b_hi = NB - 1 - 2 * tid, b_lo = b_hi - 1;
-      const uint32_t ch = F.u.h.hcnt[b_hi], cl = F.u.h.hcnt[b_lo];
+      const uint32_t b0 = NB - 1 - BPT * tid;
+      uint32_t csum = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) csum += F.u.h.hcnt[b0 - i];
       uint32_t tot;
-      const uint32_t inc = block_scan_incl<uint32_t>(ch + cl, F.red_u, &tot);
-      const uint32_t exc = inc - ch - cl;
+      uint32_t lo = block_scan_incl<uint32_t>(csum, F.red_u, &tot) - csum;
       const uint32_t need = c.k - above;
-      if (exc < need && need <= exc + ch) { F.s_u[4] = b_hi; F.s_u[5] = above + exc; }
-      else if (exc + ch < need && need <= inc) { F.s_u[4] = b_lo; F.s_u[5] = above + exc + ch; }
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) {
+        const uint32_t ch = F.u.h.hcnt[b0 - i];
+        if (lo < need && need <= lo + ch) { F.s_u[4] = b0 - i; F.s_u[5] = above + lo; }
+        lo += ch;
+      }
       __syncthreads();
       prefix |= F.s_u[4] << sh;
       pmask |= dmask << sh;
@@ -1051,7 +1331,7 @@ __device__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uin
   bool mp_close = false;
   if (tid == 0) F.s_u[7] = NONE;
   __syncthreads();
-  for (uint32_t base = 0; base < ncand; base += NT) {
+  for (uint32_t base = 0; base < ncand; base += FT) {
     const uint32_t j = base + tid;
     bool in = false, tie = false;
     uint32_t id = 0;
@@ -1100,9 +1380,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
     const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
     const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
-  __shared__ __align__(16) unsigned char smem_raw[SMEM_BYTES];
-  ChunkSmem& S = *reinterpret_cast<ChunkSmem*>(smem_raw);
-  FinSmem& F = *reinterpret_cast<FinSmem*>(smem_raw);
+  __shared__ __align__(16) ChunkSmem S;
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
 
@@ -1526,7 +1804,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
           m0 += sw;
           if (mode == M_KEEPALL) {
             const double ws = wave_sum_f64(sw);
-            if (lane() == 0) st_dev(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
+            if (lane() == 0) A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()] = ws;
           }
         }
       } else if (lane() == 0 && emit) {
@@ -1593,9 +1871,8 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         for (int e = 0; e < 4; ++e) {
           if (em[e]) {
             const uint64_t pos = cbase + off;
-            st_dev(&A.w.cand_l[pos], lv[i][e]);
-            st_dev(&A.w.cand_id[pos], e0 + (uint32_t)e);
-            if (mode == M_ALL) st_dev(&A.w.cand_w[pos], exp_neg(((double)lv[i][e] - md) * invT));
+            A.w.cand_l[pos] = lv[i][e];
+            A.w.cand_id[pos] = e0 + (uint32_t)e;
             ++off;
           }
         }
@@ -1603,40 +1880,48 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     }
   }
 
-  // ---- publish the chunk's statistics, then count arrivals ---------------
+  // ---- publish the chunk's statistics (the row finisher kernel reads them)
   stamp(A, row, chunk, 7);
   if (tid == 0) {
     // the greedy argmax: the largest (value key, ~id) of the waves' argmaxes
     unsigned long long garg = 0ull;
     if (want_arg)
       for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
-    ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + chunk];
-    st_dev(&st->maxkey, nleg ? maxkey : 0u);
-    st_dev(&st->gbest_id, garg ? ~(uint32_t)garg : NONE);
-    st_dev(&st->gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
-    st_dev(&st->nlegal, nleg);
-    st_dev(&st->ncand, ncand);
-    st_dev(&st->flags, cflags);
-    st_dev(&st->mass, mass);
-    st_dev(&st->mass_err, mass_err);
-    st_dev(&st->minkey, minkey);
-    st_dev(&st->thr, thr);
+    ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
+    st.maxkey = nleg ? maxkey : 0u;
+    st.gbest_id = garg ? ~(uint32_t)garg : NONE;
+    st.gbest_val = garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f;
+    st.nlegal = nleg;
+    st.ncand = ncand;
+    st.flags = cflags;
+    st.mass = mass;
+    st.mass_err = mass_err;
+    st.minkey = minkey;
+    st.thr = thr;
   }
-  wait_mem();
-  __syncthreads();
   stamp(A, row, chunk, 2);
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S.s_last = (prev == A.C - 1u) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!S.s_last) return;
+}
 
-  // =========================================================================
-  // Finisher: the last chunk workgroup of the row.
-  // =========================================================================
+// ---------------------------------------------------------------------------
+// The row finisher: one workgroup per row, launched after the chunk kernel
+// on the same stream (the kernel boundary makes every chunk's statistics and
+// candidates visible).  Row r runs as workgroup r, on XCD r mod 8, the XCD
+// that ran the row's chunks.
+template <typename In>
+__global__ __launch_bounds__(FT) void finish_kernel(
+    SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
+    const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
+    const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
+    const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
+  __shared__ __align__(16) FinSmem F;
+  const uint32_t row = blockIdx.x;
+  if (row >= A.b.rows) return;
+  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
+                            p_boff, row);
+  const uint32_t mode = chunk_mode(c, A.b.vocab);
+  const double invT = c.greedy ? 0.0 : 1.0 / c.T;
   stamp(A, row, MAXC, 0);
-  finish_row<In>(A, F, c, row, mode, rbase, invT);
+  finish_row<In>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT);
   stamp(A, row, MAXC, 7);
 }
 
@@ -1695,7 +1980,6 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.stat, (size_t)max_rows * mxs::MAXC * sizeof(mxs::ChunkStat));
   e = e ? e : hipMalloc(&ctx->work.cand_l, rv * sizeof(float));
   e = e ? e : hipMalloc(&ctx->work.cand_id, rv * sizeof(uint32_t));
-  e = e ? e : hipMalloc(&ctx->work.cand_w, rv * sizeof(double));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
@@ -1741,7 +2025,6 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->work.stat);
   hipFree(ctx->work.cand_l);
   hipFree(ctx->work.cand_id);
-  hipFree(ctx->work.cand_w);
   hipFree(ctx->work.seg);
   hipFree(ctx->d_zero_u32);
   hipFree(ctx->d_one_f64);
@@ -1822,12 +2105,20 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
-  if (b->dtype == MXS_F32)
+  // chunk pass, then the row finisher (stream order makes the chunk results visible)
+  if (b->dtype == MXS_F32) {
     hipLaunchKernelGGL(mxs::sample_kernel<float>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
                        p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
-  else
+    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
+                       b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
+                       A.b.bias_offsets);
+  } else {
     hipLaunchKernelGGL(mxs::sample_kernel<uint16_t>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
                        p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
+    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
+                       b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
+                       A.b.bias_offsets);
+  }
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");

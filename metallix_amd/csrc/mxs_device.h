@@ -80,29 +80,32 @@ __device__ __forceinline__ T wave_max(T v) {
   for (int o = 32; o > 0; o >>= 1) { T t = __shfl_xor(v, o); v = t > v ? t : v; }
   return v;
 }
+// The block helpers below work for any block of up to NT threads (waves
+// counted from blockDim.x).
+__device__ __forceinline__ uint32_t nwaves() { return blockDim.x >> 6; }
 template <typename T>
-__device__ T block_sum(T v, T* red) {
+__device__ __forceinline__ T block_sum(T v, T* red) {
   v = wave_sum(v);
   if (lane() == 0) red[wave()] = v;
   __syncthreads();
   T s = red[0];
-  for (int i = 1; i < NW; ++i) s += red[i];
+  for (uint32_t i = 1; i < nwaves(); ++i) s += red[i];
   __syncthreads();
   return s;
 }
 template <typename T>
-__device__ T block_max(T v, T* red) {
+__device__ __forceinline__ T block_max(T v, T* red) {
   v = wave_max(v);
   if (lane() == 0) red[wave()] = v;
   __syncthreads();
   T s = red[0];
-  for (int i = 1; i < NW; ++i) s = red[i] > s ? red[i] : s;
+  for (uint32_t i = 1; i < nwaves(); ++i) s = red[i] > s ? red[i] : s;
   __syncthreads();
   return s;
 }
 // Inclusive scan in thread order; *total receives the block total.
 template <typename T>
-__device__ T block_scan_incl(T v, T* red, T* total) {
+__device__ __forceinline__ T block_scan_incl(T v, T* red, T* total) {
   const uint32_t l = lane();
   for (int o = 1; o < 64; o <<= 1) {
     T t = __shfl_up(v, o);
@@ -111,13 +114,38 @@ __device__ T block_scan_incl(T v, T* red, T* total) {
   if (l == 63) red[wave()] = v;
   __syncthreads();
   T before = T(0), all = T(0);
-  for (int i = 0; i < NW; ++i) {
+  for (uint32_t i = 0; i < nwaves(); ++i) {
     T r = red[i];
-    if (i < (int)wave()) before += r;
+    if (i < wave()) before += r;
     all += r;
   }
   __syncthreads();
   *total = all;
+  return before + v;
+}
+// As block_scan_incl, and *excl receives the exclusive prefix computed so
+// that it is bit-identical to the previous thread's inclusive value: the
+// per-thread intervals (excl, incl] then tile (0, total] with no gap or
+// overlap even in floating point.
+template <typename T>
+__device__ __forceinline__ T block_scan_pair(T v, T* red, T* excl, T* total) {
+  const uint32_t l = lane();
+  for (int o = 1; o < 64; o <<= 1) {
+    T t = __shfl_up(v, o);
+    if (l >= (uint32_t)o) v += t;
+  }
+  T prev = __shfl_up(v, 1);
+  if (l == 63) red[wave()] = v;
+  __syncthreads();
+  T before = T(0), all = T(0);
+  for (uint32_t i = 0; i < nwaves(); ++i) {
+    T r = red[i];
+    if (i < wave()) before += r;
+    all += r;
+  }
+  __syncthreads();
+  *total = all;
+  *excl = l == 0 ? before : before + prev;
   return before + v;
 }
 
@@ -217,5 +245,179 @@ struct Quad<uint16_t> {
   __device__ static float one(const uint16_t* p) { return bf16_to_f32(*p); }
 };
 
+
+// ---------------------------------------------------------------------------
+// Block primitives with one barrier each.  `slot` is LDS scratch of the
+// given shape; consecutive calls must alternate between two slots (the
+// next-but-one call may overwrite a slot, by which time every thread has
+// read it).
+
+// Exclusive scan of u32 in thread order; *total receives the block total.
+__device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* slot /* [NW] */, uint32_t* total) {
+  const uint32_t inc = wave_scan_u32(v);
+  if (lane() == 63) slot[wave()] = inc;
+  lds_barrier();
+  uint32_t before = 0, all = 0;
+  for (uint32_t w = 0; w < nwaves(); ++w) {
+    const uint32_t t = slot[w];
+    before += w < wave() ? t : 0u;
+    all += t;
+  }
+  *total = all;
+  return before + inc - v;
+}
+
+// Inclusive scan of f64 in thread order (the addition order: lanes in a
+// fixed DPP tree, then waves in order); *total receives the block total.
+__device__ __forceinline__ double wave_scan_f64(double v) {
+  unsigned long long b;
+  b = dpp64<DPP_SHR1>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR2>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR4>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_SHR8>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC15, 0xa>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  b = dpp64<DPP_BC31, 0xc>(__builtin_bit_cast(unsigned long long, v)); v += __builtin_bit_cast(double, b);
+  return v;
+}
+__device__ __forceinline__ double block_incl_scan_f64(double v, double* slot /* [NW] */, double* total) {
+  const double inc = wave_scan_f64(v);
+  if (lane() == 63) slot[wave()] = inc;
+  lds_barrier();
+  double before = 0.0, all = 0.0;
+  for (uint32_t w = 0; w < nwaves(); ++w) {
+    const double t = slot[w];
+    if (w < wave()) before += t;
+    all += t;
+  }
+  *total = all;
+  return before + inc;
+}
+
+constexpr int NBR = 2048;                 // radix-select bins (11 bits)
+
+// The k-th largest (k >= 1) of the active 32-bit keys the workgroup's
+// threads hold (up to R each; bit r of `act` marks key[r] active), by three
+// radix passes (11, 11 and 10 bits) over LDS histograms; *above receives how
+// many active keys are larger.  Needs at least k active keys and three
+// zeroed NBR-word histograms, which it leaves dirty.
+template <int R>
+__device__ __forceinline__ uint32_t block_kth_largest(const uint32_t (&key)[R], uint64_t act, uint32_t k, uint32_t* hist,
+                                      uint32_t* above) {
+  uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
+    const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
+    uint32_t* h = hist + p * NBR;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (((act >> r) & 1ull) && (key[r] & pmask) == prefix) atomicAdd(&h[(key[r] >> sh) & dmask], 1u);
+    lds_barrier();
+    // Every wave finds the bin itself.  Lane j owns bins
+    // [NBR - 32 (j + 1), NBR - 32 j), visited from the highest.
+    const uint32_t hi = (uint32_t)NBR - 32u * lane();
+    uint32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 4u * (uint32_t)(q + 1)]);
+      s += v.x + v.y + v.z + v.w;
+    }
+    const uint32_t inc = wave_scan_u32(s);
+    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+    if (!reach) break;   // fewer than k active keys: the caller's contract is broken
+    const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+    // the crossing bin inside lane L's range (every lane walks its own,
+    // 16 bins at a time from vector reads)
+    uint32_t run = inc - s, bin = hi - 1u, before = run;
+    bool found = false;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t c[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 16u * (uint32_t)half - 4u * (uint32_t)(q + 1)]);
+        c[4 * q + 0] = v.w; c[4 * q + 1] = v.z; c[4 * q + 2] = v.y; c[4 * q + 3] = v.x;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (!found && run + c[q] >= need) {
+          found = true;
+          bin = hi - 1u - 16u * (uint32_t)half - (uint32_t)q;
+          before = run;
+        }
+        run += c[q];
+      }
+    }
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
+    const uint32_t cnt_above = (uint32_t)__builtin_amdgcn_readlane((int)before, (int)L);
+    need -= cnt_above;
+    abv += cnt_above;
+    prefix |= b << sh;
+    pmask |= dmask << sh;
+  }
+  *above = abv;
+  return prefix;
+}
+
+
+
+// As block_kth_largest, for keys fetched on demand: get(r) returns this
+// thread's r-th key, for r < R with bit r of `act` set (R <= 64).
+template <typename Get>
+__device__ __forceinline__ uint32_t block_kth_largest_fn(Get get, uint32_t R, uint64_t act, uint32_t k,
+                                                          uint32_t* hist, uint32_t* above) {
+  uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
+    const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
+    uint32_t* h = hist + p * NBR;
+    for (uint32_t r = 0; r < R; ++r) {
+      if (!((act >> r) & 1ull)) continue;
+      const uint32_t key = get(r);
+      if ((key & pmask) == prefix) atomicAdd(&h[(key >> sh) & dmask], 1u);
+    }
+    lds_barrier();
+    const uint32_t hi = (uint32_t)NBR - 32u * lane();
+    uint32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 4u * (uint32_t)(q + 1)]);
+      s += v.x + v.y + v.z + v.w;
+    }
+    const uint32_t inc = wave_scan_u32(s);
+    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+    if (!reach) break;
+    const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+    uint32_t run = inc - s, bin = hi - 1u, before = run;
+    bool found = false;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t c[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 16u * (uint32_t)half - 4u * (uint32_t)(q + 1)]);
+        c[4 * q + 0] = v.w; c[4 * q + 1] = v.z; c[4 * q + 2] = v.y; c[4 * q + 3] = v.x;
+      }
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (!found && run + c[q] >= need) {
+          found = true;
+          bin = hi - 1u - 16u * (uint32_t)half - (uint32_t)q;
+          before = run;
+        }
+        run += c[q];
+      }
+    }
+    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
+    const uint32_t cnt_above = (uint32_t)__builtin_amdgcn_readlane((int)before, (int)L);
+    need -= cnt_above;
+    abv += cnt_above;
+    prefix |= b << sh;
+    pmask |= dmask << sh;
+  }
+  *above = abv;
+  return prefix;
+}
 
 }  // namespace mxs

@@ -48,10 +48,11 @@ def unpack_bits(words, V):
 
 
 def cdf_gap(b, row, kept, adjusted):
-    """Distance in u-space from the row's uniform to the nearest boundary of
-    the inverse CDF over `kept` (ID order), in f64 (used to recognise a
+    """Distance in u-space from row `row`'s uniform to the nearest boundary of
+    the inverse CDF over `kept` (that row's kept flags, ID order) with weights
+    from `adjusted` (that row's adjusted logits), in f64 (used to recognise a
     documented boundary draw)."""
-    x = adjusted[row].astype(np.float64)
+    x = np.asarray(adjusted).astype(np.float64)
     k = np.nonzero(kept)[0]
     if len(k) == 0:
         return 1.0
