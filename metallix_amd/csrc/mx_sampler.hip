@@ -145,11 +145,22 @@ struct alignas(16) FinSmem {
       uint32_t hcnt[NB];               // radix-select histograms
       double hmass[NB];
     } h;
-    uint32_t hist3[3][NBR];            // finish_small's radix select
+    struct {                           // the fast finisher's histograms and crossing-bin members
+      uint32_t cnt[4096];
+      unsigned long long mass[4096];   // fixed-point masses
+      uint32_t mkey[FT];
+      uint32_t mpos[FT];
+      unsigned long long mw[FT];
+    } f;
   } u;
-  uint32_t kbit[CCAP / 32];            // finish_small: kept candidates after a nucleus cut
   uint32_t sc_u[2][FW];                // single-barrier scan slots
   double sc_d[2][FW];
+  unsigned long long sc_l[2][FW];
+  unsigned long long s_l[4];
+  struct {                             // the row header from the chunk statistics
+    double mass, mass_err;             // sum of chunk masses scaled to the row maximum, and its error bound
+    uint32_t flags, nlegal, Mkey, bi, ncand;
+  } hdr;
   double rd[FW][2];                    // multi-value reduction
   uint32_t ru[FW][4];
   unsigned long long rm[FW];
@@ -781,223 +792,375 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
 }
 
 // ---------------------------------------------------------------------------
-// Lean finisher for candidate sets cached in LDS: every thread holds up to
-// FR contiguous candidates (token-ID order), the top-k head comes from one
-// three-pass radix select with ties ranked in ID order, sums come from one
-// multi-value reduction, and a sort happens only when the nucleus cut falls
-// inside the min-p set.  Returns false, having written nothing, for a row
-// the general path must decide (uncertain cuts, the top_p = 1 freeze rule,
-// large sorts); the general path then recomputes from the LDS candidates.
-constexpr int FR = CCAP / FT;   // at most 32 candidates per thread (bit masks)
+// Fast finisher for candidate sets cached in LDS (at most CCAP, token-ID
+// order).  The candidate phase runs on the whole workgroup, thread t owning
+// the R contiguous candidates from t * R:
+//   E     the top-k head (the k-th largest key from a 12-bit LDS histogram
+//         and ranks inside the crossing bin; ties at the k-th key kept in ID
+//         order), the exact min-p set, or every candidate; compacted to eidx
+//         in token-ID order.
+// The E phase runs on one wave when E has at most 4 * 64 tokens (no
+// workgroup barriers at all), else on the workgroup:
+//   sums  f64 weights of E (group-contiguous, at most FE per thread), the
+//         min-p subset P, and the sums
+//   cut   when the nucleus can end inside P: a histogram of P's keys (4 bins
+//         per thread) with exact fixed-point masses finds the crossing bin,
+//         and ranks inside that bin the crossing token
+//   draw  the inverse-CDF draw over the kept tokens in token-ID order.
+// Returns false, having written nothing, for a row the general path decides
+// (more candidates or E tokens than fit, an uncertain cut, the top_p = 1
+// freeze rule, a crossing bin with more members than threads).
+constexpr int FR = CCAP / FT;      // candidates per thread
+constexpr int FE = ECAP / FT;      // E tokens per thread
+constexpr int FB = 4096;           // the candidate phase's histogram bins (12 bits)
+constexpr double WFIX = 0x1p50;    // fixed-point scale of the cut's masses (every weight is at most 1)
+static_assert(FB == 4 * FT, "each thread scans four histogram bins");
+static_assert(FR <= 32 && FE <= 32, "per-thread bit masks");
 
-__device__ __forceinline__ bool finish_small(const FinCtx& X, FinSmem& F) {
-  const RowCfg& c = *X.c;
+// Bin shift for keys in [kmin, kmax] and 2^bits bins: the bits from the
+// highest bit where they differ down (keys share every bit above it).
+__device__ __forceinline__ int fast_shift(uint32_t kmin, uint32_t kmax, int bits) {
+  const uint32_t diff = kmin ^ kmax;
+  const int hb = diff ? 31 - (int)__builtin_clz(diff) : 0;
+  return hb >= bits ? hb - bits + 1 : 0;
+}
+
+// The k-th largest of the active candidate keys (1 <= k <= active count)
+// and how many active keys are larger.  Returns false when the crossing bin
+// holds more than FT keys (the caller falls back).
+__device__ __forceinline__ bool fast_kth(FinSmem& F, const uint32_t (&key)[FR], uint32_t act, uint32_t k,
+                                         uint32_t kmin, uint32_t kmax, uint32_t* kappa, uint32_t* above) {
   const uint32_t tid = threadIdx.x;
-  const uint32_t n = X.ncand;
-  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + 3] = n;   // candidate count (diagnostics)
-  if (n == 0 || n > (uint32_t)CCAP || !X.lds_c) return false;
-  const uint32_t R = (n + FT - 1u) / FT;
-  if (R > (uint32_t)FR) return false;
-  // this thread's candidates are j = tid * R + r, r < R (token-ID order);
-  // their weights live in LDS (wl[j]), their flags in bit masks
-  auto cj = [&](uint32_t r) { return tid * R + r; };
-  double* wl = F.u.e.ew;   // CCAP doubles: ew and skey are contiguous
-  uint64_t act = 0;
-  for (uint32_t r = 0; r < R; ++r)
-    if (cj(r) < n) act |= 1ull << r;
-  // ---- the working set E: the top-k head, the exact min-p set, or all ----
-  uint64_t inE = 0;
-  uint32_t unc = 0;
-  if (X.k_path) {
-    for (uint32_t t = tid; t < 3u * NBR; t += FT) (&F.u.hist3[0][0])[t] = 0u;
-    lds_barrier();
-    uint32_t above = 0;
-    const uint32_t kappa = block_kth_largest_fn([&](uint32_t r) { return okey(F.cl[cj(r)]); }, R, act, c.k,
-                                                &F.u.hist3[0][0], &above);
-    uint32_t nt = 0;
-    for (uint32_t r = 0; r < R; ++r)
-      if (((act >> r) & 1ull) && okey(F.cl[cj(r)]) == kappa) ++nt;
-    uint32_t ttot;
-    uint32_t tr = block_excl_scan_u32(nt, F.sc_u[0], &ttot);
-    const uint32_t need_t = c.k - above;
-    for (uint32_t r = 0; r < R; ++r) {
-      if (!((act >> r) & 1ull)) continue;
-      const uint32_t key = okey(F.cl[cj(r)]);
-      if (key > kappa) inE |= 1ull << r;
-      else if (key == kappa) { if (tr < need_t) inE |= 1ull << r; ++tr; }
-    }
-    lds_barrier();   // the histograms share LDS with the weights below
-  } else if (X.mode == M_MINP) {
-    for (uint32_t r = 0; r < R; ++r) {
-      if (!((act >> r) & 1ull)) continue;
-      const double sh = ((double)F.cl[cj(r)] - X.M) / c.T;
-      if (sh >= X.L) inE |= 1ull << r;
-      if (fabs(sh - X.L) < X.Lclose) unc = 1;
-    }
-  } else {
-    inE = act;
+  if (kmin == kmax) { *kappa = kmax; *above = 0u; return true; }
+  const int sh = fast_shift(kmin, kmax, 12);
+  uint32_t* cnt = F.u.f.cnt;
+  reinterpret_cast<uint4*>(cnt)[tid] = make_uint4(0u, 0u, 0u, 0u);
+  F.u.f.mkey[tid] = 0u;   // key 0 is no finite logit's: pads the member list
+  if (tid == 0) F.s_u[10] = 0u;
+  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < FR; ++r)
+    if ((act >> r) & 1u) atomicAdd(&cnt[(key[r] >> sh) & (FB - 1)], 1u);
+  lds_barrier();
+  // thread t scans bins FB-1-4t down to FB-4-4t
+  const uint4 h4 = reinterpret_cast<const uint4*>(cnt)[FT - 1 - tid];
+  const uint32_t hv[4] = {h4.w, h4.z, h4.y, h4.x};
+  uint32_t tot;
+  uint32_t run = block_excl_scan_u32(h4.x + h4.y + h4.z + h4.w, F.sc_u[0], &tot);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (run < k && k <= run + hv[i]) { F.s_u[8] = FB - 1 - 4 * tid - (uint32_t)i; F.s_u[9] = run; }
+    run += hv[i];
   }
-  fstamp(X, 4);
-  // ---- weights, the min-p subset P, sums ----------------------------------
-  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
-  uint64_t inP = 0;
-  double epart = 0.0, ppart = 0.0;
-  unsigned long long wmin_key = ~0ull;   // smallest weight (non-negative doubles order as u64)
-  uint32_t ne = 0, pn = 0;
-  for (uint32_t r = 0; r < R; ++r) {
-    if (!((inE >> r) & 1ull)) continue;
-    const double sh = ((double)F.cl[cj(r)] - X.M) / c.T;
-    const double w = exp_neg(sh);
-    wl[cj(r)] = w;
-    epart += w;
-    ++ne;
-    const unsigned long long wk = __builtin_bit_cast(unsigned long long, w);
-    wmin_key = wk < wmin_key ? wk : wmin_key;
-    bool p = true;
-    if (apply_minp) {
-      p = sh >= X.L;
-      if (fabs(sh - X.L) < X.Lclose) unc = 1;
-    }
-    if (p) { inP |= 1ull << r; ppart += w; ++pn; }
-  }
-  {
-    const double a = wave_sum_f64(epart), b = wave_sum_f64(ppart);
-    const uint32_t e1 = wave_sum_u32(ne), e2 = wave_sum_u32(pn), e3 = wave_or_u32(unc);
-    const unsigned long long mk = ~wave_max_u64(~wmin_key);
-    if (lane() == 0) {
-      F.rd[wave()][0] = a; F.rd[wave()][1] = b;
-      F.ru[wave()][0] = e1; F.ru[wave()][1] = e2; F.ru[wave()][2] = e3;
-      F.rm[wave()] = mk;
+  lds_barrier();
+  const uint32_t bstar = F.s_u[8], abv = F.s_u[9];
+  if (sh == 0) { *kappa = (kmax & ~(uint32_t)(FB - 1)) | bstar; *above = abv; return true; }
+  // rank the crossing bin's members
+#pragma unroll
+  for (int r = 0; r < FR; ++r) {
+    if (((act >> r) & 1u) && ((key[r] >> sh) & (FB - 1)) == bstar) {
+      const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+      if (at < (uint32_t)FT) F.u.f.mkey[at] = key[r];
     }
   }
   lds_barrier();
-  double esum = 0.0, psum = 0.0;
-  uint32_t NE = 0, NP = 0;
-  unsigned long long wmk = ~0ull;
-#pragma unroll
-  for (int q = 0; q < FW; ++q) {
-    esum += F.rd[q][0]; psum += F.rd[q][1];
-    NE += F.ru[q][0]; NP += F.ru[q][1]; unc |= F.ru[q][2];
-    wmk = F.rm[q] < wmk ? F.rm[q] : wmk;
+  const uint32_t cm = F.s_u[10];
+  if (cm > (uint32_t)FT) return false;
+  const uint32_t need = k - abv;
+  if (tid < cm) {
+    const uint32_t my = F.u.f.mkey[tid];
+    uint32_t gt = 0, eq = 0;
+    for (uint32_t i = 0; i < cm; i += 4) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&F.u.f.mkey[i]);
+      gt += (v.x > my) + (v.y > my) + (v.z > my) + (v.w > my);
+      eq += (v.x == my) + (v.y == my) + (v.z == my) + (v.w == my);
+    }
+    if (gt < need && need <= gt + eq) { F.s_u[11] = my; F.s_u[12] = abv + gt; }
   }
-  const double wmin = __builtin_bit_cast(double, wmk);
-  fstamp(X, 5);
+  lds_barrier();
+  *kappa = F.s_u[11];
+  *above = F.s_u[12];
+  return true;
+}
+
+// Group primitives of the E phase: one wave (G = 64: LDS operations of one
+// wave complete in order, so no barrier is needed) or the workgroup (G = FT:
+// one LDS barrier per call; consecutive calls alternate their slots).
+template <int G>
+struct Grp;
+template <>
+struct Grp<64> {
+  __device__ static uint32_t id() { return lane(); }
+  __device__ static void sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+  __device__ static uint32_t excl_u32(uint32_t v, uint32_t*, uint32_t* total) {
+    const uint32_t i = wave_scan_u32(v);
+    *total = bcast63(i);
+    return i - v;
+  }
+  __device__ static unsigned long long excl_u64(unsigned long long v, unsigned long long*, unsigned long long* total) {
+    const unsigned long long i = wave_scan_u64(v);
+    *total = readlane64(i, 63);
+    return i - v;
+  }
+  __device__ static double incl_f64(double v, double*, double* total) {
+    const double i = wave_scan_f64(v);
+    *total = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, i), 63));
+    return i;
+  }
+  // sums of two f64 and one u32 (one reduction)
+  __device__ static void sum3(double& a, double& b, uint32_t& c, FinSmem&, int) {
+    a = wave_sum_f64(a);
+    b = wave_sum_f64(b);
+    c = wave_sum_u32(c);
+  }
+  __device__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem&) {
+    mn = ~wave_max_u32(~mn);
+    mx = wave_max_u32(mx);
+  }
+  __device__ static unsigned long long min_u64(unsigned long long v, FinSmem&) { return ~wave_max_u64(~v); }
+};
+template <>
+struct Grp<FT> {
+  __device__ static uint32_t id() { return threadIdx.x; }
+  __device__ static void sync() { lds_barrier(); }
+  __device__ static uint32_t excl_u32(uint32_t v, uint32_t* slot, uint32_t* total) {
+    return block_excl_scan_u32(v, slot, total);
+  }
+  __device__ static unsigned long long excl_u64(unsigned long long v, unsigned long long* slot,
+                                                unsigned long long* total) {
+    return block_excl_scan_u64(v, slot, total);
+  }
+  __device__ static double incl_f64(double v, double* slot, double* total) { return block_incl_scan_f64(v, slot, total); }
+  __device__ static void sum3(double& a, double& b, uint32_t& c, FinSmem& F, int s) {
+    a = wave_sum_f64(a);
+    b = wave_sum_f64(b);
+    c = wave_sum_u32(c);
+    if (lane() == 0) { F.rd[wave()][0] = a; F.rd[wave()][1] = b; F.ru[wave()][s] = c; }
+    lds_barrier();
+    const bool wl = lane() < (uint32_t)FW;
+    const uint32_t q = wl ? lane() : 0u;
+    a = wave_sum_f64(wl ? F.rd[q][0] : 0.0);
+    b = wave_sum_f64(wl ? F.rd[q][1] : 0.0);
+    c = wave_sum_u32(wl ? F.ru[q][s] : 0u);
+  }
+  __device__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem& F) {
+    mn = ~wave_max_u32(~mn);
+    mx = wave_max_u32(mx);
+    if (lane() == 0) { F.ru[wave()][2] = mn; F.ru[wave()][3] = mx; }
+    lds_barrier();
+    const bool wl = lane() < (uint32_t)FW;
+    const uint32_t q = wl ? lane() : 0u;
+    mn = ~wave_max_u32(wl ? ~F.ru[q][2] : 0u);
+    mx = wave_max_u32(wl ? F.ru[q][3] : 0u);
+  }
+  __device__ static unsigned long long min_u64(unsigned long long v, FinSmem& F) {
+    v = ~wave_max_u64(~v);
+    if (lane() == 0) F.rm[wave()] = v;
+    lds_barrier();
+    const bool wl = lane() < (uint32_t)FW;
+    return ~wave_max_u64(wl ? ~F.rm[wl ? lane() : 0u] : 0ull);
+  }
+};
+
+// The E phase (see finish_fast) on a group of G threads; E is eidx[0, ne)
+// in token-ID order, at most FE per thread.  `unc0` carries the candidate
+// phase's min-p closeness flag.  Returns false, having written nothing, for
+// the general path.
+template <int G>
+__device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t ne, uint32_t unc0) {
+  using Gr = Grp<G>;
+  constexpr int NBG = 4 * G;                 // cut histogram bins
+  constexpr int BITS = G == 64 ? 8 : 12;
+  static_assert(NBG == (1 << BITS), "4 bins per thread");
+  const RowCfg& c = *X.c;
+  const uint32_t gi = Gr::id();
+  const uint32_t RE = (ne + G - 1u) / G;
+  const uint32_t p0 = gi * RE;
+  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
+  double w[FE];
+  uint32_t ek[FE];
+  uint32_t inP = 0, unc = 0;
+  double esum = 0.0, psum = 0.0;
+  uint32_t np_unc = 0;   // P count | close flags << 16
+#pragma unroll
+  for (int r = 0; r < FE; ++r) {
+    w[r] = 0.0;
+    ek[r] = 0u;
+    if ((uint32_t)r < RE && p0 + (uint32_t)r < ne) {
+      const float l = F.cl[F.eidx[p0 + r]];
+      ek[r] = okey(l);
+      const double s = ((double)l - X.M) / c.T;
+      w[r] = exp_neg(s);
+      esum += w[r];
+      bool p = true;
+      if (apply_minp) {
+        p = s >= X.L;
+        if (fabs(s - X.L) < X.Lclose) unc = 1;
+      }
+      if (p) { inP |= 1u << r; psum += w[r]; ++np_unc; }
+    }
+  }
+  np_unc |= unc << 16;
+  Gr::sum3(esum, psum, np_unc, F, 0);
+  const uint32_t NP = np_unc & 0xffffu;
+  unc = unc0 | (np_unc >> 16);
+
   // ---- the nucleus cut ------------------------------------------------------
   double total = X.total, total_err = X.total_err;
-  if (!X.have_total) { total = esum; total_err = sum_bound(esum, NE, 8.0); }
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
   bool theta_set = false;
   double theta = 0.0, theta_err = 0.0;
   if (X.k_path) {
     if (c.top_p >= 1.0) {
+      unsigned long long wk = ~0ull;   // smallest weight (non-negative doubles order as u64)
+#pragma unroll
+      for (int r = 0; r < FE; ++r)
+        if ((uint32_t)r < RE && p0 + (uint32_t)r < ne) {
+          const unsigned long long b = __builtin_bit_cast(unsigned long long, w[r]);
+          wk = b < wk ? b : wk;
+        }
+      const double wmin = __builtin_bit_cast(double, Gr::min_u64(wk, F));
       if (!(wmin > 2.3e-16 * esum)) return false;   // the running sum may stall: replay
     } else {
       theta_set = true;
       theta = c.top_p * esum;
-      theta_err = c.top_p * sum_bound(esum, NE, 8.0) + U * theta;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
     }
   } else if (c.top_p < 1.0) {
     theta_set = true;
     theta = c.top_p * total;
     theta_err = c.top_p * total_err + U * theta;
   }
-  uint64_t kept = inP;
+  uint32_t kept = inP;
   if (theta_set && !(psum + sum_bound(psum, NP, 8.0) < theta - theta_err)) {
-    // The cut falls inside P: order P by (value desc, ID asc) and find the
-    // first prefix reaching theta.
-    constexpr uint32_t PCAP = 1024;
-    if (NP > PCAP) return false;
-    unsigned long long* pkey = reinterpret_cast<unsigned long long*>(F.eidx);   // PCAP keys
-    double* sw = reinterpret_cast<double*>(F.eidx) + PCAP;                       // PCAP sorted weights
-    uint16_t* prank = reinterpret_cast<uint16_t*>(F.kflag);                      // PCAP ranks
-    uint32_t ptot;
-    uint32_t pos = block_excl_scan_u32((uint32_t)__builtin_popcountll(inP), F.sc_u[1], &ptot);
-    for (uint32_t r = 0; r < R; ++r) {
-      if (!((inP >> r) & 1ull)) continue;
-      const uint32_t j = cj(r);
-      pkey[pos] = ((unsigned long long)okey(F.cl[j]) << 32) | (unsigned long long)(~j);
-      ++pos;
-    }
-    for (uint32_t t = tid; t < CCAP / 32; t += FT) F.kbit[t] = 0u;
-    lds_barrier();
-    for (uint32_t e = tid; e < NP; e += FT) {
-      const unsigned long long mine = pkey[e];
-      uint32_t rank = 0;
-      for (uint32_t q = 0; q < NP; ++q) rank += pkey[q] > mine ? 1u : 0u;
-      sw[rank] = wl[~(uint32_t)mine];
-      prank[e] = (uint16_t)rank;
-    }
-    if (tid == 0) { F.s_u[6] = NONE; F.s_u[7] = 0u; }
-    lds_barrier();
-    double run = 0.0;
-    for (uint32_t base = 0; base < NP; base += FT) {
-      const uint32_t p = base + tid;
-      double tot;
-      const double vv = p < NP ? sw[p] : 0.0;
-      const double inc = run + block_incl_scan_f64(vv, F.sc_d[(base / FT) & 1u], &tot);
-      const double exc = inc - vv;
-      if (p < NP) {
-        const double e_inc = sum_bound(inc, p + 65u, 8.0);
-        const double e_exc = sum_bound(exc, p + 64u, 8.0);
-        if (!(inc + e_inc < theta - theta_err) && (p == 0 || exc + e_exc < theta - theta_err)) {
-          F.s_u[6] = p;
-          if (!(inc - e_inc >= theta + theta_err)) F.s_u[7] = 1u;
-        }
-      }
-      run += tot;
-    }
-    lds_barrier();
-    const uint32_t first = F.s_u[6];
-    if (first == NONE || F.s_u[7]) return false;   // uncertain cut: replay
-    for (uint32_t e = tid; e < NP; e += FT) {
-      if (prank[e] <= first) {
-        const uint32_t j = ~(uint32_t)pkey[e];
-        atomicOr(&F.kbit[j >> 5], 1u << (j & 31u));
+    // The nucleus can end inside P.  P's keys, histogrammed with exact
+    // fixed-point masses, in descending key order: the crossing bin is where
+    // the mass prefix reaches theta; inside it the members are ordered by
+    // (key desc, token ID asc), E positions being in token-ID order.
+    uint32_t pkmin = NONE, pkmax = 0;
+#pragma unroll
+    for (int r = 0; r < FE; ++r)
+      if ((inP >> r) & 1u) { pkmin = min(pkmin, ek[r]); pkmax = max(pkmax, ek[r]); }
+    Gr::minmax_u32(pkmin, pkmax, F);
+    const int sh = fast_shift(pkmin, pkmax, BITS);
+    uint32_t* cnt = F.u.f.cnt;
+    unsigned long long* mass = F.u.f.mass;
+    reinterpret_cast<uint4*>(cnt)[gi] = make_uint4(0u, 0u, 0u, 0u);
+    reinterpret_cast<ulonglong2*>(mass)[2 * gi] = make_ulonglong2(0ull, 0ull);
+    reinterpret_cast<ulonglong2*>(mass)[2 * gi + 1] = make_ulonglong2(0ull, 0ull);
+    F.u.f.mkey[gi] = 0u;   // pads the member list (key 0 is no finite logit's)
+    if (gi == 0) { F.s_u[10] = 0u; F.s_u[11] = NONE; F.s_u[13] = 0u; }
+    Gr::sync();
+    unsigned long long W[FE];
+#pragma unroll
+    for (int r = 0; r < FE; ++r) {
+      W[r] = __double2ull_rn(w[r] * WFIX);
+      if ((inP >> r) & 1u) {
+        const uint32_t b = (ek[r] >> sh) & (NBG - 1);
+        atomicAdd(&cnt[b], 1u);
+        atomicAdd(&mass[b], W[r]);
       }
     }
-    lds_barrier();
+    Gr::sync();
+    const double theta_fx = theta * WFIX;
+    const uint4 h4 = reinterpret_cast<const uint4*>(cnt)[G - 1 - gi];
+    const ulonglong2 m01 = reinterpret_cast<const ulonglong2*>(mass)[2 * (G - 1 - gi)];
+    const ulonglong2 m23 = reinterpret_cast<const ulonglong2*>(mass)[2 * (G - 1 - gi) + 1];
+    const uint32_t hv[4] = {h4.w, h4.z, h4.y, h4.x};
+    const unsigned long long mv[4] = {m23.y, m23.x, m01.y, m01.x};
+    unsigned long long mtot;
+    unsigned long long before = Gr::excl_u64(mv[0] + mv[1] + mv[2] + mv[3], F.sc_l[0], &mtot);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (hv[i] && (double)before < theta_fx && theta_fx <= (double)(before + mv[i])) {
+        F.s_u[8] = NBG - 1 - 4 * gi - (uint32_t)i;
+        F.s_l[0] = before;
+      }
+      before += mv[i];
+    }
+    if (gi == 0 && !((double)mtot >= theta_fx)) F.s_u[8] = NONE;   // no crossing inside P
+    Gr::sync();
+    const uint32_t bstar = F.s_u[8];
+    if (bstar == NONE) return false;
+    const unsigned long long bbefore = F.s_l[0];
+#pragma unroll
+    for (int r = 0; r < FE; ++r) {
+      if (((inP >> r) & 1u) && ((ek[r] >> sh) & (NBG - 1)) == bstar) {
+        const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+        if (at < (uint32_t)G) { F.u.f.mkey[at] = ek[r]; F.u.f.mpos[at] = p0 + r; F.u.f.mw[at] = W[r]; }
+      }
+    }
+    Gr::sync();
+    const uint32_t cm = F.s_u[10];
+    if (cm > (uint32_t)G) return false;
+    if (gi < cm) {
+      const uint32_t mk = F.u.f.mkey[gi], mp = F.u.f.mpos[gi];
+      const unsigned long long mwv = F.u.f.mw[gi];
+      unsigned long long ahead = 0;   // mass of the members ordered before this one
+      for (uint32_t i = 0; i < cm; ++i) {
+        const uint32_t k2 = F.u.f.mkey[i], p2 = F.u.f.mpos[i];
+        if (k2 > mk || (k2 == mk && p2 < mp)) ahead += F.u.f.mw[i];
+      }
+      const unsigned long long prev = bbefore + ahead, incl = prev + mwv;
+      if ((double)prev < theta_fx && theta_fx <= (double)incl) {
+        F.s_u[11] = mk;
+        F.s_u[12] = mp;
+        // Certificate: the fixed-point prefixes are exact sums of weights
+        // rounded to 2^-51 (NP 2^-51 in all), the weights are within 8 ulp
+        // of the reference's, and its sequential sums in sorted order are
+        // within sum_bound; the f64 conversion adds one rounding.
+        const double dp = (double)prev / WFIX, di = (double)incl / WFIX;
+        const double fx = (double)NP * 0x1p-51;
+        const double ep = sum_bound(dp, NP, 8.0) + fx + U * dp, ei = sum_bound(di, NP, 8.0) + fx + U * di;
+        if (!(dp + ep < theta - theta_err) || !(di - ei >= theta + theta_err)) F.s_u[13] = 1u;
+      }
+    }
+    Gr::sync();
+    const uint32_t cut_key = F.s_u[11], cut_pos = F.s_u[12];
+    if (cut_key == NONE || F.s_u[13]) return false;   // uncertain cut: replay
     kept = 0;
-    for (uint32_t r = 0; r < R; ++r) {
-      const uint32_t j = cj(r);
-      if (((inP >> r) & 1ull) && ((F.kbit[j >> 5] >> (j & 31u)) & 1u)) kept |= 1ull << r;
-    }
+#pragma unroll
+    for (int r = 0; r < FE; ++r)
+      if (((inP >> r) & 1u) && (ek[r] > cut_key || (ek[r] == cut_key && p0 + (uint32_t)r <= cut_pos))) kept |= 1u << r;
   }
-  fstamp(X, 6);
+
   // ---- overflow check and the inverse-CDF draw in token-ID order ----------
   double kpart = 0.0;
   uint32_t kn = 0;
   bool bad = false;
-  for (uint32_t r = 0; r < R; ++r) {
-    if (!((kept >> r) & 1ull)) continue;
-    kpart += wl[cj(r)];
+#pragma unroll
+  for (int r = 0; r < FE; ++r) {
+    if (!((kept >> r) & 1u)) continue;
+    kpart += w[r];
     ++kn;
-    if (!isfinite(((double)F.cl[cj(r)] - X.M) / c.T)) bad = true;
+    if (!isfinite(((double)okey_value(ek[r]) - X.M) / c.T)) bad = true;
   }
-  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; F.s_u[3] = 0u; F.s_u[4] = unc; }
+  if (gi == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; F.s_u[3] = 0u; }
   uint32_t nkept;
-  (void)block_excl_scan_u32(kn, F.sc_u[0], &nkept);
-  if (bad) F.s_u[3] = 1u;
+  (void)Gr::excl_u32(kn | (bad ? 0x10000u : 0u), F.sc_u[1], &nkept);
+  const bool any_bad = (nkept >> 16) != 0u;
+  nkept &= 0xffffu;
   double S;
-  const double kinc = block_incl_scan_f64(kpart, F.sc_d[1], &S);
+  const double kinc = Gr::incl_f64(kpart, F.sc_d[0], &S);
   const double target = c.u * S;
   const double derr = sum_bound(S, nkept + 64u, 8.0);
   double cum = kinc - kpart;
-  for (uint32_t r = 0; r < R; ++r) {
-    if (!((kept >> r) & 1ull)) continue;
-    const uint32_t j = cj(r);
-    const double w = wl[j];
+#pragma unroll
+  for (int r = 0; r < FE; ++r) {
+    if (!((kept >> r) & 1u)) continue;
     const double prev = cum;
-    cum += w;
-    if (w > 0.0) {
-      atomicMax(&F.s_u[1], j + 1u);
+    cum += w[r];
+    if (w[r] > 0.0) {
+      atomicMax(&F.s_u[1], p0 + (uint32_t)r + 1u);
       if (target < cum && !(target < prev)) {
-        F.s_u[0] = j;
+        F.s_u[0] = p0 + (uint32_t)r;
         if (fabs(target - prev) <= derr || fabs(cum - target) <= derr) F.s_u[2] = 1u;
       }
     }
   }
-  lds_barrier();
-  if (F.s_u[3]) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
-  bool uncert = F.s_u[4] != 0u || F.s_u[2] != 0u;
+  Gr::sync();
+  if (any_bad) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
+  bool uncert = unc != 0u || F.s_u[2] != 0u;
   uint32_t pick = F.s_u[0];
   if (pick == NONE) {
     // rounding left the variate past the accumulated mass: last positive kept token
@@ -1005,18 +1168,96 @@ __device__ __forceinline__ bool finish_small(const FinCtx& X, FinSmem& F) {
     uncert = true;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
-  const double shifted = ((double)F.cl[pick] - X.M) / c.T;
-  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.cid[pick], shifted - log(S), nkept);
+  const uint32_t jp = F.eidx[pick];
+  const double shifted = ((double)F.cl[jp] - X.M) / c.T;
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.cid[jp], shifted - log(S), nkept);
   if (X.kbits) {
-    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
-    __syncthreads();
-    for (uint32_t r = 0; r < R; ++r) {
-      if (!((kept >> r) & 1ull)) continue;
-      const uint32_t tok = F.cid[cj(r)];
+    for (uint32_t q = gi; q < X.nwords; q += G) X.kbits[q] = 0u;
+    __builtin_amdgcn_s_waitcnt(0);   // the zeroing lands before the atomics (one group, in program order)
+    if (G == FT) __syncthreads();
+#pragma unroll
+    for (int r = 0; r < FE; ++r) {
+      if (!((kept >> r) & 1u)) continue;
+      const uint32_t tok = F.cid[F.eidx[p0 + r]];
       atomicOr(&X.kbits[tok >> 5], 1u << (tok & 31u));
     }
   }
   return true;
+}
+
+__device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
+  const RowCfg& c = *X.c;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n = X.ncand;
+  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + 3] = n;   // candidate count (diagnostics)
+  if (n == 0 || n > (uint32_t)CCAP || !X.lds_c) return false;
+  const uint32_t R = (n + FT - 1u) / FT;
+  const uint32_t j0 = tid * R;
+  uint32_t key[FR];
+  uint32_t act = 0;
+#pragma unroll
+  for (int r = 0; r < FR; ++r) {
+    const bool a = (uint32_t)r < R && j0 + (uint32_t)r < n;
+    key[r] = a ? okey(F.cl[j0 + r]) : 0u;
+    act |= a ? 1u << r : 0u;
+  }
+
+  // ---- E: the top-k head, the exact min-p set, or every candidate --------
+  uint32_t inE = 0, unc = 0;
+  if (X.k_path) {
+    uint32_t kmin = NONE, kmax = 0;
+#pragma unroll
+    for (int r = 0; r < FR; ++r)
+      if ((act >> r) & 1u) { kmin = min(kmin, key[r]); kmax = max(kmax, key[r]); }
+    Grp<FT>::minmax_u32(kmin, kmax, F);
+    uint32_t kappa, above;
+    if (!fast_kth(F, key, act, c.k, kmin, kmax, &kappa, &above)) return false;
+    // ties at kappa: the first (k - above) in token-ID order
+    uint32_t nt = 0;
+#pragma unroll
+    for (int r = 0; r < FR; ++r)
+      if ((act >> r) & 1u) nt += key[r] == kappa;
+    uint32_t ttot;
+    uint32_t tb = block_excl_scan_u32(nt, F.sc_u[1], &ttot);
+    const uint32_t need_t = c.k - above;
+#pragma unroll
+    for (int r = 0; r < FR; ++r) {
+      if (!((act >> r) & 1u)) continue;
+      if (key[r] > kappa) inE |= 1u << r;
+      else if (key[r] == kappa) { if (tb < need_t) inE |= 1u << r; ++tb; }
+    }
+  } else if (X.mode == M_MINP) {
+#pragma unroll
+    for (int r = 0; r < FR; ++r) {
+      if (!((act >> r) & 1u)) continue;
+      const double s = ((double)F.cl[j0 + r] - X.M) / c.T;
+      if (s >= X.L) inE |= 1u << r;
+      if (fabs(s - X.L) < X.Lclose) unc = 1;
+    }
+  } else {
+    inE = act;
+  }
+  uint32_t ne;
+  uint32_t ep = block_excl_scan_u32((uint32_t)__builtin_popcount(inE) | (unc << 16), F.sc_u[0], &ne);
+  unc = ne >> 16 ? 1u : 0u;
+  ne &= 0xffffu;
+  ep &= 0xffffu;
+  if (ne == 0 || ne > (uint32_t)ECAP) return false;
+#pragma unroll
+  for (int r = 0; r < FR; ++r)
+    if ((inE >> r) & 1u) F.eidx[ep++] = j0 + r;
+  lds_barrier();
+  fstamp(X, 4);
+  if (ne <= (uint32_t)(64 * FE)) {
+    // one wave decides; the others wait for its verdict
+    if (wave() == 0) {
+      const bool ok = e_finish<64>(X, F, ne, unc);
+      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
+    }
+    lds_barrier();
+    return F.s_u[15] != 0u;
+  }
+  return e_finish<FT>(X, F, ne, unc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1029,42 +1270,50 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
   const uint32_t C = A.C;
-  for (uint32_t q = tid; q < C; q += FT) {
-    const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + q];
+  // Chunk statistics: wave 0 reads them (lane q <-> chunk q, C <= 64),
+  // reduces them with DPP and publishes the row header and a copy of the
+  // statistics in LDS.
+  if (wave() == 0) {
+    const uint32_t q = lane();
     ChunkStat v;
-    v.maxkey = *(&st->maxkey);
-    v.gbest_id = *(&st->gbest_id);
-    v.gbest_val = *(&st->gbest_val);
-    v.nlegal = *(&st->nlegal);
-    v.ncand = *(&st->ncand);
-    v.flags = *(&st->flags);
-    v.mass = *(&st->mass);
-    v.mass_err = *(&st->mass_err);
-    v.minkey = *(&st->minkey);
-    F.st[q] = v;
-  }
-  __syncthreads();
-  uint32_t flags = 0, nlegal = 0, Mkey = 0;
-  float bv = 0.0f;
-  uint32_t bi = NONE;
-  for (uint32_t q = 0; q < C; ++q) {
-    const ChunkStat& v = F.st[q];
-    flags |= v.flags;
-    nlegal += v.nlegal;
-    if (v.nlegal && v.maxkey > Mkey) Mkey = v.maxkey;
-    if (better(v.gbest_val, v.gbest_id, bv, bi)) { bv = v.gbest_val; bi = v.gbest_id; }
-  }
-  const double M = (double)okey_value(Mkey);
-  if (tid == 0) {
-    uint32_t run = 0;
-    for (uint32_t q = 0; q < C; ++q) {
-      F.coff[q] = run;
-      run += F.st[q].ncand;
-      F.cscale[q] = F.st[q].nlegal ? exp_neg(((double)okey_value(F.st[q].maxkey) - M) * invT) : 0.0;
+    v.maxkey = 0u; v.gbest_id = NONE; v.gbest_val = 0.0f; v.nlegal = 0u; v.ncand = 0u; v.flags = 0u;
+    v.minkey = NONE; v.thr = 0.0f; v.mass = 0.0; v.mass_err = 0.0;
+    if (q < C) {
+      const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + q];
+      v.maxkey = st->maxkey;
+      v.gbest_id = st->gbest_id;
+      v.gbest_val = st->gbest_val;
+      v.nlegal = st->nlegal;
+      v.ncand = st->ncand;
+      v.flags = st->flags;
+      v.mass = st->mass;
+      v.mass_err = st->mass_err;
+      v.minkey = st->minkey;
     }
-    F.coff[C] = run;
+    const uint32_t fl = wave_or_u32(v.flags);
+    const uint32_t nl = wave_sum_u32(v.nlegal);
+    const uint32_t mkey = wave_max_u32(v.nlegal ? v.maxkey : 0u);
+    // the greedy argmax: largest (value key, ~id); chunk values are +0.0-normalised
+    const unsigned long long garg = wave_max_u64(
+        v.gbest_id != NONE ? ((unsigned long long)okey(v.gbest_val) << 32) | (unsigned long long)(~v.gbest_id) : 0ull);
+    const double Mw = (double)okey_value(mkey);
+    const uint32_t cinc = wave_scan_u32(v.ncand);
+    const double cs = v.nlegal ? exp_neg(((double)okey_value(v.maxkey) - Mw) * invT) : 0.0;
+    const double t = wave_sum_f64(v.mass * cs), te = wave_sum_f64(v.mass_err * cs);
+    if (q < C) {
+      F.st[q] = v;
+      F.coff[q] = cinc - v.ncand;
+      F.cscale[q] = cs;
+    }
+    if (q == 0) {
+      F.coff[C] = bcast63(cinc);
+      F.hdr.flags = fl; F.hdr.nlegal = nl; F.hdr.Mkey = mkey; F.hdr.bi = garg ? ~(uint32_t)garg : NONE;
+      F.hdr.ncand = bcast63(cinc); F.hdr.mass = t; F.hdr.mass_err = te;
+    }
   }
-  __syncthreads();
+  lds_barrier();
+  const uint32_t flags = F.hdr.flags, nlegal = F.hdr.nlegal, bi = F.hdr.bi;
+  const double M = (double)okey_value(F.hdr.Mkey);
   const int32_t err = combine_errors(c, flags, nlegal);
   const uint32_t nwords = (V + 31u) / 32u;
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
@@ -1216,30 +1465,32 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   }
 
   // =================== candidate paths ====================================
-  const uint32_t ncand = F.coff[C];
+  const uint32_t ncand = F.hdr.ncand;
   X.ncand = ncand;
   X.lds_c = ncand <= (uint32_t)CCAP;
-  // One bulk load of every candidate into LDS: all loads in flight at once.
+  // One bulk load of every candidate into LDS, all loads in flight at once.
+  // Candidate j lives in chunk q's region at j - coff[q]; j grows with u,
+  // so each thread walks the chunk offsets once.
   if (X.lds_c) {
-    for (uint32_t j0 = 0; j0 < ncand; j0 += FT * 4u) {
-      float lv8[4];
-      uint32_t iv8[4];
+    float lv[FR];
+    uint32_t iv[FR];
+    uint32_t qj = 0, nxt = C > 1 ? F.coff[1] : NONE;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t j = j0 + (uint32_t)u * FT + tid;
-        if (j < ncand) {
-          const uint64_t pos = cand_pos_of(F, C, rbase, A.CH, j);
-          lv8[u] = *(&A.w.cand_l[pos]);
-          iv8[u] = *(&A.w.cand_id[pos]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t j = j0 + (uint32_t)u * FT + tid;
-        if (j < ncand) { F.cl[j] = lv8[u]; F.cid[j] = iv8[u]; }
+    for (int u = 0; u < FR; ++u) {
+      const uint32_t j = (uint32_t)u * FT + tid;
+      if (j < ncand) {
+        while (j >= nxt) { ++qj; nxt = qj + 1 < C ? F.coff[qj + 1] : NONE; }
+        const uint64_t pos = rbase + (uint64_t)qj * A.CH + (j - F.coff[qj]);
+        lv[u] = A.w.cand_l[pos];
+        iv[u] = A.w.cand_id[pos];
       }
     }
-    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < FR; ++u) {
+      const uint32_t j = (uint32_t)u * FT + tid;
+      if (j < ncand) { F.cl[j] = lv[u]; F.cid[j] = iv[u]; }
+    }
+    lds_barrier();
   }
   stamp(A, row, MAXC, 1);
   const double L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
@@ -1254,9 +1505,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   X.total_err = 0.0;
   X.have_total = false;
   if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
-    double t = 0.0;
-    double te = 0.0;
-    for (uint32_t q = 0; q < C; ++q) { t += F.st[q].mass * F.cscale[q]; te += F.st[q].mass_err * F.cscale[q]; }
+    const double t = F.hdr.mass, te = F.hdr.mass_err;
     X.total = t;
     // chunk error bounds (f32 weights), scaled; plus both sides' f64
     // rounding of weights and sums, and the x e^x <= 1/e product term
@@ -1269,7 +1518,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
   X.kappa = 0;
   X.id_tie = NONE;
-  if (mode != M_KEEPALL && finish_small(X, F)) {
+  if (mode != M_KEEPALL && finish_fast(X, F)) {
     stamp(A, row, MAXC, 2);
     return;
   }

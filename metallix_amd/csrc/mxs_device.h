@@ -253,17 +253,40 @@ struct Quad<uint16_t> {
 // read it).
 
 // Exclusive scan of u32 in thread order; *total receives the block total.
+// The waves' totals are combined lane-parallel: lane w reads wave w's.
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, uint32_t* slot /* [NW] */, uint32_t* total) {
   const uint32_t inc = wave_scan_u32(v);
   if (lane() == 63) slot[wave()] = inc;
   lds_barrier();
-  uint32_t before = 0, all = 0;
-  for (uint32_t w = 0; w < nwaves(); ++w) {
-    const uint32_t t = slot[w];
-    before += w < wave() ? t : 0u;
-    all += t;
-  }
-  *total = all;
+  const uint32_t ws = wave_scan_u32(lane() < nwaves() ? slot[lane()] : 0u);
+  *total = bcast63(ws);
+  const uint32_t before = wave() ? (uint32_t)__builtin_amdgcn_readlane((int)ws, (int)(wave() - 1)) : 0u;
+  return before + inc - v;
+}
+
+// Exclusive scan of u64 in thread order (exact); *total receives the block total.
+__device__ __forceinline__ unsigned long long wave_scan_u64(unsigned long long v) {
+  v += dpp64<DPP_SHR1>(v);
+  v += dpp64<DPP_SHR2>(v);
+  v += dpp64<DPP_SHR4>(v);
+  v += dpp64<DPP_SHR8>(v);
+  v += dpp64<DPP_BC15, 0xa>(v);
+  v += dpp64<DPP_BC31, 0xc>(v);
+  return v;
+}
+__device__ __forceinline__ unsigned long long readlane64(unsigned long long v, uint32_t l) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, (int)l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), (int)l);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long block_excl_scan_u64(unsigned long long v, unsigned long long* slot,
+                                                                  unsigned long long* total) {
+  const unsigned long long inc = wave_scan_u64(v);
+  if (lane() == 63) slot[wave()] = inc;
+  lds_barrier();
+  const unsigned long long ws = wave_scan_u64(lane() < nwaves() ? slot[lane()] : 0ull);
+  *total = readlane64(ws, 63);
+  const unsigned long long before = wave() ? readlane64(ws, wave() - 1) : 0ull;
   return before + inc - v;
 }
 
@@ -283,13 +306,10 @@ __device__ __forceinline__ double block_incl_scan_f64(double v, double* slot /* 
   const double inc = wave_scan_f64(v);
   if (lane() == 63) slot[wave()] = inc;
   lds_barrier();
-  double before = 0.0, all = 0.0;
-  for (uint32_t w = 0; w < nwaves(); ++w) {
-    const double t = slot[w];
-    if (w < wave()) before += t;
-    all += t;
-  }
-  *total = all;
+  const double ws = wave_scan_f64(lane() < nwaves() ? slot[lane()] : 0.0);
+  const unsigned long long wb = __builtin_bit_cast(unsigned long long, ws);
+  *total = __builtin_bit_cast(double, readlane64(wb, 63));
+  const double before = wave() ? __builtin_bit_cast(double, readlane64(wb, wave() - 1)) : 0.0;
   return before + inc;
 }
 
