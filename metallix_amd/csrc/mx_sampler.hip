@@ -127,8 +127,9 @@ struct alignas(16) ChunkSmem {
   WavePart wp[NW];
   WavePart wq[NW];
 };
-// The row finisher runs 256 threads (4 waves, one per SIMD): its decision
-// logic is serial in places and wants registers more than lanes.
+// The row finisher runs 1024 threads: its candidate phase keeps at most
+// CCAP / FT = 8 candidates per thread; sets of at most 256 E tokens are
+// finished by one wave.
 constexpr int FT = 1024;
 constexpr int FW = FT / 64;
 constexpr uint32_t BPT = NB / FT;          // radix bins per finisher thread
@@ -812,7 +813,9 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
 // freeze rule, a crossing bin with more members than threads).
 constexpr int FR = CCAP / FT;      // candidates per thread
 constexpr int FE = ECAP / FT;      // E tokens per thread
-constexpr int FB = 4096;           // the candidate phase's histogram bins (12 bits)
+constexpr int FB = 4 * FT;         // the candidate phase's histogram bins
+constexpr int FB_BITS = FT == 256 ? 10 : (FT == 512 ? 11 : 12);
+static_assert(FB == (1 << FB_BITS), "power-of-two bins");
 constexpr double WFIX = 0x1p50;    // fixed-point scale of the cut's masses (every weight is at most 1)
 static_assert(FB == 4 * FT, "each thread scans four histogram bins");
 static_assert(FR <= 32 && FE <= 32, "per-thread bit masks");
@@ -832,7 +835,7 @@ __device__ __forceinline__ bool fast_kth(FinSmem& F, const uint32_t (&key)[FR], 
                                          uint32_t kmin, uint32_t kmax, uint32_t* kappa, uint32_t* above) {
   const uint32_t tid = threadIdx.x;
   if (kmin == kmax) { *kappa = kmax; *above = 0u; return true; }
-  const int sh = fast_shift(kmin, kmax, 12);
+  const int sh = fast_shift(kmin, kmax, FB_BITS);
   uint32_t* cnt = F.u.f.cnt;
   reinterpret_cast<uint4*>(cnt)[tid] = make_uint4(0u, 0u, 0u, 0u);
   F.u.f.mkey[tid] = 0u;   // key 0 is no finite logit's: pads the member list
@@ -890,48 +893,48 @@ template <int G>
 struct Grp;
 template <>
 struct Grp<64> {
-  __device__ static uint32_t id() { return lane(); }
-  __device__ static void sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-  __device__ static uint32_t excl_u32(uint32_t v, uint32_t*, uint32_t* total) {
+  __device__ __forceinline__ static uint32_t id() { return lane(); }
+  __device__ __forceinline__ static void sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+  __device__ __forceinline__ static uint32_t excl_u32(uint32_t v, uint32_t*, uint32_t* total) {
     const uint32_t i = wave_scan_u32(v);
     *total = bcast63(i);
     return i - v;
   }
-  __device__ static unsigned long long excl_u64(unsigned long long v, unsigned long long*, unsigned long long* total) {
+  __device__ __forceinline__ static unsigned long long excl_u64(unsigned long long v, unsigned long long*, unsigned long long* total) {
     const unsigned long long i = wave_scan_u64(v);
     *total = readlane64(i, 63);
     return i - v;
   }
-  __device__ static double incl_f64(double v, double*, double* total) {
+  __device__ __forceinline__ static double incl_f64(double v, double*, double* total) {
     const double i = wave_scan_f64(v);
     *total = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, i), 63));
     return i;
   }
   // sums of two f64 and one u32 (one reduction)
-  __device__ static void sum3(double& a, double& b, uint32_t& c, FinSmem&, int) {
+  __device__ __forceinline__ static void sum3(double& a, double& b, uint32_t& c, FinSmem&, int) {
     a = wave_sum_f64(a);
     b = wave_sum_f64(b);
     c = wave_sum_u32(c);
   }
-  __device__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem&) {
+  __device__ __forceinline__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem&) {
     mn = ~wave_max_u32(~mn);
     mx = wave_max_u32(mx);
   }
-  __device__ static unsigned long long min_u64(unsigned long long v, FinSmem&) { return ~wave_max_u64(~v); }
+  __device__ __forceinline__ static unsigned long long min_u64(unsigned long long v, FinSmem&) { return ~wave_max_u64(~v); }
 };
 template <>
 struct Grp<FT> {
-  __device__ static uint32_t id() { return threadIdx.x; }
-  __device__ static void sync() { lds_barrier(); }
-  __device__ static uint32_t excl_u32(uint32_t v, uint32_t* slot, uint32_t* total) {
+  __device__ __forceinline__ static uint32_t id() { return threadIdx.x; }
+  __device__ __forceinline__ static void sync() { lds_barrier(); }
+  __device__ __forceinline__ static uint32_t excl_u32(uint32_t v, uint32_t* slot, uint32_t* total) {
     return block_excl_scan_u32(v, slot, total);
   }
-  __device__ static unsigned long long excl_u64(unsigned long long v, unsigned long long* slot,
+  __device__ __forceinline__ static unsigned long long excl_u64(unsigned long long v, unsigned long long* slot,
                                                 unsigned long long* total) {
     return block_excl_scan_u64(v, slot, total);
   }
-  __device__ static double incl_f64(double v, double* slot, double* total) { return block_incl_scan_f64(v, slot, total); }
-  __device__ static void sum3(double& a, double& b, uint32_t& c, FinSmem& F, int s) {
+  __device__ __forceinline__ static double incl_f64(double v, double* slot, double* total) { return block_incl_scan_f64(v, slot, total); }
+  __device__ __forceinline__ static void sum3(double& a, double& b, uint32_t& c, FinSmem& F, int s) {
     a = wave_sum_f64(a);
     b = wave_sum_f64(b);
     c = wave_sum_u32(c);
@@ -943,7 +946,7 @@ struct Grp<FT> {
     b = wave_sum_f64(wl ? F.rd[q][1] : 0.0);
     c = wave_sum_u32(wl ? F.ru[q][s] : 0u);
   }
-  __device__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem& F) {
+  __device__ __forceinline__ static void minmax_u32(uint32_t& mn, uint32_t& mx, FinSmem& F) {
     mn = ~wave_max_u32(~mn);
     mx = wave_max_u32(mx);
     if (lane() == 0) { F.ru[wave()][2] = mn; F.ru[wave()][3] = mx; }
@@ -953,7 +956,7 @@ struct Grp<FT> {
     mn = ~wave_max_u32(wl ? ~F.ru[q][2] : 0u);
     mx = wave_max_u32(wl ? F.ru[q][3] : 0u);
   }
-  __device__ static unsigned long long min_u64(unsigned long long v, FinSmem& F) {
+  __device__ __forceinline__ static unsigned long long min_u64(unsigned long long v, FinSmem& F) {
     v = ~wave_max_u64(~v);
     if (lane() == 0) F.rm[wave()] = v;
     lds_barrier();
@@ -970,7 +973,7 @@ template <int G>
 __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t ne, uint32_t unc0) {
   using Gr = Grp<G>;
   constexpr int NBG = 4 * G;                 // cut histogram bins
-  constexpr int BITS = G == 64 ? 8 : 12;
+  constexpr int BITS = G == 64 ? 8 : (G == 256 ? 10 : (G == 512 ? 11 : 12));
   static_assert(NBG == (1 << BITS), "4 bins per thread");
   const RowCfg& c = *X.c;
   const uint32_t gi = Gr::id();
@@ -1248,7 +1251,7 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
     if ((inE >> r) & 1u) F.eidx[ep++] = j0 + r;
   lds_barrier();
   fstamp(X, 4);
-  if (ne <= (uint32_t)(64 * FE)) {
+  if (ne <= 256u) {
     // one wave decides; the others wait for its verdict
     if (wave() == 0) {
       const bool ok = e_finish<64>(X, F, ne, unc);
@@ -1786,6 +1789,9 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const bool want_arg = mode == M_GREEDY;
   const double inv_rep = 1.0 / (double)c.rep;
   float lv[PER_MAX][4];
+  float qm[PER_MAX];                  // per slice: the largest legal logit of this thread's quad
+#pragma unroll
+  for (int i = 0; i < PER_MAX; ++i) qm[i] = -INFINITY;
   uint64_t lq = 0;                    // legal bits of partial / masked slices, 4 per slice
   float t1 = -INFINITY, t2 = -INFINITY, tmin = INFINITY, gv = -INFINITY;
   uint32_t gi = NONE, nleg = 0;
@@ -1797,12 +1803,18 @@ __global__ __launch_bounds__(NT) void sample_kernel(
       const uint32_t send = min(c1, sbase + (uint32_t)SLICE);
       uint32_t tva[4] = {0u, 0u, 0u, 0u};   // count | bias flag << 31
       float bva[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      bool tab_hit = false;   // wave-uniform: some lane's quad has a history or bias entry
       if (tab_chunk) {
         const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
-        const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
+        // Most quads of most waves hold no entry: decode only when one does.
+        tab_hit = __builtin_amdgcn_ballot_w64((cw.x | cw.y) != 0u) != 0ull;
+        if (tab_hit) {
+          const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tva[e] = (h[e] & 0x7fffu) | ((h[e] & 0x8000u) << 16);
+          for (int e = 0; e < 4; ++e) tva[e] = (h[e] & 0x7fffu) | ((h[e] & 0x8000u) << 16);
+        }
       } else if (tab_slices) {
+        tab_hit = true;
         const int buf = i & 1;
         // Scatter this slice's history ids (counts) and bias ids (flag and
         // value) into the LDS table; a buffer is rewritten two slices later,
@@ -1837,7 +1849,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
       }
       float x[4];
       Quad<In>::unpack(raw[i], x);
-      if (has_tab) {
+      if (tab_hit) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool hit = tva[e] != 0u;
@@ -1878,13 +1890,16 @@ __global__ __launch_bounds__(NT) void sample_kernel(
             gi = g ? e0 + (uint32_t)e : gi;
           }
         } else if (want_top2) {
+          // top two per thread: with t1 >= t2, med3(t1, t2, x) is the new second
 #pragma unroll
-          for (int e = 0; e < 4; ++e) { t2 = fmaxf(t2, fminf(t1, x[e])); t1 = fmaxf(t1, x[e]); }
+          for (int e = 0; e < 4; ++e) { t2 = vmed3(t1, t2, x[e]); t1 = vmax(t1, x[e]); }
+          qm[i] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
         } else if (want_min) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { t1 = fmaxf(t1, x[e]); tmin = fminf(tmin, x[e]); }
+          t1 = vmax3(vmax3(t1, x[0], x[1]), x[2], x[3]);
+          tmin = vmin3(vmin3(tmin, x[0], x[1]), x[2], x[3]);
         } else {
-          t1 = fmaxf(fmaxf(t1, x[0]), fmaxf(fmaxf(x[1], x[2]), x[3]));
+          qm[i] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+          t1 = vmax(t1, qm[i]);
         }
       } else {
 #pragma unroll
@@ -1895,6 +1910,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         const float lm = lg ? x[e] : -INFINITY;
         if (want_top2) t2 = fmaxf(t2, fminf(t1, lm));
         t1 = fmaxf(t1, lm);
+        qm[i] = fmaxf(qm[i], lm);
         if (want_min) tmin = fminf(tmin, lg ? x[e] : INFINITY);
         if (want_arg) {
           const bool g = lm > gv;
@@ -2026,22 +2042,40 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         const bool full = !masked_row && min(c1, sbase + (uint32_t)SLICE) - sbase == (uint32_t)SLICE;
         const uint32_t qb = full ? 0xfu : (uint32_t)(lq >> (4 * i)) & 0xfu;
         if (emit) {
+          // screen the slice on the quad maxima (legal tokens only) first
           uint32_t cnt = 0;
+          if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
+            if (full) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((qb >> e) & 1u) && lv[i][e] >= thr));
+              for (int e = 0; e < 4; ++e) cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lv[i][e] >= thr));
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((qb >> e) & 1u) && lv[i][e] >= thr));
+            }
+          }
           cnt_i[i] = cnt;
           if (lane() == 0) S.wcnt[i * NW + wave()] = cnt;
         }
         if (mass32) {
           float sw = 0.0f, ew = 0.0f;
+          if (full) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float y = (lv[i][e] - m) * c2;
-            const float w = __builtin_amdgcn_exp2f(y);
-            const bool lg = (qb >> e) & 1u;
-            sw += lg ? w : 0.0f;
-            ew += lg ? w * -y : 0.0f;
+            for (int e = 0; e < 4; ++e) {
+              const float y = (lv[i][e] - m) * c2;
+              const float w = __builtin_amdgcn_exp2f(y);
+              sw += w;
+              ew = __builtin_fmaf(w, -y, ew);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float y = (lv[i][e] - m) * c2;
+              const float w = __builtin_amdgcn_exp2f(y);
+              const bool lg = (qb >> e) & 1u;
+              sw += lg ? w : 0.0f;
+              ew = lg ? __builtin_fmaf(w, -y, ew) : ew;
+            }
           }
           m0 += (double)sw;
           m1 += (double)ew;

@@ -223,6 +223,31 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
 }
 
 
+// f32 max / min / median of three as single VALU instructions, without the
+// NaN-quieting canonicalisation the compiler puts before fmaxf/fminf.  For
+// finite operands they equal the IEEE results; callers flag non-finite
+// logits separately, so the value they give a NaN does not matter.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  __asm__("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmin3(float a, float b, float c) {
+  float r;
+  __asm__("v_min3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmed3(float a, float b, float c) {
+  float r;
+  __asm__("v_med3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  __asm__("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 template <typename In>
