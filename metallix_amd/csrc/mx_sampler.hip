@@ -160,8 +160,10 @@ struct alignas(16) FinSmem {
   unsigned long long s_l[4];
   struct {                             // the row header from the chunk statistics
     double mass, mass_err;             // sum of chunk masses scaled to the row maximum, and its error bound
+    double L;                          // ln(min_p) (-inf for min_p = 0)
     uint32_t flags, nlegal, Mkey, bi, ncand;
   } hdr;
+  double etab[128];                    // exp_neg's tables: 2^(j/64) (high, low parts)
   double rd[FW][2];                    // multi-value reduction
   uint32_t ru[FW][4];
   unsigned long long rm[FW];
@@ -339,6 +341,7 @@ struct FinCtx {
   uint32_t* kbits;
   uint32_t nwords;
   uint64_t* timing;    // phase timestamps (diagnostics), null when off
+  const double* etab;  // exp_neg's tables in LDS
 };
 
 // Finisher phase timestamp k (slot MAXC of the row's timing record).
@@ -993,7 +996,7 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
       const float l = F.cl[F.eidx[p0 + r]];
       ek[r] = okey(l);
       const double s = ((double)l - X.M) / c.T;
-      w[r] = exp_neg(s);
+      w[r] = exp_neg_t(s, X.etab, X.etab + 64);
       esum += w[r];
       bool p = true;
       if (apply_minp) {
@@ -1096,14 +1099,24 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
     Gr::sync();
     const uint32_t cm = F.s_u[10];
     if (cm > (uint32_t)G) return false;
-    if (gi < cm) {
-      const uint32_t mk = F.u.f.mkey[gi], mp = F.u.f.mpos[gi];
-      const unsigned long long mwv = F.u.f.mw[gi];
-      unsigned long long ahead = 0;   // mass of the members ordered before this one
+    const uint32_t mk = gi < cm ? F.u.f.mkey[gi] : 0u, mp = gi < cm ? F.u.f.mpos[gi] : 0u;
+    const unsigned long long mwv = gi < cm ? F.u.f.mw[gi] : 0ull;
+    unsigned long long ahead = 0;   // mass of the members ordered before this one
+    if (G == 64) {
+      // one wave: the members sit in lanes 0..cm-1; read them lane by lane
+      for (uint32_t i = 0; i < cm; ++i) {
+        const uint32_t k2 = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)i);
+        const uint32_t p2 = (uint32_t)__builtin_amdgcn_readlane((int)mp, (int)i);
+        const unsigned long long w2 = readlane64(mwv, i);
+        if (k2 > mk || (k2 == mk && p2 < mp)) ahead += w2;
+      }
+    } else if (gi < cm) {
       for (uint32_t i = 0; i < cm; ++i) {
         const uint32_t k2 = F.u.f.mkey[i], p2 = F.u.f.mpos[i];
         if (k2 > mk || (k2 == mk && p2 < mp)) ahead += F.u.f.mw[i];
       }
+    }
+    if (gi < cm) {
       const unsigned long long prev = bbefore + ahead, incl = prev + mwv;
       if ((double)prev < theta_fx && theta_fx <= (double)incl) {
         F.s_u[11] = mk;
@@ -1188,6 +1201,20 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
   return true;
 }
 
+// The E phase on one wave (at most 256 E tokens; the other waves wait for
+// its verdict) or on the workgroup.
+__device__ __forceinline__ bool finish_e(const FinCtx& X, FinSmem& F, uint32_t ne, uint32_t unc) {
+  if (ne <= 256u) {
+    if (wave() == 0) {
+      const bool ok = e_finish<64>(X, F, ne, unc);
+      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
+    }
+    lds_barrier();
+    return F.s_u[15] != 0u;
+  }
+  return e_finish<FT>(X, F, ne, unc);
+}
+
 __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
   const RowCfg& c = *X.c;
   const uint32_t tid = threadIdx.x;
@@ -1208,6 +1235,7 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
   // ---- E: the top-k head, the exact min-p set, or every candidate --------
   uint32_t inE = 0, unc = 0;
   if (X.k_path) {
+    if (c.k > (uint32_t)ECAP) return false;
     uint32_t kmin = NONE, kmax = 0;
 #pragma unroll
     for (int r = 0; r < FR; ++r)
@@ -1215,20 +1243,28 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
     Grp<FT>::minmax_u32(kmin, kmax, F);
     uint32_t kappa, above;
     if (!fast_kth(F, key, act, c.k, kmin, kmax, &kappa, &above)) return false;
-    // ties at kappa: the first (k - above) in token-ID order
-    uint32_t nt = 0;
+    // E = the keys above kappa and the first (k - above) ties at kappa in
+    // token-ID order: one scan of (above count << 16 | tie count) places
+    // both (at most FR each per thread, k <= ECAP in all).
+    uint32_t gt = 0, nt = 0;
 #pragma unroll
     for (int r = 0; r < FR; ++r)
-      if ((act >> r) & 1u) nt += key[r] == kappa;
+      if ((act >> r) & 1u) { gt += key[r] > kappa; nt += key[r] == kappa; }
     uint32_t ttot;
-    uint32_t tb = block_excl_scan_u32(nt, F.sc_u[1], &ttot);
+    const uint32_t ex = block_excl_scan_u32((gt << 16) | nt, F.sc_u[1], &ttot);
     const uint32_t need_t = c.k - above;
+    uint32_t tb = ex & 0xffffu;
+    uint32_t ep = (ex >> 16) + min(need_t, tb);
 #pragma unroll
     for (int r = 0; r < FR; ++r) {
       if (!((act >> r) & 1u)) continue;
-      if (key[r] > kappa) inE |= 1u << r;
-      else if (key[r] == kappa) { if (tb < need_t) inE |= 1u << r; ++tb; }
+      bool in = key[r] > kappa;
+      if (key[r] == kappa) { in = tb < need_t; ++tb; }
+      if (in) F.eidx[ep++] = j0 + r;
     }
+    lds_barrier();
+    fstamp(X, 4);
+    return finish_e(X, F, c.k, 0u);
   } else if (X.mode == M_MINP) {
 #pragma unroll
     for (int r = 0; r < FR; ++r) {
@@ -1251,16 +1287,7 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
     if ((inE >> r) & 1u) F.eidx[ep++] = j0 + r;
   lds_barrier();
   fstamp(X, 4);
-  if (ne <= 256u) {
-    // one wave decides; the others wait for its verdict
-    if (wave() == 0) {
-      const bool ok = e_finish<64>(X, F, ne, unc);
-      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
-    }
-    lds_barrier();
-    return F.s_u[15] != 0u;
-  }
-  return e_finish<FT>(X, F, ne, unc);
+  return finish_e(X, F, ne, unc);
 }
 
 // ---------------------------------------------------------------------------
@@ -1273,6 +1300,23 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
   const uint32_t C = A.C;
+  // exp_neg's tables into LDS (waves 1-2), and the first candidates of each
+  // chunk, loaded speculatively while wave 0 reads the chunk statistics:
+  // thread t covers slot t mod (FT / C) of chunk t / (FT / C).
+  if (tid >= 64 && tid < 192) {
+    const uint32_t j = tid - 64u;
+    F.etab[j] = j < 64u ? kExp2Tab[j] : kExp2TabLo[j - 64u];
+  }
+  const uint32_t spc = FT / C;   // speculative slots per chunk
+  const uint32_t sq = tid / spc, sj = tid - sq * spc;
+  const bool s_ok = sq < C && sj < A.CH && (uint64_t)sq * A.CH + sj < V;
+  float s_l = 0.0f;
+  uint32_t s_id = 0;
+  if (s_ok) {
+    const uint64_t pos = rbase + (uint64_t)sq * A.CH + sj;
+    s_l = A.w.cand_l[pos];
+    s_id = A.w.cand_id[pos];
+  }
   // Chunk statistics: wave 0 reads them (lane q <-> chunk q, C <= 64),
   // reduces them with DPP and publishes the row header and a copy of the
   // statistics in LDS.
@@ -1312,6 +1356,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       F.coff[C] = bcast63(cinc);
       F.hdr.flags = fl; F.hdr.nlegal = nl; F.hdr.Mkey = mkey; F.hdr.bi = garg ? ~(uint32_t)garg : NONE;
       F.hdr.ncand = bcast63(cinc); F.hdr.mass = t; F.hdr.mass_err = te;
+      F.hdr.L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
     }
   }
   lds_barrier();
@@ -1322,7 +1367,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
   X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
-  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing;
+  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab;
   if (err) {
     write_result(X, err, -1, 0.0, 0u);
     if (kbits)
@@ -1475,28 +1520,34 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   // Candidate j lives in chunk q's region at j - coff[q]; j grows with u,
   // so each thread walks the chunk offsets once.
   if (X.lds_c) {
+    if (s_ok && sj < F.st[sq].ncand) { F.cl[F.coff[sq] + sj] = s_l; F.cid[F.coff[sq] + sj] = s_id; }
     float lv[FR];
     uint32_t iv[FR];
+    uint32_t need = 0;   // bit u: candidate u * FT + tid is past the speculative slots
     uint32_t qj = 0, nxt = C > 1 ? F.coff[1] : NONE;
 #pragma unroll
     for (int u = 0; u < FR; ++u) {
       const uint32_t j = (uint32_t)u * FT + tid;
       if (j < ncand) {
         while (j >= nxt) { ++qj; nxt = qj + 1 < C ? F.coff[qj + 1] : NONE; }
-        const uint64_t pos = rbase + (uint64_t)qj * A.CH + (j - F.coff[qj]);
-        lv[u] = A.w.cand_l[pos];
-        iv[u] = A.w.cand_id[pos];
+        const uint32_t local = j - F.coff[qj];
+        if (local >= spc) {
+          const uint64_t pos = rbase + (uint64_t)qj * A.CH + local;
+          lv[u] = A.w.cand_l[pos];
+          iv[u] = A.w.cand_id[pos];
+          need |= 1u << u;
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < FR; ++u) {
       const uint32_t j = (uint32_t)u * FT + tid;
-      if (j < ncand) { F.cl[j] = lv[u]; F.cid[j] = iv[u]; }
+      if ((need >> u) & 1u) { F.cl[j] = lv[u]; F.cid[j] = iv[u]; }
     }
     lds_barrier();
   }
   stamp(A, row, MAXC, 1);
-  const double L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
+  const double L = F.hdr.L;
   // ln(min_p) is exact for min_p = 1 (and -inf for 0); otherwise device and
   // host logs may differ in the last ulps, so a shifted logit within 4 ulp is
   // an uncertain cut.
@@ -2336,6 +2387,12 @@ int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer) {
   return MXS_OK;
 }
 
+int mxs_debug_set_split_event(mxs_ctx* ctx, void* hip_event) {
+  if (!ctx) return MXS_EINVAL;
+  ctx->split_event = (hipEvent_t)hip_event;
+  return MXS_OK;
+}
+
 int mxs_sync(mxs_ctx* ctx) {
   if (!ctx) return MXS_EINVAL;
   hipError_t e = hipStreamSynchronize(ctx->stream);
@@ -2392,12 +2449,14 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   if (b->dtype == MXS_F32) {
     hipLaunchKernelGGL(mxs::sample_kernel<float>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
                        p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
     hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
                        b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
                        A.b.bias_offsets);
   } else {
     hipLaunchKernelGGL(mxs::sample_kernel<uint16_t>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
                        p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
     hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
                        b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
                        A.b.bias_offsets);

@@ -46,6 +46,7 @@ struct mxs_ctx {
   float* d_zero_f32 = nullptr;
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
+  hipEvent_t split_event = nullptr;   // recorded between the chunk kernel and the finisher (diagnostics)
   // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
   uint32_t* topn_ctr = nullptr;
   void* topn_scratch = nullptr;

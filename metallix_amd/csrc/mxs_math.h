@@ -68,7 +68,9 @@ MXS_HD float bias_and_penalize(float l, uint32_t tv, float bias, float rep, doub
 // as a two-part table so one final rounding dominates, scaled by
 // 2^(n div 64).  Within 1 ulp of glibc's exp (checked in tests); the
 // certificate bounds in the kernels budget 4 ulp per term.  Returns 0 below -746 and for -inf.
-MXS_HD double exp_neg(double x) {
+// exp_neg_t takes the two tables by pointer (a kernel may keep a copy in
+// LDS); exp_neg reads the constant tables.
+MXS_HD double exp_neg_t(double x, const double* tab_hi, const double* tab_lo) {
   if (!(x > -746.0)) return 0.0;
   const double kInvL = 92.33248261689366;          // 64 / ln 2
   const double kLHi = 0.010830424696249145;        // ln 2 / 64, high part
@@ -84,8 +86,9 @@ MXS_HD double exp_neg(double x) {
   double q = fma(r * r, p, r);  // e^r - 1
   int j = n & 63;
   int k = n >> 6;  // arithmetic shift: floor division
-  const double th = kExp2Tab[j], tl = kExp2TabLo[j];
+  const double th = tab_hi[j], tl = tab_lo[j];
   return ldexp(th + fma(th, q, tl), k);
 }
+MXS_HD double exp_neg(double x) { return exp_neg_t(x, kExp2Tab, kExp2TabLo); }
 
 }  // namespace mxs
