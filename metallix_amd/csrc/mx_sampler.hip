@@ -1,18 +1,18 @@
 // mx_sampler.hip -- MI355X (gfx950) token sampler: kernels and the C ABI of
 // include/mx_sampler.h.
 //
-// One launch samples a batch.  Each logit row is split into C chunks of at
-// most CHUNK_MAX tokens; one 1024-thread workgroup streams a chunk from HBM
-// once into registers (16-byte loads, coalesced), applies logit bias and
-// penalties from an LDS count table, the grammar mask and the finite check,
-// reduces the chunk's statistics and writes a compact, token-ID-ordered
-// candidate list.  The last workgroup of the row to finish (a relaxed
-// device-scope counter, no grid barrier) becomes the row's finisher: it
-// merges the chunk statistics and candidates and decides top-k, top-p,
-// min-p and the inverse-CDF draw in f64.  Decisions the reference makes with
+// One mxs_sample call is two kernels on one stream.  sample_kernel splits
+// each logit row into C chunks of at most CHUNK_MAX tokens; one 1024-thread
+// workgroup streams a chunk from HBM once into registers (16-byte loads,
+// coalesced), applies logit bias and penalties from an LDS count table, the
+// grammar mask and the finite check, reduces the chunk's statistics and
+// writes a compact, token-ID-ordered candidate list.  finish_kernel runs one
+// workgroup per row after it (the kernel boundary orders the two): it merges
+// the chunk statistics and candidates and decides top-k, top-p, min-p and
+// the inverse-CDF draw in f64.  Decisions the reference makes with
 // sequential f64 sums are taken from parallel sums only when a rigorous
 // error bound certifies them; otherwise the finisher replays the
-// reference's sequential order on one lane, or reports the row uncertified.
+// reference's sequential order, or reports the row uncertified.
 //
 // Reference semantics (arclabs561/metallix):
 //   nucleus_mask            crates/app/cli/src/qwen_forward.rs:474-549
