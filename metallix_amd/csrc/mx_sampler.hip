@@ -82,6 +82,7 @@ struct SampleArgs {
   uint32_t CH;         // tokens per chunk (multiple of 4)
   uint64_t* timing;    // optional phase timestamps (diagnostics), see mxs_debug_set_timing
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
+  uint32_t epoch;      // this call's tag for Work::rowx (never 0)
 };
 
 // Phase timestamps for diagnostics: wall clock (100 MHz) at fixed points of
@@ -126,6 +127,7 @@ struct alignas(16) ChunkSmem {
   alignas(16) uint32_t wcnt[PER_MAX * NW + 32];   // candidates per (slice, wave), padded for the scan
   WavePart wp[NW];
   WavePart wq[NW];
+  uint32_t xkey;                       // min-p rows: the exchanged row-maximum lower bound
 };
 // The row finisher runs 1024 threads: its candidate phase keeps at most
 // CCAP / FT = 8 candidates per thread; sets of at most 256 E tokens are
@@ -2022,6 +2024,13 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const uint64_t rbase = (uint64_t)row * V;
   bool emit = false;
   float thr = -INFINITY;
+  // Min-p rows: the row maximum is at least every chunk maximum, so each
+  // chunk publishes its maximum key (epoch-tagged atomic max, one word per
+  // row) and later takes the largest published so far as a lower bound of
+  // the row maximum.  Any lower bound gives a superset of the min-p set;
+  // the exchange only makes it tighter.
+  bool minp_x = false;
+  uint32_t xkey = maxkey;
   if (row_ok && nleg > 0) {
     if (mode == M_TOPK) {
       emit = true;
@@ -2066,10 +2075,15 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         }
       }
     } else if (mode == M_MINP) {
-      // Superset of the min-p set: the row maximum is at least m.
+      // The threshold comes after the mass pass, from the largest chunk
+      // maximum of the row published by then (see below).
       emit = true;
-      const double lim_d = md + c.T * log(c.min_p);
-      thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(m)) * 1e-5f - 1e-30f;
+      minp_x = true;
+      if (tid == 0) {
+        const unsigned long long old = __hip_atomic_fetch_max(
+            A.w.rowx + row, ((unsigned long long)A.epoch << 32) | maxkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((uint32_t)(old >> 32) == A.epoch) xkey = max(xkey, (uint32_t)old);
+      }
     } else if (mode == M_ALL) {
       emit = true;
     }
@@ -2092,7 +2106,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         const uint32_t sbase = c0 + (uint32_t)i * SLICE;
         const bool full = !masked_row && min(c1, sbase + (uint32_t)SLICE) - sbase == (uint32_t)SLICE;
         const uint32_t qb = full ? 0xfu : (uint32_t)(lq >> (4 * i)) & 0xfu;
-        if (emit) {
+        if (emit && !minp_x) {
           // screen the slice on the quad maxima (legal tokens only) first
           uint32_t cnt = 0;
           if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
@@ -2148,6 +2162,37 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     if (mass32 || mass64) {
       const double w0s = wave_sum_f64(m0), w1s = wave_sum_f64(m1);
       if (lane() == 0) { S.wq[wave()].m0 = w0s; S.wq[wave()].m1 = w1s; }
+    }
+  }
+  if (minp_x) {
+    // the largest chunk maximum of the row published by now
+    if (tid == 0) {
+      const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
+      S.xkey = xkey;
+    }
+    lds_barrier();
+    const float mx = okey_value(S.xkey);
+    const double lim_d = (double)mx + c.T * log(c.min_p);
+    thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i) {
+      cnt_i[i] = 0u;
+      if (i < (int)A.per) {
+        const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+        const bool full = !masked_row && min(c1, sbase + (uint32_t)SLICE) - sbase == (uint32_t)SLICE;
+        const uint32_t qb = full ? 0xfu : (uint32_t)(lq >> (4 * i)) & 0xfu;
+        uint32_t cnt = 0;
+        if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((qb >> e) & 1u) && lv[i][e] >= thr));
+        }
+        cnt_i[i] = cnt;
+        if (lane() == 0) S.wcnt[i * NW + wave()] = cnt;
+      } else if (lane() == 0) {
+        S.wcnt[i * NW + wave()] = 0u;
+      }
     }
   }
   stamp(A, row, chunk, 5);
@@ -2310,12 +2355,12 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   hipSetDevice(device);
   const size_t rv = (size_t)max_rows * max_vocab;
   hipError_t e = hipSuccess;
-  e = e ? e : hipMalloc(&ctx->work.ctr, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->work.rowx, (size_t)max_rows * sizeof(unsigned long long));
   e = e ? e : hipMalloc(&ctx->work.stat, (size_t)max_rows * mxs::MAXC * sizeof(mxs::ChunkStat));
   e = e ? e : hipMalloc(&ctx->work.cand_l, rv * sizeof(float));
   e = e ? e : hipMalloc(&ctx->work.cand_id, rv * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
-  e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * sizeof(unsigned long long));
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
@@ -2355,7 +2400,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipGetDevice(&prev);
   hipSetDevice(ctx->device);
   hipDeviceSynchronize();
-  hipFree(ctx->work.ctr);
+  hipFree(ctx->work.rowx);
   hipFree(ctx->work.stat);
   hipFree(ctx->work.cand_l);
   hipFree(ctx->work.cand_id);
@@ -2420,6 +2465,8 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   A.o = *o;
   A.w = ctx->work;
   A.timing = ctx->timing;
+  if (++ctx->epoch == 0u) ctx->epoch = 1u;   // 0 is the zeroed scratch's tag
+  A.epoch = ctx->epoch;
   A.masked = b->mask_words != nullptr;
   if (!A.masked) {
     A.b.mask_words = ctx->d_mask_ones;

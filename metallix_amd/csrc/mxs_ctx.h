@@ -21,12 +21,11 @@ constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8)
 
 // Device scratch of mxs_sample, sized for the context's limits.
 struct Work {
-  uint32_t* ctr;       // [max_rows] arrival counters (reset by each finisher)
-  ChunkStat* stat;     // [max_rows * MAXC]
-  float* cand_l;       // [max_rows * max_vocab]
-  uint32_t* cand_id;   // [max_rows * max_vocab]
-  double* cand_w;      // [max_rows * max_vocab]
-  double* seg;         // [max_rows * MAXC * PER_MAX * NW]
+  unsigned long long* rowx;   // [max_rows] (call epoch << 32) | largest chunk-maximum key published so far
+  ChunkStat* stat;            // [max_rows * MAXC]
+  float* cand_l;              // [max_rows * max_vocab]
+  uint32_t* cand_id;          // [max_rows * max_vocab]
+  double* seg;                // [max_rows * MAXC * PER_MAX * NW]
 };
 
 }  // namespace mxs
@@ -47,6 +46,7 @@ struct mxs_ctx {
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
   hipEvent_t split_event = nullptr;   // recorded between the chunk kernel and the finisher (diagnostics)
+  uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
   // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
   uint32_t* topn_ctr = nullptr;
   void* topn_scratch = nullptr;
