@@ -27,6 +27,7 @@
 
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -134,6 +135,7 @@ struct alignas(16) ChunkSmem {
 // finished by one wave.
 constexpr int FT = 1024;
 constexpr int FW = FT / 64;
+static_assert(FT == NT, "the block helpers assume NT-thread blocks");
 constexpr uint32_t BPT = NB / FT;          // radix bins per finisher thread
 struct alignas(16) FinSmem {
   float cl[CCAP];                      // candidates cached in LDS, token-ID order
@@ -332,7 +334,7 @@ struct FinCtx {
   const uint32_t* cand_id;
   uint32_t CH;
   mxs_out o;
-  const RowCfg* c;
+  RowCfg c;            // a copy (a pointer to the caller's would put it in private memory)
   uint32_t row, mode, C, V, ncand, nlegal;
   uint64_t rbase;
   bool lds_c;          // candidates cached in LDS
@@ -344,6 +346,7 @@ struct FinCtx {
   uint32_t nwords;
   uint64_t* timing;    // phase timestamps (diagnostics), null when off
   const double* etab;  // exp_neg's tables in LDS
+  bool xdev;           // candidates were written by workgroups of this launch: device-scope reads
 };
 
 // Finisher phase timestamp k (slot MAXC of the row's timing record).
@@ -360,17 +363,21 @@ __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, ui
 // Candidate j (token-ID order): from LDS when cached, else from the
 // device-scope candidate arrays.
 __device__ __forceinline__ float cand_l(const FinCtx& X, const FinSmem& F, uint32_t j) {
-  return X.lds_c ? F.cl[j] : X.cand_l[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
+  if (X.lds_c) return F.cl[j];
+  const float* p = &X.cand_l[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
+  return X.xdev ? ld_dev(p) : *p;
 }
 __device__ __forceinline__ uint32_t cand_id(const FinCtx& X, const FinSmem& F, uint32_t j) {
-  return X.lds_c ? F.cid[j] : X.cand_id[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
+  if (X.lds_c) return F.cid[j];
+  const uint32_t* p = &X.cand_id[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
+  return X.xdev ? ld_dev(p) : *p;
 }
 __device__ __forceinline__ bool member(const FinCtx& X, float l, uint32_t id) {
   if (X.k_path) {
     const uint32_t key = okey(l);
     return key > X.kappa || (key == X.kappa && id <= X.id_tie);
   }
-  if (X.mode == M_MINP) return (((double)l - X.M) / X.c->T) >= X.L;
+  if (X.mode == M_MINP) return (((double)l - X.M) / X.c.T) >= X.L;
   return true;
 }
 
@@ -390,7 +397,7 @@ __device__ __forceinline__ void write_result(const FinCtx& X, int32_t status, in
 // select (11/11/10-bit passes, LDS count and f64 mass histograms) whose bin
 // decisions are certified with the same bounds as the exact path.
 __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32_t ne) {
-  const RowCfg& c = *X.c;
+  const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
   auto weight = [&](float l) { return exp_neg(((double)l - X.M) / c.T); };
@@ -617,7 +624,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
 // only P is sorted.  An uncertain crossing replays the reference's
 // sequential f64 sums over E sorted.
 __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32_t ne, bool mp_close_in) {
-  const RowCfg& c = *X.c;
+  const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
   auto el = [&](uint32_t t) { return F.cl[F.eidx[t]]; };
   auto eid = [&](uint32_t t) { return F.cid[F.eidx[t]]; };
@@ -980,7 +987,7 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
   constexpr int NBG = 4 * G;                 // cut histogram bins
   constexpr int BITS = G == 64 ? 8 : (G == 256 ? 10 : (G == 512 ? 11 : 12));
   static_assert(NBG == (1 << BITS), "4 bins per thread");
-  const RowCfg& c = *X.c;
+  const RowCfg& c = X.c;
   const uint32_t gi = Gr::id();
   const uint32_t RE = (ne + G - 1u) / G;
   const uint32_t p0 = gi * RE;
@@ -1218,7 +1225,7 @@ __device__ __forceinline__ bool finish_e(const FinCtx& X, FinSmem& F, uint32_t n
 }
 
 __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
-  const RowCfg& c = *X.c;
+  const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
   if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + 3] = n;   // candidate count (diagnostics)
@@ -1295,7 +1302,7 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
 // ---------------------------------------------------------------------------
 // The row finisher.  Runs in the last chunk workgroup of a row, after every
 // chunk published its statistics and candidates.
-template <typename In>
+template <typename In, bool XD>
 __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
                            uint64_t rbase, double invT) {
   const mxs_batch& b = A.b;
@@ -1316,8 +1323,8 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   uint32_t s_id = 0;
   if (s_ok) {
     const uint64_t pos = rbase + (uint64_t)sq * A.CH + sj;
-    s_l = A.w.cand_l[pos];
-    s_id = A.w.cand_id[pos];
+    s_l = xget<XD>(&A.w.cand_l[pos]);
+    s_id = xget<XD>(&A.w.cand_id[pos]);
   }
   // Chunk statistics: wave 0 reads them (lane q <-> chunk q, C <= 64),
   // reduces them with DPP and publishes the row header and a copy of the
@@ -1329,15 +1336,15 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     v.minkey = NONE; v.thr = 0.0f; v.mass = 0.0; v.mass_err = 0.0;
     if (q < C) {
       const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + q];
-      v.maxkey = st->maxkey;
-      v.gbest_id = st->gbest_id;
-      v.gbest_val = st->gbest_val;
-      v.nlegal = st->nlegal;
-      v.ncand = st->ncand;
-      v.flags = st->flags;
-      v.mass = st->mass;
-      v.mass_err = st->mass_err;
-      v.minkey = st->minkey;
+      v.maxkey = xget<XD>(&st->maxkey);
+      v.gbest_id = xget<XD>(&st->gbest_id);
+      v.gbest_val = xget<XD>(&st->gbest_val);
+      v.nlegal = xget<XD>(&st->nlegal);
+      v.ncand = xget<XD>(&st->ncand);
+      v.flags = xget<XD>(&st->flags);
+      v.mass = xget<XD>(&st->mass);
+      v.mass_err = xget<XD>(&st->mass_err);
+      v.minkey = xget<XD>(&st->minkey);
     }
     const uint32_t fl = wave_or_u32(v.flags);
     const uint32_t nl = wave_sum_u32(v.nlegal);
@@ -1368,8 +1375,8 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   const uint32_t nwords = (V + 31u) / 32u;
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
-  X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = &c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
-  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab;
+  X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
+  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab; X.xdev = XD;
   if (err) {
     write_result(X, err, -1, 0.0, 0u);
     if (kbits)
@@ -1395,7 +1402,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     double part = 0.0;
     for (uint32_t s = tid; s < nseg; s += FT) {
       const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-      if (F.st[q].nlegal) part += A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r] * F.cscale[q];
+      if (F.st[q].nlegal) part += xget<XD>(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
     }
     const double total = block_sum<double>(part, F.red_d);
     const double target = c.u * total;
@@ -1410,7 +1417,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       double w = 0.0;
       if (s < nseg) {
         const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-        if (F.st[q].nlegal) w = A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r] * F.cscale[q];
+        if (F.st[q].nlegal) w = xget<XD>(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
       }
       double tot;
       const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
@@ -1535,8 +1542,8 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
         const uint32_t local = j - F.coff[qj];
         if (local >= spc) {
           const uint64_t pos = rbase + (uint64_t)qj * A.CH + local;
-          lv[u] = A.w.cand_l[pos];
-          iv[u] = A.w.cand_id[pos];
+          lv[u] = xget<XD>(&A.w.cand_l[pos]);
+          iv[u] = xget<XD>(&A.w.cand_id[pos]);
           need |= 1u << u;
         }
       }
@@ -1679,13 +1686,27 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
 
 // ---------------------------------------------------------------------------
 // The sampling kernel.
-template <typename In>
+// Fused mode: the chunk pass and the row finisher share the workgroup's
+// LDS (the finisher starts after the chunk is published).
+union alignas(16) FusedSmem {
+  ChunkSmem s;
+  FinSmem f;
+};
+template <bool XD>
+struct KernelSmem { using T = ChunkSmem; };
+template <>
+struct KernelSmem<true> { using T = FusedSmem; };
+__device__ __forceinline__ ChunkSmem& chunk_smem(ChunkSmem& s) { return s; }
+__device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
+
+template <typename In, bool XD>
 __global__ __launch_bounds__(NT) void sample_kernel(
     SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
     const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
     const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
     const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
-  __shared__ __align__(16) ChunkSmem S;
+  __shared__ __align__(16) typename KernelSmem<XD>::T U;
+  ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
 
@@ -2152,7 +2173,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
           m0 += sw;
           if (mode == M_KEEPALL) {
             const double ws = wave_sum_f64(sw);
-            if (lane() == 0) A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()] = ws;
+            if (lane() == 0) xput<XD>(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
           }
         }
       } else if (lane() == 0 && emit) {
@@ -2250,8 +2271,8 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         for (int e = 0; e < 4; ++e) {
           if (em[e]) {
             const uint64_t pos = cbase + off;
-            A.w.cand_l[pos] = lv[i][e];
-            A.w.cand_id[pos] = e0 + (uint32_t)e;
+            xput<XD>(&A.w.cand_l[pos], lv[i][e]);
+            xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
             ++off;
           }
         }
@@ -2267,18 +2288,38 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     if (want_arg)
       for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
     ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
-    st.maxkey = nleg ? maxkey : 0u;
-    st.gbest_id = garg ? ~(uint32_t)garg : NONE;
-    st.gbest_val = garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f;
-    st.nlegal = nleg;
-    st.ncand = ncand;
-    st.flags = cflags;
-    st.mass = mass;
-    st.mass_err = mass_err;
-    st.minkey = minkey;
-    st.thr = thr;
+    xput<XD>(&st.maxkey, nleg ? maxkey : 0u);
+    xput<XD>(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
+    xput<XD>(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
+    xput<XD>(&st.nlegal, nleg);
+    xput<XD>(&st.ncand, ncand);
+    xput<XD>(&st.flags, cflags);
+    xput<XD>(&st.mass, mass);
+    xput<XD>(&st.mass_err, mass_err);
+    xput<XD>(&st.minkey, minkey);
+    xput<XD>(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
+  if constexpr (XD) {
+    // The row's last chunk to finish becomes its finisher.  The barrier
+    // waits for every wave's device-scope stores; then one relaxed
+    // device-scope count per chunk.
+    __syncthreads();
+    uint32_t last = 0;
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev + 1u == A.C ? 1u : 0u;
+      if (last) st_dev(&A.w.ctr[row], 0u);
+      S.xkey = last;
+    }
+    lds_barrier();
+    last = S.xkey;
+    lds_barrier();   // the finisher's LDS overlays the chunk's
+    if (!last) return;
+    stamp(A, row, MAXC, 0);
+    finish_row<In, true>(A, U.f, c, row, mode, rbase, invT);
+    stamp(A, row, MAXC, 7);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2300,7 +2341,7 @@ __global__ __launch_bounds__(FT) void finish_kernel(
   const uint32_t mode = chunk_mode(c, A.b.vocab);
   const double invT = c.greedy ? 0.0 : 1.0 / c.T;
   stamp(A, row, MAXC, 0);
-  finish_row<In>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT);
+  finish_row<In, false>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT);
   stamp(A, row, MAXC, 7);
 }
 
@@ -2355,12 +2396,20 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   hipSetDevice(device);
   const size_t rv = (size_t)max_rows * max_vocab;
   hipError_t e = hipSuccess;
+  e = e ? e : hipMalloc(&ctx->work.ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->work.rowx, (size_t)max_rows * sizeof(unsigned long long));
   e = e ? e : hipMalloc(&ctx->work.stat, (size_t)max_rows * mxs::MAXC * sizeof(mxs::ChunkStat));
   e = e ? e : hipMalloc(&ctx->work.cand_l, rv * sizeof(float));
   e = e ? e : hipMalloc(&ctx->work.cand_id, rv * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * sizeof(unsigned long long));
+  e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  {
+    // Two kernels unless MXS_SAMPLER_FUSED=1 (one kernel whose last chunk
+    // per row finishes the row; it measured no faster on config 2).
+    const char* fz = getenv("MXS_SAMPLER_FUSED");
+    ctx->split = !(fz && fz[0] == '1');
+  }
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
@@ -2400,6 +2449,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipGetDevice(&prev);
   hipSetDevice(ctx->device);
   hipDeviceSynchronize();
+  hipFree(ctx->work.ctr);
   hipFree(ctx->work.rowx);
   hipFree(ctx->work.stat);
   hipFree(ctx->work.cand_l);
@@ -2492,22 +2542,27 @@ int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
-  // chunk pass, then the row finisher (stream order makes the chunk results visible)
-  if (b->dtype == MXS_F32) {
-    hipLaunchKernelGGL(mxs::sample_kernel<float>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
-                       p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
+  // Split (default): the chunk pass, then the row finisher as a second
+  // kernel (stream order makes the chunk results visible).  Fused: one
+  // kernel; each row's last chunk finishes the row, the chunks' results
+  // handed over through device-scope stores and a per-row counter.
+#define MXS_ARGS A, b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets
+  if (!ctx->split) {
+    if (b->dtype == MXS_F32)
+      hipLaunchKernelGGL((mxs::sample_kernel<float, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    else
+      hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
     if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
-                       b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
-                       A.b.bias_offsets);
+  } else if (b->dtype == MXS_F32) {
+    hipLaunchKernelGGL((mxs::sample_kernel<float, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
+    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
   } else {
-    hipLaunchKernelGGL(mxs::sample_kernel<uint16_t>, grid, dim3(mxs::NT), 0, ctx->stream, A, b->temperature,
-                       p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets);
+    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
     if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, A,
-                       b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets,
-                       A.b.bias_offsets);
+    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
   }
+#undef MXS_ARGS
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");

@@ -21,6 +21,7 @@ constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8)
 
 // Device scratch of mxs_sample, sized for the context's limits.
 struct Work {
+  uint32_t* ctr;              // [max_rows] chunks of the row done (fused mode; the row's last chunk resets it)
   unsigned long long* rowx;   // [max_rows] (call epoch << 32) | largest chunk-maximum key published so far
   ChunkStat* stat;            // [max_rows * MAXC]
   float* cand_l;              // [max_rows * max_vocab]
@@ -47,6 +48,7 @@ struct mxs_ctx {
   uint64_t* timing = nullptr;
   hipEvent_t split_event = nullptr;   // recorded between the chunk kernel and the finisher (diagnostics)
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
+  bool split = true;                  // the row finisher as a second kernel (else fused: MXS_SAMPLER_FUSED=1)
   // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
   uint32_t* topn_ctr = nullptr;
   void* topn_scratch = nullptr;

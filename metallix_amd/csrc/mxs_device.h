@@ -53,6 +53,19 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 __device__ __forceinline__ double ld_dev(const double* p) {
   return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Stores and loads of data one workgroup hands to another within a launch
+// (X = true: device-scope, as above) or to a later launch (X = false: plain).
+template <bool X, typename T>
+__device__ __forceinline__ void xput(T* p, T v) {
+  if constexpr (X) st_dev(p, v); else *p = v;
+}
+template <bool X, typename T>
+__device__ __forceinline__ T xget(const T* p) {
+  if constexpr (X) return ld_dev(p); else return *p;
+}
 // Waits until this lane's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
@@ -80,9 +93,10 @@ __device__ __forceinline__ T wave_max(T v) {
   for (int o = 32; o > 0; o >>= 1) { T t = __shfl_xor(v, o); v = t > v ? t : v; }
   return v;
 }
-// The block helpers below work for any block of up to NT threads (waves
-// counted from blockDim.x).
-__device__ __forceinline__ uint32_t nwaves() { return blockDim.x >> 6; }
+// The block helpers below are for NT-thread blocks, the size every kernel
+// here launches with (a compile-time count spares a kernel-argument load
+// before each use).
+__device__ __forceinline__ uint32_t nwaves() { return (uint32_t)NW; }
 template <typename T>
 __device__ __forceinline__ T block_sum(T v, T* red) {
   v = wave_sum(v);
