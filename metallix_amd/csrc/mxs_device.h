@@ -103,6 +103,7 @@ __device__ __forceinline__ T block_sum(T v, T* red) {
   if (lane() == 0) red[wave()] = v;
   __syncthreads();
   T s = red[0];
+#pragma unroll 1
   for (uint32_t i = 1; i < nwaves(); ++i) s += red[i];
   __syncthreads();
   return s;
@@ -113,6 +114,7 @@ __device__ __forceinline__ T block_max(T v, T* red) {
   if (lane() == 0) red[wave()] = v;
   __syncthreads();
   T s = red[0];
+#pragma unroll 1
   for (uint32_t i = 1; i < nwaves(); ++i) s = red[i] > s ? red[i] : s;
   __syncthreads();
   return s;
@@ -128,6 +130,7 @@ __device__ __forceinline__ T block_scan_incl(T v, T* red, T* total) {
   if (l == 63) red[wave()] = v;
   __syncthreads();
   T before = T(0), all = T(0);
+#pragma unroll 1
   for (uint32_t i = 0; i < nwaves(); ++i) {
     T r = red[i];
     if (i < wave()) before += r;
@@ -152,6 +155,7 @@ __device__ __forceinline__ T block_scan_pair(T v, T* red, T* excl, T* total) {
   if (l == 63) red[wave()] = v;
   __syncthreads();
   T before = T(0), all = T(0);
+#pragma unroll 1
   for (uint32_t i = 0; i < nwaves(); ++i) {
     T r = red[i];
     if (i < wave()) before += r;
