@@ -25,6 +25,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <float.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -1699,26 +1700,390 @@ struct KernelSmem<true> { using T = FusedSmem; };
 __device__ __forceinline__ ChunkSmem& chunk_smem(ChunkSmem& s) { return s; }
 __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 
+// ---------------------------------------------------------------------------
+// The lean chunk body: rows with no grammar mask, no logit bias and a history
+// that fits the register staging (at most HCAP ids), in the greedy, top-k or
+// min-p mode.  It writes the same chunk statistics and token-ID-ordered
+// candidate list as the general body below, so the row finisher is shared.
+// It differs in how it spends instructions:
+//   - one pass per slice, as the slice's load lands: the count table is
+//     built from registers right after the history ids arrive (they are
+//     issued ahead of all but the first slice), so pass 1 overlaps the
+//     stream instead of starting after it;
+//   - every per-token decision is specialised at compile time (MODE, HIST):
+//     no per-slice mode tests;
+//   - min-p rows that need the row mass accumulate it online during the
+//     stream, relative to a running per-thread maximum (each rescale is one
+//     f32 exp2 per slice; the error bound below accounts for it), instead of
+//     in a second pass over the registers after the chunk maximum is known;
+//   - each wave publishes its maximum to the row's exchange word as soon as
+//     its pass 1 ends, so the min-p threshold sees the other chunks' maxima
+//     as early as possible.
+template <typename In, uint32_t MODE, bool HIST>
+__device__ __forceinline__ void chunk_fast(const SampleArgs& A, ChunkSmem& S, const RowCfg& c, const uint32_t row,
+                                           const uint32_t chunk, const uint32_t c0, const uint32_t c1,
+                                           const typename Quad<In>::Raw (&raw)[PER_MAX],
+                                           const uint32_t (&hreg)[HCAP / NT], const uint32_t hn) {
+  const mxs_batch& b = A.b;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t V = b.vocab;
+  const uint32_t clen = c1 - c0;
+  const double invT = MODE == M_GREEDY ? 0.0 : 1.0 / c.T;
+  uint32_t my_flags = 0;
+
+  // ---- the chunk's history count table (u16 per token) -------------------
+  if constexpr (HIST) {
+    const uint32_t n4 = A.per * (SLICE / 8);   // uint4 words covering per slices
+    for (uint32_t t = tid; t < n4; t += NT) reinterpret_cast<uint4*>(S.t.ct)[t] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  if constexpr (MODE == M_TOPK) S.hist[tid] = 0u;   // HB == NT
+  if constexpr (HIST) {
+    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) {
+      const uint32_t j = (uint32_t)r * NT + tid;
+      if (j < hn) {
+        const uint32_t id = hreg[r];
+        if (id >= V) my_flags |= F_HIST;
+        const uint32_t t = id - c0;
+        if (t < clen) atomicAdd(&S.t.ct[t >> 1], 1u << ((t & 1u) * 16u));
+      }
+    }
+    lds_barrier();
+  }
+  stamp(A, row, chunk, 3);
+
+  // ---- pass 1: penalties, finite check, statistics, online mass ----------
+  const bool top2 = MODE == M_TOPK && c.k > TOP1_MAX;
+  const bool do_mass = MODE == M_MINP && c.top_p < 1.0;
+  const float c2 = (float)(invT * 1.4426950408889634);   // log2(e) / T
+  const double inv_rep = 1.0 / (double)c.rep;
+  float lv[PER_MAX][4];
+  float qm[PER_MAX];
+  float t1 = -INFINITY, t2 = -INFINITY, gv = -INFINITY;
+  uint32_t gi = NONE;
+  uint64_t nf = 0;
+  // online mass: acc = sum of 2^((l - mrun) c2) over this thread's tokens so
+  // far (f64 across slices, f32 within a slice), eacc = the same weights
+  // times |(l - mrun) c2| (for the error bound); mrun is the running maximum
+  float mrun = -FLT_MAX;
+  double acc = 0.0, eacc = 0.0;
+#pragma unroll
+  for (int i = 0; i < PER_MAX; ++i) {
+    qm[i] = -INFINITY;
+    if (i < (int)A.per) {
+      const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+      const uint32_t e0 = sbase + tid * 4u;
+      const bool full = sbase + (uint32_t)SLICE <= c1;   // uniform
+      const uint32_t rb = full ? 0xfu : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+      float x[4];
+      Quad<In>::unpack(raw[i], x);
+      if constexpr (HIST) {
+        // Penalised tokens are rare: only an element position where some
+        // lane of the wave holds a count runs the penalty arithmetic.
+        const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
+        if (__builtin_amdgcn_ballot_w64((cw.x | cw.y) != 0u)) {
+          const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (__builtin_amdgcn_ballot_w64(h[e] != 0u))
+              x[e] = h[e] ? bias_and_penalize(x[e], h[e], 0.0f, c.rep, inv_rep, c.freq, c.pres) : x[e];
+        }
+      }
+      if (A.o.adjusted) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((rb >> e) & 1u) A.o.adjusted[(uint64_t)row * V + e0 + (uint32_t)e] = x[e];
+      }
+      if (full) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) nf |= __builtin_amdgcn_ballot_w64(!__builtin_isfinite(x[e]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool inr = (rb >> e) & 1u;
+          nf |= __builtin_amdgcn_ballot_w64(inr && !__builtin_isfinite(x[e]));
+          x[e] = inr ? x[e] : -INFINITY;
+        }
+      }
+      if constexpr (MODE == M_GREEDY) {
+        // IEEE >, first index wins (ids grow with e and i in this thread)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool g = x[e] > gv;
+          gv = g ? x[e] : gv;
+          gi = g ? e0 + (uint32_t)e : gi;
+        }
+      } else {
+        qm[i] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+        if (top2) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { t2 = vmed3(t1, t2, x[e]); t1 = vmax(t1, x[e]); }
+        } else {
+          t1 = vmax(t1, qm[i]);
+        }
+        if (do_mass) {
+          const float mnew = vmax(mrun, qm[i]);
+          const float ys = (mrun - mnew) * c2;                 // <= 0
+          const float s = __builtin_amdgcn_exp2f(ys);
+          float sw = 0.0f, ew = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool inr = (rb >> e) & 1u;
+            const float y = (x[e] - mnew) * c2;
+            const float w = inr ? __builtin_amdgcn_exp2f(y) : 0.0f;
+            sw += w;
+            ew = inr ? __builtin_fmaf(w, -y, ew) : ew;
+          }
+          // rescale what is accumulated to the new running maximum (s = 1
+          // when it did not move); a zero accumulator stays zero
+          const bool live = acc > 0.0;
+          eacc = live ? (eacc + acc * (double)(-ys)) * (double)s + (double)ew : (double)ew;
+          acc = live ? acc * (double)s + (double)sw : (double)sw;
+          mrun = mnew;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) lv[i][e] = x[e];
+    }
+  }
+  stamp(A, row, chunk, 6);
+
+  // ---- chunk statistics: one block reduction ------------------------------
+  const uint32_t nleg = clen;   // no mask: every token of the chunk is legal
+  {
+    const uint32_t kmax = wave_max_u32(okey(MODE == M_GREEDY ? gv : t1));
+    if constexpr (MODE == M_MINP) {
+      // this wave's maximum goes to the row's exchange word right away
+      if (lane() == 0)
+        __hip_atomic_fetch_max(A.w.rowx + row, ((unsigned long long)A.epoch << 32) | kmax, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const uint32_t wf = wave_or_u32(my_flags) | (nf ? (uint32_t)F_NONFINITE : 0u);
+    unsigned long long arg = 0ull;
+    if constexpr (MODE == M_GREEDY) {
+      // -0.0 ties +0.0 under IEEE >: key both as +0.0 so the lower ID wins
+      arg = gi == NONE ? 0ull : ((unsigned long long)okey(gv + 0.0f) << 32) | (unsigned long long)(~gi);
+      arg = wave_max_u64(arg);
+    }
+    double w0s = 0.0, w1s = 0.0;
+    if (do_mass) {
+      // each lane's sum, rescaled from its running maximum to the wave's
+      // (one more f32 rescale step, counted in the bound)
+      const float wm = okey_value(kmax);
+      const float ys = (mrun - wm) * c2;
+      const float s = __builtin_amdgcn_exp2f(ys);
+      const bool live = acc > 0.0;
+      const double e1 = live ? (eacc + acc * (double)(-ys)) * (double)s : 0.0;
+      const double a1 = live ? acc * (double)s : 0.0;
+      w0s = wave_sum_f64(a1);
+      w1s = wave_sum_f64(e1);
+    }
+    if (lane() == 0) {
+      WavePart& p = S.wp[wave()];
+      p.kmax = kmax; p.kmin = 0u; p.nleg = 0u; p.flags = wf; p.arg = arg; p.m0 = w0s; p.m1 = w1s;
+    }
+  }
+  lds_barrier();
+  uint32_t maxkey = 0u, cflags = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    maxkey = max(maxkey, S.wp[w].kmax);
+    cflags |= S.wp[w].flags;
+  }
+  stamp(A, row, chunk, 1);
+  const float m = okey_value(maxkey);   // chunk's largest logit
+  const double md = (double)m;
+  const bool row_ok = !(cflags & (F_HIST | F_NONFINITE));
+
+  // ---- candidate threshold and counts --------------------------------------
+  float thr = -INFINITY;
+  bool emit = false;
+  if (MODE == M_TOPK && row_ok) {
+    emit = true;
+    const uint32_t need = min(c.k, nleg);
+    if (need < nleg) {
+      // The need-th largest of the per-thread maxima (top-2 maxima for
+      // large k) is at most the chunk's need-th largest logit.  Histogram
+      // them on a 1/32-logit grid below m, find the bin where the count
+      // reaches need, and emit down to one bin below it.
+      const float scale = (float)HB / HRANGE;
+      {
+        const float d1 = (m - t1) * scale;
+        if (d1 < (float)(HB - 1)) atomicAdd(&S.hist[(uint32_t)d1], 1u);
+        if (top2) {
+          const float d2 = (m - t2) * scale;
+          if (d2 < (float)(HB - 1)) atomicAdd(&S.hist[(uint32_t)d2], 1u);
+        }
+      }
+      lds_barrier();
+      uint32_t hv[16];
+      uint32_t s = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 h4 = *reinterpret_cast<const uint4*>(&S.hist[lane() * 16u + (uint32_t)q * 4u]);
+        hv[q * 4 + 0] = h4.x; hv[q * 4 + 1] = h4.y; hv[q * 4 + 2] = h4.z; hv[q * 4 + 3] = h4.w;
+        s += h4.x + h4.y + h4.z + h4.w;
+      }
+      const uint32_t inc = wave_scan_u32(s);
+      const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+      if (reach) {
+        const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+        uint32_t run = inc - s, bin = 16u * lane() + 15u;
+        bool found = false;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          run += hv[q];
+          if (!found && run >= need) { found = true; bin = 16u * lane() + (uint32_t)q; }
+        }
+        const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
+        thr = m - (float)(tb + 2u) / scale;
+      }
+    }
+  } else if (MODE == M_MINP && row_ok) {
+    // The largest chunk maximum of the row published by now is a lower
+    // bound of the row maximum: any lower bound gives a superset of the
+    // min-p set, a tighter one fewer candidates.
+    emit = true;
+    const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t xkey = maxkey;
+    if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
+    xkey = (uint32_t)__builtin_amdgcn_readfirstlane((int)xkey);
+    const float mx = okey_value(xkey);
+    const double lim_d = (double)mx + c.T * log(c.min_p);
+    thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
+  }
+  uint32_t cnt_i[PER_MAX];
+  if (emit) {
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i) {
+      cnt_i[i] = 0u;
+      if (i < (int)A.per) {
+        // screen the slice on the quad maxima first (out-of-range tokens
+        // hold -inf; a threshold of -inf takes every in-range token)
+        uint32_t cnt = 0;
+        if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
+          const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+          const uint32_t e0 = sbase + tid * 4u;
+          const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
+                              : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((rb >> e) & 1u) && lv[i][e] >= thr));
+        }
+        cnt_i[i] = cnt;
+        if (lane() == 0) S.wcnt[i * NW + wave()] = cnt;
+      }
+    }
+  }
+  // the chunk mass, relative to the chunk maximum: wave 0 rescales the
+  // waves' sums (lane w <-> wave w) in f64
+  double mass = 0.0, mass_err = 0.0;
+  if (do_mass && row_ok && wave() == 0) {
+    const uint32_t w = lane();
+    double a = 0.0, e = 0.0;
+    if (w < (uint32_t)NW) {
+      const double sc = exp_neg(((double)okey_value(S.wp[w].kmax) - md) * invT);
+      a = S.wp[w].m0 * sc;
+      e = S.wp[w].m1 * sc;
+    }
+    const double S0 = wave_sum_f64(a), E0 = wave_sum_f64(e);
+    mass = S0;
+    // |mass - sum of exact weights| <= 1.01 (2^-22 S (per + 2) + 3 2^-24 S)
+    // for the f32 exp2 of each weight and of each of at most per + 1
+    // rescale factors (2 ulp each) and the 4-term f32 slice sums,
+    // + 1.01 ln2 3 2^-24 sum w |y| for the rounding of the exponents (three
+    // f32 roundings each, relative; a term's exponent and the rescale
+    // exponents applied to it telescope to its distance from the wave
+    // maximum), + n 2^-120 for weights and factors below 2^-126, + 2^-40 S
+    // for the f64 accumulation and the f64 rescale to the chunk maximum.
+    mass_err = 1.01 * (0x1p-22 * S0 * (double)(A.per + 2u) + 3.0 * 0x1p-24 * S0 +
+                       0.6931471805599453 * 3.0001 * 0x1p-24 * E0) +
+               (double)nleg * 0x1p-120 + 0x1p-40 * S0;
+  }
+  stamp(A, row, chunk, 5);
+  uint32_t ncand = 0;
+  if (emit) {
+    lds_barrier();
+    // exclusive offsets in (slice, wave) order == token-ID order; every wave
+    // scans the PER_MAX * NW counts itself (lane j holds j, j + 64, j + 128)
+    const uint32_t nent = A.per * NW;
+    const uint32_t v0 = lane() < nent ? S.wcnt[lane()] : 0u;
+    const uint32_t v1 = lane() + 64u < nent ? S.wcnt[lane() + 64u] : 0u;
+    const uint32_t v2 = lane() + 128u < nent ? S.wcnt[lane() + 128u] : 0u;
+    const uint32_t i0 = wave_scan_u32(v0), i1 = wave_scan_u32(v1), i2 = wave_scan_u32(v2);
+    const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)i0, 63);
+    const uint32_t s1 = (uint32_t)__builtin_amdgcn_readlane((int)i1, 63);
+    const uint32_t s2 = (uint32_t)__builtin_amdgcn_readlane((int)i2, 63);
+    ncand = s0 + s1 + s2;
+    const uint32_t x0 = i0 - v0, x1 = i1 - v1 + s0, x2 = i2 - v2 + s0 + s1;
+    const uint64_t cbase = (uint64_t)row * V + c0;
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i) {
+      if (i < (int)A.per && cnt_i[i]) {
+        const uint32_t idx = (uint32_t)i * NW + wave();
+        const uint32_t src = idx & 63u;
+        const uint32_t reg = idx >> 6;
+        const uint32_t xv = reg == 0 ? x0 : (reg == 1 ? x1 : x2);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)src);
+        const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+        const uint32_t e0 = sbase + tid * 4u;
+        const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
+                            : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+        bool em[4];
+        uint32_t before_me = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          em[e] = ((rb >> e) & 1u) && lv[i][e] >= thr;
+          before_me += lanes_below(__builtin_amdgcn_ballot_w64(em[e]));
+        }
+        uint32_t off = base + before_me;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (em[e]) {
+            const uint64_t pos = cbase + off;
+            A.w.cand_l[pos] = lv[i][e];
+            A.w.cand_id[pos] = e0 + (uint32_t)e;
+            ++off;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- publish the chunk's statistics (the row finisher kernel reads them)
+  stamp(A, row, chunk, 7);
+  if (tid == 0) {
+    unsigned long long garg = 0ull;
+    if constexpr (MODE == M_GREEDY)
+      for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
+    ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
+    st.maxkey = nleg ? maxkey : 0u;
+    st.gbest_id = garg ? ~(uint32_t)garg : NONE;
+    st.gbest_val = garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f;
+    st.nlegal = nleg;
+    st.ncand = ncand;
+    st.flags = cflags;
+    st.mass = mass;
+    st.mass_err = mass_err;
+    st.minkey = 0u;
+    st.thr = thr;
+  }
+  stamp(A, row, chunk, 2);
+}
+
+// The general chunk body: every row the lean body does not cover (grammar
+// masks, logit bias, long histories, parameter errors, the all-candidates
+// and keep-all modes) and every row of the fused mode.  The kernel has
+// already read the row's parameters (c).  The kernel's own load of the
+// first slice is not passed in (it would stay live across both bodies): the
+// general body issues its slices itself.
 template <typename In, bool XD>
-__global__ __launch_bounds__(NT) void sample_kernel(
-    SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
-    const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
-    const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
-    const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
-  __shared__ __align__(16) typename KernelSmem<XD>::T U;
+__device__ __forceinline__ void chunk_general(const SampleArgs& A, typename KernelSmem<XD>::T& U, const RowCfg& c,
+                                              const uint32_t row, const uint32_t chunk) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
-
-  // Workgroup -> (row, chunk): grid (8 * C, ceil(rows / 8)); x = chunk * 8 +
-  // xcd.  Workgroups are dealt to the 8 XCDs round robin in linear order and
-  // 8 * C is a multiple of 8, so the C chunks of a row share an XCD and their
-  // exchange stays in one L2.
-  const uint32_t xcd = blockIdx.x & 7u;
-  const uint32_t chunk = blockIdx.x >> 3;
-  const uint32_t row = blockIdx.y * 8u + xcd;
-  if (row >= b.rows) return;
-
   const uint32_t V = b.vocab;
   stamp(A, row, chunk, 0);
   const uint32_t c0 = chunk * A.CH;
@@ -1727,19 +2092,13 @@ __global__ __launch_bounds__(NT) void sample_kernel(
 
   // ---- stream the chunk ---------------------------------------------------
   // Vector loads complete in issue order, so the issue order below is the
-  // order data becomes usable: the first two slices, then the row's history
-  // and bias lists and the chunk's mask words (loaded straight into LDS, no
-  // registers), then the rest of the chunk.  A quad starting below the chunk
-  // end lies inside the row stride (a multiple of 4); past the end, the
-  // chunk's first quad is re-read and ignored.
+  // order data becomes usable: the first slice, then
+  // the row's history and bias lists and the chunk's mask words (staged into
+  // LDS), then the rest of the chunk.  A quad starting below the chunk end
+  // lies inside the row stride (a multiple of 4); past the end, the chunk's
+  // first quad is re-read and ignored.
   typename Quad<In>::Raw raw[PER_MAX];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-    raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
-  }
-  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
-                            p_boff, row);
+  raw[0] = Quad<In>::load(src + (c0 + tid * 4u < c1 ? c0 + tid * 4u : c0));
   const uint32_t mode = chunk_mode(c, V);
   const double invT = c.greedy ? 0.0 : 1.0 / c.T;
   const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
@@ -1774,7 +2133,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     for (int r = 0; r < MCAP / NT; ++r) mreg[r] = mp[min((uint32_t)r * NT + tid, nmw - 1u)];
   }
 #pragma unroll
-  for (int i = 2; i < PER_MAX; ++i) {
+  for (int i = 1; i < PER_MAX; ++i) {
     const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
     raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
   }
@@ -2320,6 +2679,64 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     finish_row<In, true>(A, U.f, c, row, mode, rbase, invT);
     stamp(A, row, MAXC, 7);
   }
+}
+
+// ---------------------------------------------------------------------------
+// The chunk kernel.  Workgroup -> (row, chunk) as in the general body.  The
+// first slice goes out before the row's parameters arrive; rows the lean
+// body covers then issue the history ids and the rest of the stream and run
+// it, the others run the general body (which issues its own loads).
+template <typename In, bool XD>
+__global__ __launch_bounds__(NT) void sample_kernel(
+    SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
+    const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
+    const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
+    const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
+  __shared__ __align__(16) typename KernelSmem<XD>::T U;
+  const mxs_batch& b = A.b;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t xcd = blockIdx.x & 7u;
+  const uint32_t chunk = blockIdx.x >> 3;
+  const uint32_t row = blockIdx.y * 8u + xcd;
+  if (row >= b.rows) return;
+  const uint32_t V = b.vocab;
+  const uint32_t c0 = chunk * A.CH;
+  const uint32_t c1 = min(V, c0 + A.CH);
+  const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
+  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
+                            p_boff, row);
+  const uint32_t mode = chunk_mode(c, V);
+  if constexpr (!XD) {
+    const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
+    if (!c.err && A.masked == 0u && bn == 0u && hn <= (uint32_t)HCAP &&
+        (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
+      stamp(A, row, chunk, 0);
+      ChunkSmem& S = chunk_smem(U);
+      typename Quad<In>::Raw raw[PER_MAX];
+      uint32_t hreg[HCAP / NT];
+      if (hn) {
+        const uint32_t* hp = b.history_ids + c.hb;
+#pragma unroll
+        for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
+      }
+#pragma unroll
+      for (int i = 0; i < PER_MAX; ++i) {
+        const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+        raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
+      }
+      if (hn) {
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
+        else chunk_fast<In, M_MINP, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
+      } else {
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
+        else chunk_fast<In, M_MINP, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
+      }
+      return;
+    }
+  }
+  chunk_general<In, XD>(A, U, c, row, chunk);
 }
 
 // ---------------------------------------------------------------------------
