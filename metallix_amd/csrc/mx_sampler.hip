@@ -1225,6 +1225,313 @@ __device__ __forceinline__ bool finish_e(const FinCtx& X, FinSmem& F, uint32_t n
   return e_finish<FT>(X, F, ne, unc);
 }
 
+// ---------------------------------------------------------------------------
+// The row finish on one wave, for rows with at most WR * 64 candidates (lane
+// l holds candidates WR l .. WR l + WR - 1, so lane order is token-ID order).
+// Every step is a wave operation (DPP, ballots, LDS ops that complete in
+// order within the wave): no workgroup barrier between the candidate load
+// and the result.  The decisions and their certificates are e_finish's; a
+// row this path cannot certify returns false having written nothing.
+constexpr int WR = 8;
+
+// Lanes of one wave exchange data through LDS below: the hardware completes
+// one wave's LDS operations in order, and this compiler barrier keeps a
+// lane's own earlier store from being forwarded to its later load of a
+// location another lane has written since.
+__device__ __forceinline__ void wave_lds_sync() { __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// The k-th largest (1 <= k <= active count) of the wave's active keys (WR
+// per lane) and how many are larger: radix select on 8-bit digits from the
+// highest bit where the keys differ, over a 256-bin LDS histogram.
+__device__ __forceinline__ bool wave_kth(uint32_t* h, const uint32_t (&key)[WR], uint32_t act, uint32_t k,
+                                         uint32_t* kappa, uint32_t* above) {
+  const uint32_t ln = lane();
+  uint32_t kmin = NONE, kmax = 0;
+#pragma unroll
+  for (int r = 0; r < WR; ++r)
+    if ((act >> r) & 1u) { kmin = min(kmin, key[r]); kmax = max(kmax, key[r]); }
+  kmin = ~wave_max_u32(~kmin);
+  kmax = wave_max_u32(kmax);
+  if (kmin == kmax) { *kappa = kmax; *above = 0u; return true; }
+  int hb = 31 - (int)__builtin_clz(kmin ^ kmax);
+  uint32_t pmask = hb >= 31 ? 0u : ~((2u << hb) - 1u);
+  uint32_t prefix = kmax & pmask, need = k, abv = 0;
+  while (hb >= 0) {
+    const int sh = hb >= 7 ? hb - 7 : 0;
+    const uint32_t dm = (2u << (hb - sh)) - 1u;
+    *reinterpret_cast<uint4*>(&h[4u * ln]) = make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if (((act >> r) & 1u) && (key[r] & pmask) == prefix) atomicAdd(&h[(key[r] >> sh) & dm], 1u);
+    wave_lds_sync();
+    // lane l reads bins 255 - 4l .. 252 - 4l: lane order is descending digit order
+    const uint4 v = *reinterpret_cast<const uint4*>(&h[252u - 4u * ln]);
+    const uint32_t c4[4] = {v.w, v.z, v.y, v.x};
+    const uint32_t s = c4[0] + c4[1] + c4[2] + c4[3];
+    const uint32_t inc = wave_scan_u32(s);
+    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+    if (!reach) return false;   // fewer active keys than k: the caller's contract is broken
+    const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+    uint32_t run = inc - s, dig = 0u, bef = 0u;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (!found && run + c4[i] >= need) { found = true; dig = 255u - 4u * ln - (uint32_t)i; bef = run; }
+      run += c4[i];
+    }
+    dig = (uint32_t)__builtin_amdgcn_readlane((int)dig, (int)L);
+    bef = (uint32_t)__builtin_amdgcn_readlane((int)bef, (int)L);
+    need -= bef;
+    abv += bef;
+    prefix |= dig << sh;
+    pmask |= dm << sh;
+    hb = sh - 1;
+  }
+  *kappa = prefix;
+  *above = abv;
+  return true;
+}
+
+// Bitonic sort of one (key, position) pair per lane into descending key
+// order, ascending position among equal keys (sort_key order).
+__device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long v) {
+  const uint32_t ln = lane();
+#pragma unroll
+  for (uint32_t size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (uint32_t stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, (int)stride);
+      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), (int)stride);
+      const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+      // descending blocks when (lane & size) == 0; the lower lane keeps the larger
+      const bool desc = (ln & size) == 0u;
+      const bool lower = (ln & stride) == 0u;
+      const bool take_max = desc == lower;
+      v = take_max ? (o > v ? o : v) : (o < v ? o : v);
+    }
+  }
+  return v;
+}
+
+__device__ __forceinline__ bool wave_finish(const FinCtx& X, FinSmem& F) {
+  const RowCfg& c = X.c;
+  const uint32_t n = X.ncand, ln = lane(), j0 = ln * (uint32_t)WR;
+  if (n == 0u) return false;
+  float lv[WR];
+  uint32_t key[WR];
+  uint32_t act = 0;
+  {
+    const float4 a0 = *reinterpret_cast<const float4*>(&F.cl[j0]);
+    const float4 a1 = *reinterpret_cast<const float4*>(&F.cl[j0 + 4u]);
+    lv[0] = a0.x; lv[1] = a0.y; lv[2] = a0.z; lv[3] = a0.w;
+    lv[4] = a1.x; lv[5] = a1.y; lv[6] = a1.z; lv[7] = a1.w;
+  }
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    const bool a = j0 + (uint32_t)r < n;
+    act |= a ? 1u << r : 0u;
+    key[r] = a ? okey(lv[r]) : 0u;
+  }
+
+  // ---- E: the top-k head, the exact min-p set, or every candidate --------
+  uint32_t inE = 0;
+  bool unc = false;
+  double s[WR];
+#pragma unroll
+  for (int r = 0; r < WR; ++r) s[r] = ((act >> r) & 1u) ? ((double)lv[r] - X.M) / c.T : 0.0;
+  if (X.k_path) {
+    if (c.k > n) return false;
+    uint32_t kappa, above;
+    if (!wave_kth(F.u.f.cnt, key, act, c.k, &kappa, &above)) return false;
+    // the keys above kappa and the first (k - above) ties at kappa in token-ID order
+    const uint32_t need_t = c.k - above;
+    uint32_t tie = 0;
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      if (!((act >> r) & 1u)) continue;
+      if (key[r] > kappa) inE |= 1u << r;
+      if (key[r] == kappa) tie |= 1u << r;
+    }
+    const uint32_t tc = (uint32_t)__builtin_popcount(tie);
+    uint32_t t = wave_scan_u32(tc) - tc;
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if ((tie >> r) & 1u) { if (t < need_t) inE |= 1u << r; ++t; }
+  } else if (X.mode == M_MINP) {
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      if (!((act >> r) & 1u)) continue;
+      if (s[r] >= X.L) inE |= 1u << r;
+      if (fabs(s[r] - X.L) < X.Lclose) unc = true;
+    }
+  } else {
+    inE = act;
+  }
+
+  // ---- weights, the min-p subset P and the sums ---------------------------
+  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
+  double w[WR];
+  uint32_t inP = 0, ne = 0, np = 0;
+  double esum = 0.0, psum = 0.0;
+  unsigned long long wmin = ~0ull;   // smallest weight (non-negative doubles order as u64)
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    w[r] = 0.0;
+    if (!((inE >> r) & 1u)) continue;
+    w[r] = exp_neg_t(s[r], X.etab, X.etab + 64);
+    esum += w[r];
+    ++ne;
+    const unsigned long long bits = __builtin_bit_cast(unsigned long long, w[r]);
+    wmin = bits < wmin ? bits : wmin;
+    bool p = true;
+    if (apply_minp) {
+      p = s[r] >= X.L;
+      if (fabs(s[r] - X.L) < X.Lclose) unc = true;
+    }
+    if (p) { inP |= 1u << r; psum += w[r]; ++np; }
+  }
+  esum = wave_sum_f64(esum);
+  psum = wave_sum_f64(psum);
+  const uint32_t cnts = wave_sum_u32(ne | (np << 16));
+  ne = cnts & 0xffffu;
+  np = cnts >> 16;
+  unc = __builtin_amdgcn_ballot_w64(unc) != 0ull;
+  if (ne == 0u) return false;
+
+  // ---- the nucleus cut ------------------------------------------------------
+  double total = X.total, total_err = X.total_err;
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
+  bool theta_set = false;
+  double theta = 0.0, theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      // the running sum may stall before reaching the total: the general path replays it
+      const double wm = __builtin_bit_cast(double, ~wave_max_u64(~wmin));
+      if (!(wm > 2.3e-16 * esum)) return false;
+    } else {
+      theta_set = true;
+      theta = c.top_p * esum;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
+    }
+  } else if (c.top_p < 1.0) {
+    theta_set = true;
+    theta = c.top_p * total;
+    theta_err = c.top_p * total_err + U * theta;
+  }
+  uint32_t kept = inP;
+  if (theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) {
+    // The nucleus can end inside P: sort P (at most 64 members, one per
+    // lane) by (key desc, token ID asc) and walk the prefix sums.
+    if (np > 64u) return false;
+    const uint32_t pc = (uint32_t)__builtin_popcount(inP);
+    uint32_t at = wave_scan_u32(pc) - pc;
+    unsigned long long* mk = F.u.f.mass;   // sort keys (key << 32 | ~position), slot by P rank
+    double* mw = reinterpret_cast<double*>(F.u.f.mw);
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if ((inP >> r) & 1u) {
+        mk[at] = ((unsigned long long)key[r] << 32) | (unsigned long long)(~(j0 + (uint32_t)r));
+        mw[at] = w[r];
+        ++at;
+      }
+    wave_lds_sync();
+    const bool mine = ln < np;
+    const unsigned long long sk = wave_sort_desc(mine ? mk[ln] : 0ull);
+    const uint32_t pos = ~(uint32_t)sk;   // candidate index of this lane's sorted member
+    // the member's weight, fetched by its P rank: P ranks follow candidate order
+    uint32_t wr = 0;
+    if (mine) {
+      // rank of `pos` in P = number of P members before it in candidate order;
+      // search the rank table written above
+      for (uint32_t i = 0; i < np; ++i) wr += (~(uint32_t)mk[i]) < pos ? 1u : 0u;
+    }
+    const double wv = mine ? mw[wr] : 0.0;
+    const double cum = wave_scan_f64(wv);   // inclusive, in sorted order
+    const double prev = cum - wv;
+    // the reference stops at the first member whose running sum reaches theta
+    const double e_i = sum_bound(cum, ln + 1u, 8.0), e_p = sum_bound(prev, ln + 1u, 8.0);
+    const bool reach = mine && cum >= theta;
+    const uint64_t rb = __builtin_amdgcn_ballot_w64(reach);
+    if (!rb) return false;   // the bound allowed a crossing the sums do not show: replay
+    const uint32_t istar = (uint32_t)__builtin_ctzll(rb);
+    const bool cert_i = cum - e_i >= theta + theta_err;
+    const bool cert_p = ln == 0u || prev + e_p < theta - theta_err;
+    if (!__builtin_amdgcn_readlane((int)(cert_i && cert_p), (int)istar)) return false;
+    // kept = the sorted members 0 .. istar: flag them by candidate index
+    uint8_t* kf = F.kflag;
+#pragma unroll
+    for (int r = 0; r < WR; ++r) kf[j0 + (uint32_t)r] = 0u;
+    wave_lds_sync();
+    if (mine && ln <= istar) kf[pos] = 1u;
+    wave_lds_sync();
+    kept = 0;
+#pragma unroll
+    for (int r = 0; r < WR; ++r) kept |= kf[j0 + (uint32_t)r] ? 1u << r : 0u;
+  }
+
+  // ---- overflow check and the inverse-CDF draw in token-ID order ----------
+  double kpart = 0.0;
+  uint32_t kn = 0;
+  bool bad = false;
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    if (!((kept >> r) & 1u)) continue;
+    kpart += w[r];
+    ++kn;
+    if (!isfinite(s[r])) bad = true;
+  }
+  const uint32_t nkept = wave_sum_u32(kn);
+  if (__builtin_amdgcn_ballot_w64(bad)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
+  const double kinc = wave_scan_f64(kpart);
+  const double S = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, kinc), 63));
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  double cum = kinc - kpart;
+  uint32_t found = NONE, last = NONE;
+  bool fnear = false;
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    if (!((kept >> r) & 1u)) continue;
+    const double prev = cum;
+    cum += w[r];
+    if (w[r] > 0.0) {
+      last = j0 + (uint32_t)r;
+      if (found == NONE && target < cum && !(target < prev)) {
+        found = j0 + (uint32_t)r;
+        fnear = fabs(target - prev) <= derr || fabs(cum - target) <= derr;
+      }
+    }
+  }
+  bool uncert = unc;
+  uint32_t pick = NONE;
+  const uint64_t fb = __builtin_amdgcn_ballot_w64(found != NONE);
+  if (fb) {
+    const uint32_t L = (uint32_t)__builtin_ctzll(fb);
+    pick = (uint32_t)__builtin_amdgcn_readlane((int)found, (int)L);
+    uncert = uncert || __builtin_amdgcn_readlane((int)fnear, (int)L) != 0;
+  } else {
+    // rounding left the variate past the accumulated mass: the last positive kept token
+    const uint64_t lb = __builtin_amdgcn_ballot_w64(last != NONE);
+    if (lb) pick = (uint32_t)__builtin_amdgcn_readlane((int)last, (int)(63 - __builtin_clzll(lb)));
+    uncert = true;
+  }
+  if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
+  const double shifted = ((double)F.cl[pick] - X.M) / c.T;
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.cid[pick], shifted - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = ln; q < X.nwords; q += 64u) X.kbits[q] = 0u;
+    __builtin_amdgcn_s_waitcnt(0);   // the zeroing lands before the atomics (one wave, in program order)
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      if (!((kept >> r) & 1u)) continue;
+      const uint32_t tok = F.cid[j0 + (uint32_t)r];
+      atomicOr(&X.kbits[tok >> 5], 1u << (tok & 31u));
+    }
+  }
+  return true;
+}
+
 __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
   const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
@@ -1582,6 +1889,19 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
   X.kappa = 0;
   X.id_tie = NONE;
+  if (mode != M_KEEPALL && X.lds_c && ncand <= (uint32_t)(WR * 64)) {
+    // at most WR * 64 candidates: one wave finishes the row
+    if (wave() == 0) {
+      const bool ok = wave_finish(X, F);
+      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
+    }
+    lds_barrier();
+    if (F.s_u[15]) {
+      stamp(A, row, MAXC, 2);
+      return;
+    }
+    lds_barrier();   // wave 0's LDS scratch is reused below
+  }
   if (mode != M_KEEPALL && finish_fast(X, F)) {
     stamp(A, row, MAXC, 2);
     return;
@@ -1722,11 +2042,36 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 template <typename In, uint32_t MODE, bool HIST>
 __device__ __forceinline__ void chunk_fast(const SampleArgs& A, ChunkSmem& S, const RowCfg& c, const uint32_t row,
                                            const uint32_t chunk, const uint32_t c0, const uint32_t c1,
-                                           const typename Quad<In>::Raw (&raw)[PER_MAX],
-                                           const uint32_t (&hreg)[HCAP / NT], const uint32_t hn) {
+                                           const uint32_t hn) {
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
+  // The loads are issued here, per instantiation, so that no stream register
+  // is live across the kernel's dispatch between the bodies (values live
+  // across it made the register allocator spill, and a spill reload, being a
+  // vector memory instruction, waits for every earlier load of the wave: the
+  // whole stream).  The history ids go out first: the count table needs them
+  // before pass 1.
+  // (identical loads in every instantiation would otherwise be hoisted above
+  // the dispatch as common code; an opaque use of the chunk offset keeps them
+  // inside this body)
+  uint32_t c0k = c0;
+  __asm__ volatile("" : "+s"(c0k));
+  uint32_t hreg[HCAP / NT];
+  if constexpr (HIST) {
+    const uint32_t* hp = b.history_ids + c.hb;
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
+  }
+  typename Quad<In>::Raw raw[PER_MAX];
+  {
+    const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i) {
+      const uint32_t e0 = c0k + (uint32_t)i * SLICE + tid * 4u;
+      raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0k));
+    }
+  }
   const uint32_t clen = c1 - c0;
   const double invT = MODE == M_GREEDY ? 0.0 : 1.0 / c.T;
   uint32_t my_flags = 0;
@@ -2694,7 +3039,6 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
   __shared__ __align__(16) typename KernelSmem<XD>::T U;
   const mxs_batch& b = A.b;
-  const uint32_t tid = threadIdx.x;
   const uint32_t xcd = blockIdx.x & 7u;
   const uint32_t chunk = blockIdx.x >> 3;
   const uint32_t row = blockIdx.y * 8u + xcd;
@@ -2702,7 +3046,6 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const uint32_t V = b.vocab;
   const uint32_t c0 = chunk * A.CH;
   const uint32_t c1 = min(V, c0 + A.CH);
-  const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
   const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
                             p_boff, row);
   const uint32_t mode = chunk_mode(c, V);
@@ -2712,26 +3055,14 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
       ChunkSmem& S = chunk_smem(U);
-      typename Quad<In>::Raw raw[PER_MAX];
-      uint32_t hreg[HCAP / NT];
       if (hn) {
-        const uint32_t* hp = b.history_ids + c.hb;
-#pragma unroll
-        for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
-      }
-#pragma unroll
-      for (int i = 0; i < PER_MAX; ++i) {
-        const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-        raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
-      }
-      if (hn) {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
-        else chunk_fast<In, M_MINP, true>(A, S, c, row, chunk, c0, c1, raw, hreg, hn);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, S, c, row, chunk, c0, c1, hn);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, S, c, row, chunk, c0, c1, hn);
+        else chunk_fast<In, M_MINP, true>(A, S, c, row, chunk, c0, c1, hn);
       } else {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
-        else chunk_fast<In, M_MINP, false>(A, S, c, row, chunk, c0, c1, raw, hreg, 0u);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, S, c, row, chunk, c0, c1, 0u);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, S, c, row, chunk, c0, c1, 0u);
+        else chunk_fast<In, M_MINP, false>(A, S, c, row, chunk, c0, c1, 0u);
       }
       return;
     }
