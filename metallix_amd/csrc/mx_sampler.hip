@@ -2039,10 +2039,11 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 //   - each wave publishes its maximum to the row's exchange word as soon as
 //     its pass 1 ends, so the min-p threshold sees the other chunks' maxima
 //     as early as possible.
-template <typename In, uint32_t MODE, bool HIST>
-__device__ __forceinline__ void chunk_fast(const SampleArgs& A, ChunkSmem& S, const RowCfg& c, const uint32_t row,
-                                           const uint32_t chunk, const uint32_t c0, const uint32_t c1,
-                                           const uint32_t hn) {
+template <typename In, uint32_t MODE, bool HIST, bool XD>
+__device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelSmem<XD>::T& U, const RowCfg& c,
+                                           const uint32_t row, const uint32_t chunk, const uint32_t c0,
+                                           const uint32_t c1, const uint32_t hn) {
+  ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
@@ -2387,8 +2388,8 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, ChunkSmem& S, co
         for (int e = 0; e < 4; ++e) {
           if (em[e]) {
             const uint64_t pos = cbase + off;
-            A.w.cand_l[pos] = lv[i][e];
-            A.w.cand_id[pos] = e0 + (uint32_t)e;
+            xput<XD>(&A.w.cand_l[pos], lv[i][e]);
+            xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
             ++off;
           }
         }
@@ -2403,18 +2404,38 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, ChunkSmem& S, co
     if constexpr (MODE == M_GREEDY)
       for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
     ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
-    st.maxkey = nleg ? maxkey : 0u;
-    st.gbest_id = garg ? ~(uint32_t)garg : NONE;
-    st.gbest_val = garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f;
-    st.nlegal = nleg;
-    st.ncand = ncand;
-    st.flags = cflags;
-    st.mass = mass;
-    st.mass_err = mass_err;
-    st.minkey = 0u;
-    st.thr = thr;
+    xput<XD>(&st.maxkey, nleg ? maxkey : 0u);
+    xput<XD>(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
+    xput<XD>(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
+    xput<XD>(&st.nlegal, nleg);
+    xput<XD>(&st.ncand, ncand);
+    xput<XD>(&st.flags, cflags);
+    xput<XD>(&st.mass, mass);
+    xput<XD>(&st.mass_err, mass_err);
+    xput<XD>(&st.minkey, 0u);
+    xput<XD>(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
+  if constexpr (XD) {
+    // The row's last chunk to finish becomes its finisher: the barrier waits
+    // for every wave's device-scope stores, then one relaxed device-scope
+    // count per chunk.
+    __syncthreads();
+    uint32_t last = 0;
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = prev + 1u == A.C ? 1u : 0u;
+      if (last) st_dev(&A.w.ctr[row], 0u);
+      S.xkey = last;
+    }
+    lds_barrier();
+    last = S.xkey;
+    lds_barrier();   // the finisher's LDS overlays the chunk's
+    if (!last) return;
+    stamp(A, row, MAXC, 0);
+    finish_row<In, true>(A, U.f, c, row, MODE, (uint64_t)row * V, invT);
+    stamp(A, row, MAXC, 7);
+  }
 }
 
 // The general chunk body: every row the lean body does not cover (grammar
@@ -3049,20 +3070,19 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
                             p_boff, row);
   const uint32_t mode = chunk_mode(c, V);
-  if constexpr (!XD) {
+  {
     const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
     if (!c.err && A.masked == 0u && bn == 0u && hn <= (uint32_t)HCAP &&
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
-      ChunkSmem& S = chunk_smem(U);
       if (hn) {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, S, c, row, chunk, c0, c1, hn);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, S, c, row, chunk, c0, c1, hn);
-        else chunk_fast<In, M_MINP, true>(A, S, c, row, chunk, c0, c1, hn);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true, XD>(A, U, c, row, chunk, c0, c1, hn);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true, XD>(A, U, c, row, chunk, c0, c1, hn);
+        else chunk_fast<In, M_MINP, true, XD>(A, U, c, row, chunk, c0, c1, hn);
       } else {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, S, c, row, chunk, c0, c1, 0u);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, S, c, row, chunk, c0, c1, 0u);
-        else chunk_fast<In, M_MINP, false>(A, S, c, row, chunk, c0, c1, 0u);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
+        else chunk_fast<In, M_MINP, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
       }
       return;
     }
