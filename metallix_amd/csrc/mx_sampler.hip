@@ -2110,10 +2110,11 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
   uint32_t gi = NONE;
   uint64_t nf = 0;
   // online mass: acc = sum of 2^((l - mrun) c2) over this thread's tokens so
-  // far (f64 across slices, f32 within a slice), eacc = the same weights
-  // times |(l - mrun) c2| (for the error bound); mrun is the running maximum
+  // far, eacc = the same weights times |(l - mrun) c2| (for the error
+  // bound); mrun is the running maximum.  f32 throughout: one fused rescale
+  // and add per slice.
   float mrun = -FLT_MAX;
-  double acc = 0.0, eacc = 0.0;
+  float acc = 0.0f, eacc = 0.0f;
 #pragma unroll
   for (int i = 0; i < PER_MAX; ++i) {
     qm[i] = -INFINITY;
@@ -2173,19 +2174,29 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
           const float ys = (mrun - mnew) * c2;                 // <= 0
           const float s = __builtin_amdgcn_exp2f(ys);
           float sw = 0.0f, ew = 0.0f;
+          if (full) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool inr = (rb >> e) & 1u;
-            const float y = (x[e] - mnew) * c2;
-            const float w = inr ? __builtin_amdgcn_exp2f(y) : 0.0f;
-            sw += w;
-            ew = inr ? __builtin_fmaf(w, -y, ew) : ew;
+            for (int e = 0; e < 4; ++e) {
+              const float y = (x[e] - mnew) * c2;
+              const float w = __builtin_amdgcn_exp2f(y);
+              sw += w;
+              ew = __builtin_fmaf(w, -y, ew);
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const bool inr = (rb >> e) & 1u;
+              const float y = (x[e] - mnew) * c2;
+              const float w = inr ? __builtin_amdgcn_exp2f(y) : 0.0f;
+              sw += w;
+              ew = inr ? __builtin_fmaf(w, -y, ew) : ew;
+            }
           }
           // rescale what is accumulated to the new running maximum (s = 1
           // when it did not move); a zero accumulator stays zero
-          const bool live = acc > 0.0;
-          eacc = live ? (eacc + acc * (double)(-ys)) * (double)s + (double)ew : (double)ew;
-          acc = live ? acc * (double)s + (double)sw : (double)sw;
+          const bool live = acc > 0.0f;
+          eacc = live ? __builtin_fmaf(__builtin_fmaf(acc, -ys, eacc), s, ew) : ew;
+          acc = live ? __builtin_fmaf(acc, s, sw) : sw;
           mrun = mnew;
         }
       }
@@ -2219,9 +2230,9 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
       const float wm = okey_value(kmax);
       const float ys = (mrun - wm) * c2;
       const float s = __builtin_amdgcn_exp2f(ys);
-      const bool live = acc > 0.0;
-      const double e1 = live ? (eacc + acc * (double)(-ys)) * (double)s : 0.0;
-      const double a1 = live ? acc * (double)s : 0.0;
+      const bool live = acc > 0.0f;
+      const double e1 = live ? ((double)eacc + (double)acc * (double)(-ys)) * (double)s : 0.0;
+      const double a1 = live ? (double)acc * (double)s : 0.0;
       w0s = wave_sum_f64(a1);
       w1s = wave_sum_f64(e1);
     }
@@ -2289,14 +2300,16 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
   } else if (MODE == M_MINP && row_ok) {
     // The largest chunk maximum of the row published by now is a lower
     // bound of the row maximum: any lower bound gives a superset of the
-    // min-p set, a tighter one fewer candidates.
+    // min-p set, a tighter one fewer candidates.  ln(min_p) in f32: its
+    // error (a few ulp of |ln min_p|, times T) is far inside the threshold's
+    // 1e-5 relative margin.
     emit = true;
     const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t xkey = maxkey;
     if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
     xkey = (uint32_t)__builtin_amdgcn_readfirstlane((int)xkey);
     const float mx = okey_value(xkey);
-    const double lim_d = (double)mx + c.T * log(c.min_p);
+    const double lim_d = (double)mx + c.T * (double)__logf((float)c.min_p);
     thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
   }
   uint32_t cnt_i[PER_MAX];
@@ -2326,24 +2339,28 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
   // waves' sums (lane w <-> wave w) in f64
   double mass = 0.0, mass_err = 0.0;
   if (do_mass && row_ok && wave() == 0) {
+    // lane w rescales wave w's sum from the wave maximum to the chunk
+    // maximum (one more f32 rescale step, counted in the bound)
     const uint32_t w = lane();
     double a = 0.0, e = 0.0;
     if (w < (uint32_t)NW) {
-      const double sc = exp_neg(((double)okey_value(S.wp[w].kmax) - md) * invT);
-      a = S.wp[w].m0 * sc;
-      e = S.wp[w].m1 * sc;
+      const float ys = (okey_value(S.wp[w].kmax) - m) * c2;   // <= 0
+      const double sc = (double)__builtin_amdgcn_exp2f(ys);
+      const double m0w = S.wp[w].m0;
+      a = m0w > 0.0 ? m0w * sc : 0.0;
+      e = m0w > 0.0 ? (S.wp[w].m1 + m0w * (double)(-ys)) * sc : 0.0;
     }
     const double S0 = wave_sum_f64(a), E0 = wave_sum_f64(e);
     mass = S0;
-    // |mass - sum of exact weights| <= 1.01 (2^-22 S (per + 2) + 3 2^-24 S)
-    // for the f32 exp2 of each weight and of each of at most per + 1
-    // rescale factors (2 ulp each) and the 4-term f32 slice sums,
-    // + 1.01 ln2 3 2^-24 sum w |y| for the rounding of the exponents (three
-    // f32 roundings each, relative; a term's exponent and the rescale
-    // exponents applied to it telescope to its distance from the wave
-    // maximum), + n 2^-120 for weights and factors below 2^-126, + 2^-40 S
-    // for the f64 accumulation and the f64 rescale to the chunk maximum.
-    mass_err = 1.01 * (0x1p-22 * S0 * (double)(A.per + 2u) + 3.0 * 0x1p-24 * S0 +
+    // |mass - sum of exact weights| <= 1.01 (2^-22 S (per + 3) +
+    // (per + 5) 2^-24 S) for the f32 exp2 of each weight and of each of at
+    // most per + 2 rescale factors (2 ulp each), the 4-term f32 slice sums
+    // and the per fused f32 rescale-and-adds, + 1.01 ln2 3 2^-24 sum w |y|
+    // for the rounding of the exponents (three f32 roundings each,
+    // relative; a term's exponent and the rescale exponents applied to it
+    // telescope to its distance from the chunk maximum), + n 2^-120 for
+    // weights and factors below 2^-126, + 2^-40 S for the f64 sums.
+    mass_err = 1.01 * (0x1p-22 * S0 * (double)(A.per + 3u) + (double)(A.per + 5u) * 0x1p-24 * S0 +
                        0.6931471805599453 * 3.0001 * 0x1p-24 * E0) +
                (double)nleg * 0x1p-120 + 0x1p-40 * S0;
   }
@@ -2364,6 +2381,12 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     ncand = s0 + s1 + s2;
     const uint32_t x0 = i0 - v0, x1 = i1 - v1 + s0, x2 = i2 - v2 + s0 + s1;
     const uint64_t cbase = (uint64_t)row * V + c0;
+    // Candidates are staged in LDS (the count table is dead by now) and then
+    // copied out with coalesced stores: scattered per-element global stores
+    // cost an address-unit pass per store instruction, tens per wave.
+    const bool staged = ncand <= (uint32_t)(CHUNK_MAX / 4);   // uniform
+    float* stl = reinterpret_cast<float*>(S.t.ct);
+    uint32_t* sti = S.t.ct + CHUNK_MAX / 4;
 #pragma unroll
     for (int i = 0; i < PER_MAX; ++i) {
       if (i < (int)A.per && cnt_i[i]) {
@@ -2387,12 +2410,24 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (em[e]) {
-            const uint64_t pos = cbase + off;
-            xput<XD>(&A.w.cand_l[pos], lv[i][e]);
-            xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+            if (staged) {
+              stl[off] = lv[i][e];
+              sti[off] = e0 + (uint32_t)e;
+            } else {
+              const uint64_t pos = cbase + off;
+              xput<XD>(&A.w.cand_l[pos], lv[i][e]);
+              xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+            }
             ++off;
           }
         }
+      }
+    }
+    if (staged) {
+      lds_barrier();
+      for (uint32_t j = tid; j < ncand; j += NT) {
+        xput<XD>(&A.w.cand_l[cbase + j], stl[j]);
+        xput<XD>(&A.w.cand_id[cbase + j], sti[j]);
       }
     }
   }
