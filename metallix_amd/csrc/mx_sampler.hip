@@ -138,6 +138,14 @@ constexpr int FT = 1024;
 constexpr int FW = FT / 64;
 static_assert(FT == NT, "the block helpers assume NT-thread blocks");
 constexpr uint32_t BPT = NB / FT;          // radix bins per finisher thread
+// The selection finisher keeps SR candidate slots per chunk and thread in
+// registers, histograms them into NBS value bins, and finishes rows whose
+// min-p subset P has at most PCAP members (one per lane of a wave).
+constexpr int SR = 6;
+constexpr int NBS = 2048;
+constexpr int PCAP = 64;
+constexpr int PMAX = 1024;
+static_assert(NBS == 32 * 64, "a lane scans 32 bins");
 struct alignas(16) FinSmem {
   float cl[CCAP];                      // candidates cached in LDS, token-ID order
   uint32_t cid[CCAP];
@@ -158,15 +166,26 @@ struct alignas(16) FinSmem {
       uint32_t mpos[FT];
       unsigned long long mw[FT];
     } f;
+    struct {                           // the selection finisher (finish_sel)
+      alignas(16) uint32_t cnt[NBS];   // value histogram of the candidates
+      alignas(16) unsigned long long mass[NBS];   // fixed-point mass histogram of P
+      uint32_t mk[PCAP], mi[PCAP];     // crossing-bin members: key, token ID, fixed-point mass
+      unsigned long long mw[PCAP];
+      double sw[PCAP];                 // weights in (key desc, ID asc) rank order
+      uint32_t pk[PMAX], pid[PMAX];    // P in token-ID order: key, token ID, logit
+      float pl[PMAX];
+    } s;
   } u;
   uint32_t sc_u[2][FW];                // single-barrier scan slots
   double sc_d[2][FW];
   unsigned long long sc_l[2][FW];
   unsigned long long s_l[4];
   struct {                             // the row header from the chunk statistics
-    double mass, mass_err;             // sum of chunk masses scaled to the row maximum, and its error bound
+    double mass, mass_err;             // sum of chunk masses scaled to the row maximum, and the row total's error bound
     double L;                          // ln(min_p) (-inf for min_p = 0)
     uint32_t flags, nlegal, Mkey, bi, ncand;
+    uint32_t qmax;                     // the largest candidate count of a chunk
+    float lo;                          // no candidate is below it (the chunks' smallest threshold)
   } hdr;
   double etab[128];                    // exp_neg's tables: 2^(j/64) (high, low parts)
   double rd[FW][2];                    // multi-value reduction
@@ -230,6 +249,11 @@ __device__ __forceinline__ RowCfg load_cfg(const double* __restrict__ temperatur
   c.he = hoff[row + 1];
   c.bb = boff[row];
   c.be = boff[row + 1];
+  // every load goes out before the first wait: the checks below would
+  // otherwise pull the loads they guard into their branches, one round
+  // trip each
+  __asm__ volatile("" ::"s"(c.T), "s"(c.top_p), "s"(c.min_p), "s"(c.u), "s"(c.k), "s"(c.rep), "s"(c.pres),
+                   "s"(c.freq), "s"(c.hb), "s"(c.he), "s"(c.bb), "s"(c.be));
   c.err = 0;
   c.greedy = c.T == 0.0;
   if (!(c.T >= 0.0) || !isfinite(c.T)) c.err = MXS_ROW_INVALID_TEMPERATURE;
@@ -1608,72 +1632,717 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
 }
 
 // ---------------------------------------------------------------------------
+// The finisher's candidate slots.  For C <= FW chunks, wave w serves chunk
+// w mod C as its (w div C)-th wave, so a row's chunks spread over the four
+// SIMDs (wave w runs on SIMD w mod 4) and lane order within a wave is
+// candidate order; for C > FW, thread t serves chunk t div (FT / C).
+// Thread (q, j) holds slots SR j .. SR j + SR - 1 of chunk q, so every
+// chunk's first slot_cov(C) slots are in registers.
+__device__ __forceinline__ void slot_map(uint32_t C, uint32_t* q, uint32_t* j) {
+  const uint32_t tid = threadIdx.x;
+  if (C <= (uint32_t)FW) {
+    const uint32_t w = tid >> 6;
+    *q = w % C;
+    *j = (w / C) * 64u + (tid & 63u);
+  } else {
+    const uint32_t spc = FT / C;
+    *q = tid / spc;
+    *j = tid - *q * spc;
+  }
+}
+__device__ __forceinline__ uint32_t slot_cov(uint32_t C) {
+  return C <= (uint32_t)FW ? (uint32_t)SR * 64u * ((uint32_t)FW / C) : (uint32_t)SR * ((uint32_t)FT / C);
+}
+
+// The finisher's first loads, issued before anything waits: the chunk
+// statistics (waves 0 and 1, lane q <-> chunk q) and the register slots
+// (slot_map).  Slots past a chunk's count hold stale values and are
+// ignored once the statistics are in.
+struct FinLoads {
+  float l[SR];
+  uint32_t id[SR];
+  ChunkStat v;
+};
+static_assert(SR % 2 == 0, "slot pairs");
+template <bool XD>
+__device__ __forceinline__ void fin_issue(const SampleArgs& A, uint32_t row, FinLoads& P) {
+  const uint32_t C = A.C, V = A.b.vocab, CH = A.CH;
+  uint32_t sq, sj;
+  slot_map(C, &sq, &sj);
+  // the row's region ends at V, the chunk's at CH: slots below both are in bounds
+  const uint32_t lim = sq < C ? min(CH, V - sq * CH) : 0u;
+  const uint64_t base = (uint64_t)row * V + (uint64_t)sq * CH + (uint64_t)sj * SR;
+  // an even vocabulary makes base even (CH and SR are): 8-byte pairs
+  const bool pairs = (V & 1u) == 0u;
+#pragma unroll
+  for (int u = 0; u < SR; u += 2) {
+    const uint32_t slot = sj * (uint32_t)SR + (uint32_t)u;
+    float2 lv = make_float2(0.0f, 0.0f);
+    uint2 iv = make_uint2(0u, 0u);
+    if (pairs && slot + 1u < lim) {
+      lv = xget<XD>(reinterpret_cast<const float2*>(&A.w.cand_l[base + u]));
+      iv = xget<XD>(reinterpret_cast<const uint2*>(&A.w.cand_id[base + u]));
+    } else {
+      if (slot < lim) {
+        lv.x = xget<XD>(&A.w.cand_l[base + u]);
+        iv.x = xget<XD>(&A.w.cand_id[base + u]);
+      }
+      if (slot + 1u < lim) {
+        lv.y = xget<XD>(&A.w.cand_l[base + u + 1]);
+        iv.y = xget<XD>(&A.w.cand_id[base + u + 1]);
+      }
+    }
+    P.l[u] = lv.x; P.l[u + 1] = lv.y;
+    P.id[u] = iv.x; P.id[u + 1] = iv.y;
+  }
+  ChunkStat& v = P.v;
+  v.maxkey = 0u; v.gbest_id = NONE; v.gbest_val = 0.0f; v.nlegal = 0u; v.ncand = 0u; v.flags = 0u;
+  v.minkey = NONE; v.thr = 0.0f; v.mass = 0.0; v.mass_err = 0.0;
+  if (wave() < 2u && lane() < C) {   // wave 0: the header; wave 1: the chunk masses
+    const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + lane()];
+    v.maxkey = xget<XD>(&st->maxkey);
+    v.gbest_id = xget<XD>(&st->gbest_id);
+    v.gbest_val = xget<XD>(&st->gbest_val);
+    v.nlegal = xget<XD>(&st->nlegal);
+    v.ncand = xget<XD>(&st->ncand);
+    v.flags = xget<XD>(&st->flags);
+    v.mass = xget<XD>(&st->mass);
+    v.mass_err = xget<XD>(&st->mass_err);
+    v.minkey = xget<XD>(&st->minkey);
+    v.thr = xget<XD>(&st->thr);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The selection finisher: top-k and min-p rows of at most FW chunks whose
+// candidates all sit in the register slots (slot_map: lane order within a
+// wave is candidate order; waves order by (chunk, rank in the chunk)).  The
+// decisions and their certificates
+// are wave_finish's and e_finish's; the work is spread differently:
+//   - E's top-k bound comes from a value histogram of the register-held
+//     candidates: bin (M - l) (NBS - 1) / (M - lo) is non-increasing in l
+//     (each f32 step is monotone), so the k-th largest candidate lies in the
+//     first bin where the running count from bin 0 reaches k; the crossing
+//     bin's members (at most PCAP) are ranked by (key desc, ID asc);
+//   - E's mass (which only sets theta = top_p * mass) is summed from f32
+//     weights 2^((l - M) log2(e) / T) with an error bound, like the chunk
+//     masses; only P's members (E with the min-p test, decided in f32 away
+//     from the threshold and in f64 near it) get f64 weights;
+//   - P is compacted in token-ID order by a block scan; P of at most 64
+//     members is finished by one wave (lane = P member), larger P (at most
+//     PMAX) by the workgroup: the nucleus cut from a fixed-point mass
+//     histogram on the same value bins, the draw from a block scan.
+// Returns false, having written nothing, for the general paths; every
+// early return is taken by all waves alike (it depends only on values
+// every wave computes identically, or on LDS read after a barrier).
+struct SelSums {
+  double esum, esum_err;   // E's mass (from f32 weights) and its error bound
+  double wlo;              // a lower bound of E's smallest weight
+  uint32_t ne, np;
+  bool unc;
+};
+
+// The value bin of logit l (non-increasing in l; l <= M).
+__device__ __forceinline__ uint32_t sel_bin(float l, float Mf, float sc) {
+  const float d = (Mf - l) * sc;
+  return d < (float)(NBS - 1) ? (uint32_t)d : (uint32_t)(NBS - 1);
+}
+
+// theta (the nucleus mass) and its error; false when the general path must
+// replay the row
+__device__ __forceinline__ bool sel_theta(const FinCtx& X, const SelSums& Q, bool* set, double* theta,
+                                          double* theta_err) {
+  const RowCfg& c = X.c;
+  *set = false;
+  *theta = 0.0;
+  *theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      // the running sum may stall before reaching the total
+      if (!(Q.wlo > 2.3e-16 * (Q.esum + Q.esum_err))) return false;
+    } else {
+      *set = true;
+      *theta = c.top_p * Q.esum;
+      *theta_err = c.top_p * Q.esum_err + U * *theta;
+    }
+  } else if (c.top_p < 1.0) {
+    const double total = X.have_total ? X.total : Q.esum;
+    const double total_err = X.have_total ? X.total_err : Q.esum_err;
+    *set = true;
+    *theta = c.top_p * total;
+    *theta_err = c.top_p * total_err + U * *theta;
+  }
+  return true;
+}
+
+// The first position (0-based) where an inclusive prefix of the wave's
+// lane-ordered counts reaches `need`, scanning 32-entry groups: lane i holds
+// the total of group i (hs) and its inclusive scan (inc); the crossing
+// group's 32 entries are then read lane-parallel from `h`.  Returns NONE
+// when the total stays below need; *before receives the count ahead of the
+// position.
+__device__ __forceinline__ uint32_t wave_cross32(const uint32_t* h, uint32_t hs, uint32_t inc, uint32_t need,
+                                                 uint32_t* before) {
+  const uint32_t ln = lane();
+  const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+  if (!reach) return NONE;
+  const uint32_t g = (uint32_t)__builtin_ctzll(reach);
+  const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - hs), (int)g);
+  const uint32_t v = ln < 32u ? h[32u * g + ln] : 0u;
+  const uint32_t vi = base + wave_scan_u32(v);
+  const uint64_t r2 = __builtin_amdgcn_ballot_w64(ln < 32u && vi >= need);
+  const uint32_t i = (uint32_t)__builtin_ctzll(r2);
+  *before = (uint32_t)__builtin_amdgcn_readlane((int)(vi - v), (int)i);
+  return 32u * g + i;
+}
+
+// The draw over the kept members of P in token-ID order (one wave: lane =
+// member); writes the result.
+__device__ __forceinline__ void sel_draw_wave(const FinCtx& X, bool kept, double w, double s, uint32_t id, bool unc) {
+  const RowCfg& c = X.c;
+  const uint32_t nkept = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(kept));
+  if (__builtin_amdgcn_ballot_w64(kept && !isfinite(s))) {
+    write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+    return;
+  }
+  const double dw = kept ? w : 0.0;
+  const double inc = wave_scan_f64(dw);
+  const double S = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, inc), 63));
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  const double before = inc - dw;
+  const bool hit = dw > 0.0 && target < inc && !(target < before);
+  const bool near = fabs(target - before) <= derr || fabs(inc - target) <= derr;
+  bool uncert = unc;
+  uint32_t pick = NONE;
+  const uint64_t fb = __builtin_amdgcn_ballot_w64(hit);
+  if (fb) {
+    pick = (uint32_t)__builtin_ctzll(fb);
+    uncert = uncert || __builtin_amdgcn_readlane((int)near, (int)pick) != 0;
+  } else {
+    // rounding left the variate past the accumulated mass: the last positive kept token
+    const uint64_t lb = __builtin_amdgcn_ballot_w64(dw > 0.0);
+    if (lb) pick = (uint32_t)(63 - __builtin_clzll(lb));
+    uncert = true;
+  }
+  if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+  const int32_t tok = __builtin_amdgcn_readlane((int)id, (int)pick);
+  const double sp = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, s), pick));
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, tok, sp - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = lane(); q < X.nwords; q += 64u) X.kbits[q] = 0u;
+    __builtin_amdgcn_s_waitcnt(0);   // the zeroing lands before the atomics (one wave, in program order)
+    if (kept) atomicOr(&X.kbits[id >> 5], 1u << (id & 31u));
+  }
+}
+
+// P of at most 64 members, on one wave: lane i holds P member i (ID order).
+__device__ __forceinline__ bool sel_small(const FinCtx& X, FinSmem& F, const SelSums& Q) {
+  const RowCfg& c = X.c;
+  const uint32_t ln = lane(), np = Q.np;
+  const bool mine = ln < np;
+  const uint32_t mk = mine ? F.u.s.pk[ln] : 0u, mi = mine ? F.u.s.pid[ln] : NONE;
+  const float ml = mine ? F.u.s.pl[ln] : 0.0f;
+  const double s = mine ? ((double)ml - X.M) / c.T : 0.0;
+  const double mw = mine ? exp_neg_t(s, X.etab, X.etab + 64) : 0.0;
+  const double psum = wave_sum_f64(mw);
+  bool theta_set;
+  double theta, theta_err;
+  if (!sel_theta(X, Q, &theta_set, &theta, &theta_err)) return false;
+  bool kept = mine;
+  if (theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) {
+    // The nucleus can end inside P: prefix sums in (key desc, ID asc)
+    // order; the reference stops at the first member whose running sum
+    // reaches theta.
+    uint32_t rk = 0;
+    for (uint32_t j = 0; j < np; ++j) {
+      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)j);
+      const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)mi, (int)j);
+      rk += (kj > mk || (kj == mk && ij < mi)) ? 1u : 0u;
+    }
+    double* sw = F.u.s.sw;
+    if (mine) sw[rk] = mw;
+    wave_lds_sync();
+    const double wv = mine ? sw[ln] : 0.0;
+    const double cum = wave_scan_f64(wv);   // inclusive, in rank order
+    const double prev = cum - wv;
+    const double e_i = sum_bound(cum, ln + 1u, 8.0), e_p = sum_bound(prev, ln + 1u, 8.0);
+    const uint64_t rb = __builtin_amdgcn_ballot_w64(mine && cum >= theta);
+    if (!rb) return false;   // the bound allowed a crossing the sums do not show: replay
+    const uint32_t istar = (uint32_t)__builtin_ctzll(rb);
+    const bool cert_i = cum - e_i >= theta + theta_err;
+    const bool cert_p = ln == 0u || prev + e_p < theta - theta_err;
+    if (!__builtin_amdgcn_readlane((int)(cert_i && cert_p), (int)istar)) return false;
+    kept = mine && rk <= istar;
+  }
+  sel_draw_wave(X, kept, mw, s, mi, Q.unc);
+  return true;
+}
+
+// P of more than 64 (at most PMAX = FT) members, on the workgroup: thread i
+// holds P member i (ID order).
+__device__ __forceinline__ bool sel_large(const FinCtx& X, FinSmem& F, const SelSums& Q) {
+  const RowCfg& c = X.c;
+  const uint32_t tid = threadIdx.x, np = Q.np;
+  const bool mine = tid < np;
+  const uint32_t mk = mine ? F.u.s.pk[tid] : 0u, mi = mine ? F.u.s.pid[tid] : NONE;
+  const float ml = mine ? F.u.s.pl[tid] : 0.0f;
+  const double s = mine ? ((double)ml - X.M) / c.T : 0.0;
+  const double mw = mine ? exp_neg_t(s, X.etab, X.etab + 64) : 0.0;
+  double* part = reinterpret_cast<double*>(F.eidx);
+  part[tid] = mw;
+  lds_barrier();
+  // wave 0: P's mass, theta and whether the nucleus can end inside P
+  if (wave() == 0) {
+    double p = 0.0;
+#pragma unroll
+    for (int i = 0; i < FT / 64; ++i) p += part[lane() + 64u * (uint32_t)i];
+    const double psum = wave_sum_f64(p);
+    bool theta_set;
+    double theta, theta_err;
+    const bool ok = sel_theta(X, Q, &theta_set, &theta, &theta_err);
+    if (lane() == 0) {
+      F.s_u[14] = ok ? 1u : 0u;
+      F.s_u[15] = (ok && theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) ? 1u : 0u;
+      F.s_d[3] = theta;
+      F.s_d[4] = theta_err;
+    }
+  }
+  lds_barrier();
+  if (!F.s_u[14]) return false;
+  bool kept = mine;
+  if (F.s_u[15]) {
+    // The nucleus can end inside P.  P's weights, as exact fixed-point
+    // masses, histogrammed on the value bins; the bin where the mass prefix
+    // in descending value order reaches theta, then its members ranked by
+    // (key desc, ID asc), give the crossing member, certified as e_finish
+    // does.
+    const double theta = F.s_d[3], theta_err = F.s_d[4];
+    const double theta_fx = theta * WFIX;
+    // integer threshold: the first prefix at or above theta_fx
+    const unsigned long long tfx = (unsigned long long)ceil(theta_fx);
+    const float Mf = okey_value(F.hdr.Mkey), lo = F.hdr.lo;
+    const float span = Mf - lo;
+    const float sc = span > 1e-30f ? (float)(NBS - 1) / span : 0.0f;
+    unsigned long long* mass = F.u.s.mass;
+    const unsigned long long W = __double2ull_rn(mw * WFIX);
+    const uint32_t bn = sel_bin(ml, Mf, sc);
+    if (mine) atomicAdd(&mass[bn], W);
+    if (tid == 0) F.s_u[10] = 0u;
+    lds_barrier();
+    if (wave() == 0) {
+      // lane i: bins 32i .. 32i + 31; the crossing group, then its bins lane-parallel
+      const uint32_t ln = lane();
+      unsigned long long hs = 0;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const ulonglong2 m2 = *reinterpret_cast<const ulonglong2*>(&mass[32u * ln + 2u * (uint32_t)q]);
+        hs += m2.x + m2.y;
+      }
+      const unsigned long long inc = wave_scan_u64(hs);
+      const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= tfx);
+      uint32_t bc = NONE;
+      unsigned long long bb = 0;
+      if (reach) {
+        const uint32_t g = (uint32_t)__builtin_ctzll(reach);
+        const unsigned long long base = readlane64(inc - hs, g);
+        const unsigned long long v = ln < 32u ? mass[32u * g + ln] : 0ull;
+        const unsigned long long vi = base + wave_scan_u64(v);
+        const uint64_t r2 = __builtin_amdgcn_ballot_w64(ln < 32u && vi >= tfx);
+        const uint32_t i = (uint32_t)__builtin_ctzll(r2);
+        bc = 32u * g + i;
+        bb = readlane64(vi - v, i);
+      }
+      if (ln == 0) { F.s_u[12] = bc; F.s_l[0] = bb; }
+    }
+    lds_barrier();
+    const uint32_t bc = F.s_u[12];
+    if (bc == NONE) return false;   // no crossing inside P: replay
+    if (mine && bn == bc) {
+      const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+      if (at < 64u) { F.u.s.mk[at] = mk; F.u.s.mi[at] = mi; F.u.s.mw[at] = W; }
+    }
+    lds_barrier();
+    const uint32_t cm = F.s_u[10];
+    if (cm > 64u) return false;
+    if (wave() == 0) {
+      const uint32_t ln = lane();
+      const bool mm = ln < cm;
+      const uint32_t a = mm ? F.u.s.mk[ln] : 0u, bi = mm ? F.u.s.mi[ln] : NONE;
+      const unsigned long long aw = mm ? F.u.s.mw[ln] : 0ull;
+      unsigned long long ahead = 0;   // mass of the members ordered before this one
+      for (uint32_t j = 0; j < cm; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)j);
+        const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)bi, (int)j);
+        const unsigned long long wj = readlane64(aw, j);
+        if (kj > a || (kj == a && ij < bi)) ahead += wj;
+      }
+      const unsigned long long prev = F.s_l[0] + ahead, incl = prev + aw;
+      const bool cross = mm && (double)prev < theta_fx && theta_fx <= (double)incl;
+      // Certificate: the fixed-point prefixes are exact sums of weights
+      // rounded to 2^-51 (np 2^-51 in all), the weights are within 8 ulp
+      // of the reference's, and its sequential sums in sorted order are
+      // within sum_bound; the f64 conversion adds one rounding.
+      const double dp = (double)prev / WFIX, di = (double)incl / WFIX;
+      const double fx = (double)np * 0x1p-51;
+      const double ep = sum_bound(dp, np, 8.0) + fx + U * dp, ei = sum_bound(di, np, 8.0) + fx + U * di;
+      const bool cert = dp + ep < theta - theta_err && di - ei >= theta + theta_err;
+      const uint64_t xb = __builtin_amdgcn_ballot_w64(cross);
+      uint32_t ok = 0u, ck = 0u, ci = 0u;
+      if (xb) {
+        const uint32_t Lx = (uint32_t)__builtin_ctzll(xb);
+        ck = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)Lx);
+        ci = (uint32_t)__builtin_amdgcn_readlane((int)bi, (int)Lx);
+        ok = __builtin_amdgcn_readlane((int)cert, (int)Lx) ? 1u : 0u;
+      }
+      if (ln == 0) { F.s_u[12] = ck; F.s_u[13] = ci; F.s_u[14] = ok; }
+    }
+    lds_barrier();
+    if (!F.s_u[14]) return false;   // no certified crossing inside P: replay
+    const uint32_t ck = F.s_u[12], ci = F.s_u[13];
+    kept = mine && (mk > ck || (mk == ck && mi <= ci));
+  }
+
+  // ---- overflow check and the inverse-CDF draw in token-ID order ----------
+  const double dw = kept ? mw : 0.0;
+  const double winc = wave_scan_f64(dw);
+  const uint32_t wk = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(kept));
+  const bool wbad = __builtin_amdgcn_ballot_w64(kept && !isfinite(s)) != 0ull;
+  const uint64_t pos = __builtin_amdgcn_ballot_w64(dw > 0.0);
+  if (lane() == 63) {
+    F.rd[wave()][0] = winc;
+    F.ru[wave()][2] = wk;
+    F.ru[wave()][3] = wbad ? 1u : 0u;
+  }
+  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; }
+  if (X.kbits) {
+    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
+    __builtin_amdgcn_s_waitcnt(0);   // the zeroing lands before any wave's atomics below
+  }
+  lds_barrier();
+  const bool wl = lane() < (uint32_t)FW;
+  const double ws = wave_scan_f64(wl ? F.rd[lane()][0] : 0.0);
+  const double S = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, ws), 63));
+  const double wbefore =
+      wave() ? __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, ws), wave() - 1)) : 0.0;
+  const uint32_t nkept = wave_sum_u32(wl ? F.ru[lane()][2] : 0u);
+  const bool bad = __builtin_amdgcn_ballot_w64(wl && F.ru[lane()][3] != 0u) != 0ull;
+  if (bad) {
+    write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+    return true;
+  }
+  const double cum = wbefore + winc, before = cum - dw;
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  // the last positive kept member: one atomic per wave
+  if (pos && lane() == 0) atomicMax(&F.s_u[1], wave() * 64u + (uint32_t)(64 - __builtin_clzll(pos)));
+  if (dw > 0.0 && target < cum && !(target < before)) {
+    F.kflag[tid] = (fabs(target - before) <= derr || fabs(cum - target) <= derr) ? 1u : 0u;
+    atomicMin(&F.s_u[0], tid);
+  }
+  lds_barrier();
+  uint32_t pick = F.s_u[0];
+  bool uncert = Q.unc;
+  if (pick != NONE) {
+    uncert = uncert || F.kflag[pick] != 0u;
+  } else {
+    // rounding left the variate past the accumulated mass: the last positive kept token
+    pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
+    uncert = true;
+  }
+  if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
+  const double sp = ((double)F.u.s.pl[pick] - X.M) / c.T;
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)F.u.s.pid[pick], sp - log(S), nkept);
+  if (X.kbits && kept) atomicOr(&X.kbits[mi >> 5], 1u << (mi & 31u));
+  return true;
+}
+
+__device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const FinLoads& P, uint32_t sq, uint32_t sj) {
+  const RowCfg& c = X.c;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nq = sq < X.C ? F.st[sq].ncand : 0u;
+  uint32_t act = 0, key[SR];
+#pragma unroll
+  for (int u = 0; u < SR; ++u) {
+    const bool a = sj * (uint32_t)SR + (uint32_t)u < nq;
+    act |= a ? 1u << u : 0u;
+    key[u] = a ? okey(P.l[u]) : 0u;
+  }
+  const float Mf = okey_value(F.hdr.Mkey);   // the row maximum (X.M in f64)
+  // waves holding no candidate skip the per-slot work (the rows' few
+  // candidates sit in one wave per chunk); they still meet every barrier
+  const bool wact = __builtin_amdgcn_ballot_w64(act != 0u) != 0ull;
+  uint32_t kap = 0, idk = 0;
+  if (X.k_path) {
+    if (c.k > X.ncand) return false;
+    const float lo = F.hdr.lo;
+    const float span = Mf - lo;
+    const float sc = span > 1e-30f ? (float)(NBS - 1) / span : 0.0f;
+    uint32_t bin[SR];
+    if (wact) {
+#pragma unroll
+      for (int u = 0; u < SR; ++u) {
+        bin[u] = sel_bin(P.l[u], Mf, sc);
+        if ((act >> u) & 1u) atomicAdd(&F.u.s.cnt[bin[u]], 1u);
+      }
+    }
+    lds_barrier();
+    // wave 0 finds the crossing bin (bin order = descending value)
+    if (wave() == 0) {
+      const uint32_t ln = lane();
+      uint32_t hs = 0;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint4 h4 = *reinterpret_cast<const uint4*>(&F.u.s.cnt[32u * ln + 4u * (uint32_t)q]);
+        hs += h4.x + h4.y + h4.z + h4.w;
+      }
+      uint32_t bb = 0;
+      const uint32_t bf = wave_cross32(F.u.s.cnt, hs, wave_scan_u32(hs), c.k, &bb);
+      if (ln == 0) { F.s_u[12] = bf; F.s_u[13] = bb; }   // NONE: fewer candidates than k
+    }
+    lds_barrier();
+    const uint32_t bstar = F.s_u[12], abv = F.s_u[13];
+    if (bstar == NONE) return false;
+    // the crossing bin's members
+    if (wact) {
+#pragma unroll
+      for (int u = 0; u < SR; ++u) {
+        if (((act >> u) & 1u) && bin[u] == bstar) {
+          const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+          if (at < (uint32_t)PCAP) { F.u.s.mk[at] = key[u]; F.u.s.mi[at] = P.id[u]; }
+        }
+      }
+    }
+    lds_barrier();
+    const uint32_t cm = F.s_u[10];
+    if (cm > (uint32_t)PCAP) return false;
+    // wave 0 ranks the members: the (k - abv)-th in (key desc, ID asc)
+    // order is the last one E takes (the need-th exists: cm >= need >= 1)
+    if (wave() == 0) {
+      const uint32_t need = c.k - abv;
+      const uint32_t ln = lane();
+      const bool mm = ln < cm;
+      const uint32_t a = mm ? F.u.s.mk[ln] : 0u, bi = mm ? F.u.s.mi[ln] : NONE;
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < cm; ++j) {
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)j);
+        const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)bi, (int)j);
+        rank += (kj > a || (kj == a && ij < bi)) ? 1u : 0u;
+      }
+      if (ln == 0) F.s_u[12] = NONE;   // no finite logit's key
+      if (mm && rank == need - 1u) { F.s_u[12] = a; F.s_u[13] = bi; }
+    }
+    lds_barrier();
+    kap = F.s_u[12];
+    idk = F.s_u[13];
+    if (kap == NONE) return false;   // not reached: the members hold the need-th
+  }
+
+  // ---- E, its f32 mass, and P ----------------------------------------------
+  // The min-p test s = (l - M) / T >= L, i.e. l >= M + T L, on the f32
+  // logit away from that threshold (the band is far wider than the f32
+  // threshold's rounding), in f64 near it (with the closeness flag).
+  const bool need_wlo = X.k_path && c.top_p >= 1.0;   // only this case reads the minimum weight
+  bool unc = false;
+  uint32_t inP = 0, ne = 0;
+  float e32 = 0.0f, eab32 = 0.0f;
+  float wlo = FLT_MAX;
+  if (wact) {
+    const double L = X.L;
+    const bool minp_on = c.min_p > 0.0;
+    const float lthr = minp_on ? Mf + (float)(c.T * L) : -FLT_MAX;
+    const float band = minp_on ? 1e-5f * (fabsf(Mf) + fabsf((float)(c.T * L))) + 1e-30f : 0.0f;
+    // (a non-finite threshold or band sends every candidate to the f64 test)
+    const bool lfin = __builtin_isfinite(lthr + band) && __builtin_isfinite(lthr - band);
+    const float lhi = lfin ? lthr + band : INFINITY, llo = lfin ? lthr - band : -INFINITY;
+    const float c2 = (float)(1.4426950408889634 / c.T);   // log2(e) / T
+#pragma unroll
+    for (int u = 0; u < SR; ++u) {
+      if (!((act >> u) & 1u)) continue;
+      const float l = P.l[u];
+      bool pm = l >= lhi;   // the min-p test (every token when min_p = 0)
+      if (minp_on && l >= llo && l < lhi) {
+        const double sd = ((double)l - X.M) / c.T;
+        pm = sd >= L;
+        if (fabs(sd - L) < X.Lclose) unc = true;
+      }
+      const bool in = X.k_path ? (key[u] > kap || (key[u] == kap && P.id[u] <= idk)) : pm;
+      if (!in) continue;
+      ++ne;
+      const float y = (l - Mf) * c2;   // <= 0
+      const float wf = __builtin_amdgcn_exp2f(y);
+      e32 += wf;
+      eab32 = __builtin_fmaf(wf, -y, eab32);
+      if (need_wlo) wlo = fminf(wlo, wf * (1.0f - (0x1p-21f + 2.5e-7f * -y)));
+      if (pm) inP |= 1u << u;
+    }
+  }
+  // per-thread partial sums to LDS (the E index space is free); wave 0
+  // alone reduces them
+  static_assert(2 * FT * sizeof(double) <= ECAP * sizeof(uint32_t), "partial sums fit eidx");
+  double* part = reinterpret_cast<double*>(F.eidx);
+  part[tid] = (double)e32;
+  part[FT + tid] = (double)eab32;
+  const uint32_t pc = (uint32_t)__builtin_popcount(inP);
+  uint32_t pinc = 0;
+  if (wact) {
+    pinc = wave_scan_u32(pc);
+    const uint32_t wne = wave_sum_u32(ne);
+    const bool uw = __builtin_amdgcn_ballot_w64(unc) != 0ull;
+    if (need_wlo) wlo = okey_value(~wave_max_u32(~okey(wlo)));   // the wave's minimum
+    if (lane() == 63) {
+      F.ru[wave()][0] = pinc;
+      F.ru[wave()][1] = wne;
+      F.ru[wave()][2] = uw ? 1u : 0u;
+      F.red_f[wave()] = wlo;
+    }
+  } else if (lane() == 0) {
+    F.ru[wave()][0] = 0u;
+    F.ru[wave()][1] = 0u;
+    F.ru[wave()][2] = 0u;
+    F.red_f[wave()] = FLT_MAX;
+  }
+  lds_barrier();
+  SelSums Q;
+  {
+    const uint32_t ln = lane();
+    const bool wl = ln < (uint32_t)FW;
+    const uint32_t cw = wl ? F.ru[ln][0] : 0u;
+    Q.np = wave_sum_u32(cw);
+    Q.ne = wave_sum_u32(wl ? F.ru[ln][1] : 0u);
+    if (Q.ne == 0u || Q.np > (uint32_t)PMAX) return false;
+    // P in token-ID order: waves order by (chunk, rank in the chunk), lanes
+    // and slots in order within a wave
+    if (__builtin_amdgcn_ballot_w64(inP != 0u)) {
+      const uint32_t C = X.C, w = wave();
+      const uint32_t q = w % C, m = w / C, lq = ln % C, lm = ln / C;
+      const uint32_t ahead = wave_sum_u32(wl && (lq < q || (lq == q && lm < m)) ? cw : 0u);
+      uint32_t at = ahead + pinc - pc;
+#pragma unroll
+      for (int u = 0; u < SR; ++u) {
+        if ((inP >> u) & 1u) {
+          F.u.s.pk[at] = key[u];
+          F.u.s.pid[at] = P.id[u];
+          F.u.s.pl[at] = P.l[u];
+          ++at;
+        }
+      }
+    }
+    if (wave() == 0) {
+      // E's mass: f32 weights, summed in f32 per thread (at most SR terms)
+      // and in f64 across threads (any order: the bound holds for every
+      // order).  |f32 weight - exact| <= 2^-22 w (exp2f) + ln2 3.0001 2^-24
+      // w |y| (the three f32 roundings of y) + 2^-120 below 2^-126; the
+      // per-thread f32 sums add (SR + 1) 2^-24 of the mass; plus both sides'
+      // f64 sums (sum_bound, 8 ulp terms).
+      double e = 0.0, ea = 0.0;
+#pragma unroll
+      for (int i = 0; i < FT / 64; ++i) {
+        e += part[ln + 64u * (uint32_t)i];
+        ea += part[FT + ln + 64u * (uint32_t)i];
+      }
+      Q.esum = wave_sum_f64(e);
+      const double eab = wave_sum_f64(ea);
+      Q.esum_err = 1.01 * ((0x1p-22 + (double)(SR + 1) * 0x1p-24) * Q.esum +
+                           0.6931471805599453 * 3.0001 * 0x1p-24 * eab) +
+                   (double)Q.ne * 0x1p-120 + sum_bound(Q.esum, Q.ne, 8.0);
+      Q.unc = __builtin_amdgcn_ballot_w64(wl && F.ru[ln][2] != 0u) != 0ull;
+      Q.wlo = need_wlo ? (double)okey_value(~wave_max_u32(wl ? ~okey(F.red_f[ln]) : 0u)) : 0.0;
+      if (ln == 0) {
+        F.s_d[0] = Q.esum;
+        F.s_d[1] = Q.esum_err;
+        F.s_d[2] = Q.wlo;
+        F.s_u[9] = Q.unc ? 1u : 0u;
+      }
+    }
+  }
+  lds_barrier();
+  if (Q.np <= 64u) {
+    if (wave() == 0) {
+      const bool ok = sel_small(X, F, Q);
+      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
+    }
+    lds_barrier();
+    return F.s_u[15] != 0u;
+  }
+  Q.esum = F.s_d[0];
+  Q.esum_err = F.s_d[1];
+  Q.wlo = F.s_d[2];
+  Q.unc = F.s_u[9] != 0u;
+  return sel_large(X, F, Q);
+}
+
+// ---------------------------------------------------------------------------
 // The row finisher.  Runs in the last chunk workgroup of a row, after every
 // chunk published its statistics and candidates.
 template <typename In, bool XD>
 __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
-                           uint64_t rbase, double invT) {
+                           uint64_t rbase, double invT, const FinLoads& P) {
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
   const uint32_t V = b.vocab;
   const uint32_t C = A.C;
-  // exp_neg's tables into LDS (waves 1-2), and the first candidates of each
-  // chunk, loaded speculatively while wave 0 reads the chunk statistics:
-  // thread t covers slot t mod (FT / C) of chunk t / (FT / C).
-  if (tid >= 64 && tid < 192) {
-    const uint32_t j = tid - 64u;
+  // exp_neg's tables into LDS (waves 2-3) while waves 0-1 reduce the chunk
+  // statistics; the selection finisher's histogram and list counters are
+  // cleared in the same interval.
+  if (tid >= 128 && tid < 256) {
+    const uint32_t j = tid - 128u;
     F.etab[j] = j < 64u ? kExp2Tab[j] : kExp2TabLo[j - 64u];
   }
-  const uint32_t spc = FT / C;   // speculative slots per chunk
-  const uint32_t sq = tid / spc, sj = tid - sq * spc;
-  const bool s_ok = sq < C && sj < A.CH && (uint64_t)sq * A.CH + sj < V;
-  float s_l = 0.0f;
-  uint32_t s_id = 0;
-  if (s_ok) {
-    const uint64_t pos = rbase + (uint64_t)sq * A.CH + sj;
-    s_l = xget<XD>(&A.w.cand_l[pos]);
-    s_id = xget<XD>(&A.w.cand_id[pos]);
+  reinterpret_cast<uint2*>(F.u.s.cnt)[tid] = make_uint2(0u, 0u);
+  reinterpret_cast<ulonglong2*>(F.u.s.mass)[tid] = make_ulonglong2(0ull, 0ull);
+  static_assert(NBS == 2 * FT && PMAX == FT, "two histogram bins per thread; one P member per thread");
+  if (tid == 256) {   // wave 4: off the statistics' waves
+    F.s_u[10] = 0u;
+    F.s_u[11] = 0u;
+    F.hdr.L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
   }
-  // Chunk statistics: wave 0 reads them (lane q <-> chunk q, C <= 64),
-  // reduces them with DPP and publishes the row header and a copy of the
-  // statistics in LDS.
+  uint32_t sq, sj;                // this thread's chunk and slot group (slot_map)
+  slot_map(C, &sq, &sj);
+  const uint32_t cov = slot_cov(C);   // candidates per chunk held in registers
+  // Chunk statistics (lane q of wave 0 holds chunk q's, C <= 64): reduced
+  // with DPP into the row header, and copied to LDS.
   if (wave() == 0) {
     const uint32_t q = lane();
-    ChunkStat v;
-    v.maxkey = 0u; v.gbest_id = NONE; v.gbest_val = 0.0f; v.nlegal = 0u; v.ncand = 0u; v.flags = 0u;
-    v.minkey = NONE; v.thr = 0.0f; v.mass = 0.0; v.mass_err = 0.0;
-    if (q < C) {
-      const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + q];
-      v.maxkey = xget<XD>(&st->maxkey);
-      v.gbest_id = xget<XD>(&st->gbest_id);
-      v.gbest_val = xget<XD>(&st->gbest_val);
-      v.nlegal = xget<XD>(&st->nlegal);
-      v.ncand = xget<XD>(&st->ncand);
-      v.flags = xget<XD>(&st->flags);
-      v.mass = xget<XD>(&st->mass);
-      v.mass_err = xget<XD>(&st->mass_err);
-      v.minkey = xget<XD>(&st->minkey);
-    }
+    const ChunkStat& v = P.v;
     const uint32_t fl = wave_or_u32(v.flags);
     const uint32_t nl = wave_sum_u32(v.nlegal);
     const uint32_t mkey = wave_max_u32(v.nlegal ? v.maxkey : 0u);
+    const uint32_t qmax = wave_max_u32(v.ncand);
+    // the smallest candidate threshold (order keys; chunks without candidates do not count)
+    const uint32_t lokey = ~wave_max_u32(v.ncand ? ~okey(v.thr) : 0u);
     // the greedy argmax: largest (value key, ~id); chunk values are +0.0-normalised
     const unsigned long long garg = wave_max_u64(
         v.gbest_id != NONE ? ((unsigned long long)okey(v.gbest_val) << 32) | (unsigned long long)(~v.gbest_id) : 0ull);
-    const double Mw = (double)okey_value(mkey);
     const uint32_t cinc = wave_scan_u32(v.ncand);
-    const double cs = v.nlegal ? exp_neg(((double)okey_value(v.maxkey) - Mw) * invT) : 0.0;
-    const double t = wave_sum_f64(v.mass * cs), te = wave_sum_f64(v.mass_err * cs);
     if (q < C) {
       F.st[q] = v;
       F.coff[q] = cinc - v.ncand;
-      F.cscale[q] = cs;
     }
     if (q == 0) {
       F.coff[C] = bcast63(cinc);
       F.hdr.flags = fl; F.hdr.nlegal = nl; F.hdr.Mkey = mkey; F.hdr.bi = garg ? ~(uint32_t)garg : NONE;
-      F.hdr.ncand = bcast63(cinc); F.hdr.mass = t; F.hdr.mass_err = te;
-      F.hdr.L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
+      F.hdr.ncand = bcast63(cinc);
+      F.hdr.qmax = qmax;
+      F.hdr.lo = okey_value(lokey);
+    }
+  } else if (wave() == 1 && !c.greedy) {
+    // the chunk masses rescaled to the row maximum (f64: off wave 0's path)
+    const uint32_t q = lane();
+    const bool qa = q < C;
+    const uint32_t nlg = P.v.nlegal, mxk = P.v.maxkey;
+    const double ms = P.v.mass, me = P.v.mass_err;
+    const uint32_t mkey = wave_max_u32(nlg ? mxk : 0u);
+    const double Mw = (double)okey_value(mkey);
+    const double cs = nlg ? exp_neg(((double)okey_value(mxk) - Mw) * invT) : 0.0;
+    const double t = wave_sum_f64(ms * cs), te = wave_sum_f64(me * cs);
+    const uint32_t nl = wave_sum_u32(nlg);
+    if (qa) F.cscale[q] = cs;
+    if (q == 0) {
+      F.hdr.mass = t;
+      // chunk error bounds (f32 weights), scaled; plus both sides' f64
+      // rounding of weights and sums, and the x e^x <= 1/e product term
+      F.hdr.mass_err = te * 1.000001 + sum_bound(t, nl + C, 12.0) + 2.0 * 0.37 * (double)nl * U;
     }
   }
   lds_barrier();
@@ -1833,11 +2502,50 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   const uint32_t ncand = F.hdr.ncand;
   X.ncand = ncand;
   X.lds_c = ncand <= (uint32_t)CCAP;
+  const double L = F.hdr.L;
+  // ln(min_p) is exact for min_p = 1 (and -inf for 0); otherwise device and
+  // host logs may differ in the last ulps, so a shifted logit within 4 ulp is
+  // an uncertain cut.
+  X.L = L;
+  X.Lclose = (c.min_p > 0.0 && c.min_p < 1.0) ? 4.0 * U * fabs(L) : 0.0;
+
+  // total = sum over every legal token of exp((l - M) / T), from chunk masses
+  X.total = 0.0;
+  X.total_err = 0.0;
+  X.have_total = false;
+  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
+    X.total = F.hdr.mass;
+    X.total_err = F.hdr.mass_err;
+    X.have_total = true;
+  }
+
+  // top-k head: kappa = the k-th largest key; the head takes every candidate
+  // above it and the lowest-ID ties at it.
+  X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
+  X.kappa = 0;
+  X.id_tie = NONE;
+
+  // rows whose candidates all sit in the register slots: the selection finisher
+  if ((mode == M_TOPK || mode == M_MINP) && ncand > 0u && C <= (uint32_t)FW && F.hdr.qmax <= cov) {
+    if (finish_sel(X, F, P, sq, sj)) {
+      stamp(A, row, MAXC, 2);
+      return;
+    }
+  }
   // One bulk load of every candidate into LDS, all loads in flight at once.
   // Candidate j lives in chunk q's region at j - coff[q]; j grows with u,
   // so each thread walks the chunk offsets once.
   if (X.lds_c) {
-    if (s_ok && sj < F.st[sq].ncand) { F.cl[F.coff[sq] + sj] = s_l; F.cid[F.coff[sq] + sj] = s_id; }
+    // the register slots first (every chunk's first cov candidates)
+    {
+      const uint32_t nq = sq < C ? F.st[sq].ncand : 0u;
+      const uint32_t o = sq < C ? F.coff[sq] : 0u;
+#pragma unroll
+      for (int u = 0; u < SR; ++u) {
+        const uint32_t slot = sj * (uint32_t)SR + (uint32_t)u;
+        if (slot < nq) { F.cl[o + slot] = P.l[u]; F.cid[o + slot] = P.id[u]; }
+      }
+    }
     float lv[FR];
     uint32_t iv[FR];
     uint32_t need = 0;   // bit u: candidate u * FT + tid is past the speculative slots
@@ -1848,7 +2556,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       if (j < ncand) {
         while (j >= nxt) { ++qj; nxt = qj + 1 < C ? F.coff[qj + 1] : NONE; }
         const uint32_t local = j - F.coff[qj];
-        if (local >= spc) {
+        if (local >= cov) {
           const uint64_t pos = rbase + (uint64_t)qj * A.CH + local;
           lv[u] = xget<XD>(&A.w.cand_l[pos]);
           iv[u] = xget<XD>(&A.w.cand_id[pos]);
@@ -1864,31 +2572,6 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     lds_barrier();
   }
   stamp(A, row, MAXC, 1);
-  const double L = F.hdr.L;
-  // ln(min_p) is exact for min_p = 1 (and -inf for 0); otherwise device and
-  // host logs may differ in the last ulps, so a shifted logit within 4 ulp is
-  // an uncertain cut.
-  X.L = L;
-  X.Lclose = (c.min_p > 0.0 && c.min_p < 1.0) ? 4.0 * U * fabs(L) : 0.0;
-
-  // total = sum over every legal token of exp((l - M) / T), from chunk masses
-  X.total = 0.0;
-  X.total_err = 0.0;
-  X.have_total = false;
-  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
-    const double t = F.hdr.mass, te = F.hdr.mass_err;
-    X.total = t;
-    // chunk error bounds (f32 weights), scaled; plus both sides' f64
-    // rounding of weights and sums, and the x e^x <= 1/e product term
-    X.total_err = te * 1.000001 + sum_bound(t, nlegal + C, 12.0) + 2.0 * 0.37 * (double)nlegal * U;
-    X.have_total = true;
-  }
-
-  // top-k head: kappa = the k-th largest key; the head takes every candidate
-  // above it and the lowest-ID ties at it.
-  X.k_path = k_act && (mode == M_TOPK || mode == M_ALL);
-  X.kappa = 0;
-  X.id_tie = NONE;
   if (mode != M_KEEPALL && X.lds_c && ncand <= (uint32_t)(WR * 64)) {
     // at most WR * 64 candidates: one wave finishes the row
     if (wave() == 0) {
@@ -2468,7 +3151,9 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     lds_barrier();   // the finisher's LDS overlays the chunk's
     if (!last) return;
     stamp(A, row, MAXC, 0);
-    finish_row<In, true>(A, U.f, c, row, MODE, (uint64_t)row * V, invT);
+    FinLoads P;
+    fin_issue<true>(A, row, P);
+    finish_row<In, true>(A, U.f, c, row, MODE, (uint64_t)row * V, invT, P);
     stamp(A, row, MAXC, 7);
   }
 }
@@ -3077,7 +3762,9 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
     lds_barrier();   // the finisher's LDS overlays the chunk's
     if (!last) return;
     stamp(A, row, MAXC, 0);
-    finish_row<In, true>(A, U.f, c, row, mode, rbase, invT);
+    FinLoads P;
+    fin_issue<true>(A, row, P);
+    finish_row<In, true>(A, U.f, c, row, mode, rbase, invT, P);
     stamp(A, row, MAXC, 7);
   }
 }
@@ -3137,14 +3824,17 @@ __global__ __launch_bounds__(FT) void finish_kernel(
     const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
     const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
   __shared__ __align__(16) FinSmem F;
-  const uint32_t row = blockIdx.x;
-  if (row >= A.b.rows) return;
+  const uint32_t row = blockIdx.x;   // the grid holds exactly one workgroup per row
+  // the statistics and candidate loads go out before the parameter loads
+  // are waited for
+  FinLoads P;
+  fin_issue<false>(A, row, P);
   const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
                             p_boff, row);
   const uint32_t mode = chunk_mode(c, A.b.vocab);
   const double invT = c.greedy ? 0.0 : 1.0 / c.T;
   stamp(A, row, MAXC, 0);
-  finish_row<In, false>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT);
+  finish_row<In, false>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT, P);
   stamp(A, row, MAXC, 7);
 }
 

@@ -53,6 +53,16 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 __device__ __forceinline__ double ld_dev(const double* p) {
   return __hip_atomic_load(const_cast<double*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ float2 ld_dev(const float2* p) {
+  const unsigned long long v = __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<float2*>(p)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+__device__ __forceinline__ uint2 ld_dev(const uint2* p) {
+  const unsigned long long v = __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<uint2*>(p)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint2((uint32_t)v, (uint32_t)(v >> 32));
+}
 __device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
