@@ -188,3 +188,44 @@ def test_history_and_bias_validation(torch_mod, sampler, orc):
               bias_values=np.array([1.0, 2.0, math.nan], np.float32))
     gpu, ref = check(torch_mod, sampler, orc, b)
     assert list(ref["status"]) == [0, -11, -12, -12]
+
+
+def selection_batch(seed, rows, V):
+    """Peaked rows (noise plus a few high logits) over the parameter ranges
+    the register-slot finisher decides: top-k from 1 to 4096, top-p and
+    min-p on and off, low and high temperatures, and rows whose top logits
+    tie exactly (the crossing-bin ranking and the general paths)."""
+    from metallix_amd.synth import Batch
+
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((rows, V)) * 2.0).astype(np.float32)
+    for r in range(rows):
+        npk = int(rng.integers(1, 60))
+        ids = rng.choice(V, size=npk, replace=False)
+        x[r, ids] += rng.uniform(3.0, 10.0, size=npk).astype(np.float32)
+        if r % 7 == 3:   # a tied plateau at the top
+            ids = rng.choice(V, size=int(rng.integers(2, 200)), replace=False)
+            x[r, ids] = np.float32(x[r].max() + 0.5)
+    T = rng.choice([0.3, 0.8, 1.5, 3.0], size=rows)
+    topk = rng.choice([0, 1, 20, 64, 500, 1000, 2000, 4096], size=rows).astype(np.uint32)
+    topp = rng.choice([1.0, 0.95, 0.7, 0.5], size=rows)
+    minp = rng.choice([0.0, 0.001, 0.05, 0.3], size=rows)
+    return Batch(name=f"selection-{seed}", logits=x, temperature=T, uniform=rng.random(rows), top_k=topk,
+                 top_p=topp, min_p=minp)
+
+
+@pytest.mark.parametrize("seed", [1, 2])
+def test_selection_finisher_mix(torch_mod, sampler, orc, seed):
+    """Parity over the selection finisher's range.  Rows whose nucleus holds
+    more than 8192 tokens (min_p 0.001 at high temperature) take the
+    large-set path, whose nucleus cut rests on the chunk pass's f32 row mass
+    (error bound about 5e-6 of the total): there a cut that falls within
+    the bound of a token boundary is flagged uncertified, and only there."""
+    b = selection_batch(seed, 64, 151936)
+    say(f"case {b.name}: rows {b.rows} vocab {b.vocab}")
+    ref = orc.sample_batch(b, debug=True)
+    gpu = run_gpu(torch_mod, sampler, b)
+    wide = np.asarray(ref["kept"]).sum(axis=1) > 8192
+    unc = np.asarray(gpu["status"]) == 1
+    assert not (unc & ~wide).any(), f"uncertified outside the wide-nucleus rows: {np.nonzero(unc & ~wide)[0]}"
+    compare(b, gpu, ref, allow_uncertified=int(wide.sum()))
