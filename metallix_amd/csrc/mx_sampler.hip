@@ -1889,29 +1889,11 @@ __device__ __forceinline__ bool sel_large(const FinCtx& X, FinSmem& F, const Sel
   const float ml = mine ? F.u.s.pl[tid] : 0.0f;
   const double s = mine ? ((double)ml - X.M) / c.T : 0.0;
   const double mw = mine ? exp_neg_t(s, X.etab, X.etab + 64) : 0.0;
-  double* part = reinterpret_cast<double*>(F.eidx);
-  part[tid] = mw;
-  lds_barrier();
-  // wave 0: P's mass, theta and whether the nucleus can end inside P
-  if (wave() == 0) {
-    double p = 0.0;
-#pragma unroll
-    for (int i = 0; i < FT / 64; ++i) p += part[lane() + 64u * (uint32_t)i];
-    const double psum = wave_sum_f64(p);
-    bool theta_set;
-    double theta, theta_err;
-    const bool ok = sel_theta(X, Q, &theta_set, &theta, &theta_err);
-    if (lane() == 0) {
-      F.s_u[14] = ok ? 1u : 0u;
-      F.s_u[15] = (ok && theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) ? 1u : 0u;
-      F.s_d[3] = theta;
-      F.s_d[4] = theta_err;
-    }
-  }
-  lds_barrier();
-  if (!F.s_u[14]) return false;
+  // theta, and whether the nucleus can end inside P (P's f32 mass could not
+  // rule it out), come from finish_sel
+  const bool cut = F.s_u[15] != 0u;
   bool kept = mine;
-  if (F.s_u[15]) {
+  if (cut) {
     // The nucleus can end inside P.  P's weights, as exact fixed-point
     // masses, histogrammed on the value bins; the bin where the mass prefix
     // in descending value order reaches theta, then its members ranked by
@@ -1941,9 +1923,15 @@ __device__ __forceinline__ bool sel_large(const FinCtx& X, FinSmem& F, const Sel
       }
       const unsigned long long inc = wave_scan_u64(hs);
       const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= tfx);
-      uint32_t bc = NONE;
+      uint32_t bc = NONE, nocut = 0u;
       unsigned long long bb = 0;
-      if (reach) {
+      if (!reach) {
+        // P's exact mass stays below theta: every member is kept when the
+        // bound clears it
+        const double dt = (double)readlane64(inc, 63) / WFIX;
+        const double et = sum_bound(dt, np, 8.0) + (double)np * 0x1p-51 + U * dt;
+        nocut = dt + et < theta - theta_err ? 1u : 0u;
+      } else {
         const uint32_t g = (uint32_t)__builtin_ctzll(reach);
         const unsigned long long base = readlane64(inc - hs, g);
         const unsigned long long v = ln < 32u ? mass[32u * g + ln] : 0ull;
@@ -1953,11 +1941,21 @@ __device__ __forceinline__ bool sel_large(const FinCtx& X, FinSmem& F, const Sel
         bc = 32u * g + i;
         bb = readlane64(vi - v, i);
       }
-      if (ln == 0) { F.s_u[12] = bc; F.s_l[0] = bb; }
+      if (ln == 0) { F.s_u[12] = bc; F.s_u[13] = nocut; F.s_l[0] = bb; }
     }
     lds_barrier();
     const uint32_t bc = F.s_u[12];
-    if (bc == NONE) return false;   // no crossing inside P: replay
+    if (bc == NONE && !F.s_u[13]) return false;   // no certified crossing or total: replay
+  }
+  if (cut && F.s_u[12] != NONE) {
+    const double theta = F.s_d[3], theta_err = F.s_d[4];
+    const double theta_fx = theta * WFIX;
+    const float Mf = okey_value(F.hdr.Mkey), lo = F.hdr.lo;
+    const float span = Mf - lo;
+    const float sc = span > 1e-30f ? (float)(NBS - 1) / span : 0.0f;
+    const unsigned long long W = __double2ull_rn(mw * WFIX);
+    const uint32_t bn = sel_bin(ml, Mf, sc);
+    const uint32_t bc = F.s_u[12];
     if (mine && bn == bc) {
       const uint32_t at = atomicAdd(&F.s_u[10], 1u);
       if (at < 64u) { F.u.s.mk[at] = mk; F.u.s.mi[at] = mi; F.u.s.mw[at] = W; }
@@ -2145,7 +2143,7 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
   const bool need_wlo = X.k_path && c.top_p >= 1.0;   // only this case reads the minimum weight
   bool unc = false;
   uint32_t inP = 0, ne = 0;
-  float e32 = 0.0f, eab32 = 0.0f;
+  float e32 = 0.0f, eab32 = 0.0f, p32 = 0.0f, pab32 = 0.0f;
   float wlo = FLT_MAX;
   if (wact) {
     const double L = X.L;
@@ -2174,15 +2172,18 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
       e32 += wf;
       eab32 = __builtin_fmaf(wf, -y, eab32);
       if (need_wlo) wlo = fminf(wlo, wf * (1.0f - (0x1p-21f + 2.5e-7f * -y)));
-      if (pm) inP |= 1u << u;
+      if (pm) {
+        inP |= 1u << u;
+        p32 += wf;
+        pab32 = __builtin_fmaf(wf, -y, pab32);
+      }
     }
   }
   // per-thread partial sums to LDS (the E index space is free); wave 0
   // alone reduces them
-  static_assert(2 * FT * sizeof(double) <= ECAP * sizeof(uint32_t), "partial sums fit eidx");
-  double* part = reinterpret_cast<double*>(F.eidx);
-  part[tid] = (double)e32;
-  part[FT + tid] = (double)eab32;
+  static_assert(FT * sizeof(float4) <= ECAP * sizeof(uint32_t), "partial sums fit eidx");
+  float4* part = reinterpret_cast<float4*>(F.eidx);
+  part[tid] = make_float4(e32, eab32, p32, pab32);
   const uint32_t pc = (uint32_t)__builtin_popcount(inP);
   uint32_t pinc = 0;
   if (wact) {
@@ -2235,11 +2236,14 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
       // w |y| (the three f32 roundings of y) + 2^-120 below 2^-126; the
       // per-thread f32 sums add (SR + 1) 2^-24 of the mass; plus both sides'
       // f64 sums (sum_bound, 8 ulp terms).
-      double e = 0.0, ea = 0.0;
+      double e = 0.0, ea = 0.0, pp = 0.0, pa = 0.0;
 #pragma unroll
       for (int i = 0; i < FT / 64; ++i) {
-        e += part[ln + 64u * (uint32_t)i];
-        ea += part[FT + ln + 64u * (uint32_t)i];
+        const float4 v = part[ln + 64u * (uint32_t)i];
+        e += (double)v.x;
+        ea += (double)v.y;
+        pp += (double)v.z;
+        pa += (double)v.w;
       }
       Q.esum = wave_sum_f64(e);
       const double eab = wave_sum_f64(ea);
@@ -2248,11 +2252,28 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
                    (double)Q.ne * 0x1p-120 + sum_bound(Q.esum, Q.ne, 8.0);
       Q.unc = __builtin_amdgcn_ballot_w64(wl && F.ru[ln][2] != 0u) != 0ull;
       Q.wlo = need_wlo ? (double)okey_value(~wave_max_u32(wl ? ~okey(F.red_f[ln]) : 0u)) : 0.0;
+      // For the workgroup finish of a large P: theta, and whether the
+      // nucleus can end inside P, from P's f32 mass (same bound as E's).
+      bool theta_set = false;
+      double theta = 0.0, theta_err = 0.0;
+      const bool tok = sel_theta(X, Q, &theta_set, &theta, &theta_err);
+      bool cut = false;
+      if (Q.np > 64u && tok && theta_set) {
+        const double ps = wave_sum_f64(pp), pab = wave_sum_f64(pa);
+        const double ps_err = 1.01 * ((0x1p-22 + (double)(SR + 1) * 0x1p-24) * ps +
+                                      0.6931471805599453 * 3.0001 * 0x1p-24 * pab) +
+                              (double)Q.np * 0x1p-120 + sum_bound(ps, Q.np, 8.0);
+        cut = !(ps + ps_err < theta - theta_err);
+      }
       if (ln == 0) {
         F.s_d[0] = Q.esum;
         F.s_d[1] = Q.esum_err;
         F.s_d[2] = Q.wlo;
         F.s_u[9] = Q.unc ? 1u : 0u;
+        F.s_u[14] = tok ? 1u : 0u;
+        F.s_u[15] = cut ? 1u : 0u;
+        F.s_d[3] = theta;
+        F.s_d[4] = theta_err;
       }
     }
   }
@@ -2265,6 +2286,7 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
     lds_barrier();
     return F.s_u[15] != 0u;
   }
+  if (!F.s_u[14]) return false;   // the running sum may stall: the general path replays it
   Q.esum = F.s_d[0];
   Q.esum_err = F.s_d[1];
   Q.wlo = F.s_d[2];
