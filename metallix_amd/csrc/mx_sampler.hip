@@ -2979,26 +2979,23 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
         }
       }
       lds_barrier();
-      uint32_t hv[16];
+      // every wave: lane j sums bins 16 j .. 16 j + 15; the crossing group's
+      // bins are then scanned lane-parallel (no per-bin serial walk)
       uint32_t s = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const uint4 h4 = *reinterpret_cast<const uint4*>(&S.hist[lane() * 16u + (uint32_t)q * 4u]);
-        hv[q * 4 + 0] = h4.x; hv[q * 4 + 1] = h4.y; hv[q * 4 + 2] = h4.z; hv[q * 4 + 3] = h4.w;
         s += h4.x + h4.y + h4.z + h4.w;
       }
       const uint32_t inc = wave_scan_u32(s);
       const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
       if (reach) {
-        const uint32_t L = (uint32_t)__builtin_ctzll(reach);
-        uint32_t run = inc - s, bin = 16u * lane() + 15u;
-        bool found = false;
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          run += hv[q];
-          if (!found && run >= need) { found = true; bin = 16u * lane() + (uint32_t)q; }
-        }
-        const uint32_t tb = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
+        const uint32_t g = (uint32_t)__builtin_ctzll(reach);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - s), (int)g);
+        const uint32_t v = lane() < 16u ? S.hist[16u * g + lane()] : 0u;
+        const uint32_t vi = base + wave_scan_u32(v);
+        const uint64_t r2 = __builtin_amdgcn_ballot_w64(lane() < 16u && vi >= need);
+        const uint32_t tb = 16u * g + (uint32_t)__builtin_ctzll(r2);
         thr = m - (float)(tb + 2u) / scale;
       }
     }
@@ -3018,22 +3015,31 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
   }
   uint32_t cnt_i[PER_MAX];
+  // Out-of-range tokens hold -inf: a finite threshold needs no range mask
+  // (a threshold of -inf takes every in-range token, so it does).
+  const bool thr_fin = thr > -INFINITY;   // uniform
   if (emit) {
 #pragma unroll
     for (int i = 0; i < PER_MAX; ++i) {
       cnt_i[i] = 0u;
       if (i < (int)A.per) {
-        // screen the slice on the quad maxima first (out-of-range tokens
-        // hold -inf; a threshold of -inf takes every in-range token)
+        // screen the slice on the quad maxima first
         uint32_t cnt = 0;
         if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
-          const uint32_t sbase = c0 + (uint32_t)i * SLICE;
-          const uint32_t e0 = sbase + tid * 4u;
-          const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
-                              : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+          if (thr_fin) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(((rb >> e) & 1u) && lv[i][e] >= thr));
+            for (int e = 0; e < 4; ++e)
+              cnt += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lv[i][e] >= thr));
+          } else {
+            const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+            const uint32_t e0 = sbase + tid * 4u;
+            const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
+                                : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              cnt += (uint32_t)__builtin_popcountll(
+                  __builtin_amdgcn_ballot_w64(((rb >> e) & 1u) && lv[i][e] >= thr));
+          }
         }
         cnt_i[i] = cnt;
         if (lane() == 0) S.wcnt[i * NW + wave()] = cnt;
@@ -3108,7 +3114,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
         uint32_t before_me = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          em[e] = ((rb >> e) & 1u) && lv[i][e] >= thr;
+          em[e] = (thr_fin || ((rb >> e) & 1u)) && lv[i][e] >= thr;
           before_me += lanes_below(__builtin_amdgcn_ballot_w64(em[e]));
         }
         uint32_t off = base + before_me;
