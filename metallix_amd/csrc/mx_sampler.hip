@@ -3098,38 +3098,64 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     const bool staged = ncand <= (uint32_t)(CHUNK_MAX / 4);   // uniform
     float* stl = reinterpret_cast<float*>(S.t.ct);
     uint32_t* sti = S.t.ct + CHUNK_MAX / 4;
+    if (staged && thr_fin) {
+      // the common case: staged, and a finite threshold (no range masks)
 #pragma unroll
-    for (int i = 0; i < PER_MAX; ++i) {
-      if (i < (int)A.per && cnt_i[i]) {
-        const uint32_t idx = (uint32_t)i * NW + wave();
-        const uint32_t src = idx & 63u;
-        const uint32_t reg = idx >> 6;
-        const uint32_t xv = reg == 0 ? x0 : (reg == 1 ? x1 : x2);
-        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)src);
-        const uint32_t sbase = c0 + (uint32_t)i * SLICE;
-        const uint32_t e0 = sbase + tid * 4u;
-        const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
-                            : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
-        bool em[4];
-        uint32_t before_me = 0;
+      for (int i = 0; i < PER_MAX; ++i) {
+        if (i < (int)A.per && cnt_i[i]) {
+          const uint32_t idx = (uint32_t)i * NW + wave();
+          const uint32_t src = idx & 63u;
+          const uint32_t reg = idx >> 6;
+          const uint32_t xv = reg == 0 ? x0 : (reg == 1 ? x1 : x2);
+          const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)src);
+          const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+          uint32_t off = base;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          em[e] = (thr_fin || ((rb >> e) & 1u)) && lv[i][e] >= thr;
-          before_me += lanes_below(__builtin_amdgcn_ballot_w64(em[e]));
-        }
-        uint32_t off = base + before_me;
+          for (int e = 0; e < 4; ++e) off += lanes_below(__builtin_amdgcn_ballot_w64(lv[i][e] >= thr));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (em[e]) {
-            if (staged) {
+          for (int e = 0; e < 4; ++e) {
+            if (lv[i][e] >= thr) {
               stl[off] = lv[i][e];
               sti[off] = e0 + (uint32_t)e;
-            } else {
-              const uint64_t pos = cbase + off;
-              xput<XD>(&A.w.cand_l[pos], lv[i][e]);
-              xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+              ++off;
             }
-            ++off;
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER_MAX; ++i) {
+        if (i < (int)A.per && cnt_i[i]) {
+          const uint32_t idx = (uint32_t)i * NW + wave();
+          const uint32_t src = idx & 63u;
+          const uint32_t reg = idx >> 6;
+          const uint32_t xv = reg == 0 ? x0 : (reg == 1 ? x1 : x2);
+          const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)src);
+          const uint32_t sbase = c0 + (uint32_t)i * SLICE;
+          const uint32_t e0 = sbase + tid * 4u;
+          const uint32_t rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu
+                              : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+          bool em[4];
+          uint32_t before_me = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            em[e] = (thr_fin || ((rb >> e) & 1u)) && lv[i][e] >= thr;
+            before_me += lanes_below(__builtin_amdgcn_ballot_w64(em[e]));
+          }
+          uint32_t off = base + before_me;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (em[e]) {
+              if (staged) {
+                stl[off] = lv[i][e];
+                sti[off] = e0 + (uint32_t)e;
+              } else {
+                const uint64_t pos = cbase + off;
+                xput<XD>(&A.w.cand_l[pos], lv[i][e]);
+                xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+              }
+              ++off;
+            }
           }
         }
       }
