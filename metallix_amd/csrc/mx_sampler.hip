@@ -2070,13 +2070,16 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
   // waves holding no candidate skip the per-slot work (the rows' few
   // candidates sit in one wave per chunk); they still meet every barrier
   const bool wact = __builtin_amdgcn_ballot_w64(act != 0u) != 0ull;
-  uint32_t kap = 0, idk = 0;
+  uint32_t kap = 0, idk = 0, bstar = NONE;
+  bool whole = false;     // E takes the whole crossing bin (exactly, or as a bracket)
+  bool bracket = false;   // ... with surplus members whose mass bext bounds
+  double bext = 0.0;
+  uint32_t bin[SR];
   if (X.k_path) {
     if (c.k > X.ncand) return false;
     const float lo = F.hdr.lo;
     const float span = Mf - lo;
     const float sc = span > 1e-30f ? (float)(NBS - 1) / span : 0.0f;
-    uint32_t bin[SR];
     if (wact) {
 #pragma unroll
       for (int u = 0; u < SR; ++u) {
@@ -2096,44 +2099,74 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
       }
       uint32_t bb = 0;
       const uint32_t bf = wave_cross32(F.u.s.cnt, hs, wave_scan_u32(hs), c.k, &bb);
-      if (ln == 0) { F.s_u[12] = bf; F.s_u[13] = bb; }   // NONE: fewer candidates than k
-    }
-    lds_barrier();
-    const uint32_t bstar = F.s_u[12], abv = F.s_u[13];
-    if (bstar == NONE) return false;
-    // the crossing bin's members
-    if (wact) {
-#pragma unroll
-      for (int u = 0; u < SR; ++u) {
-        if (((act >> u) & 1u) && bin[u] == bstar) {
-          const uint32_t at = atomicAdd(&F.s_u[10], 1u);
-          if (at < (uint32_t)PCAP) { F.u.s.mk[at] = key[u]; F.u.s.mi[at] = P.id[u]; }
+      // NONE: fewer candidates than k.  Whole: the crossing bin holds
+      // exactly the members E still needs, so E is every candidate in bins
+      // 0 .. bf.  Bracket: the crossing bin lies below the min-p band (no
+      // member is in P), so E may take the whole bin too; its surplus
+      // members' mass (at most (count - need) times the largest weight the
+      // bin allows, one bin wider for the f32 binning) widens E's mass bound.
+      const uint32_t cb = bf != NONE ? F.u.s.cnt[bf] : 0u;
+      uint32_t mode = 0u;
+      double extra = 0.0;
+      if (bf != NONE) {
+        if (bb + cb == c.k) {
+          mode = 1u;
+        } else if (c.min_p > 0.0 && sc > 0.0f) {
+          const float band = 1e-5f * (fabsf(Mf) + fabsf((float)(c.T * X.L))) + 1e-30f;
+          const float llo = Mf + (float)(c.T * X.L) - band;
+          const float top = Mf - (float)((int)bf - 1) / sc;   // above every value in bin bf
+          if (__builtin_isfinite(llo) && top < llo) {
+            mode = 2u;
+            const float c2 = (float)(1.4426950408889634 / c.T);
+            const double whi = fmin(1.0, (double)__builtin_amdgcn_exp2f((top - Mf) * c2) * 1.0001);
+            extra = (double)(bb + cb - c.k) * whi;
+          }
         }
       }
+      if (ln == 0) { F.s_u[12] = bf; F.s_u[13] = bb; F.s_u[8] = mode; F.s_d[5] = extra; }
     }
     lds_barrier();
-    const uint32_t cm = F.s_u[10];
-    if (cm > (uint32_t)PCAP) return false;
-    // wave 0 ranks the members: the (k - abv)-th in (key desc, ID asc)
-    // order is the last one E takes (the need-th exists: cm >= need >= 1)
-    if (wave() == 0) {
-      const uint32_t need = c.k - abv;
-      const uint32_t ln = lane();
-      const bool mm = ln < cm;
-      const uint32_t a = mm ? F.u.s.mk[ln] : 0u, bi = mm ? F.u.s.mi[ln] : NONE;
-      uint32_t rank = 0;
-      for (uint32_t j = 0; j < cm; ++j) {
-        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)j);
-        const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)bi, (int)j);
-        rank += (kj > a || (kj == a && ij < bi)) ? 1u : 0u;
+    bstar = F.s_u[12];
+    const uint32_t abv = F.s_u[13];
+    if (bstar == NONE) return false;
+    whole = F.s_u[8] != 0u;
+    bracket = F.s_u[8] == 2u;
+    bext = F.s_d[5];
+    if (!whole) {   // rank the crossing bin's members
+      // the crossing bin's members
+      if (wact) {
+#pragma unroll
+        for (int u = 0; u < SR; ++u) {
+          if (((act >> u) & 1u) && bin[u] == bstar) {
+            const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+            if (at < (uint32_t)PCAP) { F.u.s.mk[at] = key[u]; F.u.s.mi[at] = P.id[u]; }
+          }
+        }
       }
-      if (ln == 0) F.s_u[12] = NONE;   // no finite logit's key
-      if (mm && rank == need - 1u) { F.s_u[12] = a; F.s_u[13] = bi; }
+      lds_barrier();
+      const uint32_t cm = F.s_u[10];
+      if (cm > (uint32_t)PCAP) return false;
+      // wave 0 ranks the members: the (k - abv)-th in (key desc, ID asc)
+      // order is the last one E takes (the need-th exists: cm >= need >= 1)
+      if (wave() == 0) {
+        const uint32_t need = c.k - abv;
+        const uint32_t ln = lane();
+        const bool mm = ln < cm;
+        const uint32_t a = mm ? F.u.s.mk[ln] : 0u, bi = mm ? F.u.s.mi[ln] : NONE;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < cm; ++j) {
+          const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)j);
+          const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)bi, (int)j);
+          rank += (kj > a || (kj == a && ij < bi)) ? 1u : 0u;
+        }
+        if (ln == 0) F.s_u[12] = NONE;   // no finite logit's key
+        if (mm && rank == need - 1u) { F.s_u[12] = a; F.s_u[13] = bi; }
+      }
+      lds_barrier();
+      kap = F.s_u[12];
+      idk = F.s_u[13];
+      if (kap == NONE) return false;   // not reached: the members hold the need-th
     }
-    lds_barrier();
-    kap = F.s_u[12];
-    idk = F.s_u[13];
-    if (kap == NONE) return false;   // not reached: the members hold the need-th
   }
 
   // ---- E, its f32 mass, and P ----------------------------------------------
@@ -2164,7 +2197,9 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
         pm = sd >= L;
         if (fabs(sd - L) < X.Lclose) unc = true;
       }
-      const bool in = X.k_path ? (key[u] > kap || (key[u] == kap && P.id[u] <= idk)) : pm;
+      const bool in = !X.k_path ? pm
+                      : whole ? bin[u] <= bstar
+                              : (key[u] > kap || (key[u] == kap && P.id[u] <= idk));
       if (!in) continue;
       ++ne;
       const float y = (l - Mf) * c2;   // <= 0
@@ -2250,6 +2285,11 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
       Q.esum_err = 1.01 * ((0x1p-22 + (double)(SR + 1) * 0x1p-24) * Q.esum +
                            0.6931471805599453 * 3.0001 * 0x1p-24 * eab) +
                    (double)Q.ne * 0x1p-120 + sum_bound(Q.esum, Q.ne, 8.0);
+      if (bracket) {
+        // E's mass lies in [sum - extra, sum]: take the middle
+        Q.esum -= 0.5 * bext;
+        Q.esum_err += 0.5 * bext * 1.0001;
+      }
       Q.unc = __builtin_amdgcn_ballot_w64(wl && F.ru[ln][2] != 0u) != 0ull;
       Q.wlo = need_wlo ? (double)okey_value(~wave_max_u32(wl ? ~okey(F.red_f[ln]) : 0u)) : 0.0;
       // For the workgroup finish of a large P: theta, and whether the
