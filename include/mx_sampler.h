@@ -17,6 +17,10 @@
  *                                (crates/app/cli/src/chat_generation.rs:2213-2231) and the
  *                                grammar-mask consumption of
  *                                crates/core/engine/src/constraint.rs:793-806, 895-932.
+ *   mxs_sample_race           <- Qwen3TokenPicks::start_with with Qwen3Selection::Race
+ *                                (picks.rs:40-66, 296-336) and its host settle, SamplingPolicy::
+ *                                sample under Entropy::Race (qwen_forward.rs:221-278, 310-341)
+ *                                -> sample_race (crates/core/engine/src/sampling/race.rs:114-147).
  *   mxs_logsoftmax_topn       <- token_logprob (crates/app/cli/src/chat_turn.rs:506-563) and
  *                                Qwen3RowCandidates (picks.rs:97-129).
  *   mxs_spec_verify           <- engine::speculative::accept_or_resample
@@ -128,6 +132,22 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
 int mxs_destroy(mxs_ctx* ctx);
 int mxs_set_stream(mxs_ctx* ctx, void* stream);
 int mxs_sample(mxs_ctx* ctx, const mxs_batch* batch, const mxs_out* out);
+/* race-v2 keys (engine::sampling::race::RaceKey plus the generated
+ * position, race.rs:29-37, 66-80): device arrays of `rows` entries. */
+typedef struct {
+  const uint64_t* seed;           /* required: the request seed of each row */
+  const uint32_t* choice;         /* NULL => 0: the completion index within the request */
+  const uint32_t* position;       /* required: the generated position of each row's token */
+} mxs_race;
+
+/* As mxs_sample, but every non-greedy row takes the race-v2 winner over its
+ * kept set: the kept token with the largest f64(adjusted logit) / T +
+ * Gumbel(Philox4x32-10 bits of (seed, choice, position, token)), lowest ID on
+ * ties.  batch->uniform is ignored (race-v2 draws none).  sampling_logprob is
+ * the winner's log probability over the kept set at temperature T.  Status 1
+ * when the two best scores are too close to order against the reference's
+ * libm.  out->kept_bits may be NULL (the context's scratch holds the set). */
+int mxs_sample_race(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const mxs_out* out);
 int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dtype, uint32_t rows,
                         uint32_t vocab, uint64_t row_stride, uint32_t n, int32_t* ids,
                         double* logprobs, double* maximum, double* log_normalizer, int32_t* status);

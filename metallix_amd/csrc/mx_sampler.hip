@@ -289,14 +289,7 @@ __device__ __forceinline__ uint32_t chunk_mode(const RowCfg& c, uint32_t V) {
 // Logit-bias and penalty stage for one token (BUILD-DEFINED semantics, f32,
 // every operation rounded separately).
 __device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, float bias, const RowCfg& c) {
-  if (slot) l = l + bias;
-  if (cnt) {
-    l = l < 0.0f ? l * c.rep : l / c.rep;
-    const float cf = (float)cnt * c.freq;
-    l = l - cf;
-    l = l - c.pres;
-  }
-  return l;
+  return penalize_logit(l, cnt, slot != 0u, bias, c.rep, c.pres, c.freq);
 }
 
 // Re-derives adjusted logits and legality for `cnt` tokens starting at `id0`
@@ -4003,9 +3996,14 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->spec_scratch, mxs::spec_scratch_bytes(max_rows));
+  e = e ? e : hipMalloc(&ctx->race_ctr, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->race_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->race_scratch, mxs::race_scratch_bytes(max_rows, max_vocab));
+  e = e ? e : hipMalloc(&ctx->race_kept, (size_t)max_rows * ((max_vocab + 31u) / 32u) * sizeof(uint32_t));
   const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;
   e = e ? e : hipMalloc(&ctx->d_zero_u32, nr * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->d_one_f64, nr * sizeof(double));
+  e = e ? e : hipMalloc(&ctx->d_race_u, nr * sizeof(double));
   e = e ? e : hipMalloc(&ctx->d_zero_f64, nr * sizeof(double));
   e = e ? e : hipMalloc(&ctx->d_one_f32, nr * sizeof(float));
   e = e ? e : hipMalloc(&ctx->d_zero_f32, nr * sizeof(float));
@@ -4019,6 +4017,8 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
     e = e ? e : hipMemset(ctx->d_mask_ones, 0xff, nwords * sizeof(uint32_t));
     e = e ? e : hipMemcpy(ctx->d_one_f64, one64.data(), nr * sizeof(double), hipMemcpyHostToDevice);
     e = e ? e : hipMemcpy(ctx->d_one_f32, one32.data(), nr * sizeof(float), hipMemcpyHostToDevice);
+    const std::vector<double> race_u(nr, mxs::RACE_DRAW_UNIFORM);
+    e = e ? e : hipMemcpy(ctx->d_race_u, race_u.data(), nr * sizeof(double), hipMemcpyHostToDevice);
   }
   e = e ? e : hipDeviceSynchronize();
   hipSetDevice(prev);
@@ -4044,6 +4044,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->work.seg);
   hipFree(ctx->d_zero_u32);
   hipFree(ctx->d_one_f64);
+  hipFree(ctx->d_race_u);
   hipFree(ctx->d_zero_f64);
   hipFree(ctx->d_one_f32);
   hipFree(ctx->d_zero_f32);
@@ -4052,6 +4053,9 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->topn_scratch);
   hipFree(ctx->spec_ctr);
   hipFree(ctx->spec_scratch);
+  hipFree(ctx->race_ctr);
+  hipFree(ctx->race_scratch);
+  hipFree(ctx->race_kept);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;

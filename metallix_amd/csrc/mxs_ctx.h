@@ -13,10 +13,19 @@ namespace mxs {
 
 struct ChunkStat;
 
+// mxs_sample_race runs mxs_sample's pipeline for the kept set and discards
+// its inverse-CDF draw.  That draw still certifies itself: a uniform on a
+// CDF boundary (u = 0 always is) would flag the row uncertified.  This
+// value (the golden-ratio conjugate) keeps the draw's target off the
+// boundaries of equal-weight plateaus and, for other weights, on one only
+// with a probability of about the draw's error bound per kept token.
+constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
+
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);
 size_t spec_scratch_bytes(uint32_t max_rows);
+size_t race_scratch_bytes(uint32_t max_rows, uint32_t max_vocab);
 constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8), one per row
 
 // Device scratch of mxs_sample, sized for the context's limits.
@@ -55,6 +64,13 @@ struct mxs_ctx {
   // mxs_spec_verify: per-position arrival counters and per-chunk results
   uint32_t* spec_ctr = nullptr;
   void* spec_scratch = nullptr;
+  // mxs_sample_race: per-row arrival counters, per-chunk results and the
+  // kept set when the caller asks for none
+  uint32_t* race_ctr = nullptr;
+  void* race_scratch = nullptr;
+  uint32_t* race_kept = nullptr;
+  // the uniform of the inverse-CDF draw mxs_sample_race discards (below)
+  double* d_race_u = nullptr;
   std::string last_error;
 };
 

@@ -276,6 +276,22 @@ __device__ __forceinline__ float vmax(float a, float b) {
   return r;
 }
 
+// Logit-bias and penalty stage for one token (BUILD-DEFINED semantics, f32,
+// every operation rounded separately): bias, then for a token seen cnt > 0
+// times the repetition penalty once (l < 0 ? l * rep : l / rep), then
+// - cnt * freq, then - pres.
+__device__ __forceinline__ float penalize_logit(float l, uint32_t cnt, bool has_bias, float bias, float rep,
+                                                float pres, float freq) {
+  if (has_bias) l = l + bias;
+  if (cnt) {
+    l = l < 0.0f ? l * rep : l / rep;
+    const float cf = (float)cnt * freq;
+    l = l - cf;
+    l = l - pres;
+  }
+  return l;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 template <typename In>

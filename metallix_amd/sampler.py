@@ -62,6 +62,10 @@ class MxsOut(ctypes.Structure):
     ]
 
 
+class MxsRace(ctypes.Structure):
+    _fields_ = [("seed", _vp), ("choice", _vp), ("position", _vp)]
+
+
 # Exported symbols and their prototypes, as declared in include/mx_sampler.h.
 PROTOTYPES = {
     "mxs_abi_version": (ctypes.c_int, []),
@@ -70,6 +74,8 @@ PROTOTYPES = {
     "mxs_destroy": (ctypes.c_int, [_vp]),
     "mxs_set_stream": (ctypes.c_int, [_vp, _vp]),
     "mxs_sample": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), ctypes.POINTER(MxsOut)]),
+    "mxs_sample_race": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), ctypes.POINTER(MxsRace),
+                                       ctypes.POINTER(MxsOut)]),
     "mxs_logsoftmax_topn": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
                                            ctypes.c_uint64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "mxs_spec_verify": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
@@ -158,11 +164,14 @@ class Sampler:
     def sample(self, logits, temperature, *, top_k=None, top_p=None, min_p=None, repetition=None,
                presence=None, frequency=None, uniform=None, history=None, bias=None, mask=None,
                tokenizer_vocab=None, debug: bool = False, out: Optional[SampleResult] = None,
-               vocab: Optional[int] = None) -> SampleResult:
+               vocab: Optional[int] = None, race=None) -> SampleResult:
         """Queues one batched pick.  All tensor arguments live on the GPU.
 
         history: (offsets u32[rows+1], ids u32) CSR; bias: (offsets, ids, values f32);
         mask: u32[rows, mask_stride].
+        race: (seed u64 as int64[rows], choice u32[rows] or None, position u32[rows])
+        selects race-v2 (Qwen3Selection::Race, picks.rs:40-66) instead of the
+        inverse-CDF draw; `uniform` is then unused.
         """
         torch = self.torch
         rows = logits.shape[0]
@@ -207,6 +216,13 @@ class Sampler:
         o.kept_count = _ptr(out.kept_count)
         o.adjusted = _ptr(out.adjusted)
         o.kept_bits = _ptr(out.kept_bits)
+        if race is not None:
+            r = MxsRace()
+            r.seed, r.choice, r.position = _ptr(race[0]), _ptr(race[1]), _ptr(race[2])
+            self._check(self.lib.mxs_sample_race(self.ctx, ctypes.byref(b), ctypes.byref(r), ctypes.byref(o)),
+                        "mxs_sample_race")
+            self._keep = (b, o, r)
+            return out
         self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
         self._keep = (b, o)
         return out
@@ -215,7 +231,7 @@ class Sampler:
         """Pre-built launch for repeated picks with the same parameters and
         outputs: returns f(logits) that only swaps the logits pointer."""
         out = self.sample(logits, **kw)
-        b, o = self._keep
+        b, o = self._keep[:2]
         bp, op = ctypes.byref(b), ctypes.byref(o)
         fn, ctx = self.lib.mxs_sample, self.ctx
 
