@@ -90,6 +90,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--race", action="store_true", help="also time race-v2 picks (mxs_sample_race)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device copies (scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -208,11 +209,52 @@ def main():
             "device": props.name,
         },
     }
+    if args.race:
+        res["race"] = race_bench(torch, s, stream, bufs, kw, b, args.steps, args.warmup)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(b, args.cpu_seconds)
     else:
         res["cpu_baseline"] = None
     print(json.dumps(res), flush=True)
+
+
+def race_bench(torch, s, stream, bufs, kw, b, steps, warmup):
+    """race-v2 picks (mxs_sample_race) on the same resident config-2 logits:
+    the batch's own rules (a kept set of 1 to ~600 tokens per row), and every
+    row a whole-row race (top_k 0, top_p 1, min_p 0: the race kernel scores
+    all V tokens).  Time per call, back to back, from events on the stream."""
+    import numpy as np
+
+    from metallix_amd import synth
+
+    st = synth.Stream(0x72616365)
+    dev = bufs[0].device
+    race = (torch.from_numpy(st.u64(b.rows).view(np.int64)).to(dev),
+            None, torch.from_numpy(np.arange(b.rows, dtype=np.int32)).to(dev))
+    whole = dict(kw)
+    whole["top_k"] = torch.zeros_like(kw["top_k"])
+    whole["top_p"] = torch.ones_like(kw["top_p"])
+    whole["min_p"] = torch.zeros_like(kw["min_p"])
+    res = {}
+    for name, args_ in (("cfg2_rules", kw), ("whole_row", whole)):
+        with torch.cuda.stream(stream):
+            launch = s.launcher(bufs[0], race=race, **args_)
+            for i in range(warmup):
+                launch(bufs[i % NBUF])
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for i in range(steps):
+                launch(bufs[i % NBUF])
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        stat = launch.out.status.cpu().numpy()
+        assert (stat >= 0).all(), f"row errors in the race benchmark: {stat}"
+        res[name] = {"ms_per_step": round(ms, 6), "rows_per_s": round(b.rows / (ms / 1e3), 1),
+                     "uncertified_rows": int((stat == 1).sum())}
+    return res
 
 
 if __name__ == "__main__":

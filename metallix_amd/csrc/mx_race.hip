@@ -120,6 +120,29 @@ __device__ __forceinline__ double gumbel_from_bits(uint64_t bits) {
   return -log(e);
 }
 
+// The same noise in f32, for screening: E from the bits' f32 image (relative
+// error about 2^-22 either branch; the w branch keeps log1p's precision for
+// small w), then f32 logs (about 2 ulp each).  |g32 - g| < 1e-5.
+__device__ __forceinline__ float gumbel32(uint64_t bits) {
+  const uint32_t hi = (uint32_t)(bits >> 32), lo = (uint32_t)bits;
+  float e;
+  if (!(hi >> 31)) {
+    const float w = ((float)hi + ((float)lo + 0.5f) * 0x1p-32f) * 0x1p-32f;
+    e = -log1pf(-w);
+  } else {
+    const float v = ((float)(~hi) + ((float)(~lo) + 0.5f) * 0x1p-32f) * 0x1p-32f;
+    e = -logf(v);
+  }
+  return -logf(e);
+}
+
+// Bound on |s32 - (l / T + g - m / T)| for the f32 screening score
+// s32 = (l - m) * (1/T)_f32 + g32 (m the chunk's largest kept logit):
+// (l - m) / T <= 0 and g <= 45.1 give |(l - m) / T| <= |s32| + 46, whose
+// three f32 roundings cost under 2^-22.4 (|s32| + 46); plus |g32 - g| and
+// the final rounding.  The form below is several times larger than that.
+__device__ __forceinline__ float err32(float s32) { return 0x1p-10f + fabsf(s32) * 0x1p-19f; }
+
 // Certification margin between the two best device scores.
 __device__ __forceinline__ double race_margin(double s1, double s2) {
   return 0x1p-46 * (64.0 + fabs(s1) + fabs(s2));
@@ -145,11 +168,12 @@ __device__ __forceinline__ void best_merge(Best& a, double s1, double s2, uint32
 
 struct RaceSmem {
   uint32_t cnt[RT];          // history counts of the chunk's tokens
-  float redf[RNW];
+  float redf[RNW], redf2[RNW];
   double redd[RNW];
   double b1[RNW], b2[RNW];
   uint32_t bid[RNW];
   float bl[RNW];
+  float ss[RT];              // f32 screening scores of the chunk's kept tokens
   uint32_t any, last;
 };
 
@@ -214,14 +238,41 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     for (int i = 1; i < RNW; ++i) m = fmaxf(m, S.redf[i]);
     const uint64_t seed = A.seed[row];
     const uint32_t choice = A.choice[row], position = A.position[row];
+    const float invT32 = (float)(1.0 / T);
+    // f32 screening scores and the f64 mass
+    float smax = -INFINITY;
     for (uint32_t r = word; r; r &= r - 1u) {
       const uint32_t id = id0 + (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
       mass += exp(((double)l - (double)m) / T);
+      const float s32 = (l - m) * invT32 + gumbel32(race_bits(seed, choice, position, id));
+      S.ss[id - base] = s32;
+      smax = fmaxf(smax, s32);
+    }
+    smax = wave_max(smax);
+    if (lane() == 0) S.redf2[wave()] = smax;
+    __syncthreads();
+    smax = S.redf2[0];
+    for (int i = 1; i < RNW; ++i) smax = fmaxf(smax, S.redf2[i]);
+    // Exact f64 scores for tokens whose f32 upper bound reaches the chunk
+    // maximum's lower bound (less 2^-10).  A token screened out scores below
+    // that threshold plus m / T, at least 2^-10 under the winner: the bound
+    // stands in for its score as a runner-up.
+    // (No screen when 1/T overflows f32: every kept token is then scored in
+    // f64; the finisher has already checked that (l - M) / T is finite.)
+    const bool screen = __builtin_isfinite(invT32) && __builtin_isfinite(smax);
+    const float cut = smax - err32(smax) - 0x1p-10f;
+    uint32_t out = 0u;
+    for (uint32_t r = word; r; r &= r - 1u) {
+      const uint32_t id = id0 + (uint32_t)__builtin_ctz(r);
+      const float s32 = S.ss[id - base];
+      if (screen && !(s32 + err32(s32) >= cut)) { ++out; continue; }
+      const float l = adjusted(id);
       const double s = (double)l / T + gumbel_from_bits(race_bits(seed, choice, position, id));
       if (!isfinite(s)) flags |= RF_NONFINITE;
       best_merge(b, s, -INFINITY, id, l);
     }
+    if (out) b.s2 = fmax(b.s2, (double)cut + (double)m / T);
   }
   // block reductions: mass, flags, best
   mass = wave_sum(mass);
@@ -257,44 +308,57 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     st_dev(&p->flags, flags | (any ? RF_ANY : 0u));
     wait_mem();
     const uint32_t prev = __hip_atomic_fetch_add(&A.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (prev != A.C - 1u) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the merge's loads stay after the arrival
-    // ---- the row's last chunk: merge in chunk (token ID) order ----------
-    st_dev(&A.ctr[row], 0u);
-    uint32_t rf = 0u;
-    float M = -INFINITY;
-    for (uint32_t q = 0; q < A.C; ++q) {
-      const RaceStat* s = &A.stat[(uint64_t)row * A.C + q];
-      const uint32_t f = ld_dev(&s->flags);
-      rf |= f;
-      if (f & RF_ANY) M = fmaxf(M, ld_dev(&s->m));
-    }
-    Best r{-INFINITY, -INFINITY, NONE, 0.0f};
-    double S_ = 0.0;
-    for (uint32_t q = 0; q < A.C; ++q) {
-      const RaceStat* s = &A.stat[(uint64_t)row * A.C + q];
-      if (!(ld_dev(&s->flags) & RF_ANY)) continue;
-      S_ += ld_dev(&s->mass) * exp(((double)ld_dev(&s->m) - (double)M) / T);
-      best_merge(r, ld_dev(&s->best), ld_dev(&s->second), ld_dev(&s->id), ld_dev(&s->lbest));
-    }
-    if (!(rf & RF_ANY)) {
-      A.status[row] = MXS_ROW_EMPTY_SUPPORT;
-      A.token[row] = -1;
-      if (A.logprob) A.logprob[row] = 0.0;
-      return;
-    }
-    if (rf & RF_NONFINITE) {
-      A.status[row] = MXS_ROW_INVALID_TEMPERATURE;
-      A.token[row] = -1;
-      if (A.logprob) A.logprob[row] = 0.0;
-      return;
-    }
-    // a lone kept token (no runner-up) needs no margin
-    const bool certified = r.s2 == -INFINITY || r.s1 - r.s2 > race_margin(r.s1, r.s2);
-    A.token[row] = (int32_t)r.id;
-    A.status[row] = (st0 == MXS_ROW_OK && certified) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED;
-    if (A.logprob) A.logprob[row] = ((double)r.l - (double)M) / T - log(S_);
+    S.last = prev == A.C - 1u ? 1u : 0u;
   }
+  __syncthreads();
+  if (!S.last || wave() != 0) return;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the merge's loads stay after the arrival
+  // ---- the row's last chunk: wave 0 merges the chunks' records, lane q
+  // taking chunks q, q + 64, ... (all loads in flight at once) ------------
+  const uint32_t ln = lane();
+  if (ln == 0) st_dev(&A.ctr[row], 0u);
+  const RaceStat* rs = &A.stat[(uint64_t)row * A.C];
+  uint32_t rf = 0u;
+  float M = -INFINITY;
+  for (uint32_t q = ln; q < A.C; q += 64u) {
+    const uint32_t f = ld_dev(&rs[q].flags);
+    rf |= f;
+    if (f & RF_ANY) M = fmaxf(M, ld_dev(&rs[q].m));
+  }
+  rf = wave_or_u32(rf);
+  M = wave_max(M);
+  Best r{-INFINITY, -INFINITY, NONE, 0.0f};
+  double S_ = 0.0;
+  for (uint32_t q = ln; q < A.C; q += 64u) {
+    if (!(ld_dev(&rs[q].flags) & RF_ANY)) continue;
+    S_ += ld_dev(&rs[q].mass) * exp(((double)ld_dev(&rs[q].m) - (double)M) / T);
+    best_merge(r, ld_dev(&rs[q].best), ld_dev(&rs[q].second), ld_dev(&rs[q].id), ld_dev(&rs[q].lbest));
+  }
+  S_ = wave_sum(S_);
+  for (int o = 32; o > 0; o >>= 1) {
+    const double s1 = __shfl_xor(r.s1, o), s2 = __shfl_xor(r.s2, o);
+    const uint32_t id = __shfl_xor(r.id, o);
+    const float l = __shfl_xor(r.l, o);
+    best_merge(r, s1, s2, id, l);
+  }
+  if (ln != 0) return;
+  if (!(rf & RF_ANY)) {
+    A.status[row] = MXS_ROW_EMPTY_SUPPORT;
+    A.token[row] = -1;
+    if (A.logprob) A.logprob[row] = 0.0;
+    return;
+  }
+  if (rf & RF_NONFINITE) {
+    A.status[row] = MXS_ROW_INVALID_TEMPERATURE;
+    A.token[row] = -1;
+    if (A.logprob) A.logprob[row] = 0.0;
+    return;
+  }
+  // a lone kept token (no runner-up) needs no margin
+  const bool certified = r.s2 == -INFINITY || r.s1 - r.s2 > race_margin(r.s1, r.s2);
+  A.token[row] = (int32_t)r.id;
+  A.status[row] = (st0 == MXS_ROW_OK && certified) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED;
+  if (A.logprob) A.logprob[row] = ((double)r.l - (double)M) / T - log(S_);
 }
 
 }  // namespace mxs
@@ -310,7 +374,7 @@ extern "C" int mxs_sample_race(mxs_ctx* ctx, const mxs_batch* b, const mxs_race*
   b2.uniform = ctx->d_race_u;
   mxs_out o2 = *o;
   if (!o2.kept_bits) o2.kept_bits = ctx->race_kept;
-  int rc = mxs_sample(ctx, &b2, &o2);
+  int rc = mxs::sample_launch(ctx, &b2, &o2, true);
   if (rc != MXS_OK) return rc;
   mxs::RaceArgs A;
   A.logits = b->logits;

@@ -85,6 +85,7 @@ struct SampleArgs {
   uint64_t* timing;    // optional phase timestamps (diagnostics), see mxs_debug_set_timing
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
   uint32_t epoch;      // this call's tag for Work::rowx (never 0)
+  uint32_t nodraw;     // keep-all rows skip the inverse-CDF draw (race-v2 calls)
 };
 
 // Phase timestamps for diagnostics: wall clock (100 MHz) at fixed points of
@@ -292,20 +293,24 @@ __device__ __forceinline__ float adjust(float l, uint32_t cnt, uint32_t slot, fl
   return penalize_logit(l, cnt, slot != 0u, bias, c.rep, c.pres, c.freq);
 }
 
-// Re-derives adjusted logits and legality for `cnt` tokens starting at `id0`
-// (one lane per token, cnt <= 64, one wave).  Used by the finisher to locate
-// a draw inside a 256-token segment without the chunk's registers.
+// Re-derives the adjusted logit and legality of token `id`, whose history
+// count `cnt` the caller supplies.  Used by the finisher to locate a draw
+// inside a 256-token segment without the chunk's registers.  Bias ids are
+// strictly increasing (the chunk pass rejects the row otherwise): binary
+// search.
 template <typename In>
 __device__ __forceinline__ void rederive_token(const SampleArgs& A, const RowCfg& c, uint32_t row, uint32_t id,
-                               float* l_out, bool* legal_out) {
+                                               uint32_t cnt, float* l_out, bool* legal_out) {
   const mxs_batch& b = A.b;
   const In* p = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
-  float l = Quad<In>::one(p + id);
-  uint32_t cnt = 0, slot = 0;
-  for (uint32_t h = c.hb; h < c.he; ++h) cnt += b.history_ids[h] == id;
-  for (uint32_t j = c.bb; j < c.be; ++j)
-    if (b.bias_ids[j] == id) slot = j - c.bb + 1;
-  *l_out = adjust(l, cnt, slot, slot ? b.bias_values[c.bb + slot - 1] : 0.0f, c);
+  const float l = Quad<In>::one(p + id);
+  uint32_t lo = c.bb, hi = c.be;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (b.bias_ids[mid] < id) lo = mid + 1u; else hi = mid;
+  }
+  const bool hasb = lo < c.be && b.bias_ids[lo] == id;
+  *l_out = penalize_logit(l, cnt, hasb, hasb ? b.bias_values[lo] : 0.0f, c.rep, c.pres, c.freq);
   const uint32_t w = b.mask_words[(uint64_t)row * b.mask_stride + (id >> 5)];
   *legal_out = ((w >> (id & 31)) & 1u) && id < b.tokenizer_vocab;
 }
@@ -2330,6 +2335,24 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
 // ---------------------------------------------------------------------------
 // The row finisher.  Runs in the last chunk workgroup of a row, after every
 // chunk published its statistics and candidates.
+// The kept set of a keep-all row: every legal token.
+__device__ __forceinline__ void keepall_bits(const SampleArgs& A, uint32_t row, uint32_t* kbits, uint32_t nwords,
+                                             uint32_t V) {
+  if (!kbits) return;
+  const mxs_batch& b = A.b;
+  for (uint32_t q = threadIdx.x; q < nwords; q += FT) {
+    uint32_t wv = 0xffffffffu;
+    if (q == nwords - 1 && (V & 31u)) wv = (1u << (V & 31u)) - 1u;
+    if (A.masked) {
+      wv &= b.mask_words[(uint64_t)row * b.mask_stride + q];
+      const uint32_t tv = b.tokenizer_vocab;
+      if (q * 32u >= tv) wv = 0u;
+      else if (q * 32u + 32u > tv) wv &= (1u << (tv - q * 32u)) - 1u;
+    }
+    kbits[q] = wv;
+  }
+}
+
 template <typename In, bool XD>
 __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
                            uint64_t rbase, double invT, const FinLoads& P) {
@@ -2429,6 +2452,11 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     for (uint32_t q = 0; q < C; ++q)
       if (F.st[q].nlegal && F.st[q].minkey < mink) mink = F.st[q].minkey;
     if (!isfinite(((double)okey_value(mink) - M) / c.T)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+    if (A.nodraw) {   // race-v2: the kept set is every legal token; the race kernel picks
+      write_result(X, 0, -1, 0.0, nlegal);
+      keepall_bits(A, row, kbits, nwords, V);
+      return;
+    }
     const uint32_t segs_per_chunk = A.per * NW;   // the chunk kernel's 256-token (slice, wave) segments
     const uint32_t nseg = C * segs_per_chunk;
     double part = 0.0;
@@ -2478,7 +2506,18 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       const uint32_t q = seg / segs_per_chunk, r = seg % segs_per_chunk;
       const uint32_t i = r / NW, w = r % NW;
       const uint32_t q1 = min(V, q * A.CH + A.CH);
-      const uint32_t id0 = q * A.CH + i * SLICE + w * 256u + lane() * 4u;
+      const uint32_t seg0 = q * A.CH + i * SLICE + w * 256u;
+      const uint32_t id0 = seg0 + lane() * 4u;
+      // the segment's history counts, counted by the whole wave in LDS
+      // (one coalesced pass over the row's history)
+      uint32_t* scnt = F.eidx;
+      for (uint32_t j = lane(); j < 256u; j += 64u) scnt[j] = 0u;
+      wave_lds_sync();
+      for (uint32_t h = c.hb + lane(); h < c.he; h += 64u) {
+        const uint32_t d = b.history_ids[h] - seg0;
+        if (d < 256u) atomicAdd(&scnt[d], 1u);
+      }
+      wave_lds_sync();
       double wl[4], sh[4];
       double lsum = 0.0;
       for (int e = 0; e < 4; ++e) {
@@ -2488,7 +2527,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
         if (id < q1) {
           float l;
           bool lg;
-          rederive_token<In>(A, c, row, id, &l, &lg);
+          rederive_token<In>(A, c, row, id, scnt[lane() * 4u + (uint32_t)e], &l, &lg);
           if (lg) { sh[e] = ((double)l - M) / c.T; wl[e] = exp_neg(sh[e]); }
         }
         lsum += wl[e];
@@ -2537,19 +2576,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
     near = near || F.s_u[4] != 0u;
     write_result(X, near ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, F.s_d[1] - log(total), nlegal);
-    if (kbits) {
-      for (uint32_t q = tid; q < nwords; q += FT) {
-        uint32_t wv = 0xffffffffu;
-        if (q == nwords - 1 && (V & 31u)) wv = (1u << (V & 31u)) - 1u;
-        if (A.masked) {
-          wv &= b.mask_words[(uint64_t)row * b.mask_stride + q];
-          const uint32_t tv = b.tokenizer_vocab;
-          if (q * 32u >= tv) wv = 0u;
-          else if (q * 32u + 32u > tv) wv &= (1u << (tv - q * 32u)) - 1u;
-        }
-        kbits[q] = wv;
-      }
-    }
+    keepall_bits(A, row, kbits, nwords, V);
     return;
   }
 
@@ -3931,6 +3958,83 @@ __global__ __launch_bounds__(FT) void finish_kernel(
 // Host side: context, validation, launch.
 // ===========================================================================
 
+namespace mxs {
+
+int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw) {
+  if (!ctx || !b || !o) return MXS_EINVAL;
+  if (b->rows == 0) return MXS_OK;
+  if (!b->logits || !b->temperature || !o->token || !o->status) return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
+  if (b->rows > ctx->max_rows || b->vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
+  if (b->vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
+  if (b->dtype != MXS_F32 && b->dtype != MXS_BF16) return fail(ctx, MXS_EINVAL, "dtype must be MXS_F32 or MXS_BF16");
+  if (b->row_stride < b->vocab || (b->row_stride & 3u)) return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");
+  const size_t align = b->dtype == MXS_F32 ? 16 : 8;
+  if (((uintptr_t)b->logits) % align) return fail(ctx, MXS_EINVAL, "logits must be 16-byte (f32) or 8-byte (bf16) aligned");
+  if (b->mask_words && b->mask_stride < (b->vocab + 31u) / 32u) return fail(ctx, MXS_EINVAL, "mask_stride must be >= ceil(vocab / 32)");
+  if ((b->history_offsets == nullptr) != (b->history_ids == nullptr)) return fail(ctx, MXS_EINVAL, "history offsets and ids go together");
+  if ((b->bias_offsets == nullptr) != (b->bias_ids == nullptr) || (b->bias_offsets && !b->bias_values)) return fail(ctx, MXS_EINVAL, "bias offsets, ids and values go together");
+  mxs::SampleArgs A;
+  A.b = *b;
+  A.o = *o;
+  A.w = ctx->work;
+  A.timing = ctx->timing;
+  if (++ctx->epoch == 0u) ctx->epoch = 1u;   // 0 is the zeroed scratch's tag
+  A.epoch = ctx->epoch;
+  A.nodraw = nodraw ? 1u : 0u;
+  A.masked = b->mask_words != nullptr;
+  if (!A.masked) {
+    A.b.mask_words = ctx->d_mask_ones;
+    A.b.mask_stride = 0;
+    A.b.tokenizer_vocab = b->vocab;
+  }
+  if (!b->history_offsets) { A.b.history_offsets = ctx->d_zero_u32; A.b.history_ids = ctx->d_zero_u32; }
+  if (!b->bias_offsets) { A.b.bias_offsets = ctx->d_zero_u32; A.b.bias_ids = ctx->d_zero_u32; A.b.bias_values = ctx->d_zero_f32; }
+  const double* p_tp = b->top_p ? b->top_p : ctx->d_one_f64;
+  const double* p_mp = b->min_p ? b->min_p : ctx->d_zero_f64;
+  const double* p_u = b->uniform ? b->uniform : ctx->d_zero_f64;
+  const uint32_t* p_k = b->top_k ? b->top_k : ctx->d_zero_u32;
+  const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
+  const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
+  const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
+  const mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
+  const uint32_t C = L.C;
+  A.C = L.C;
+  A.CH = L.CH;
+  A.per = L.per;
+  if (A.per > (uint32_t)mxs::PER_MAX || C > (uint32_t)mxs::MAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
+  const dim3 grid(8u * C, (b->rows + 7u) / 8u);
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  // Split (default): the chunk pass, then the row finisher as a second
+  // kernel (stream order makes the chunk results visible).  Fused: one
+  // kernel; each row's last chunk finishes the row, the chunks' results
+  // handed over through device-scope stores and a per-row counter.
+#define MXS_ARGS A, b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets
+  if (!ctx->split) {
+    if (b->dtype == MXS_F32)
+      hipLaunchKernelGGL((mxs::sample_kernel<float, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    else
+      hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
+  } else if (b->dtype == MXS_F32) {
+    hipLaunchKernelGGL((mxs::sample_kernel<float, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
+    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
+  } else {
+    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
+    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
+  }
+#undef MXS_ARGS
+  hipError_t e = hipGetLastError();
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");
+  return MXS_OK;
+}
+
+}  // namespace mxs
+
 extern "C" {
 
 int mxs_abi_version(void) { return MXS_ABI_VERSION; }
@@ -4088,76 +4192,6 @@ int mxs_sync(mxs_ctx* ctx) {
 
 const char* mxs_last_error(const mxs_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
 
-int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) {
-  if (!ctx || !b || !o) return MXS_EINVAL;
-  if (b->rows == 0) return MXS_OK;
-  if (!b->logits || !b->temperature || !o->token || !o->status) return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
-  if (b->rows > ctx->max_rows || b->vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
-  if (b->vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
-  if (b->dtype != MXS_F32 && b->dtype != MXS_BF16) return fail(ctx, MXS_EINVAL, "dtype must be MXS_F32 or MXS_BF16");
-  if (b->row_stride < b->vocab || (b->row_stride & 3u)) return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");
-  const size_t align = b->dtype == MXS_F32 ? 16 : 8;
-  if (((uintptr_t)b->logits) % align) return fail(ctx, MXS_EINVAL, "logits must be 16-byte (f32) or 8-byte (bf16) aligned");
-  if (b->mask_words && b->mask_stride < (b->vocab + 31u) / 32u) return fail(ctx, MXS_EINVAL, "mask_stride must be >= ceil(vocab / 32)");
-  if ((b->history_offsets == nullptr) != (b->history_ids == nullptr)) return fail(ctx, MXS_EINVAL, "history offsets and ids go together");
-  if ((b->bias_offsets == nullptr) != (b->bias_ids == nullptr) || (b->bias_offsets && !b->bias_values)) return fail(ctx, MXS_EINVAL, "bias offsets, ids and values go together");
-  mxs::SampleArgs A;
-  A.b = *b;
-  A.o = *o;
-  A.w = ctx->work;
-  A.timing = ctx->timing;
-  if (++ctx->epoch == 0u) ctx->epoch = 1u;   // 0 is the zeroed scratch's tag
-  A.epoch = ctx->epoch;
-  A.masked = b->mask_words != nullptr;
-  if (!A.masked) {
-    A.b.mask_words = ctx->d_mask_ones;
-    A.b.mask_stride = 0;
-    A.b.tokenizer_vocab = b->vocab;
-  }
-  if (!b->history_offsets) { A.b.history_offsets = ctx->d_zero_u32; A.b.history_ids = ctx->d_zero_u32; }
-  if (!b->bias_offsets) { A.b.bias_offsets = ctx->d_zero_u32; A.b.bias_ids = ctx->d_zero_u32; A.b.bias_values = ctx->d_zero_f32; }
-  const double* p_tp = b->top_p ? b->top_p : ctx->d_one_f64;
-  const double* p_mp = b->min_p ? b->min_p : ctx->d_zero_f64;
-  const double* p_u = b->uniform ? b->uniform : ctx->d_zero_f64;
-  const uint32_t* p_k = b->top_k ? b->top_k : ctx->d_zero_u32;
-  const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
-  const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
-  const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
-  const mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
-  const uint32_t C = L.C;
-  A.C = L.C;
-  A.CH = L.CH;
-  A.per = L.per;
-  if (A.per > (uint32_t)mxs::PER_MAX || C > (uint32_t)mxs::MAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
-  const dim3 grid(8u * C, (b->rows + 7u) / 8u);
-  int prev = 0;
-  hipGetDevice(&prev);
-  if (prev != ctx->device) hipSetDevice(ctx->device);
-  // Split (default): the chunk pass, then the row finisher as a second
-  // kernel (stream order makes the chunk results visible).  Fused: one
-  // kernel; each row's last chunk finishes the row, the chunks' results
-  // handed over through device-scope stores and a per-row counter.
-#define MXS_ARGS A, b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets
-  if (!ctx->split) {
-    if (b->dtype == MXS_F32)
-      hipLaunchKernelGGL((mxs::sample_kernel<float, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    else
-      hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-  } else if (b->dtype == MXS_F32) {
-    hipLaunchKernelGGL((mxs::sample_kernel<float, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
-  } else {
-    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
-  }
-#undef MXS_ARGS
-  hipError_t e = hipGetLastError();
-  if (prev != ctx->device) hipSetDevice(prev);
-  if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");
-  return MXS_OK;
-}
+int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) { return mxs::sample_launch(ctx, b, o, false); }
 
 }  // extern "C"

@@ -21,6 +21,10 @@ struct ChunkStat;
 // with a probability of about the draw's error bound per kept token.
 constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 
+// mxs_sample's launch; `nodraw` makes keep-all rows skip the inverse-CDF
+// draw (token -1, status 0, the kept set still written).
+int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
+
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);

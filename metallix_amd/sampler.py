@@ -231,15 +231,22 @@ class Sampler:
         """Pre-built launch for repeated picks with the same parameters and
         outputs: returns f(logits) that only swaps the logits pointer."""
         out = self.sample(logits, **kw)
-        b, o = self._keep[:2]
+        keep = self._keep
+        b, o = keep[:2]
         bp, op = ctypes.byref(b), ctypes.byref(o)
-        fn, ctx = self.lib.mxs_sample, self.ctx
+        ctx = self.ctx
+        if len(keep) == 3:   # race-v2
+            rp, fr = ctypes.byref(keep[2]), self.lib.mxs_sample_race
+            fn, what = (lambda: fr(ctx, bp, rp, op)), "mxs_sample_race"
+        else:
+            fs = self.lib.mxs_sample
+            fn, what = (lambda: fs(ctx, bp, op)), "mxs_sample"
 
         def launch(t):
             b.logits = t.data_ptr()
-            rc = fn(ctx, bp, op)
+            rc = fn()
             if rc != 0:
-                self._check(rc, "mxs_sample")
+                self._check(rc, what)
 
         launch.out = out
         return launch

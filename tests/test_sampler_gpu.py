@@ -229,3 +229,26 @@ def test_selection_finisher_mix(torch_mod, sampler, orc, seed):
     unc = np.asarray(gpu["status"]) == 1
     assert not (unc & ~wide).any(), f"uncertified outside the wide-nucleus rows: {np.nonzero(unc & ~wide)[0]}"
     compare(b, gpu, ref, allow_uncertified=int(wide.sum()))
+
+
+def test_keepall_rows_with_history_and_bias(torch_mod, sampler, orc):
+    """Keep-all rows (top_k 0, top_p 1, min_p 0) over config 2's 2048-id
+    histories plus a logit bias: the inverse-CDF draw over the whole row
+    re-derives its segment's penalised logits (history counts, bias lookup)."""
+    from metallix_amd import synth
+
+    b = synth.config2(rows=16)
+    b.name = "keepall-history"
+    b.top_k[:] = 0
+    b.top_p[:] = 1.0
+    b.min_p[:] = 0.0
+    s = synth.Stream(0xb1a5)
+    ids, offs = [], [0]
+    for r in range(b.rows):
+        u = np.unique(s.u64(64) % np.uint64(b.vocab)).astype(np.uint32)
+        ids.append(u)
+        offs.append(offs[-1] + len(u))
+    b.bias_ids = np.concatenate(ids)
+    b.bias_offsets = np.array(offs, dtype=np.uint32)
+    b.bias_values = (3.0 * (s.uniform(len(b.bias_ids)) - 0.5)).astype(np.float32)
+    check(torch_mod, sampler, orc, b)
