@@ -143,3 +143,21 @@ def test_race_keys_move_the_pick(torch_mod, sampler, orc):
     b = synth.Batch(name="race-flat", logits=x, temperature=np.ones(R), uniform=np.zeros(R))
     gpu, _ = check(torch_mod, sampler, orc, b, 11)
     assert len(set(gpu["token"].tolist())) > R // 2
+
+
+@pytest.mark.parametrize("T", [0.01, 0.3, 20.0])
+def test_race_whole_row_temperature_extremes(torch_mod, sampler, orc, T):
+    """Whole-row races at extreme temperatures: at T = 0.01 the f32
+    screening scores reach magnitudes near 1e3 (the error bound's relative
+    term matters), at T = 20 the noise dominates and many tokens lie close
+    to the winner."""
+    from metallix_amd import synth
+
+    b = synth.config2(rows=8, vocab=151936)
+    b.name = f"race-whole-T{T}"
+    b.top_k[:] = 0
+    b.top_p[:] = 1.0
+    b.min_p[:] = 0.0
+    b.temperature[:] = T
+    gpu, _ = check(torch_mod, sampler, orc, b, 13)
+    assert (gpu["status"] == 0).all()
