@@ -29,7 +29,7 @@ def torch_mod():
 def sampler(torch_mod):
     from metallix_amd import Sampler
 
-    s = Sampler(max_rows=64, max_vocab=262144)
+    s = Sampler(max_rows=256, max_vocab=262144)
     yield s
     s.close()
 
@@ -118,6 +118,12 @@ def mixed(rows, vocab):
 def test_race_mixed_rules(torch_mod, sampler, orc, vocab, salt):
     gpu, ref = check(torch_mod, sampler, orc, mixed(24, vocab), salt)
     assert (gpu["status"] == 0).sum() == 24
+
+
+def test_race_past_64_rows(torch_mod, sampler, orc):
+    """96 rows: race row groups and race scratch past row 64."""
+    gpu, ref = check(torch_mod, sampler, orc, mixed(96, 20000), 5)
+    assert (gpu["status"] == 0).sum() == 96
 
 
 def test_race_masked_bf16(torch_mod, sampler, orc):

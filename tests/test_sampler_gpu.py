@@ -71,9 +71,11 @@ def test_config3_bf16_grammar_masks(torch_mod, sampler, orc):
 
 
 def test_config4_large_vocab(torch_mod, sampler, orc):
+    """BASELINE config 4 at its stated size, 256 x 262144."""
     from metallix_amd import synth
 
-    b = synth.config4(rows=64)
+    b = synth.config4()
+    assert b.rows == 256 and b.vocab == 262144
     check(torch_mod, sampler, orc, b)
 
 
@@ -138,6 +140,15 @@ def test_random_ties_penalties_bias(torch_mod, sampler, orc, rows, V):
 @pytest.mark.parametrize("rows,V", SHAPES)
 def test_random_masked(torch_mod, sampler, orc, rows, V):
     check(torch_mod, sampler, orc, random_batch(3000 + V, rows, V, mask=True, penalties=True))
+
+
+def test_random_batch_past_128_rows(torch_mod, sampler, orc):
+    """160 rows: grid row groups past 16 and every per-row scratch region
+    past row 128 (counters, exchange words, chunk statistics, candidates)."""
+    b = random_batch(4160, 160, 20003, penalties=True, bias=True)
+    check(torch_mod, sampler, orc, b)
+    b = random_batch(4161, 160, 20003, mask=True)
+    check(torch_mod, sampler, orc, b)
 
 
 def test_error_matrix(torch_mod, sampler, orc):

@@ -85,7 +85,8 @@ def check(torch, sampler, orc, x, n, bf16_bits=None, name=""):
 def test_config4_top20_plus_8(torch_mod, sampler, orc):
     from metallix_amd import synth
 
-    b = synth.config4(rows=64)
+    b = synth.config4()
+    assert b.rows == 256 and b.vocab == 262144
     check(torch_mod, sampler, orc, b.logits, 28, name="cfg4")
 
 
