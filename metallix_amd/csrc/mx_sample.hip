@@ -1,0 +1,1555 @@
+// mx_sample.hip -- mxs_sample: the single-kernel token pick for MI355X (gfx950).
+//
+// One launch per call.  A row of V logits is split into C balanced chunks of
+// at most 20480 tokens; one 512-thread workgroup streams a chunk into
+// registers (16-byte quads, ten per thread, every load issued up front),
+// while the row's history ids, which are issued first, build an LDS count
+// table.  As each quad lands it gets logit bias and penalties, the grammar
+// mask, the finite check and the running maximum.  The chunk then publishes
+// its maximum, picks a candidate threshold that is a proven lower bound of
+// every token the row's decision can need, writes its candidates in token-ID
+// order, and arrives on the row's counter.  The last chunk of the row to
+// arrive (agent-scope release/acquire) decides the row: greedy argmax, or
+// top-k -> top-p -> min-p -> inverse-CDF draw over the candidates.
+//
+// Reference semantics (arclabs561/metallix):
+//   nucleus_mask        crates/app/cli/src/qwen_forward.rs:474-549
+//   sample_categorical  crates/core/engine/src/sampling.rs:56-158
+//   greedy_token        crates/app/cli/src/chat_generation.rs:2213-2231
+//   masked_argmax       crates/core/engine/src/constraint.rs:895-932
+//   fill_legal_mask     crates/core/engine/src/constraint.rs:793-806
+// plus the penalty, bias, min-p and mask-with-nucleus stages this sampler
+// defines (the oracle's orc_sample_row states them executably).
+//
+// Exactness.  The reference sums f64 weights sequentially; this kernel sums
+// them in parallel.  Every comparison against such a sum (the top-p cut, the
+// draw) is taken only when its margin exceeds a rigorous bound on the
+// difference of the two computations (both summation orders, 1 ulp of
+// exp on each side, the f64 rounding of the shifted logit).  A decision
+// inside its bound leaves the row with status 1 (uncertified) and the
+// device's best decision.
+
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+
+#include "../../include/mx_sampler.h"
+#include "mxs_ctx.h"
+#include "mxs_device.h"
+#include "mxs_math.h"
+#include "mxs_pick.h"
+
+namespace mxs {
+namespace pk {
+
+constexpr double U53 = 1.1102230246251565e-16;   // 2^-53
+constexpr float U24 = 5.9604644775390625e-08f;   // 2^-24
+constexpr double LOG2E = 1.4426950408889634;
+
+// Workgroup barrier for LDS traffic only (outstanding global loads keep
+// streaming across it).
+__device__ __forceinline__ void bar() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ uint32_t popc(uint32_t x) { return (uint32_t)__builtin_popcount(x); }
+__device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+__device__ __forceinline__ float fmax_(float a, float b) { return vmax(a, b); }
+__device__ __forceinline__ double rd_lane(double v, uint32_t l) {
+  return __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, v), l));
+}
+
+// ---------------------------------------------------------------------------
+// LDS: one static pool, carved per phase.
+struct FinHdr {
+  uint32_t Mkey, flags, nl, N, thrkey, complete, gid, mink;
+  double total, terr;
+};
+constexpr uint32_t NCL = 4096;       // candidates the finisher keeps in LDS
+struct alignas(16) Lds {
+  union {
+    struct {
+      uint32_t ctab[CHMAX / 2];      // per token a u16: history count (15 bits) | bias flag (bit 15)
+      uint32_t mask[CHMAX / 32];     // the chunk's grammar-mask words
+      uint32_t bid[BCAP];            // the row's bias list (when it has at most BCAP entries)
+      float bval[BCAP];
+    } c;
+    uint32_t hist[NB];               // chunk top-k threshold histogram (after the quad loop)
+    struct {
+      float cl[NCL];                 // the finisher's working candidate list
+      uint32_t cid[NCL];
+      double bm[NB];                 // per-bin f64 mass
+      uint32_t bc[NB];               // per-bin count
+      uint32_t mkey[64], mid[64];    // gathered members of one bin
+      double mw[64];
+      uint32_t nmem;
+      uint32_t segtab[256];          // the draw segment's history counts (keep-all rows)
+    } f;
+  } u;
+  uint32_t wcnt[QMAX * PW];          // candidates per (quad round, wave)
+  uint32_t woff[QMAX * PW];
+  uint32_t ru[4 * PW];
+  unsigned long long r64[PW];
+  double rd[2 * PW];
+  uint32_t coff[MAXCH + 1];          // candidate offsets of the row's chunks
+  FinHdr h;
+  uint32_t bc[8];                    // broadcast words
+  double bd[4];
+};
+
+// ---------------------------------------------------------------------------
+// Block helpers for PT-thread workgroups (every thread participates).
+__device__ __forceinline__ uint32_t lane_() { return threadIdx.x & 63u; }
+__device__ __forceinline__ uint32_t wave_() { return threadIdx.x >> 6; }
+
+// Inclusive scan of u32 in thread order; *total receives the block total.
+__device__ __forceinline__ uint32_t bscan_u32(uint32_t v, Lds& S, uint32_t* total) {
+  const uint32_t inc = wave_scan_u32(v);
+  if (lane_() == 63u) S.ru[wave_()] = inc;
+  bar();
+  uint32_t before = 0u, all = 0u;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const uint32_t r = S.ru[i];
+    before += (uint32_t)i < wave_() ? r : 0u;
+    all += r;
+  }
+  bar();
+  *total = all;
+  return before + inc;
+}
+// Inclusive scan of f64 in thread order (waves in order after the lane tree).
+__device__ __forceinline__ double bscan_f64(double v, Lds& S, double* total) {
+  const double inc = wave_scan_f64(v);
+  if (lane_() == 63u) S.rd[wave_()] = inc;
+  bar();
+  double before = 0.0, all = 0.0;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const double r = S.rd[i];
+    if ((uint32_t)i < wave_()) before += r;
+    all += r;
+  }
+  bar();
+  *total = all;
+  return before + inc;
+}
+__device__ __forceinline__ double bsum_f64(double v, Lds& S) {
+  double tot;
+  (void)bscan_f64(v, S, &tot);
+  return tot;
+}
+__device__ __forceinline__ uint32_t bsum_u32(uint32_t v, Lds& S) {
+  uint32_t tot;
+  (void)bscan_u32(v, S, &tot);
+  return tot;
+}
+__device__ __forceinline__ uint32_t bmin_u32(uint32_t v, Lds& S) {
+  v = ~wave_max_u32(~v);
+  if (lane_() == 0u) S.ru[wave_()] = v;
+  bar();
+  uint32_t m = NONE;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) m = min(m, S.ru[i]);
+  bar();
+  return m;
+}
+// Minimum of nonnegative f64 values (their bit patterns order as u64).
+__device__ __forceinline__ double bmin_pos_f64(double v, Lds& S) {
+  const unsigned long long m = ~wave_max_u64(~__builtin_bit_cast(unsigned long long, v));
+  if (lane_() == 0u) S.r64[wave_()] = m;
+  bar();
+  unsigned long long r = ~0ull;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) r = min(r, S.r64[i]);
+  bar();
+  return __builtin_bit_cast(double, r);
+}
+__device__ __forceinline__ uint32_t bor_u32(uint32_t v, Lds& S) {
+  v = wave_or_u32(v);
+  if (lane_() == 0u) S.ru[wave_()] = v;
+  bar();
+  uint32_t m = 0u;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) m |= S.ru[i];
+  bar();
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// Row parameters.  Parameter errors in the oracle's precedence: temperature,
+// top_p, min_p, penalties (decided before any data), then history ids, bias
+// ids and the uniform (carried as chunk flags).
+struct Cfg {
+  double T, top_p, min_p, u, inv_rep, invT;
+  uint32_t k, h0, hlen, b0, blen;
+  float rep, pres, freq;
+  int32_t err;
+  bool greedy, uerr;
+};
+__device__ __forceinline__ Cfg load_cfg(const Args& A, uint32_t row) {
+  Cfg c;
+  c.T = A.T[row];
+  c.k = A.topk[row];
+  c.top_p = A.topp[row];
+  c.min_p = A.minp[row];
+  c.rep = A.rep[row];
+  c.pres = A.pres[row];
+  c.freq = A.freq[row];
+  c.u = A.u[row];
+  c.h0 = A.hoff[row];
+  c.hlen = A.hoff[row + 1] - c.h0;
+  c.b0 = A.boff[row];
+  c.blen = A.boff[row + 1] - c.b0;
+  c.greedy = c.T == 0.0;
+  int32_t e = 0;
+  if (!(c.T >= 0.0) || !isfinite(c.T)) e = MXS_ROW_INVALID_TEMPERATURE;
+  else if (!c.greedy && !(c.top_p > 0.0 && c.top_p <= 1.0)) e = MXS_ROW_INVALID_TOP_P;
+  else if (!c.greedy && !(c.min_p >= 0.0 && c.min_p <= 1.0)) e = MXS_ROW_INVALID_MIN_P;
+  else if (!(isfinite(c.rep) && c.rep > 0.0f) || !isfinite(c.pres) || !isfinite(c.freq)) e = MXS_ROW_INVALID_PENALTY;
+  c.err = e;
+  c.uerr = !c.greedy && !(isfinite(c.u) && c.u >= 0.0 && c.u < 1.0);
+  c.inv_rep = 1.0 / (double)c.rep;
+  c.invT = c.greedy ? 0.0 : 1.0 / c.T;
+  return c;
+}
+
+__device__ __forceinline__ void stamp(const Args& A, uint32_t row, uint32_t slot, uint32_t k) {
+  if (A.timing) A.timing[((uint64_t)row * MXS_DEBUG_TIMING_SLOTS + slot) * 8u + k] = wall_clock64();
+}
+
+// The bias value of token `tok` (which has an entry): binary search in the
+// row's sorted list, in LDS when it has at most BCAP entries.
+__device__ __forceinline__ float bias_of(const Args& A, const Cfg& cf, const Lds& S, uint32_t tok) {
+  uint32_t lo = 0, hi = cf.blen;
+  if (cf.blen <= BCAP) {
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (S.u.c.bid[mid] < tok) lo = mid + 1u; else hi = mid;
+    }
+    return S.u.c.bval[min(lo, cf.blen - 1u)];
+  }
+  const uint32_t* ids = A.bids + cf.b0;
+  while (lo < hi) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (ids[mid] < tok) lo = mid + 1u; else hi = mid;
+  }
+  return A.bvals[cf.b0 + min(lo, cf.blen - 1u)];
+}
+
+// The keep-all rows' f64 segment mass: exp((l - ref) / T) with the shift
+// multiplied by 1/T (an extra rounding the draw's error bound covers).
+__device__ __forceinline__ double seg_w(float l, float ref, double invT) {
+  return exp_neg(((double)l - (double)ref) * invT);
+}
+
+// ===========================================================================
+// The row finisher.  Runs on the last-arriving chunk workgroup of the row.
+// ===========================================================================
+
+// The row's working candidate list (token-ID order): compacted into LDS
+// when it fits, else read in place from the chunks' global lists.
+struct Work {
+  uint32_t n;
+  bool lds;
+  float thr;   // entries below thr are not candidates (the global lists hold some)
+};
+
+__device__ __forceinline__ void wget(const Args& A, const Lds& S, uint32_t row, const Work& W, uint32_t i, float* l,
+                                     uint32_t* id) {
+  if (W.lds) {
+    *l = S.u.f.cl[i];
+    *id = S.u.f.cid[i];
+    return;
+  }
+  uint32_t lo = 0, hi = A.C;   // the last chunk c with coff[c] <= i
+  while (hi - lo > 1u) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (S.coff[mid] <= i) lo = mid; else hi = mid;
+  }
+  const uint2 e = A.s.cand[(uint64_t)row * A.s.cand_stride + (uint64_t)lo * A.CH + (i - S.coff[lo])];
+  *l = __uint_as_float(e.x);
+  *id = e.y;
+}
+
+// Copies the entries of the chunks' global lists that satisfy keep(l, id)
+// into LDS, in token-ID order (each thread a contiguous range, then a block
+// scan).  Returns the count; the caller checks it fits beforehand.
+template <typename Keep>
+__device__ __forceinline__ uint32_t compact(const Args& A, Lds& S, uint32_t row, uint32_t N, Keep keep) {
+  const uint32_t t = threadIdx.x;
+  const Work G{N, false, -INFINITY};
+  const uint32_t R = (N + PT - 1u) / PT, i0 = min(N, t * R), i1 = min(N, i0 + R);
+  uint32_t mine = 0u;
+  for (uint32_t i = i0; i < i1; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, G, i, &l, &id);
+    mine += keep(l, id) ? 1u : 0u;
+  }
+  uint32_t tot;
+  uint32_t p = bscan_u32(mine, S, &tot) - mine;
+  for (uint32_t i = i0; i < i1; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, G, i, &l, &id);
+    if (keep(l, id) && p < NCL) {
+      S.u.f.cl[p] = l;
+      S.u.f.cid[p] = id;
+      ++p;
+    }
+  }
+  bar();
+  return tot;
+}
+
+// Error bound for comparing an f64 sum of n weights (each at most 1, total
+// S) formed here with the reference's sequential sum of the same weights:
+// 1 ulp of exp on each side, the shift rounded once more here, both sides'
+// summation errors, and the weights' own absolute rounding.
+__device__ __forceinline__ double sum_err(double S, double n) { return (S * (2.0 * n + 40.0) + n) * U53; }
+
+// The reference's descending comparator: total order of the value, then
+// ascending id.  better(a, b): a sorts before b.
+__device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, uint32_t ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+// In the descending order (key desc, id asc) over the working list's members
+// (member(l, id)), finds the first member at which the running measure
+// reaches `need`.  The measure is 1 per member (MASS = false: the need-th
+// member) or its weight exp((l - M) / T) (MASS = true: the first member whose
+// inclusive running mass is >= need).  Bins of d = Mkey - key, refined 11 bits
+// at a time; a bin of at most 64 members is finished on one wave; equal keys
+// are taken in ID order.  Outputs the member's key and id, the running
+// measure before it (*before) and its own (*wself).  *found = false when the
+// members' total stays below `need` (*before then holds that total).
+template <bool MASS, typename Mem>
+__device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, const Work& W, Mem member,
+                                         uint32_t Mkey, double Md, double invT, uint32_t dmax, double need,
+                                         bool* found, uint32_t* kout, uint32_t* iout, double* before,
+                                         double* wself) {
+  const uint32_t t = threadIdx.x;
+  uint32_t lo = 0;
+  int sh = 32 - __builtin_clz(dmax | 1u) - 11;
+  if (sh < 0) sh = 0;
+  double cum = 0.0;   // measure of the members before the current range
+  for (;;) {
+    for (uint32_t b = t; b < (uint32_t)NB; b += PT) {
+      S.u.f.bc[b] = 0u;
+      if (MASS) S.u.f.bm[b] = 0.0;
+    }
+    if (t == 0) S.u.f.nmem = 0u;
+    bar();
+    const uint32_t span = sh >= 21 ? 0xffffffffu : (((uint32_t)NB << sh) - 1u);
+    for (uint32_t i = t; i < W.n; i += PT) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      if (!(l >= W.thr) || !member(l, id)) continue;
+      const uint32_t d = Mkey - okey(l);
+      if (d < lo || d - lo > span) continue;
+      const uint32_t b = (d - lo) >> sh;
+      atomicAdd(&S.u.f.bc[b], 1u);
+      if (MASS) atomicAdd(&S.u.f.bm[b], exp_neg(((double)l - Md) * invT));
+    }
+    bar();
+    // thread t owns bins 4t .. 4t+3 (descending value order)
+    double m4[4];
+    uint32_t c4[4];
+    double msum = 0.0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = S.u.f.bc[4u * t + (uint32_t)q];
+      m4[q] = MASS ? S.u.f.bm[4u * t + (uint32_t)q] : (double)c4[q];
+      msum += m4[q];
+    }
+    double tot;
+    const double incl = bscan_f64(msum, S, &tot);
+    if (t == 0) S.bc[0] = NONE;
+    bar();
+    const double tb = cum + (incl - msum);
+    if (tb < need && cum + incl >= need) {
+      double r = tb;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (r + m4[q] >= need) {
+          S.bc[0] = 4u * t + (uint32_t)q;
+          S.bc[1] = c4[q];
+          S.bd[0] = r;
+          break;
+        }
+        r += m4[q];
+      }
+    }
+    bar();
+    const uint32_t bstar = S.bc[0];
+    if (bstar == NONE) {
+      *found = false;
+      *before = cum + tot;
+      *wself = 0.0;
+      bar();
+      return;
+    }
+    const uint32_t bcnt = S.bc[1];
+    cum = S.bd[0];
+    lo += bstar << sh;
+    bar();
+    if (bcnt <= 64u) {
+      const uint32_t bspan = sh >= 32 ? 0xffffffffu : ((1u << sh) - 1u);
+      for (uint32_t i = t; i < W.n; i += PT) {
+        float l;
+        uint32_t id;
+        wget(A, S, row, W, i, &l, &id);
+        if (!(l >= W.thr) || !member(l, id)) continue;
+        const uint32_t d = Mkey - okey(l);
+        if (d < lo || d - lo > bspan) continue;
+        const uint32_t p = atomicAdd(&S.u.f.nmem, 1u);
+        if (p < 64u) {
+          S.u.f.mkey[p] = okey(l);
+          S.u.f.mid[p] = id;
+          S.u.f.mw[p] = MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
+        }
+      }
+      bar();
+      if (t < 64u) {
+        const uint32_t n = min(S.u.f.nmem, 64u);
+        uint32_t mk = 0u, mi = NONE;
+        double mw = 0.0;
+        if (t < n) { mk = S.u.f.mkey[t]; mi = S.u.f.mid[t]; mw = S.u.f.mw[t]; }
+        double bef = 0.0;
+        for (uint32_t j = 0; j < n; ++j)
+          if (t < n && better(S.u.f.mkey[j], S.u.f.mid[j], mk, mi)) bef += S.u.f.mw[j];
+        const uint64_t hm = ballot(t < n && cum + bef < need && cum + bef + mw >= need);
+        if (hm) {
+          if (t == (uint32_t)__builtin_ctzll(hm)) {
+            S.bc[2] = mk;
+            S.bc[3] = mi;
+            S.bd[1] = cum + bef;
+            S.bd[2] = mw;
+            S.bc[4] = 1u;
+          }
+        } else if (t == 0u) {
+          double all = cum;
+          for (uint32_t j = 0; j < n; ++j) all += S.u.f.mw[j];
+          S.bc[4] = 0u;
+          S.bd[1] = all;
+          S.bd[2] = 0.0;
+        }
+      }
+      bar();
+      *found = S.bc[4] != 0u;
+      *kout = S.bc[2];
+      *iout = S.bc[3];
+      *before = S.bd[1];
+      *wself = S.bd[2];
+      bar();
+      return;
+    }
+    if (sh == 0) break;
+    sh = sh > 11 ? sh - 11 : 0;
+  }
+  // equal keys (Mkey - lo) in ID order: contiguous ranges and a block scan
+  const uint32_t kk = Mkey - lo;
+  const uint32_t R = (W.n + PT - 1u) / PT, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
+  double mine = 0.0;
+  for (uint32_t i = i0; i < i1; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, W, i, &l, &id);
+    if (l >= W.thr && member(l, id) && okey(l) == kk) mine += MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
+  }
+  double tot;
+  const double incl = bscan_f64(mine, S, &tot);
+  double r = cum + incl - mine;
+  uint32_t best = NONE;
+  double bb = 0.0, bw = 0.0;
+  for (uint32_t i = i0; i < i1 && best == NONE; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, W, i, &l, &id);
+    if (!(l >= W.thr) || !member(l, id) || okey(l) != kk) continue;
+    const double m = MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
+    if (r < need && r + m >= need) { best = id; bb = r; bw = m; }
+    r += m;
+  }
+  const uint32_t win = bmin_u32(best, S);
+  if (win != NONE && best == win) {
+    S.bd[1] = bb;
+    S.bd[2] = bw;
+  }
+  bar();
+  *found = win != NONE;
+  *kout = kk;
+  *iout = win;
+  *before = win != NONE ? S.bd[1] : cum + tot;
+  *wself = win != NONE ? S.bd[2] : 0.0;
+  bar();
+}
+
+// Writes one row's outputs.
+__device__ __forceinline__ void put_row(const Args& A, uint32_t row, int32_t status, int32_t token, double lp,
+                                        uint32_t kept) {
+  A.token[row] = token;
+  A.status[row] = status;
+  if (A.lp) A.lp[row] = lp;
+  if (A.kept_count) A.kept_count[row] = kept;
+}
+
+// The inverse-CDF draw over the working list's kept entries (kept(l, id)),
+// token-ID order, and the row's outputs.  `unc` carries an earlier
+// uncertain decision (status 1).
+template <typename Kept>
+__device__ __forceinline__ void draw_row(const Args& A, Lds& S, const Cfg& cf, uint32_t row, const Work& W,
+                                         Kept kept, double Md, bool unc) {
+  const uint32_t t = threadIdx.x;
+  const uint32_t R = (W.n + PT - 1u) / PT, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
+  const uint32_t kwords = (A.V + 31u) / 32u;
+  uint32_t nk = 0u, bad = 0u, n1 = 0u;
+  double mass = 0.0;
+  for (uint32_t i = i0; i < i1; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, W, i, &l, &id);
+    if (!(l >= W.thr) || !kept(l, id)) continue;
+    ++nk;
+    n1 += (double)l == Md ? 1u : 0u;
+    if (!isfinite(((double)l - Md) / cf.T)) bad = 1u;
+    mass += exp_neg(((double)l - Md) * cf.invT);
+    if (A.kept_bits) atomicOr(A.kept_bits + (uint64_t)row * kwords + (id >> 5), 1u << (id & 31u));
+  }
+  const uint32_t nkept = bsum_u32(nk, S);
+  const uint32_t nones = bsum_u32(n1, S);
+  if (bor_u32(bad, S)) {
+    // sample_categorical's shifted_logit check over the kept set
+    if (t == 0) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+    return;
+  }
+  if (A.nodraw) {
+    if (t == 0) put_row(A, row, unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_OK, -1, 0.0, nkept);
+    return;
+  }
+  double Ssum;
+  const double incl = bscan_f64(mass, S, &Ssum);
+  const double target = cf.u * Ssum;
+  // every kept weight exactly 1 (ties at the maximum): the sums are small
+  // integers on both sides and target is the same product, so the
+  // comparisons are exact
+  const double E = nones == nkept ? 0.0 : 2.0 * sum_err(Ssum, (double)nkept) + U53 * target;
+  double r = incl - mass;
+  uint32_t hit = NONE, last = NONE, hid = NONE, lid = NONE;
+  double hb = 0.0, ha = 0.0;
+  float hl = 0.0f, ll = 0.0f;
+  for (uint32_t i = i0; i < i1; ++i) {
+    float l;
+    uint32_t id;
+    wget(A, S, row, W, i, &l, &id);
+    if (!(l >= W.thr) || !kept(l, id)) continue;
+    const double wv = exp_neg(((double)l - Md) * cf.invT);
+    if (hit == NONE && target < r + wv) { hit = i; hb = r; ha = r + wv; hl = l; hid = id; }
+    if (wv > 0.0) { last = i; ll = l; lid = id; }
+    r += wv;
+  }
+  uint32_t win = bmin_u32(hit, S);
+  const bool fallback = win == NONE;
+  if (fallback) win = ~bmin_u32(~last, S);   // target past every running mass (rounding)
+  if (win != NONE && ((!fallback && hit == win) || (fallback && last == win))) {
+    S.bc[5] = fallback ? lid : hid;
+    S.bd[3] = ((double)(fallback ? ll : hl) - Md) / cf.T - log(Ssum);
+    S.bc[6] = (!fallback && target - hb >= E && ha - target > E) ? 1u : 0u;
+  }
+  bar();
+  if (t == 0) {
+    if (win == NONE) put_row(A, row, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u);
+    else put_row(A, row, (S.bc[6] && !unc) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)S.bc[5], S.bd[3], nkept);
+  }
+}
+
+// Keep-all rows: the draw walks the row's 256-token segment masses, then
+// re-derives the crossing segment's weights exactly.
+template <typename In>
+__device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, const Cfg& cf, uint32_t row, uint32_t Mkey,
+                                                 uint32_t nl) {
+  const uint32_t t = threadIdx.x, L = lane_();
+  const double Md = (double)okey_value(Mkey);
+  const uint32_t nseg = A.C * (uint32_t)NSEG;
+  const Seg* sg = A.s.seg + (uint64_t)row * A.s.cm * NSEG;
+  // segment s = c NSEG + j PW + w covers chunk c's tokens [4 (j PT + w 64), + 256);
+  // thread t sums segments [t R, t R + R)
+  const uint32_t R = (nseg + PT - 1u) / PT, s0 = min(nseg, t * R), s1 = min(nseg, s0 + R);
+  auto segmass = [&](uint32_t s) {
+    const uint32_t c = s / NSEG, j = (s - c * NSEG) / PW;
+    if (j >= A.per) return 0.0;
+    const Seg e = sg[s];
+    return e.mass > 0.0 ? e.mass * exp_neg(((double)e.ref - Md) * cf.invT) : 0.0;
+  };
+  double mine = 0.0;
+  for (uint32_t s = s0; s < s1; ++s) mine += segmass(s);
+  double Ssum;
+  const double incl = bscan_f64(mine, S, &Ssum);
+  const double target = cf.u * Ssum;
+  // each weight differs from the reference's by a few ulp (two exp
+  // evaluations, two extra roundings); both sides' summation orders
+  const double E = (Ssum * (4.0 * (double)nl + 64.0) + 4.0 * (double)nl) * U53 + U53 * target;
+  double r = incl - mine;
+  uint32_t hs = NONE, ls = NONE;
+  double hb = 0.0, lb = 0.0;
+  for (uint32_t s = s0; s < s1; ++s) {
+    const double m = segmass(s);
+    if (hs == NONE && target < r + m) { hs = s; hb = r; }
+    if (m > 0.0) { ls = s; lb = r; }
+    r += m;
+  }
+  uint32_t seg = bmin_u32(hs, S);
+  const bool fallback = seg == NONE;
+  if (fallback) seg = ~bmin_u32(~ls, S);
+  if ((!fallback && hs == seg) || (fallback && ls == seg)) S.bd[0] = fallback ? lb : hb;
+  if (t < 256u) S.u.f.segtab[t] = 0u;
+  bar();
+  const double sbefore = S.bd[0];
+  const uint32_t c = seg / NSEG, rr = seg - c * NSEG, j = rr / PW, wv = rr - j * PW;
+  const uint32_t c0 = c * A.CH, cend = min(c0 + A.CH, A.V);
+  const uint32_t sbase = c0 + 4u * (j * PT + wv * 64u);
+  for (uint32_t i = t; i < cf.hlen; i += PT) {
+    const uint32_t id = A.hids[cf.h0 + i];
+    if (id - sbase < 256u) atomicAdd(&S.u.f.segtab[id - sbase], 1u);
+  }
+  bar();
+  if (t >= 64u) return;
+  const uint32_t g0 = sbase + 4u * L;
+  float x[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  uint32_t leg = 0u;
+  if (g0 < cend) {
+    const In* lrow = (const In*)A.logits + (uint64_t)row * A.stride;
+    Quad<In>::unpack(Quad<In>::load(lrow + g0), x);
+    const uint32_t tvl = A.masked ? min(A.tv, A.V) : A.V;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t tok = g0 + (uint32_t)i;
+      if (tok >= cend) continue;
+      const uint32_t cnt = S.u.f.segtab[tok - sbase];
+      bool hb2 = false;
+      float bv = 0.0f;
+      if (cf.blen) {
+        uint32_t lo = 0, hi = cf.blen;
+        const uint32_t* ids = A.bids + cf.b0;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (ids[mid] < tok) lo = mid + 1u; else hi = mid;
+        }
+        if (lo < cf.blen && ids[lo] == tok) { hb2 = true; bv = A.bvals[cf.b0 + lo]; }
+      }
+      if (cnt || hb2)
+        x[i] = bias_and_penalize(x[i], ((hb2 ? 1u : 0u) << 31) | cnt, bv, cf.rep, cf.inv_rep, cf.freq, cf.pres);
+      bool lg = tok < tvl;
+      if (A.masked) lg = lg && ((A.mask[(uint64_t)row * A.mstride + (tok >> 5)] >> (tok & 31u)) & 1u);
+      if (lg) leg |= 1u << i;
+    }
+  }
+  double wq[4], lsum = 0.0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    wq[i] = ((leg >> i) & 1u) ? exp_neg(((double)x[i] - Md) / cf.T) : 0.0;
+    lsum += wq[i];
+  }
+  double r2 = sbefore + wave_scan_f64(lsum) - lsum;
+  uint32_t hit = NONE, lastp = NONE;
+  double hb3 = 0.0, ha3 = 0.0;
+  float hl = 0.0f, lastl = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if ((leg >> i) & 1u) {
+      if (hit == NONE && target < r2 + wq[i]) { hit = g0 + (uint32_t)i; hb3 = r2; ha3 = r2 + wq[i]; hl = x[i]; }
+      if (wq[i] > 0.0) { lastp = g0 + (uint32_t)i; lastl = x[i]; }
+      r2 += wq[i];
+    }
+  }
+  const uint64_t hm = ballot(hit != NONE), lm = ballot(lastp != NONE);
+  uint32_t src = NONE;
+  bool fb = fallback;
+  if (!fallback && hm) src = (uint32_t)__builtin_ctzll(hm);
+  else if (lm) { src = 63u - (uint32_t)__builtin_clzll(lm); fb = true; }
+  if (L == src) {
+    const uint32_t tok = fb ? lastp : hit;
+    const double sft = ((double)(fb ? lastl : hl) - Md) / cf.T;
+    // the fallback (target past every running mass) only happens by rounding
+    const bool cert = !fb && target - hb3 >= E && ha3 - target > E;
+    put_row(A, row, cert ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)tok, sft - log(Ssum), nl);
+  }
+  if (src == NONE && L == 0u) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, nl);
+}
+
+template <typename In>
+__device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf, uint32_t row) {
+  const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
+  const uint32_t C = A.C;
+  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 0u);
+  // ---- header: wave 0 merges the chunk statistics, lane q <-> chunk q
+  if (w == 0u) {
+    Stat s{};
+    s.thr = -INFINITY;
+    s.minkey = NONE;
+    if (L < C) s = A.s.stat[(uint64_t)row * A.s.cm + L];
+    const uint32_t Mkey = wave_max_u32(s.maxkey);
+    const uint32_t mink = ~wave_max_u32(~s.minkey);
+    const uint32_t fl = wave_or_u32(s.flags);
+    const uint32_t nl = wave_sum_u32(s.nlegal);
+    const unsigned long long g =
+        wave_max_u64(s.gkey ? (((unsigned long long)s.gkey << 32) | (unsigned long long)(~s.gid)) : 0ull);
+    const uint32_t nc = s.ncand;
+    const uint32_t inc = wave_scan_u32(nc);
+    if (L < C) S.coff[L] = inc - nc;
+    const uint32_t N = bcast63(inc);
+    if (L == 0u) S.coff[C] = N;
+    const uint32_t tk = wave_max_u32(L < C ? okey(s.thr) : 0u);
+    const uint32_t notall = wave_or_u32(L < C && s.ncand != s.nlegal ? 1u : 0u);
+    // chunk masses rescaled to the row maximum
+    const double Md = (double)okey_value(Mkey);
+    double rm = 0.0, re = 0.0;
+    if (L < C && s.maxkey && s.mass > 0.0) {
+      const double f = exp_neg(((double)okey_value(s.maxkey) - Md) * cf.invT);
+      rm = s.mass * f;
+      re = s.mass_err * f + rm * 8.0 * U53;
+    }
+    const double tot = wave_sum_f64(rm);
+    const double terr = wave_sum_f64(re) + tot * 80.0 * U53;
+    if (L == 0u) {
+      S.h.Mkey = Mkey;
+      S.h.flags = fl;
+      S.h.nl = nl;
+      S.h.N = N;
+      S.h.thrkey = tk;
+      S.h.complete = notall ? 0u : 1u;
+      S.h.gid = g ? ~(uint32_t)g : NONE;
+      S.h.mink = mink;
+      S.h.total = tot;
+      S.h.terr = terr;
+    }
+  }
+  bar();
+  const uint32_t Mkey = S.h.Mkey, fl = S.h.flags, nl = S.h.nl, N = S.h.N;
+  const float thr = okey_value(S.h.thrkey);
+  const bool complete = S.h.complete != 0u;
+  if (t == 0) {
+    A.s.arrive[row] = 0u;
+    A.s.rowmax[row] = 0u;
+  }
+  int32_t status = MXS_ROW_OK;
+  if (fl & F_BADHIST) status = MXS_ROW_INVALID_HISTORY;
+  else if (fl & F_BADBIAS) status = MXS_ROW_INVALID_BIAS;
+  else if (fl & F_UNIFORM) status = MXS_ROW_INVALID_UNIFORM;
+  else if (fl & F_NONFINITE) status = MXS_ROW_NON_FINITE_LOGIT;
+  else if (nl == 0u) status = MXS_ROW_EMPTY_SUPPORT;
+  if (status != MXS_ROW_OK) {
+    if (t == 0) put_row(A, row, status, -1, 0.0, 0u);
+    return;
+  }
+  const uint32_t kwords = (A.V + 31u) / 32u;
+  if (cf.greedy) {
+    if (t == 0) {
+      const uint32_t id = S.h.gid;
+      put_row(A, row, MXS_ROW_OK, (int32_t)id, 0.0, 1u);
+      if (A.kept_bits) atomicOr(A.kept_bits + (uint64_t)row * kwords + (id >> 5), 1u << (id & 31u));
+    }
+    return;
+  }
+  const bool kact = cf.k > 0u && cf.k < nl;
+  const double Md = (double)okey_value(Mkey);
+  if (!kact && cf.top_p >= 1.0 && cf.min_p == 0.0 && !complete) {
+    // keep-all without a complete candidate list
+    if (A.nodraw) {
+      if (t == 0) put_row(A, row, MXS_ROW_OK, -1, 0.0, nl);
+      return;
+    }
+    // the reference's legal_shifted_sum checks every legal token's shifted
+    // logit; the smallest overflows first
+    if (S.h.mink != NONE && !isfinite(((double)okey_value(S.h.mink) - Md) / cf.T)) {
+      if (t == 0) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+      return;
+    }
+    keepall_segments<In>(A, S, cf, row, Mkey, nl);
+    return;
+  }
+  // ---- the working candidate list
+  Work W{N, false, thr};
+  uint32_t dmax = Mkey - okey(thr);
+  if (kact && N > NCL) {
+    // stream the global lists once: the bin holding the k-th member bounds it
+    int sh = 32 - __builtin_clz(dmax | 1u) - 11;
+    if (sh < 0) sh = 0;
+    for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.f.bc[b] = 0u;
+    bar();
+    for (uint32_t i = t; i < N; i += PT) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      if (l >= thr) atomicAdd(&S.u.f.bc[(Mkey - okey(l)) >> sh], 1u);
+    }
+    bar();
+    uint32_t c4[4], cs = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c4[q] = S.u.f.bc[4u * t + (uint32_t)q];
+      cs += c4[q];
+    }
+    uint32_t tot;
+    const uint32_t inc = bscan_u32(cs, S, &tot);
+    if (t == 0) S.bc[0] = NONE;
+    bar();
+    if (inc - cs < cf.k && inc >= cf.k) {
+      uint32_t r = inc - cs;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (r < cf.k && r + c4[q] >= cf.k) { S.bc[0] = 4u * t + (uint32_t)q; S.bc[1] = r + c4[q]; }
+        r += c4[q];
+      }
+    }
+    bar();
+    if (S.bc[0] != NONE && S.bc[1] <= NCL) {
+      const uint32_t dlim = ((S.bc[0] + 1u) << sh) - 1u;
+      const uint32_t n = compact(A, S, row, N, [&](float l, uint32_t) { return l >= thr && Mkey - okey(l) <= dlim; });
+      W = Work{n, true, thr};
+      dmax = dlim;
+    }
+  } else if (N <= NCL) {
+    const uint32_t n = compact(A, S, row, N, [&](float l, uint32_t) { return l >= thr; });
+    W = Work{n, true, thr};
+  }
+  bool unc = false;
+  const double L_mp = cf.min_p > 0.0 ? log(cf.min_p) : -INFINITY;
+  auto minp_ok = [&](float l) { return cf.min_p <= 0.0 || ((double)l - Md) / cf.T >= L_mp; };
+  // a shifted logit within an ulp of ln(min_p) could fall on either side of
+  // the reference's logarithm
+  auto minp_close = [&](float l) {
+    if (cf.min_p <= 0.0 || cf.min_p >= 1.0) return false;
+    return fabs(((double)l - Md) / cf.T - L_mp) <= 4.0 * U53 * fabs(L_mp);
+  };
+  auto any_close = [&](auto member) {
+    uint32_t close = 0u;
+    for (uint32_t i = t; i < W.n; i += PT) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      if (l >= W.thr && member(l, id) && minp_close(l)) close = 1u;
+    }
+    return bor_u32(close, S) != 0u;
+  };
+  if (kact) {
+    // ---- top-k: the k-th member, the kept mass, the nucleus cut
+    bool f1;
+    uint32_t kk, ki;
+    double bef, wsf;
+    auto all = [&](float, uint32_t) { return true; };
+    crossing<false>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, (double)cf.k, &f1, &kk, &ki, &bef, &wsf);
+    if (!f1) {   // fewer candidates than k: the candidate bound failed
+      if (t == 0) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, 0u);
+      return;
+    }
+    auto inK = [&](float l, uint32_t id) {
+      const uint32_t key = okey(l);
+      return key > kk || (key == kk && id <= ki);
+    };
+    double km = 0.0, wmin = 1.0;
+    for (uint32_t i = t; i < W.n; i += PT) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      if (l >= W.thr && inK(l, id)) {
+        const double wv = exp_neg(((double)l - Md) * cf.invT);
+        km += wv;
+        wmin = fmin(wmin, wv);
+      }
+    }
+    const double kept = bsum_f64(km, S);
+    wmin = bmin_pos_f64(wmin, S);
+    // every top-k token tied at the maximum: kept is exactly k on both sides
+    const bool kones = kk == Mkey;
+    const double Ekept = kones ? 0.0 : sum_err(kept, (double)cf.k);
+    uint32_t ck = kk, ci = ki;
+    double habs = -1.0, hlo = 0.0, hhi = 0.0;   // top_p = 1: weights at or below habs are absorbed
+    if (cf.top_p < 1.0) {
+      const double target = cf.top_p * kept;
+      bool f2;
+      double b2, w2;
+      crossing<true>(A, S, row, W, inK, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+      // running masses inside the maximum's plateau are exact integers
+      const double Ec = ck == Mkey ? 0.0 : Ekept;
+      const double E = cf.top_p * Ekept + Ec + (kones ? 0.0 : U53 * target);
+      if (!f2) {
+        // covered never reaches the target: every top-k token is kept
+        ck = kk;
+        ci = ki;
+        if (!(b2 < target - E)) unc = true;
+      } else if (!(target - b2 > E && b2 + w2 - target >= E)) {
+        unc = true;
+      }
+    } else {
+      // top_p = 1: the reference stops at the first running mass equal to
+      // kept, i.e. before the first weight that adding to kept no longer
+      // changes (at or below half an ulp of kept; weights descend)
+      int e2;
+      (void)frexp(kept, &e2);                 // kept in [2^(e2-1), 2^e2)
+      const double h = ldexp(1.0, e2 - 54);   // half an ulp of kept
+      // the reference's kept may sit in the neighbouring binade when ours is
+      // within its error of a power of two: its half ulp is then h/2 or 2h
+      hlo = kept - ldexp(1.0, e2 - 1) <= Ekept ? 0.5 * h : h;
+      hhi = ldexp(1.0, e2) - kept <= Ekept ? 2.0 * h : h;
+      if (!(wmin > hhi * (1.0 + 4.0 * U53))) habs = h;
+    }
+    auto keptf = [&](float l, uint32_t id) {
+      const uint32_t key = okey(l);
+      if (!(key > ck || (key == ck && id <= ci))) return false;
+      if (habs >= 0.0 && !(exp_neg(((double)l - Md) * cf.invT) > habs)) return false;
+      return minp_ok(l);
+    };
+    if (habs >= 0.0) {
+      // a weight within its rounding of habs could fall on either side
+      uint32_t close = 0u;
+      for (uint32_t i = t; i < W.n; i += PT) {
+        float l;
+        uint32_t id;
+        wget(A, S, row, W, i, &l, &id);
+        if (l >= W.thr && inK(l, id)) {
+          const double wv = exp_neg(((double)l - Md) * cf.invT);
+          if (wv >= hlo * (1.0 - 4.0 * U53) && wv <= hhi * (1.0 + 4.0 * U53)) close = 1u;
+        }
+      }
+      if (bor_u32(close, S)) unc = true;
+    }
+    if (any_close(inK)) unc = true;
+    draw_row(A, S, cf, row, W, keptf, Md, unc);
+    return;
+  }
+  // ---- no top-k: nucleus (top_p < 1), min-p only, or keep-all (complete list)
+  auto all = [&](float, uint32_t) { return true; };
+  bool reached = true;
+  uint32_t ck = 0u, ci = NONE;
+  if (cf.top_p < 1.0) {
+    double total = S.h.total, terr = S.h.terr;
+    bool tones = false;
+    if (complete) {
+      // every legal token is a candidate: the total from the candidates
+      double tm = 0.0;
+      uint32_t n1 = 0u;
+      for (uint32_t i = t; i < W.n; i += PT) {
+        float l;
+        uint32_t id;
+        wget(A, S, row, W, i, &l, &id);
+        if (l >= W.thr) {
+          tm += exp_neg(((double)l - Md) * cf.invT);
+          n1 += (double)l == Md ? 1u : 0u;
+        }
+      }
+      total = bsum_f64(tm, S);
+      terr = sum_err(total, (double)nl);
+      tones = bsum_u32(n1, S) == nl;   // every weight 1: the total is exactly nl
+    }
+    const double target = cf.top_p * total;
+    bool f2;
+    double b2, w2;
+    crossing<true>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+    // running masses inside the maximum's plateau are exact integers; a
+    // complete list tied at the maximum has an exact total
+    const double E = (tones ? 0.0 : cf.top_p * terr + U53 * target) + (ck == Mkey ? 0.0 : sum_err(total, (double)N));
+    if (!f2) {
+      // the candidates' whole mass stays below the target: the kept set is
+      // the min-p set (or, for a complete list, every token)
+      reached = false;
+      if (!(b2 < target - E)) unc = true;
+      if (!complete && cf.min_p <= 0.0) unc = true;
+    } else if (!(target - b2 > E && b2 + w2 - target >= E)) {
+      unc = true;
+    }
+  }
+  const bool cut = cf.top_p < 1.0 && reached;
+  auto keptf = [&](float l, uint32_t id) {
+    if (cut) {
+      const uint32_t key = okey(l);
+      if (!(key > ck || (key == ck && id <= ci))) return false;
+    }
+    return minp_ok(l);
+  };
+  if (any_close(all)) unc = true;
+  draw_row(A, S, cf, row, W, keptf, Md, unc);
+}
+
+// ===========================================================================
+// The chunk pass.
+// ===========================================================================
+enum : int { LM_GREEDY = 0, LM_PLAIN = 1, LM_TOP4 = 2, LM_SEG = 3 };
+
+template <typename In>
+__global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
+  __shared__ Lds S;
+  using Q = Quad<In>;
+  const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
+  // XCD-aware mapping: workgroup g runs on XCD g mod 8; a row's chunks share
+  // one XCD (and its L2), rows r = 8 ri + ((x - ri) mod 8)
+  const uint32_t g = blockIdx.x, xcd = g & 7u, slot = g >> 3;
+  const uint32_t ri = slot / A.C, c = slot - ri * A.C;
+  const uint32_t row = 8u * ri + ((xcd - ri) & 7u);
+  if (row >= A.rows) return;
+  const uint32_t V = A.V, c0 = c * A.CH;
+  const uint32_t ntok = min(A.CH, V - c0);
+  const uint32_t nq = (ntok + 3u) / 4u;
+  stamp(A, row, c, 0u);
+  const Cfg cf = load_cfg(A, row);
+  if (cf.err) {
+    if (c == 0 && t == 0) put_row(A, row, cf.err, -1, 0.0, 0u);
+    return;
+  }
+  const bool greedy = cf.greedy;
+  const uint32_t k = cf.k;
+  const bool kknown = !greedy && !A.masked && k > 0u && k < V;
+  const bool kmaybe = !greedy && A.masked && k > 0u;
+  const bool keepall_possible = !greedy && !kknown && cf.top_p >= 1.0 && cf.min_p == 0.0;
+  const bool need_seg = keepall_possible && !A.nodraw && !kmaybe;
+  const bool need_mass = !greedy && !kknown && cf.top_p < 1.0;
+  const uint32_t topr = (kknown || kmaybe) ? (k <= 512u ? 1u : (k <= 2048u ? 4u : 40u)) : 0u;
+  const int lm = greedy ? LM_GREEDY : (need_seg ? LM_SEG : (topr == 4u ? LM_TOP4 : LM_PLAIN));
+  const bool has_hist = cf.hlen > 0u, has_bias = cf.blen > 0u;
+  const bool long_hist = cf.hlen > HTAB_MAX;
+  const bool use_tab = has_hist || has_bias;
+
+  // ---- loads: history ids first, then bias, mask words and the logits
+  uint32_t hreg[4];
+  const uint32_t hfirst = min(cf.hlen, 4u * (uint32_t)PT);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint32_t i = t + (uint32_t)r * PT;
+    hreg[r] = i < hfirst ? A.hids[cf.h0 + i] : 0u;
+  }
+  uint32_t bid0 = 0u;
+  float bval0 = 0.0f;
+  if (has_bias && cf.blen <= BCAP && t < cf.blen) {
+    bid0 = A.bids[cf.b0 + t];
+    bval0 = A.bvals[cf.b0 + t];
+  }
+  const uint32_t nmw = (ntok + 31u) / 32u;
+  uint32_t mw0 = 0xffffffffu, mw1 = 0xffffffffu;
+  if (A.masked) {
+    const uint32_t* mrow = A.mask + (uint64_t)row * A.mstride + (c0 >> 5);
+    if (t < nmw) mw0 = mrow[t];
+    if (t + PT < nmw) mw1 = mrow[t + PT];
+  }
+  typename Q::Raw raw[QMAX];
+  const In* lrow = (const In*)A.logits + (uint64_t)row * A.stride + c0;
+#pragma unroll
+  for (int j = 0; j < QMAX; ++j) {
+    const uint32_t q = (uint32_t)j * PT + t;
+    if (j < (int)A.per && q < nq) raw[j] = Q::load(lrow + 4u * q);
+    else raw[j] = typename Q::Raw{};
+  }
+  stamp(A, row, c, 1u);
+
+  // ---- LDS: count table, mask words, bias list
+  if (use_tab)
+    for (uint32_t q = t; q < nq; q += PT) *reinterpret_cast<uint2*>(&S.u.c.ctab[2u * q]) = make_uint2(0u, 0u);
+  if (A.masked) {
+    if (t < nmw) S.u.c.mask[t] = mw0;
+    if (t + PT < nmw) S.u.c.mask[t + PT] = mw1;
+  }
+  if (has_bias && cf.blen <= BCAP && t < cf.blen) {
+    S.u.c.bid[t] = bid0;
+    S.u.c.bval[t] = bval0;
+  }
+  uint32_t* gt = A.s.gtab + (uint64_t)row * A.s.gtab_stride + c0;
+  if (long_hist) {
+    // counts past 15 bits: u32 counts in global scratch, LDS marks presence
+    for (uint32_t q = t; q < nq; q += PT) *reinterpret_cast<uint4*>(gt + 4u * q) = make_uint4(0u, 0u, 0u, 0u);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  bar();
+  uint32_t flags = cf.uerr ? F_UNIFORM : 0u;
+  const uint32_t span = nq * 4u;
+  auto scat = [&](uint32_t id) {
+    if (id >= V) { flags |= F_BADHIST; return; }
+    const uint32_t r = id - c0;
+    if (r < span) {
+      if (long_hist) {
+        atomicOr(&S.u.c.ctab[r >> 1], 1u << (16u * (r & 1u)));
+        atomicAdd(gt + r, 1u);
+      } else {
+        atomicAdd(&S.u.c.ctab[r >> 1], 1u << (16u * (r & 1u)));
+      }
+    }
+  };
+  if (has_hist) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (t + (uint32_t)r * PT < hfirst) scat(hreg[r]);
+    for (uint32_t i = 4u * PT + t; i < cf.hlen; i += PT) scat(A.hids[cf.h0 + i]);
+  }
+  if (has_bias) {
+    auto mark = [&](uint32_t id, float v, bool bad) {
+      if (bad || id >= V || !isfinite(v)) { flags |= F_BADBIAS; return; }
+      const uint32_t r = id - c0;
+      if (r < span) atomicOr(&S.u.c.ctab[r >> 1], 0x8000u << (16u * (r & 1u)));
+    };
+    if (cf.blen <= BCAP) {
+      if (t < cf.blen) mark(bid0, bval0, t > 0 && A.bids[cf.b0 + t - 1u] >= bid0);
+    } else {
+      for (uint32_t i = t; i < cf.blen; i += PT) {
+        const uint32_t id = A.bids[cf.b0 + i];
+        mark(id, A.bvals[cf.b0 + i], i > 0 && A.bids[cf.b0 + i - 1u] >= id);
+      }
+    }
+  }
+  if (long_hist) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
+  }
+  bar();
+  stamp(A, row, c, 2u);
+
+  // ---- the quad loop: bias and penalties, the finite check, the mask and
+  // the running maximum as each quad lands; top-p rows also sum their f32
+  // mass online, relative to the thread's running maximum
+  const uint32_t tvl = A.masked ? min(A.tv, V) : V;
+  // x: the adjusted values (for f32, the loaded registers themselves);
+  // lg0/lg1: legal bits, 4 per quad round; val(j, i) is x[j][i] when legal,
+  // else -inf
+  float x[QMAX][4];
+  uint32_t lg0 = 0u, lg1 = 0u;
+  auto val = [&](int j, int i) -> float {
+    return (((j < 8 ? lg0 : lg1) >> (4 * (j & 7) + i)) & 1u) ? x[j][i] : -INFINITY;
+  };
+  float tmax = -INFINITY;
+  uint32_t nfin = 0u, nleg = 0u;
+  const float c32 = need_mass ? (float)(LOG2E * cf.invT) : 0.0f;
+  float ms = 0.0f, meb = 0.0f, mex = 0.0f, mref = -INFINITY;
+  uint32_t mn = 0u;
+  const uint32_t kwords = (V + 31u) / 32u;
+#pragma unroll
+  for (int j = 0; j < QMAX; ++j) {
+    Q::unpack(raw[j], x[j]);
+    if (j < (int)A.per) {
+      const uint32_t q = (uint32_t)j * PT + t;
+      const bool inq = q < nq;
+      const uint32_t g0 = c0 + 4u * q;
+      uint32_t rng = 0u;
+      if (inq) rng = g0 + 4u <= V ? 0xfu : ((1u << (V - g0)) - 1u);
+      if (use_tab) {
+        const uint2 e = inq ? *reinterpret_cast<const uint2*>(&S.u.c.ctab[2u * q]) : make_uint2(0u, 0u);
+        if (ballot((e.x | e.y) != 0u)) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t f = ((i < 2 ? e.x : e.y) >> (16 * (i & 1))) & 0xffffu;
+            if (f && ((rng >> i) & 1u)) {
+              const uint32_t tok = g0 + (uint32_t)i;
+              uint32_t cnt = f & 0x7fffu;
+              if (long_hist && cnt)
+                cnt = __hip_atomic_load(gt + (tok - c0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              const uint32_t hb = f >> 15;
+              const float bv = hb ? bias_of(A, cf, S, tok) : 0.0f;
+              x[j][i] = bias_and_penalize(x[j][i], (hb << 31) | cnt, bv, cf.rep, cf.inv_rep, cf.freq, cf.pres);
+            }
+          }
+        }
+      }
+      if (A.adjusted && inq) {
+        float* ap = A.adjusted + (uint64_t)row * V + g0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((rng >> i) & 1u) ap[i] = x[j][i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (((rng >> i) & 1u) && !isfinite(x[j][i])) nfin = 1u;
+      uint32_t leg = rng;
+      if (A.masked) {
+        leg &= (S.u.c.mask[q >> 3] >> ((q & 7u) * 4u)) & 0xfu;
+        if (g0 + 4u > tvl) leg &= g0 >= tvl ? 0u : ((1u << (tvl - g0)) - 1u);
+      }
+      nleg += popc(leg);
+      if (j < 8) lg0 |= leg << (4 * j); else lg1 |= leg << (4 * (j - 8));
+      const float qm = fmax_(fmax_(val(j, 0), val(j, 1)), fmax_(val(j, 2), val(j, 3)));
+      tmax = fmax_(tmax, qm);
+      if (need_mass && qm > -INFINITY) {
+        if (qm > mref) {
+          if (mref > -INFINITY) {
+            // rescale to the new reference; its own error joins the bound
+            const float y = (mref - qm) * c32;
+            const float f = __builtin_amdgcn_exp2f(y);
+            mex = mex * f + ms * f * (-2.1f * y * U24 + 6.0f * U24);
+            ms *= f;
+            meb *= f;
+          }
+          mref = qm;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((leg >> i) & 1u) {
+            const float y = (x[j][i] - mref) * c32;
+            const float e = __builtin_amdgcn_exp2f(y);
+            ms += e;
+            meb = fmaf(e, -y, meb);
+            ++mn;
+          }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // greedy: IEEE argmax, lowest id on ties (-0 ties +0)
+  float gv = 0.0f;
+  uint32_t gi = NONE;
+  if (greedy) {
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (val(j, i) > -INFINITY && (gi == NONE || val(j, i) > gv)) {
+          gv = val(j, i);
+          gi = c0 + 4u * ((uint32_t)j * PT + t) + (uint32_t)i;
+        }
+  }
+  // top-k over 512: each thread's four largest values bound the chunk's k-th
+  float tp0 = -INFINITY, tp1 = -INFINITY, tp2 = -INFINITY, tp3 = -INFINITY;
+  if (topr == 4u) {
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y = val(j, i);
+        const float a0 = fmax_(tp0, y), b0 = fminf(tp0, y);
+        const float a1 = fmax_(tp1, b0), b1 = fminf(tp1, b0);
+        const float a2 = fmax_(tp2, b1), b2 = fminf(tp2, b1);
+        tp0 = a0; tp1 = a1; tp2 = a2; tp3 = fmax_(tp3, b2);
+      }
+  }
+  // keep-all rows: f64 mass of each 256-token segment (wave w, round j)
+  float tmin = INFINITY;
+  if (need_seg) {
+    Seg* segp = A.s.seg + ((uint64_t)row * A.s.cm + c) * NSEG;
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j) {
+      if (j < (int)A.per) {
+        const float qm = fmax_(fmax_(val(j, 0), val(j, 1)), fmax_(val(j, 2), val(j, 3)));
+        const uint32_t wk = wave_max_u32(qm > -INFINITY ? okey(qm) : 0u);
+        double sm = 0.0;
+        float ref = -INFINITY;
+        if (wk) {
+          ref = okey_value(wk);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (val(j, i) > -INFINITY) {
+              sm += seg_w(val(j, i), ref, cf.invT);
+              tmin = fminf(tmin, val(j, i));
+            }
+        }
+        sm = wave_sum_f64(sm);
+        if (L == 0u) {
+          Seg e;
+          e.ref = ref;
+          e.pad = 0u;
+          e.mass = wk ? sm : 0.0;
+          segp[(uint32_t)j * PW + w] = e;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  stamp(A, row, c, 3u);
+  // kept bits: keep-all rows (the legal set, unless a top-k may apply) write
+  // the chunk's legal words; every other row clears them for the finisher
+  if (A.kept_bits) {
+    uint32_t* kb = A.kept_bits + (uint64_t)row * kwords + (c0 >> 5);
+    const bool legal_bits = keepall_possible && !kmaybe;
+    for (uint32_t i = t; i < nmw; i += PT) {
+      uint32_t bits = 0u;
+      if (legal_bits) {
+        const uint32_t tok0 = c0 + 32u * i;
+        bits = A.masked ? S.u.c.mask[i] : 0xffffffffu;
+        if (tok0 + 32u > tvl) bits &= tok0 >= tvl ? 0u : ((1u << (tvl - tok0)) - 1u);
+      }
+      kb[i] = bits;
+    }
+  }
+  bar();   // every wave is done with the count table (the LDS pool is reused)
+
+  // ---- chunk reductions
+  const bool want_hist = topr > 0u && topr <= 40u;
+  if (want_hist)
+    for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.hist[b] = 0u;
+  {
+    const uint32_t wk = wave_max_u32(tmax > -INFINITY ? okey(tmax) : 0u);
+    const uint32_t wmin = ~wave_max_u32(tmin < INFINITY ? ~okey(tmin) : 0u);
+    const uint32_t wf = wave_or_u32(flags | (nfin ? F_NONFINITE : 0u));
+    const uint32_t wl = wave_sum_u32(nleg);
+    const unsigned long long gk =
+        wave_max_u64(gi != NONE ? (((unsigned long long)okey(gv == 0.0f ? 0.0f : gv) << 32) | (unsigned long long)(~gi))
+                                : 0ull);
+    if (L == 0u) {
+      S.ru[w] = wk;
+      S.ru[PW + w] = wf;
+      S.ru[2 * PW + w] = wl;
+      S.ru[3 * PW + w] = wmin;
+      S.r64[w] = gk;
+    }
+  }
+  bar();
+  uint32_t Mkey = 0u, cfl = 0u, nl_c = 0u, minkey = NONE;
+  unsigned long long gbest = 0ull;
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    minkey = min(minkey, S.ru[3 * PW + i]);
+    Mkey = max(Mkey, S.ru[i]);
+    cfl |= S.ru[PW + i];
+    nl_c += S.ru[2 * PW + i];
+    gbest = max(gbest, S.r64[i]);
+  }
+  const float Mc = okey_value(Mkey);
+  bar();
+  // publish the chunk maximum (min-p and top-p bounds use the best seen)
+  if (!greedy && Mkey && t == 0)
+    S.bc[0] = max(atomicMax(A.s.rowmax + row, Mkey), Mkey);
+  // top-k bound: a value grid of 1/64 logit below the chunk maximum
+  const bool k_here = kknown || (kmaybe && nl_c > k);
+  if (want_hist && k_here && Mkey) {
+    auto add = [&](float y) {
+      const float d = (Mc - y) * 64.0f;
+      if (d < (float)NB) atomicAdd(&S.u.hist[(uint32_t)d], 1u);
+    };
+    if (topr == 1u) {
+      if (tmax > -INFINITY) add(tmax);
+    } else if (topr == 4u) {
+      if (tp0 > -INFINITY) add(tp0);
+      if (tp1 > -INFINITY) add(tp1);
+      if (tp2 > -INFINITY) add(tp2);
+      if (tp3 > -INFINITY) add(tp3);
+    } else {
+#pragma unroll
+      for (int j = 0; j < QMAX; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (val(j, i) > -INFINITY) add(val(j, i));
+    }
+  }
+  // chunk mass for the top-p total: each thread's online f32 sum scaled to
+  // the chunk maximum in f64, with a rigorous bound.  Per term: |y| ln2 3u
+  // (y rounded thrice) + 4u (v_exp_f32); f32 additions n u; results below
+  // 2^-126 absolute; rescales (mex) as accumulated in the loop.
+  double cmass = 0.0, cerr = 0.0;
+  if (need_mass && Mkey) {
+    double sm = 0.0, b = 0.0;
+    if (mref > -INFINITY) {
+      const double g = exp_neg(((double)mref - (double)Mc) * cf.invT);
+      sm = (double)ms * g;
+      b = ((double)meb * 2.1 * (double)U24 + (double)ms * (4.0 + (double)mn) * 1.01 * (double)U24 + (double)mex +
+           (double)mn * 1.1754943508222875e-38) * g * 1.001 + sm * 4.0 * U53;
+    }
+    cmass = bsum_f64(sm, S);
+    cerr = bsum_f64(b, S) + cmass * 16.0 * U53;
+  }
+  bar();
+  uint32_t bstar = NONE;
+  if (want_hist && k_here && Mkey) {
+    uint32_t h4[4];
+    uint32_t hs = 0u;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      h4[q] = S.u.hist[4u * t + (uint32_t)q];
+      hs += h4[q];
+    }
+    uint32_t tot;
+    const uint32_t inc = bscan_u32(hs, S, &tot);
+    if (t == 0) S.bc[1] = NONE;
+    bar();
+    if (inc - hs < k && inc >= k) {
+      uint32_t r = inc - hs;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (r < k && r + h4[q] >= k) { S.bc[1] = 4u * t + (uint32_t)q; }
+        r += h4[q];
+      }
+    }
+    bar();
+    bstar = S.bc[1];
+  }
+  // ---- the candidate threshold: a proven lower bound of every token the
+  // row's decision can need
+  float thr = greedy ? INFINITY : -INFINITY;   // a chunk without legal tokens bounds nothing
+  if (!greedy && Mkey) {
+    const float Mb = okey_value(S.bc[0]);   // best row maximum seen (>= Mc)
+    if (k_here) {
+      thr = -INFINITY;
+      if (topr <= 40u && bstar != NONE) {
+        const float lim = Mc - (float)(bstar + 1u) * (1.0f / 64.0f);
+        thr = lim - (fabsf(Mc) + 32.0f) * 4.0f * U24;
+      }
+    } else if (kmaybe || (A.masked && nl_c <= 4096u && !keepall_possible)) {
+      // at most k legal tokens here (or few under a grammar mask): all of
+      // them, so the finisher sees the complete legal set
+      thr = -INFINITY;
+    } else if (keepall_possible) {
+      thr = INFINITY;      // keep-all: segment masses, no candidates
+    } else {
+      double lim = -INFINITY;
+      if (cf.min_p > 0.0) lim = fmax(lim, (double)Mb + cf.T * log(cf.min_p));
+      if (cf.top_p < 1.0 && 1.0 - cf.top_p > 8.0 * (double)V * U53)
+        lim = fmax(lim, (double)Mb + cf.T * log((1.0 - cf.top_p) / (2.0 * (double)V)));
+      if (lim > -INFINITY) {
+        const float lf = (float)lim;
+        thr = lf - (fabsf(lf) + fabsf(Mb)) * 1e-6f - 1e-37f;
+        if (!(thr > -INFINITY)) thr = -INFINITY;
+      } else {
+        thr = -INFINITY;
+      }
+    }
+  }
+  stamp(A, row, c, 4u);
+
+  // ---- candidate emission in token-ID order: (quad round, wave, lane,
+  // token); each lane's candidate bits are packed 4 per round
+  uint32_t ncand = 0u;
+  if (thr < INFINITY) {
+    uint32_t pk0 = 0u, pk1 = 0u;
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j) {
+      uint32_t bits = 0u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bits |= (val(j, i) > -INFINITY && val(j, i) >= thr) ? (1u << i) : 0u;
+      if (j < 8) pk0 |= bits << (4 * j); else pk1 |= bits << (4 * (j - 8));
+    }
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j) {
+      const uint32_t bits = ((j < 8 ? pk0 : pk1) >> (4 * (j & 7))) & 0xfu;
+      const uint32_t tot = wave_sum_u32(popc(bits));
+      if (L == 0u && j < (int)A.per) S.wcnt[(uint32_t)j * PW + w] = tot;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bar();
+    if (w == 0u) {
+      const uint32_t ne = A.per * (uint32_t)PW;
+      const uint32_t a = 2u * L < ne ? S.wcnt[2u * L] : 0u;
+      const uint32_t b = 2u * L + 1u < ne ? S.wcnt[2u * L + 1u] : 0u;
+      const uint32_t inc = wave_scan_u32(a + b);
+      if (2u * L < ne) S.woff[2u * L] = inc - a - b;
+      if (2u * L + 1u < ne) S.woff[2u * L + 1u] = inc - b;
+      if (L == 63u) S.bc[2] = inc;
+    }
+    bar();
+    ncand = S.bc[2];
+    uint2* cb = A.s.cand + (uint64_t)row * A.s.cand_stride + (uint64_t)c * A.CH;
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j) {
+      const uint32_t bits = ((j < 8 ? pk0 : pk1) >> (4 * (j & 7))) & 0xfu;
+      if (j < (int)A.per && ballot(bits != 0u)) {
+        const uint32_t cnt = popc(bits);
+        uint32_t p = S.woff[(uint32_t)j * PW + w] + wave_scan_u32(cnt) - cnt;
+        const uint32_t g0 = c0 + 4u * ((uint32_t)j * PT + t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((bits >> i) & 1u) cb[p++] = make_uint2(__float_as_uint(val(j, i)), g0 + (uint32_t)i);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  stamp(A, row, c, 5u);
+
+  // ---- statistics, then arrive
+  if (t == 0) {
+    Stat st;
+    st.maxkey = Mkey;
+    st.gkey = (uint32_t)(gbest >> 32);
+    st.gid = gbest ? ~(uint32_t)gbest : NONE;
+    st.nlegal = nl_c;
+    st.ncand = ncand;
+    st.flags = cfl;
+    st.thr = thr;
+    st.minkey = minkey;
+    st.mass = cmass;
+    st.mass_err = cerr;
+    A.s.stat[(uint64_t)row * A.s.cm + c] = st;
+  }
+  // Every thread's candidate, segment, statistics and kept-bit stores are
+  // released at agent scope before the row counter moves; the last arriver
+  // acquires them.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  bar();
+  if (t == 0) S.bc[3] = __hip_atomic_fetch_add(A.s.arrive + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  bar();
+  if (S.bc[3] != A.C - 1u) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  finish_row<In>(A, S, cf, row);
+  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 1u);
+}
+
+}  // namespace pk
+
+// mxs_sample's launch (also the kept-set pass of mxs_sample_race, with
+// `nodraw`: no inverse-CDF draw, token -1, status certifies the kept set).
+int pick_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw) {
+  if (!ctx || !b || !o) return MXS_EINVAL;
+  if (b->rows == 0) return MXS_OK;
+  if (!b->logits || !b->temperature || !o->token || !o->status)
+    return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
+  if (b->rows > ctx->max_rows || b->vocab > ctx->max_vocab)
+    return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
+  if (b->vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
+  if (b->vocab > pk::VMAX) return fail(ctx, MXS_EINVAL, "vocab exceeds 1310720");
+  if (b->dtype != MXS_F32 && b->dtype != MXS_BF16) return fail(ctx, MXS_EINVAL, "dtype must be MXS_F32 or MXS_BF16");
+  if (b->row_stride < b->vocab || (b->row_stride & 3u))
+    return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");
+  const size_t align = b->dtype == MXS_F32 ? 16 : 8;
+  if (((uintptr_t)b->logits) % align) return fail(ctx, MXS_EINVAL, "logits must be 16-byte (f32) or 8-byte (bf16) aligned");
+  if (b->mask_words && b->mask_stride < (b->vocab + 31u) / 32u)
+    return fail(ctx, MXS_EINVAL, "mask_stride must be >= ceil(vocab / 32)");
+  if ((b->history_offsets == nullptr) != (b->history_ids == nullptr))
+    return fail(ctx, MXS_EINVAL, "history offsets and ids go together");
+  if ((b->bias_offsets == nullptr) != (b->bias_ids == nullptr) || (b->bias_offsets && !b->bias_values))
+    return fail(ctx, MXS_EINVAL, "bias offsets, ids and values go together");
+  const pk::Layout Ly = pk::layout(b->vocab);
+  if (Ly.C > ctx->pick.cm || Ly.per > (uint32_t)pk::QMAX || Ly.C > pk::MAXCH)
+    return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
+  pk::Args A{};
+  A.logits = b->logits;
+  A.stride = b->row_stride;
+  A.rows = b->rows;
+  A.V = b->vocab;
+  A.C = Ly.C;
+  A.CH = Ly.CH;
+  A.per = Ly.per;
+  A.masked = b->mask_words != nullptr;
+  A.tv = A.masked ? b->tokenizer_vocab : b->vocab;
+  A.nodraw = nodraw ? 1u : 0u;
+  A.mstride = b->mask_stride;
+  A.T = b->temperature;
+  A.topk = b->top_k ? b->top_k : ctx->d_zero_u32;
+  A.topp = b->top_p ? b->top_p : ctx->d_one_f64;
+  A.minp = b->min_p ? b->min_p : ctx->d_zero_f64;
+  A.rep = b->repetition ? b->repetition : ctx->d_one_f32;
+  A.pres = b->presence ? b->presence : ctx->d_zero_f32;
+  A.freq = b->frequency ? b->frequency : ctx->d_zero_f32;
+  A.u = b->uniform ? b->uniform : ctx->d_zero_f64;
+  A.hoff = b->history_offsets ? b->history_offsets : ctx->d_zero_u32;
+  A.hids = b->history_ids ? b->history_ids : ctx->d_zero_u32;
+  A.boff = b->bias_offsets ? b->bias_offsets : ctx->d_zero_u32;
+  A.bids = b->bias_ids ? b->bias_ids : ctx->d_zero_u32;
+  A.bvals = b->bias_values ? b->bias_values : ctx->d_zero_f32;
+  A.mask = b->mask_words ? b->mask_words : ctx->d_mask_ones;
+  A.token = o->token;
+  A.lp = o->sampling_logprob;
+  A.status = o->status;
+  A.kept_count = o->kept_count;
+  A.adjusted = o->adjusted;
+  A.kept_bits = o->kept_bits;
+  A.s = ctx->pick;
+  A.timing = ctx->timing;
+  const uint32_t groups = (b->rows + 7u) / 8u;
+  const dim3 grid(8u * Ly.C * groups);
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  if (b->dtype == MXS_F32)
+    hipLaunchKernelGGL(pk::pick_kernel<float>, grid, dim3(pk::PT), 0, ctx->stream, A);
+  else
+    hipLaunchKernelGGL(pk::pick_kernel<uint16_t>, grid, dim3(pk::PT), 0, ctx->stream, A);
+  if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
+  hipError_t e = hipGetLastError();
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "pick_kernel launch");
+  return MXS_OK;
+}
+
+}  // namespace mxs

@@ -3062,16 +3062,16 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
   } else if (MODE == M_MINP && row_ok) {
     // The largest chunk maximum of the row published by now is a lower
     // bound of the row maximum: any lower bound gives a superset of the
-    // min-p set, a tighter one fewer candidates.  ln(min_p) in f32: its
-    // error (a few ulp of |ln min_p|, times T) is far inside the threshold's
-    // 1e-5 relative margin.
+    // min-p set, a tighter one fewer candidates.  ln(min_p) in f64 (an f32
+    // logarithm's error, T * 2^-24 absolute, is not covered by a margin
+    // relative to the logits when they and T ln(min_p) are near 0).
     emit = true;
     const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t xkey = maxkey;
     if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
     xkey = (uint32_t)__builtin_amdgcn_readfirstlane((int)xkey);
     const float mx = okey_value(xkey);
-    const double lim_d = (double)mx + c.T * (double)__logf((float)c.min_p);
+    const double lim_d = (double)mx + c.T * log(c.min_p);
     thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
   }
   uint32_t cnt_i[PER_MAX];
@@ -3961,6 +3961,7 @@ __global__ __launch_bounds__(FT) void finish_kernel(
 namespace mxs {
 
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw) {
+  if (ctx && ctx->use_pick) return pick_launch(ctx, b, o, nodraw);
   if (!ctx || !b || !o) return MXS_EINVAL;
   if (b->rows == 0) return MXS_OK;
   if (!b->logits || !b->temperature || !o->token || !o->status) return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
@@ -4094,6 +4095,25 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
     const char* fz = getenv("MXS_SAMPLER_FUSED");
     ctx->split = !(fz && fz[0] == '1');
   }
+  {
+    const char* pz = getenv("MXS_SAMPLER_PICK");
+    ctx->use_pick = pz && pz[0] == '1';
+  }
+  {
+    const mxs::pk::Layout ly = mxs::pk::layout(max_vocab);
+    mxs::pk::Scratch& P = ctx->pick;
+    P.cm = ly.C;
+    P.cand_stride = (uint64_t)max_vocab + 32u * ly.C + 32u;
+    P.gtab_stride = ((uint64_t)max_vocab + 8u) & ~(uint64_t)3u;
+    e = e ? e : hipMalloc(&P.arrive, (size_t)max_rows * sizeof(uint32_t));
+    e = e ? e : hipMemset(P.arrive, 0, (size_t)max_rows * sizeof(uint32_t));
+    e = e ? e : hipMalloc(&P.rowmax, (size_t)max_rows * sizeof(uint32_t));
+    e = e ? e : hipMemset(P.rowmax, 0, (size_t)max_rows * sizeof(uint32_t));
+    e = e ? e : hipMalloc(&P.stat, (size_t)max_rows * P.cm * sizeof(mxs::pk::Stat));
+    e = e ? e : hipMalloc(&P.cand, (size_t)max_rows * P.cand_stride * sizeof(uint2));
+    e = e ? e : hipMalloc(&P.seg, (size_t)max_rows * P.cm * mxs::pk::NSEG * sizeof(mxs::pk::Seg));
+    e = e ? e : hipMalloc(&P.gtab, (size_t)max_rows * P.gtab_stride * sizeof(uint32_t));
+  }
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
@@ -4160,6 +4180,12 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->race_ctr);
   hipFree(ctx->race_scratch);
   hipFree(ctx->race_kept);
+  hipFree(ctx->pick.arrive);
+  hipFree(ctx->pick.rowmax);
+  hipFree(ctx->pick.stat);
+  hipFree(ctx->pick.cand);
+  hipFree(ctx->pick.seg);
+  hipFree(ctx->pick.gtab);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;

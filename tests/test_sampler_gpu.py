@@ -242,6 +242,26 @@ def test_selection_finisher_mix(torch_mod, sampler, orc, seed):
     compare(b, gpu, ref, allow_uncertified=int(wide.sum()))
 
 
+def test_min_p_near_one_over_log_softmax(torch_mod, sampler, orc):
+    """min_p 0.999 (and neighbours) over rows whose maximum is exactly 0
+    with a few hundred tokens within 0.01 of it, so T ln(min_p) (about -1e-3)
+    cuts among them: an f32 logarithm of min_p, whose error is absolute
+    (T 2^-24), would misplace that cut when the logits give no relative
+    margin."""
+    from metallix_amd.synth import Batch
+
+    rng = np.random.default_rng(999)
+    rows, V = 16, 151936
+    x = rng.standard_normal((rows, V)) * 0.5 - 12.0
+    x[:, :400] = rng.standard_normal((rows, 400)) * 0.002    # near-maximal tokens
+    x = (x - x.max(axis=1, keepdims=True)).astype(np.float32)  # maximum exactly 0
+    b = Batch(name="minp-near-one", logits=x, temperature=rng.choice([0.5, 1.0, 2.0], size=rows),
+              uniform=rng.random(rows), top_k=np.zeros(rows, np.uint32),
+              top_p=rng.choice([1.0, 0.9], size=rows), min_p=rng.choice([0.999, 0.9999, 0.99], size=rows))
+    gpu, ref = check(torch_mod, sampler, orc, b)
+    assert (np.asarray(ref["kept"]).sum(axis=1) > 1).any()
+
+
 def test_keepall_rows_with_history_and_bias(torch_mod, sampler, orc):
     """Keep-all rows (top_k 0, top_p 1, min_p 0) over config 2's 2048-id
     histories plus a logit bias: the inverse-CDF draw over the whole row
