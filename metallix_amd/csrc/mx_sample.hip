@@ -64,7 +64,7 @@ struct FinHdr {
   uint32_t Mkey, flags, nl, N, thrkey, complete, gid, mink;
   double total, terr;
 };
-constexpr uint32_t NCL = 4096;       // candidates the finisher keeps in LDS
+constexpr uint32_t NCL = 8192;       // candidates the finisher keeps in LDS
 struct alignas(16) Lds {
   union {
     struct {
@@ -89,6 +89,8 @@ struct alignas(16) Lds {
   uint32_t woff[QMAX * PW];
   uint32_t ru[4 * PW];
   unsigned long long r64[PW];
+  uint32_t wr[4 * PW];               // per-wave chunk reductions (max key, flags, legal count, min key)
+  unsigned long long wg[PW];         // per-wave greedy keys
   double rd[2 * PW];
   uint32_t coff[MAXCH + 1];          // candidate offsets of the row's chunks
   FinHdr h;
@@ -181,25 +183,35 @@ __device__ __forceinline__ uint32_t bor_u32(uint32_t v, Lds& S) {
 // ids and the uniform (carried as chunk flags).
 struct Cfg {
   double T, top_p, min_p, u, inv_rep, invT;
+  double L_mp;    // ln(min_p) (-inf when min_p = 0)
+  double L_nuc;   // ln((1 - top_p) / (2 V)), the nucleus bound's offset (-inf: no bound)
   uint32_t k, h0, hlen, b0, blen;
   float rep, pres, freq;
   int32_t err;
   bool greedy, uerr;
 };
+// Row-uniform values moved to scalar registers (the compiler cannot prove
+// the parameter arrays read-only, so it loads them into vector registers).
+__device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+__device__ __forceinline__ float uni(float v) { return __uint_as_float(uni(__float_as_uint(v))); }
+__device__ __forceinline__ double uni(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  return __builtin_bit_cast(double, ((unsigned long long)uni((uint32_t)(b >> 32)) << 32) | uni((uint32_t)b));
+}
 __device__ __forceinline__ Cfg load_cfg(const Args& A, uint32_t row) {
   Cfg c;
-  c.T = A.T[row];
-  c.k = A.topk[row];
-  c.top_p = A.topp[row];
-  c.min_p = A.minp[row];
-  c.rep = A.rep[row];
-  c.pres = A.pres[row];
-  c.freq = A.freq[row];
-  c.u = A.u[row];
-  c.h0 = A.hoff[row];
-  c.hlen = A.hoff[row + 1] - c.h0;
-  c.b0 = A.boff[row];
-  c.blen = A.boff[row + 1] - c.b0;
+  c.T = uni(A.T[row]);
+  c.k = uni(A.topk[row]);
+  c.top_p = uni(A.topp[row]);
+  c.min_p = uni(A.minp[row]);
+  c.rep = uni(A.rep[row]);
+  c.pres = uni(A.pres[row]);
+  c.freq = uni(A.freq[row]);
+  c.u = uni(A.u[row]);
+  c.h0 = uni(A.hoff[row]);
+  c.hlen = uni(A.hoff[row + 1]) - c.h0;
+  c.b0 = uni(A.boff[row]);
+  c.blen = uni(A.boff[row + 1]) - c.b0;
   c.greedy = c.T == 0.0;
   int32_t e = 0;
   if (!(c.T >= 0.0) || !isfinite(c.T)) e = MXS_ROW_INVALID_TEMPERATURE;
@@ -208,8 +220,8 @@ __device__ __forceinline__ Cfg load_cfg(const Args& A, uint32_t row) {
   else if (!(isfinite(c.rep) && c.rep > 0.0f) || !isfinite(c.pres) || !isfinite(c.freq)) e = MXS_ROW_INVALID_PENALTY;
   c.err = e;
   c.uerr = !c.greedy && !(isfinite(c.u) && c.u >= 0.0 && c.u < 1.0);
-  c.inv_rep = 1.0 / (double)c.rep;
-  c.invT = c.greedy ? 0.0 : 1.0 / c.T;
+  c.inv_rep = uni(1.0 / (double)c.rep);
+  c.invT = uni(c.greedy ? 0.0 : 1.0 / c.T);
   return c;
 }
 
@@ -330,7 +342,7 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
                                          double* wself) {
   const uint32_t t = threadIdx.x;
   uint32_t lo = 0;
-  int sh = 32 - __builtin_clz(dmax | 1u) - 11;
+  int sh = 32 - __builtin_clz(dmax | 1u) - NBB;
   if (sh < 0) sh = 0;
   double cum = 0.0;   // measure of the members before the current range
   for (;;) {
@@ -340,7 +352,7 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
     }
     if (t == 0) S.u.f.nmem = 0u;
     bar();
-    const uint32_t span = sh >= 21 ? 0xffffffffu : (((uint32_t)NB << sh) - 1u);
+    const uint32_t span = sh >= 32 - NBB ? 0xffffffffu : (((uint32_t)NB << sh) - 1u);
     for (uint32_t i = t; i < W.n; i += PT) {
       float l;
       uint32_t id;
@@ -446,7 +458,7 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
       return;
     }
     if (sh == 0) break;
-    sh = sh > 11 ? sh - 11 : 0;
+    sh = sh > NBB ? sh - NBB : 0;
   }
   // equal keys (Mkey - lo) in ID order: contiguous ranges and a block scan
   const uint32_t kk = Mkey - lo;
@@ -726,12 +738,13 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     }
   }
   bar();
+  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 2u);
   const uint32_t Mkey = S.h.Mkey, fl = S.h.flags, nl = S.h.nl, N = S.h.N;
   const float thr = okey_value(S.h.thrkey);
   const bool complete = S.h.complete != 0u;
   if (t == 0) {
-    A.s.arrive[row] = 0u;
-    A.s.rowmax[row] = 0u;
+    A.s.sync[(uint64_t)row * SYNC] = 0u;
+    A.s.sync[(uint64_t)row * SYNC + 1u] = 0u;
   }
   int32_t status = MXS_ROW_OK;
   if (fl & F_BADHIST) status = MXS_ROW_INVALID_HISTORY;
@@ -774,7 +787,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
   uint32_t dmax = Mkey - okey(thr);
   if (kact && N > NCL) {
     // stream the global lists once: the bin holding the k-th member bounds it
-    int sh = 32 - __builtin_clz(dmax | 1u) - 11;
+    int sh = 32 - __builtin_clz(dmax | 1u) - NBB;
     if (sh < 0) sh = 0;
     for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.f.bc[b] = 0u;
     bar();
@@ -814,8 +827,9 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     const uint32_t n = compact(A, S, row, N, [&](float l, uint32_t) { return l >= thr; });
     W = Work{n, true, thr};
   }
+  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 3u);
   bool unc = false;
-  const double L_mp = cf.min_p > 0.0 ? log(cf.min_p) : -INFINITY;
+  const double L_mp = cf.L_mp;
   auto minp_ok = [&](float l) { return cf.min_p <= 0.0 || ((double)l - Md) / cf.T >= L_mp; };
   // a shifted logit within an ulp of ln(min_p) could fall on either side of
   // the reference's logarithm
@@ -840,6 +854,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     double bef, wsf;
     auto all = [&](float, uint32_t) { return true; };
     crossing<false>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, (double)cf.k, &f1, &kk, &ki, &bef, &wsf);
+    stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 4u);
     if (!f1) {   // fewer candidates than k: the candidate bound failed
       if (t == 0) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, 0u);
       return;
@@ -861,6 +876,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     }
     const double kept = bsum_f64(km, S);
     wmin = bmin_pos_f64(wmin, S);
+    stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 5u);
     // every top-k token tied at the maximum: kept is exactly k on both sides
     const bool kones = kk == Mkey;
     const double Ekept = kones ? 0.0 : sum_err(kept, (double)cf.k);
@@ -871,6 +887,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
       bool f2;
       double b2, w2;
       crossing<true>(A, S, row, W, inK, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+      stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 6u);
       // running masses inside the maximum's plateau are exact integers
       const double Ec = ck == Mkey ? 0.0 : Ekept;
       const double E = cf.top_p * Ekept + Ec + (kones ? 0.0 : U53 * target);
@@ -916,6 +933,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
       if (bor_u32(close, S)) unc = true;
     }
     if (any_close(inK)) unc = true;
+    stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 7u);
     draw_row(A, S, cf, row, W, keptf, Md, unc);
     return;
   }
@@ -946,7 +964,9 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     const double target = cf.top_p * total;
     bool f2;
     double b2, w2;
+    stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 5u);
     crossing<true>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+    stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 6u);
     // running masses inside the maximum's plateau are exact integers; a
     // complete list tied at the maximum has an exact total
     const double E = (tones ? 0.0 : cf.top_p * terr + U53 * target) + (ck == Mkey ? 0.0 : sum_err(total, (double)N));
@@ -969,16 +989,26 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     return minp_ok(l);
   };
   if (any_close(all)) unc = true;
+  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 7u);
   draw_row(A, S, cf, row, W, keptf, Md, unc);
 }
 
 // ===========================================================================
 // The chunk pass.
 // ===========================================================================
-enum : int { LM_GREEDY = 0, LM_PLAIN = 1, LM_TOP4 = 2, LM_SEG = 3 };
+// What the quad loop accumulates besides the maximum: the two largest
+// values (top-k rows with 128 < k <= 1024) or the online f32 mass (top-p
+// rows without a top-k).
+enum : int { M_PLAIN = 0, M_TOP2 = 1, M_MASS = 2 };
+
+__device__ __forceinline__ float vmin(float a, float b) {
+  float r;
+  __asm__("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
 
 template <typename In>
-__global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
+__global__ __launch_bounds__(PT) void pick_kernel(Args A) {
   __shared__ Lds S;
   using Q = Quad<In>;
   const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
@@ -991,8 +1021,47 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
   const uint32_t V = A.V, c0 = c * A.CH;
   const uint32_t ntok = min(A.CH, V - c0);
   const uint32_t nq = (ntok + 3u) / 4u;
+
+  // ---- loads.  The side inputs (history ids, the bias list, mask words)
+  // go out first, so they land ahead of the chunk's stream and the LDS
+  // tables are ready while most of the stream is still in flight; then
+  // every quad round of the logits.
+  const uint32_t h0 = A.hoff[row], hlen = A.hoff[row + 1] - h0;
+  const uint32_t b0 = A.boff[row], blen = A.boff[row + 1] - b0;
+  constexpr uint32_t HR = 2;
+  uint32_t hreg[HR];
+  const uint32_t hfirst = min(hlen, HR * (uint32_t)PT);
+#pragma unroll
+  for (uint32_t r = 0; r < HR; ++r) {
+    const uint32_t i = t + r * PT;
+    hreg[r] = i < hfirst ? A.hids[h0 + i] : 0u;
+  }
+  uint32_t bid0 = 0u, bprev = 0u;
+  float bval0 = 0.0f;
+  if (blen > 0u && blen <= BCAP && t < blen) {
+    bid0 = A.bids[b0 + t];
+    bval0 = A.bvals[b0 + t];
+    if (t > 0) bprev = A.bids[b0 + t - 1u];
+  }
+  const uint32_t nmw = (ntok + 31u) / 32u;
+  uint32_t mw0 = 0xffffffffu, mw1 = 0xffffffffu;
+  if (A.masked) {
+    const uint32_t* mrow = A.mask + (uint64_t)row * A.mstride + (c0 >> 5);
+    if (t < nmw) mw0 = mrow[t];
+    if (t + PT < nmw) mw1 = mrow[t + PT];
+  }
+  __asm__ volatile("" ::: "memory");
+  typename Q::Raw raw[QMAX];
+  const In* lrow = (const In*)A.logits + (uint64_t)row * A.stride + c0;
+#pragma unroll
+  for (int j = 0; j < QMAX; ++j) {
+    const uint32_t q = (uint32_t)j * PT + t;
+    if (j < (int)A.per && q < nq) raw[j] = Q::load(lrow + 4u * q);
+    else raw[j] = typename Q::Raw{};
+  }
+  __asm__ volatile("" ::: "memory");
+  Cfg cf = load_cfg(A, row);
   stamp(A, row, c, 0u);
-  const Cfg cf = load_cfg(A, row);
   if (cf.err) {
     if (c == 0 && t == 0) put_row(A, row, cf.err, -1, 0.0, 0u);
     return;
@@ -1004,54 +1073,17 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
   const bool keepall_possible = !greedy && !kknown && cf.top_p >= 1.0 && cf.min_p == 0.0;
   const bool need_seg = keepall_possible && !A.nodraw && !kmaybe;
   const bool need_mass = !greedy && !kknown && cf.top_p < 1.0;
-  const uint32_t topr = (kknown || kmaybe) ? (k <= 512u ? 1u : (k <= 2048u ? 4u : 40u)) : 0u;
-  const int lm = greedy ? LM_GREEDY : (need_seg ? LM_SEG : (topr == 4u ? LM_TOP4 : LM_PLAIN));
-  const bool has_hist = cf.hlen > 0u, has_bias = cf.blen > 0u;
-  const bool long_hist = cf.hlen > HTAB_MAX;
+  // top-k bound from each thread's largest value (k <= 128), two largest
+  // (k <= 1024) or every value
+  const uint32_t topr = (kknown || kmaybe) ? (k <= 128u ? 1u : (k <= 1024u ? 2u : 40u)) : 0u;
+  const int mode = need_mass ? M_MASS : (topr == 2u ? M_TOP2 : M_PLAIN);
+  const bool has_hist = hlen > 0u, has_bias = blen > 0u;
+  const bool long_hist = hlen > HTAB_MAX;
   const bool use_tab = has_hist || has_bias;
-
-  // ---- loads: history ids first, then bias, mask words and the logits
-  uint32_t hreg[4];
-  const uint32_t hfirst = min(cf.hlen, 4u * (uint32_t)PT);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const uint32_t i = t + (uint32_t)r * PT;
-    hreg[r] = i < hfirst ? A.hids[cf.h0 + i] : 0u;
-  }
-  uint32_t bid0 = 0u;
-  float bval0 = 0.0f;
-  if (has_bias && cf.blen <= BCAP && t < cf.blen) {
-    bid0 = A.bids[cf.b0 + t];
-    bval0 = A.bvals[cf.b0 + t];
-  }
-  const uint32_t nmw = (ntok + 31u) / 32u;
-  uint32_t mw0 = 0xffffffffu, mw1 = 0xffffffffu;
-  if (A.masked) {
-    const uint32_t* mrow = A.mask + (uint64_t)row * A.mstride + (c0 >> 5);
-    if (t < nmw) mw0 = mrow[t];
-    if (t + PT < nmw) mw1 = mrow[t + PT];
-  }
-  typename Q::Raw raw[QMAX];
-  const In* lrow = (const In*)A.logits + (uint64_t)row * A.stride + c0;
-#pragma unroll
-  for (int j = 0; j < QMAX; ++j) {
-    const uint32_t q = (uint32_t)j * PT + t;
-    if (j < (int)A.per && q < nq) raw[j] = Q::load(lrow + 4u * q);
-    else raw[j] = typename Q::Raw{};
-  }
-  stamp(A, row, c, 1u);
 
   // ---- LDS: count table, mask words, bias list
   if (use_tab)
     for (uint32_t q = t; q < nq; q += PT) *reinterpret_cast<uint2*>(&S.u.c.ctab[2u * q]) = make_uint2(0u, 0u);
-  if (A.masked) {
-    if (t < nmw) S.u.c.mask[t] = mw0;
-    if (t + PT < nmw) S.u.c.mask[t + PT] = mw1;
-  }
-  if (has_bias && cf.blen <= BCAP && t < cf.blen) {
-    S.u.c.bid[t] = bid0;
-    S.u.c.bval[t] = bval0;
-  }
   uint32_t* gt = A.s.gtab + (uint64_t)row * A.s.gtab_stride + c0;
   if (long_hist) {
     // counts past 15 bits: u32 counts in global scratch, LDS marks presence
@@ -1059,7 +1091,20 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
+  // the logarithms the thresholds and the finisher use
+  cf.L_mp = uni(cf.min_p > 0.0 ? log(cf.min_p) : -INFINITY);
+  cf.L_nuc = uni((cf.top_p < 1.0 && 1.0 - cf.top_p > 8.0 * (double)V * U53)
+                     ? log((1.0 - cf.top_p) / (2.0 * (double)V))
+                     : -INFINITY);
   bar();
+  if (A.masked) {
+    if (t < nmw) S.u.c.mask[t] = mw0;
+    if (t + PT < nmw) S.u.c.mask[t + PT] = mw1;
+  }
+  if (has_bias && blen <= BCAP && t < blen) {
+    S.u.c.bid[t] = bid0;
+    S.u.c.bval[t] = bval0;
+  }
   uint32_t flags = cf.uerr ? F_UNIFORM : 0u;
   const uint32_t span = nq * 4u;
   auto scat = [&](uint32_t id) {
@@ -1076,9 +1121,9 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
   };
   if (has_hist) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (t + (uint32_t)r * PT < hfirst) scat(hreg[r]);
-    for (uint32_t i = 4u * PT + t; i < cf.hlen; i += PT) scat(A.hids[cf.h0 + i]);
+    for (uint32_t r = 0; r < HR; ++r)
+      if (t + r * PT < hfirst) scat(hreg[r]);
+    for (uint32_t i = HR * PT + t; i < hlen; i += PT) scat(A.hids[h0 + i]);
   }
   if (has_bias) {
     auto mark = [&](uint32_t id, float v, bool bad) {
@@ -1086,12 +1131,12 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
       const uint32_t r = id - c0;
       if (r < span) atomicOr(&S.u.c.ctab[r >> 1], 0x8000u << (16u * (r & 1u)));
     };
-    if (cf.blen <= BCAP) {
-      if (t < cf.blen) mark(bid0, bval0, t > 0 && A.bids[cf.b0 + t - 1u] >= bid0);
+    if (blen <= BCAP) {
+      if (t < blen) mark(bid0, bval0, t > 0 && bprev >= bid0);
     } else {
-      for (uint32_t i = t; i < cf.blen; i += PT) {
-        const uint32_t id = A.bids[cf.b0 + i];
-        mark(id, A.bvals[cf.b0 + i], i > 0 && A.bids[cf.b0 + i - 1u] >= id);
+      for (uint32_t i = t; i < blen; i += PT) {
+        const uint32_t id = A.bids[b0 + i];
+        mark(id, A.bvals[b0 + i], i > 0 && A.bids[b0 + i - 1u] >= id);
       }
     }
   }
@@ -1100,122 +1145,208 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");
   }
   bar();
-  stamp(A, row, c, 2u);
+  stamp(A, row, c, 1u);
 
-  // ---- the quad loop: bias and penalties, the finite check, the mask and
-  // the running maximum as each quad lands; top-p rows also sum their f32
-  // mass online, relative to the thread's running maximum
+  // ---- the quad loop, as the stream lands: bias and penalties for the
+  // listed tokens, the grammar mask, the finite check, the maximum and (by
+  // mode) the two largest values or the online f32 mass
   const uint32_t tvl = A.masked ? min(A.tv, V) : V;
-  // x: the adjusted values (for f32, the loaded registers themselves);
-  // lg0/lg1: legal bits, 4 per quad round; val(j, i) is x[j][i] when legal,
-  // else -inf
+  // x: the adjusted values (for f32, the loaded registers themselves).  After
+  // the loop, a token outside the chunk, past V or illegal under the mask
+  // holds -inf, so later passes read x alone.
   float x[QMAX][4];
-  uint32_t lg0 = 0u, lg1 = 0u;
-  auto val = [&](int j, int i) -> float {
-    return (((j < 8 ? lg0 : lg1) >> (4 * (j & 7) + i)) & 1u) ? x[j][i] : -INFINITY;
-  };
-  float tmax = -INFINITY;
-  uint32_t nfin = 0u, nleg = 0u;
+  uint32_t lg0 = 0u, lg1 = 0u, nleg = 0u;
+  float tmax = -INFINITY, t1 = -INFINITY;
+  float nfa = 0.0f;   // sum of x * 0 over the in-range values: NaN iff one is not finite
   const float c32 = need_mass ? (float)(LOG2E * cf.invT) : 0.0f;
   float ms = 0.0f, meb = 0.0f, mex = 0.0f, mref = -INFINITY;
   uint32_t mn = 0u;
   const uint32_t kwords = (V + 31u) / 32u;
+  // tokens of quad round j this thread holds that lie in the chunk and below V
+  auto in_range = [&](int j) -> uint32_t {
+    const uint32_t q = (uint32_t)j * PT + t;
+    const uint32_t g0 = c0 + 4u * q;
+    if (q >= nq) return 0u;
+    return g0 + 4u <= V ? 0xfu : ((1u << (V - g0)) - 1u);
+  };
+  // bias and penalties of listed token `tok` (table entry f != 0)
+  auto adjust = [&](float v, uint32_t f, uint32_t tok) {
+    uint32_t cnt = f & 0x7fffu;
+    if (long_hist && cnt) cnt = __hip_atomic_load(gt + (tok - c0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t hb = f >> 15;
+    float bv = 0.0f;
+    if (hb) bv = bias_of(A, cf, S, tok);
+    return bias_and_penalize(v, (hb << 31) | cnt, bv, cf.rep, cf.inv_rep, cf.freq, cf.pres);
+  };
+  // the online f32 mass of one quad's legal values (leg), whose maximum is qm
+  auto mass_quad = [&](int j, float qm, uint32_t leg) {
+    if (qm > mref) {
+      if (mref > -INFINITY) {
+        // rescale to the new reference; its own error joins the bound
+        const float y = (mref - qm) * c32;
+        const float f = __builtin_amdgcn_exp2f(y);
+        mex = mex * f + ms * f * (-2.1f * y * U24 + 6.0f * U24);
+        ms *= f;
+        meb *= f;
+      }
+      mref = qm;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if ((leg >> i) & 1u) {
+        const float y = (x[j][i] - mref) * c32;
+        const float ev = __builtin_amdgcn_exp2f(y);
+        ms += ev;
+        meb = fmaf(ev, -y, meb);
+        ++mn;
+      }
+    }
+  };
+  // the penalties alone (no bias entry, count in 15 bits): bias_and_penalize
+  // for that case
+  auto penalize = [&](float v, uint32_t cnt) {
+    const float r = v < 0.0f ? v * cf.rep : div_by_recip(v, cf.inv_rep);
+    const float fq = (float)cnt * cf.freq;
+    return (r - fq) - cf.pres;
+  };
+  // the listed tokens of a quad in any case: one slot per pass, every pass
+  // running the whole bias-and-penalty stage (the lanes of a wave rarely
+  // hold more than one listed token of a round)
+  auto adjust_quad = [&](int j, uint2 e, uint32_t rng, uint32_t g0) {
+    uint32_t pend = (((e.x & 0xffffu) != 0u) ? 1u : 0u) | (((e.x >> 16) != 0u) ? 2u : 0u) |
+                    (((e.y & 0xffffu) != 0u) ? 4u : 0u) | (((e.y >> 16) != 0u) ? 8u : 0u);
+    pend &= rng;
+    while (pend) {
+      const uint32_t i = (uint32_t)__builtin_ctz(pend);
+      pend &= pend - 1u;
+      const uint32_t f = (((i & 2u) ? e.y : e.x) >> (16u * (i & 1u))) & 0xffffu;
+      const float v = (i & 2u) ? ((i & 1u) ? x[j][3] : x[j][2]) : ((i & 1u) ? x[j][1] : x[j][0]);
+      const float nv = adjust(v, f, g0 + i);
+      x[j][0] = i == 0u ? nv : x[j][0];
+      x[j][1] = i == 1u ? nv : x[j][1];
+      x[j][2] = i == 2u ? nv : x[j][2];
+      x[j][3] = i == 3u ? nv : x[j][3];
+    }
+  };
+  // rows without a grammar mask whose listed tokens are history entries
+  // only, counted in LDS
+  const bool fast = !A.masked && blen == 0u && !long_hist;
+  // full rounds: every lane's quad complete and below V
+  const uint32_t nfull = (ntok / 4u) / (uint32_t)PT;
 #pragma unroll
   for (int j = 0; j < QMAX; ++j) {
     Q::unpack(raw[j], x[j]);
     if (j < (int)A.per) {
       const uint32_t q = (uint32_t)j * PT + t;
-      const bool inq = q < nq;
       const uint32_t g0 = c0 + 4u * q;
-      uint32_t rng = 0u;
-      if (inq) rng = g0 + 4u <= V ? 0xfu : ((1u << (V - g0)) - 1u);
-      if (use_tab) {
-        const uint2 e = inq ? *reinterpret_cast<const uint2*>(&S.u.c.ctab[2u * q]) : make_uint2(0u, 0u);
-        if (ballot((e.x | e.y) != 0u)) {
+      if (fast && (uint32_t)j < nfull) {
+        // a full round without a grammar mask or bias list: every token in
+        // range and legal
+        if (use_tab) {
+          const uint2 e = *reinterpret_cast<const uint2*>(&S.u.c.ctab[2u * q]);
+          if (ballot((e.x | e.y) != 0u)) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t f = ((i < 2 ? e.x : e.y) >> (16 * (i & 1))) & 0xffffu;
-            if (f && ((rng >> i) & 1u)) {
-              const uint32_t tok = g0 + (uint32_t)i;
-              uint32_t cnt = f & 0x7fffu;
-              if (long_hist && cnt)
-                cnt = __hip_atomic_load(gt + (tok - c0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              const uint32_t hb = f >> 15;
-              const float bv = hb ? bias_of(A, cf, S, tok) : 0.0f;
-              x[j][i] = bias_and_penalize(x[j][i], (hb << 31) | cnt, bv, cf.rep, cf.inv_rep, cf.freq, cf.pres);
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t f = ((i < 2 ? e.x : e.y) >> (16 * (i & 1))) & 0xffffu;
+              if (ballot(f != 0u) && f) x[j][i] = penalize(x[j][i], f);
             }
           }
         }
-      }
-      if (A.adjusted && inq) {
-        float* ap = A.adjusted + (uint64_t)row * V + g0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if ((rng >> i) & 1u) ap[i] = x[j][i];
-      }
+        for (int i = 0; i < 4; ++i) nfa = fmaf(x[j][i], 0.0f, nfa);
+        nleg += 4u;
+        if (mode == M_TOP2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (((rng >> i) & 1u) && !isfinite(x[j][i])) nfin = 1u;
-      uint32_t leg = rng;
-      if (A.masked) {
-        leg &= (S.u.c.mask[q >> 3] >> ((q & 7u) * 4u)) & 0xfu;
-        if (g0 + 4u > tvl) leg &= g0 >= tvl ? 0u : ((1u << (tvl - g0)) - 1u);
-      }
-      nleg += popc(leg);
-      if (j < 8) lg0 |= leg << (4 * j); else lg1 |= leg << (4 * (j - 8));
-      const float qm = fmax_(fmax_(val(j, 0), val(j, 1)), fmax_(val(j, 2), val(j, 3)));
-      tmax = fmax_(tmax, qm);
-      if (need_mass && qm > -INFINITY) {
-        if (qm > mref) {
-          if (mref > -INFINITY) {
-            // rescale to the new reference; its own error joins the bound
-            const float y = (mref - qm) * c32;
-            const float f = __builtin_amdgcn_exp2f(y);
-            mex = mex * f + ms * f * (-2.1f * y * U24 + 6.0f * U24);
-            ms *= f;
-            meb *= f;
+          for (int i = 0; i < 4; ++i) {
+            const float b = vmin(tmax, x[j][i]);
+            tmax = vmax(tmax, x[j][i]);
+            t1 = vmax(t1, b);
           }
-          mref = qm;
+        } else if (mode == M_MASS) {
+          const float qm = vmax3(x[j][0], x[j][1], vmax(x[j][2], x[j][3]));
+          tmax = vmax(tmax, qm);
+          mass_quad(j, qm, 0xfu);
+        } else {
+          tmax = vmax3(tmax, x[j][0], x[j][1]);
+          tmax = vmax3(tmax, x[j][2], x[j][3]);
+        }
+      } else {
+        // the chunk's last partial round, a grammar-masked row, or a row
+        // with a bias list or a long history
+        const uint32_t rng = in_range(j);
+        if (use_tab) {
+          const uint2 e = rng ? *reinterpret_cast<const uint2*>(&S.u.c.ctab[2u * q]) : make_uint2(0u, 0u);
+          if (ballot((e.x | e.y) != 0u)) adjust_quad(j, e, rng, g0);
+        }
+        uint32_t leg = rng;
+        if (A.masked) {
+          leg &= (S.u.c.mask[q >> 3] >> ((q & 7u) * 4u)) & 0xfu;
+          if (g0 + 4u > tvl) leg &= g0 >= tvl ? 0u : ((1u << (tvl - g0)) - 1u);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if ((leg >> i) & 1u) {
-            const float y = (x[j][i] - mref) * c32;
-            const float e = __builtin_amdgcn_exp2f(y);
-            ms += e;
-            meb = fmaf(e, -y, meb);
-            ++mn;
+          if ((rng >> i) & 1u) nfa = fmaf(x[j][i], 0.0f, nfa);
+        if (j < 8) lg0 |= leg << (4 * j); else lg1 |= leg << (4 * (j - 8));
+        nleg += popc(leg);
+        float v4[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v4[i] = ((leg >> i) & 1u) ? x[j][i] : -INFINITY;
+        const float qm = vmax3(v4[0], v4[1], vmax(v4[2], v4[3]));
+        if (mode == M_TOP2) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float b = vmin(tmax, v4[i]);
+            tmax = vmax(tmax, v4[i]);
+            t1 = vmax(t1, b);
           }
+        } else {
+          tmax = vmax(tmax, qm);
+        }
+        if (mode == M_MASS && qm > -INFINITY) mass_quad(j, qm, leg);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+  const uint32_t nfin = nfa == 0.0f ? 0u : 1u;
+  stamp(A, row, c, 2u);
+
+  // the adjusted logits (debug output), from the registers
+  if (A.adjusted) {
+#pragma unroll
+    for (int j = 0; j < QMAX; ++j) {
+      if (j < (int)A.per) {
+        const uint32_t rng = in_range(j);
+        float* ap = A.adjusted + (uint64_t)row * V + c0 + 4u * ((uint32_t)j * PT + t);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if ((rng >> i) & 1u) ap[i] = x[j][i];
+      }
+    }
+  }
+  // from here on x alone tells legality: every other slot becomes -inf
+#pragma unroll
+  for (int j = 0; j < QMAX; ++j) {
+    if (j < (int)A.per && (A.masked || (uint32_t)j >= nfull)) {
+      const uint32_t leg = ((j < 8 ? lg0 : lg1) >> (4 * (j & 7))) & 0xfu;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[j][i] = ((leg >> i) & 1u) ? x[j][i] : -INFINITY;
+    } else if (j >= (int)A.per) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[j][i] = -INFINITY;
+    }
+  }
   // greedy: IEEE argmax, lowest id on ties (-0 ties +0)
-  float gv = 0.0f;
+  float gv = -INFINITY;
   uint32_t gi = NONE;
   if (greedy) {
 #pragma unroll
     for (int j = 0; j < QMAX; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (val(j, i) > -INFINITY && (gi == NONE || val(j, i) > gv)) {
-          gv = val(j, i);
+        if (x[j][i] > gv) {
+          gv = x[j][i];
           gi = c0 + 4u * ((uint32_t)j * PT + t) + (uint32_t)i;
         }
-  }
-  // top-k over 512: each thread's four largest values bound the chunk's k-th
-  float tp0 = -INFINITY, tp1 = -INFINITY, tp2 = -INFINITY, tp3 = -INFINITY;
-  if (topr == 4u) {
-#pragma unroll
-    for (int j = 0; j < QMAX; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float y = val(j, i);
-        const float a0 = fmax_(tp0, y), b0 = fminf(tp0, y);
-        const float a1 = fmax_(tp1, b0), b1 = fminf(tp1, b0);
-        const float a2 = fmax_(tp2, b1), b2 = fminf(tp2, b1);
-        tp0 = a0; tp1 = a1; tp2 = a2; tp3 = fmax_(tp3, b2);
-      }
   }
   // keep-all rows: f64 mass of each 256-token segment (wave w, round j)
   float tmin = INFINITY;
@@ -1224,7 +1355,7 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
 #pragma unroll
     for (int j = 0; j < QMAX; ++j) {
       if (j < (int)A.per) {
-        const float qm = fmax_(fmax_(val(j, 0), val(j, 1)), fmax_(val(j, 2), val(j, 3)));
+        const float qm = vmax3(x[j][0], x[j][1], vmax(x[j][2], x[j][3]));
         const uint32_t wk = wave_max_u32(qm > -INFINITY ? okey(qm) : 0u);
         double sm = 0.0;
         float ref = -INFINITY;
@@ -1232,9 +1363,9 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
           ref = okey_value(wk);
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (val(j, i) > -INFINITY) {
-              sm += seg_w(val(j, i), ref, cf.invT);
-              tmin = fminf(tmin, val(j, i));
+            if (x[j][i] > -INFINITY) {
+              sm += seg_w(x[j][i], ref, cf.invT);
+              tmin = fminf(tmin, x[j][i]);
             }
         }
         sm = wave_sum_f64(sm);
@@ -1249,7 +1380,6 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  stamp(A, row, c, 3u);
   // kept bits: keep-all rows (the legal set, unless a top-k may apply) write
   // the chunk's legal words; every other row clears them for the finisher
   if (A.kept_bits) {
@@ -1265,85 +1395,72 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
       kb[i] = bits;
     }
   }
-  bar();   // every wave is done with the count table (the LDS pool is reused)
+  stamp(A, row, c, 4u);
 
   // ---- chunk reductions
-  const bool want_hist = topr > 0u && topr <= 40u;
-  if (want_hist)
-    for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.hist[b] = 0u;
   {
     const uint32_t wk = wave_max_u32(tmax > -INFINITY ? okey(tmax) : 0u);
     const uint32_t wmin = ~wave_max_u32(tmin < INFINITY ? ~okey(tmin) : 0u);
     const uint32_t wf = wave_or_u32(flags | (nfin ? F_NONFINITE : 0u));
     const uint32_t wl = wave_sum_u32(nleg);
-    const unsigned long long gk =
-        wave_max_u64(gi != NONE ? (((unsigned long long)okey(gv == 0.0f ? 0.0f : gv) << 32) | (unsigned long long)(~gi))
-                                : 0ull);
     if (L == 0u) {
-      S.ru[w] = wk;
-      S.ru[PW + w] = wf;
-      S.ru[2 * PW + w] = wl;
-      S.ru[3 * PW + w] = wmin;
-      S.r64[w] = gk;
+      S.wr[w] = wk;
+      S.wr[PW + w] = wf;
+      S.wr[2 * PW + w] = wl;
+      S.wr[3 * PW + w] = wmin;
+    }
+    if (greedy) {
+      const unsigned long long gk = wave_max_u64(
+          gi != NONE ? (((unsigned long long)okey(gv == 0.0f ? 0.0f : gv) << 32) | (unsigned long long)(~gi)) : 0ull);
+      if (L == 0u) S.wg[w] = gk;
     }
   }
-  bar();
-  uint32_t Mkey = 0u, cfl = 0u, nl_c = 0u, minkey = NONE;
-  unsigned long long gbest = 0ull;
+  bar();   // (also: every wave is done with the count table, whose LDS the histogram reuses)
+  // the chunk maximum and legal count now; flags, minimum and greedy key
+  // only where the statistics are written
+  uint32_t Mkey = 0u, nl_c = 0u;
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
-    minkey = min(minkey, S.ru[3 * PW + i]);
-    Mkey = max(Mkey, S.ru[i]);
-    cfl |= S.ru[PW + i];
-    nl_c += S.ru[2 * PW + i];
-    gbest = max(gbest, S.r64[i]);
+    Mkey = max(Mkey, S.wr[i]);
+    nl_c += S.wr[2 * PW + i];
   }
+  Mkey = uni(Mkey);
+  nl_c = uni(nl_c);
   const float Mc = okey_value(Mkey);
-  bar();
-  // publish the chunk maximum (min-p and top-p bounds use the best seen)
-  if (!greedy && Mkey && t == 0)
-    S.bc[0] = max(atomicMax(A.s.rowmax + row, Mkey), Mkey);
-  // top-k bound: a value grid of 1/64 logit below the chunk maximum
+  const bool want_hist = topr > 0u && topr <= 40u;
   const bool k_here = kknown || (kmaybe && nl_c > k);
-  if (want_hist && k_here && Mkey) {
+  const bool hist_now = want_hist && k_here && Mkey;
+  // rows whose threshold rests on the row maximum publish the chunk's and
+  // read back the best seen so far
+  const bool need_rowmax = !greedy && Mkey && !k_here && !kmaybe && !keepall_possible &&
+                           !(A.masked && nl_c <= 4096u) && (cf.min_p > 0.0 || cf.L_nuc > -INFINITY);
+  if (hist_now)
+    for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.hist[b] = 0u;
+  if (need_rowmax && t == 0)
+    S.bc[0] = max(__hip_atomic_fetch_max(A.s.sync + (uint64_t)row * SYNC + 1u, Mkey, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT),
+                  Mkey);
+  bar();
+  // top-k bound: a value grid of 1/64 logit below the chunk maximum
+  uint32_t bstar = NONE;
+  if (hist_now) {
     auto add = [&](float y) {
       const float d = (Mc - y) * 64.0f;
       if (d < (float)NB) atomicAdd(&S.u.hist[(uint32_t)d], 1u);
     };
     if (topr == 1u) {
       if (tmax > -INFINITY) add(tmax);
-    } else if (topr == 4u) {
-      if (tp0 > -INFINITY) add(tp0);
-      if (tp1 > -INFINITY) add(tp1);
-      if (tp2 > -INFINITY) add(tp2);
-      if (tp3 > -INFINITY) add(tp3);
+    } else if (topr == 2u) {
+      if (tmax > -INFINITY) add(tmax);
+      if (t1 > -INFINITY) add(t1);
     } else {
 #pragma unroll
       for (int j = 0; j < QMAX; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          if (val(j, i) > -INFINITY) add(val(j, i));
+          if (x[j][i] > -INFINITY) add(x[j][i]);
     }
-  }
-  // chunk mass for the top-p total: each thread's online f32 sum scaled to
-  // the chunk maximum in f64, with a rigorous bound.  Per term: |y| ln2 3u
-  // (y rounded thrice) + 4u (v_exp_f32); f32 additions n u; results below
-  // 2^-126 absolute; rescales (mex) as accumulated in the loop.
-  double cmass = 0.0, cerr = 0.0;
-  if (need_mass && Mkey) {
-    double sm = 0.0, b = 0.0;
-    if (mref > -INFINITY) {
-      const double g = exp_neg(((double)mref - (double)Mc) * cf.invT);
-      sm = (double)ms * g;
-      b = ((double)meb * 2.1 * (double)U24 + (double)ms * (4.0 + (double)mn) * 1.01 * (double)U24 + (double)mex +
-           (double)mn * 1.1754943508222875e-38) * g * 1.001 + sm * 4.0 * U53;
-    }
-    cmass = bsum_f64(sm, S);
-    cerr = bsum_f64(b, S) + cmass * 16.0 * U53;
-  }
-  bar();
-  uint32_t bstar = NONE;
-  if (want_hist && k_here && Mkey) {
+    bar();
     uint32_t h4[4];
     uint32_t hs = 0u;
 #pragma unroll
@@ -1353,15 +1470,15 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
     }
     uint32_t tot;
     const uint32_t inc = bscan_u32(hs, S, &tot);
-    if (t == 0) S.bc[1] = NONE;
-    bar();
     if (inc - hs < k && inc >= k) {
       uint32_t r = inc - hs;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        if (r < k && r + h4[q] >= k) { S.bc[1] = 4u * t + (uint32_t)q; }
+        if (r < k && r + h4[q] >= k) S.bc[1] = 4u * t + (uint32_t)q;
         r += h4[q];
       }
+    } else if (t == PT - 1u && inc < k) {
+      S.bc[1] = NONE;   // fewer than k values on the grid
     }
     bar();
     bstar = S.bc[1];
@@ -1370,10 +1487,9 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
   // row's decision can need
   float thr = greedy ? INFINITY : -INFINITY;   // a chunk without legal tokens bounds nothing
   if (!greedy && Mkey) {
-    const float Mb = okey_value(S.bc[0]);   // best row maximum seen (>= Mc)
     if (k_here) {
       thr = -INFINITY;
-      if (topr <= 40u && bstar != NONE) {
+      if (bstar != NONE) {
         const float lim = Mc - (float)(bstar + 1u) * (1.0f / 64.0f);
         thr = lim - (fabsf(Mc) + 32.0f) * 4.0f * U24;
       }
@@ -1383,49 +1499,55 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
       thr = -INFINITY;
     } else if (keepall_possible) {
       thr = INFINITY;      // keep-all: segment masses, no candidates
-    } else {
+    } else if (need_rowmax) {
+      const float Mb = okey_value(S.bc[0]);   // best row maximum seen (>= Mc)
       double lim = -INFINITY;
-      if (cf.min_p > 0.0) lim = fmax(lim, (double)Mb + cf.T * log(cf.min_p));
-      if (cf.top_p < 1.0 && 1.0 - cf.top_p > 8.0 * (double)V * U53)
-        lim = fmax(lim, (double)Mb + cf.T * log((1.0 - cf.top_p) / (2.0 * (double)V)));
-      if (lim > -INFINITY) {
-        const float lf = (float)lim;
-        thr = lf - (fabsf(lf) + fabsf(Mb)) * 1e-6f - 1e-37f;
-        if (!(thr > -INFINITY)) thr = -INFINITY;
-      } else {
-        thr = -INFINITY;
-      }
+      if (cf.min_p > 0.0) lim = fmax(lim, (double)Mb + cf.T * cf.L_mp);
+      if (cf.L_nuc > -INFINITY) lim = fmax(lim, (double)Mb + cf.T * cf.L_nuc);
+      const float lf = (float)lim;
+      thr = lf - (fabsf(lf) + fabsf(Mb)) * 1e-6f - 1e-37f;
+      if (!(thr > -INFINITY)) thr = -INFINITY;
     }
   }
-  stamp(A, row, c, 4u);
+  stamp(A, row, c, 5u);
 
   // ---- candidate emission in token-ID order: (quad round, wave, lane,
-  // token); each lane's candidate bits are packed 4 per round
+  // token).  Candidates are the values >= thr (-inf excluded); the four
+  // slots' wave masks give each (round, wave) segment's count, then each
+  // lane's place in it.
   uint32_t ncand = 0u;
   if (thr < INFINITY) {
-    uint32_t pk0 = 0u, pk1 = 0u;
+    const float te = fmaxf(thr, -3.402823466e38f);
 #pragma unroll
     for (int j = 0; j < QMAX; ++j) {
-      uint32_t bits = 0u;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bits |= (val(j, i) > -INFINITY && val(j, i) >= thr) ? (1u << i) : 0u;
-      if (j < 8) pk0 |= bits << (4 * j); else pk1 |= bits << (4 * (j - 8));
-    }
-#pragma unroll
-    for (int j = 0; j < QMAX; ++j) {
-      const uint32_t bits = ((j < 8 ? pk0 : pk1) >> (4 * (j & 7))) & 0xfu;
-      const uint32_t tot = wave_sum_u32(popc(bits));
-      if (L == 0u && j < (int)A.per) S.wcnt[(uint32_t)j * PW + w] = tot;
-      __builtin_amdgcn_sched_barrier(0);
+      if (j < (int)A.per) {
+        const uint64_t m0 = ballot(x[j][0] >= te), m1 = ballot(x[j][1] >= te);
+        const uint64_t m2 = ballot(x[j][2] >= te), m3 = ballot(x[j][3] >= te);
+        const uint32_t cnt = (uint32_t)(__builtin_popcountll(m0) + __builtin_popcountll(m1) +
+                                        __builtin_popcountll(m2) + __builtin_popcountll(m3));
+        if (L == 0u) S.wcnt[(uint32_t)j * PW + w] = cnt;
+      }
     }
     bar();
     if (w == 0u) {
+      // (quad round, wave) counts in order, QMAX * PW of them over 64 lanes
       const uint32_t ne = A.per * (uint32_t)PW;
-      const uint32_t a = 2u * L < ne ? S.wcnt[2u * L] : 0u;
-      const uint32_t b = 2u * L + 1u < ne ? S.wcnt[2u * L + 1u] : 0u;
-      const uint32_t inc = wave_scan_u32(a + b);
-      if (2u * L < ne) S.woff[2u * L] = inc - a - b;
-      if (2u * L + 1u < ne) S.woff[2u * L + 1u] = inc - b;
+      constexpr uint32_t PER_LANE = (QMAX * PW + 63) / 64;
+      uint32_t a[PER_LANE], sum = 0u;
+#pragma unroll
+      for (uint32_t r = 0; r < PER_LANE; ++r) {
+        const uint32_t i = PER_LANE * L + r;
+        a[r] = i < ne ? S.wcnt[i] : 0u;
+        sum += a[r];
+      }
+      const uint32_t inc = wave_scan_u32(sum);
+      uint32_t off = inc - sum;
+#pragma unroll
+      for (uint32_t r = 0; r < PER_LANE; ++r) {
+        const uint32_t i = PER_LANE * L + r;
+        if (i < ne) S.woff[i] = off;
+        off += a[r];
+      }
       if (L == 63u) S.bc[2] = inc;
     }
     bar();
@@ -1433,22 +1555,56 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
     uint2* cb = A.s.cand + (uint64_t)row * A.s.cand_stride + (uint64_t)c * A.CH;
 #pragma unroll
     for (int j = 0; j < QMAX; ++j) {
-      const uint32_t bits = ((j < 8 ? pk0 : pk1) >> (4 * (j & 7))) & 0xfu;
-      if (j < (int)A.per && ballot(bits != 0u)) {
-        const uint32_t cnt = popc(bits);
-        uint32_t p = S.woff[(uint32_t)j * PW + w] + wave_scan_u32(cnt) - cnt;
-        const uint32_t g0 = c0 + 4u * ((uint32_t)j * PT + t);
+      if (j < (int)A.per) {
+        const uint64_t m0 = ballot(x[j][0] >= te), m1 = ballot(x[j][1] >= te);
+        const uint64_t m2 = ballot(x[j][2] >= te), m3 = ballot(x[j][3] >= te);
+        if (m0 | m1 | m2 | m3) {
+          const uint32_t below = __builtin_amdgcn_mbcnt_hi((uint32_t)(m0 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m0, 0u)) +
+                                 __builtin_amdgcn_mbcnt_hi((uint32_t)(m1 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m1, 0u)) +
+                                 __builtin_amdgcn_mbcnt_hi((uint32_t)(m2 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m2, 0u)) +
+                                 __builtin_amdgcn_mbcnt_hi((uint32_t)(m3 >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m3, 0u));
+          uint32_t p = S.woff[(uint32_t)j * PW + w] + below;
+          const uint32_t g0 = c0 + 4u * ((uint32_t)j * PT + t);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if ((bits >> i) & 1u) cb[p++] = make_uint2(__float_as_uint(val(j, i)), g0 + (uint32_t)i);
+          for (int i = 0; i < 4; ++i) {
+            if (x[j][i] >= te) {
+              cb[p] = make_uint2(__float_as_uint(x[j][i]), g0 + (uint32_t)i);
+              ++p;
+            }
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  stamp(A, row, c, 5u);
+  stamp(A, row, c, 6u);
+
+  // chunk mass for the top-p total: each thread's online f32 sum scaled to
+  // the chunk maximum in f64, with a rigorous bound.  Per term: |y| ln2 3u
+  // (y rounded thrice) + 4u (v_exp_f32); f32 additions n u; results below
+  // 2^-126 absolute; rescales (mex) as accumulated in the loop.
+  double cmass = 0.0, cerr = 0.0;
+  if (need_mass && Mkey) {
+    double sm = 0.0, b = 0.0;
+    if (mref > -INFINITY) {
+      const double gsc = exp_neg(((double)mref - (double)Mc) * cf.invT);
+      sm = (double)ms * gsc;
+      b = ((double)meb * 2.1 * (double)U24 + (double)ms * (4.0 + (double)mn) * 1.01 * (double)U24 + (double)mex +
+           (double)mn * 1.1754943508222875e-38) * gsc * 1.001 + sm * 4.0 * U53;
+    }
+    cmass = bsum_f64(sm, S);
+    cerr = bsum_f64(b, S) + cmass * 16.0 * U53;
+  }
 
   // ---- statistics, then arrive
   if (t == 0) {
+    uint32_t cfl = 0u, minkey = NONE;
+    unsigned long long gbest = 0ull;
+    for (int i = 0; i < PW; ++i) {
+      cfl |= S.wr[PW + i];
+      minkey = min(minkey, S.wr[3 * PW + i]);
+      if (greedy) gbest = max(gbest, S.wg[i]);
+    }
     Stat st;
     st.maxkey = Mkey;
     st.gkey = (uint32_t)(gbest >> 32);
@@ -1462,15 +1618,17 @@ __global__ __launch_bounds__(PT, 4) void pick_kernel(Args A) {
     st.mass_err = cerr;
     A.s.stat[(uint64_t)row * A.s.cm + c] = st;
   }
-  // Every thread's candidate, segment, statistics and kept-bit stores are
-  // released at agent scope before the row counter moves; the last arriver
-  // acquires them.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  bar();
-  if (t == 0) S.bc[3] = __hip_atomic_fetch_add(A.s.arrive + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  bar();
+  // Every thread's candidate, segment, statistics and kept-bit stores happen
+  // before the workgroup barrier, which happens before thread 0's release
+  // on the row counter; the last arriver's acquire fence then makes all of
+  // them visible to its workgroup.
+  __syncthreads();
+  if (t == 0)
+    S.bc[3] = __hip_atomic_fetch_add(A.s.sync + (uint64_t)row * SYNC, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
   if (S.bc[3] != A.C - 1u) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (t == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __syncthreads();
   finish_row<In>(A, S, cf, row);
   stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 1u);
 }
@@ -1487,7 +1645,7 @@ int pick_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw)
   if (b->rows > ctx->max_rows || b->vocab > ctx->max_vocab)
     return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
   if (b->vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
-  if (b->vocab > pk::VMAX) return fail(ctx, MXS_EINVAL, "vocab exceeds 1310720");
+  if (b->vocab > pk::VMAX) return fail(ctx, MXS_EINVAL, "vocab exceeds 2621440");
   if (b->dtype != MXS_F32 && b->dtype != MXS_BF16) return fail(ctx, MXS_EINVAL, "dtype must be MXS_F32 or MXS_BF16");
   if (b->row_stride < b->vocab || (b->row_stride & 3u))
     return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");

@@ -4105,10 +4105,8 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
     P.cm = ly.C;
     P.cand_stride = (uint64_t)max_vocab + 32u * ly.C + 32u;
     P.gtab_stride = ((uint64_t)max_vocab + 8u) & ~(uint64_t)3u;
-    e = e ? e : hipMalloc(&P.arrive, (size_t)max_rows * sizeof(uint32_t));
-    e = e ? e : hipMemset(P.arrive, 0, (size_t)max_rows * sizeof(uint32_t));
-    e = e ? e : hipMalloc(&P.rowmax, (size_t)max_rows * sizeof(uint32_t));
-    e = e ? e : hipMemset(P.rowmax, 0, (size_t)max_rows * sizeof(uint32_t));
+    e = e ? e : hipMalloc(&P.sync, (size_t)max_rows * mxs::pk::SYNC * sizeof(uint32_t));
+    e = e ? e : hipMemset(P.sync, 0, (size_t)max_rows * mxs::pk::SYNC * sizeof(uint32_t));
     e = e ? e : hipMalloc(&P.stat, (size_t)max_rows * P.cm * sizeof(mxs::pk::Stat));
     e = e ? e : hipMalloc(&P.cand, (size_t)max_rows * P.cand_stride * sizeof(uint2));
     e = e ? e : hipMalloc(&P.seg, (size_t)max_rows * P.cm * mxs::pk::NSEG * sizeof(mxs::pk::Seg));
@@ -4180,8 +4178,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->race_ctr);
   hipFree(ctx->race_scratch);
   hipFree(ctx->race_kept);
-  hipFree(ctx->pick.arrive);
-  hipFree(ctx->pick.rowmax);
+  hipFree(ctx->pick.sync);
   hipFree(ctx->pick.stat);
   hipFree(ctx->pick.cand);
   hipFree(ctx->pick.seg);

@@ -2,12 +2,13 @@
 // single-kernel token pick behind mxs_sample (mx_sample.hip).
 //
 // One launch handles a whole batch.  Each logit row is split into C
-// balanced chunks of at most CHMAX tokens; a 512-thread workgroup streams
+// balanced chunks of at most CHMAX tokens; a 1024-thread workgroup streams
 // one chunk into registers (10 four-token quads per thread), applies logit
 // bias, penalties, the grammar mask and the finite check, reduces the
 // chunk's statistics and writes its candidate tokens.  The last workgroup
-// of a row to arrive (an agent-scope acquire-release counter) then decides
-// the row: greedy argmax, top-k -> top-p -> min-p and the inverse-CDF draw.
+// of a row to arrive (an agent-scope release / acquire on the row's
+// counter) then decides the row: greedy argmax, top-k -> top-p -> min-p and
+// the inverse-CDF draw.
 #pragma once
 #include <stdint.h>
 
@@ -16,16 +17,19 @@
 namespace mxs {
 namespace pk {
 
-constexpr int PT = 512;                         // threads per workgroup
+constexpr int PT = 1024;                        // threads per workgroup
 constexpr int PW = PT / 64;                     // waves per workgroup
 constexpr int QMAX = 10;                        // quads (4 tokens) per thread per chunk
-constexpr uint32_t CHMAX = (uint32_t)PT * QMAX * 4u;  // 20480 tokens per chunk at most
+constexpr uint32_t CHMAX = (uint32_t)PT * QMAX * 4u;  // 40960 tokens per chunk at most
 constexpr uint32_t MAXCH = 64;                  // chunks per row at most
-constexpr uint32_t VMAX = MAXCH * CHMAX;        // largest vocabulary (1,310,720)
+constexpr uint32_t VMAX = MAXCH * CHMAX;        // largest vocabulary (2,621,440)
 constexpr int NSEG = QMAX * PW;                 // 256-token segments per chunk (one per wave and quad round)
 constexpr uint32_t HTAB_MAX = 32767;            // longest history the 15-bit LDS counts take
 constexpr uint32_t BCAP = PT;                   // bias entries staged in LDS
-constexpr int NB = 2048;                        // histogram bins of the selection passes
+constexpr int NBB = 12;                         // log2 of the selection passes' histogram bins
+constexpr int NB = 1 << NBB;                    // 4096 bins, four per thread
+static_assert(NB == 4 * PT, "four histogram bins per thread");
+constexpr uint32_t SYNC = 32;                   // u32 words per row of the row-sync array (one 128-byte line)
 constexpr uint32_t NONE = 0xffffffffu;
 
 // Balanced chunk layout of a row of V tokens: C chunks of CH tokens (a
@@ -69,8 +73,11 @@ struct alignas(16) Seg {
 
 // Device scratch of mxs_sample, sized for the context's limits.
 struct Scratch {
-  uint32_t* arrive;   // [max_rows] chunks of the row done; the row's finisher resets it
-  uint32_t* rowmax;   // [max_rows] largest chunk-maximum key published so far; reset by the finisher
+  // [max_rows * SYNC]: per row, word 0 counts the chunks done and word 1
+  // holds the largest chunk-maximum key published so far; the row's
+  // finisher resets both.  Rows sit on separate cache lines, so the
+  // atomics of different rows do not queue on one line.
+  uint32_t* sync;
   Stat* stat;         // [max_rows * cm]
   uint2* cand;        // [max_rows * cand_stride] (value bits, token id)
   Seg* seg;           // [max_rows * cm * NSEG]
