@@ -60,11 +60,11 @@ __device__ __forceinline__ double rd_lane(double v, uint32_t l) {
 
 // ---------------------------------------------------------------------------
 // LDS: one static pool, carved per phase.
-struct FinHdr {
-  uint32_t Mkey, flags, nl, N, thrkey, complete, gid, mink;
-  double total, terr;
+constexpr uint32_t NCL = 6144;       // candidates the finisher keeps in LDS
+struct alignas(16) Mem {             // one gathered member of a histogram bin
+  uint32_t key, id;
+  double w;
 };
-constexpr uint32_t NCL = 8192;       // candidates the finisher keeps in LDS
 struct alignas(16) Lds {
   union {
     struct {
@@ -75,106 +75,137 @@ struct alignas(16) Lds {
     } c;
     uint32_t hist[NB];               // chunk top-k threshold histogram (after the quad loop)
     struct {
-      float cl[NCL];                 // the finisher's working candidate list
+      float cl[NCL];                 // the finisher's working candidate list (token-ID order)
       uint32_t cid[NCL];
+      double cw[NCL];                // each entry's weight exp((l - M) / T) (0 below the threshold)
       double bm[NB];                 // per-bin f64 mass
       uint32_t bc[NB];               // per-bin count
-      uint32_t mkey[64], mid[64];    // gathered members of one bin
-      double mw[64];
+      Mem mem[64];                   // gathered members of one bin
+      Mem dmem[64];                  // the register finisher's survivors in token order
+      uint32_t mix[64];              // their token-order indices
+      uint32_t dkf[64];              // kept flags in token order
       uint32_t nmem;
       uint32_t segtab[256];          // the draw segment's history counts (keep-all rows)
     } f;
   } u;
   uint32_t wcnt[QMAX * PW];          // candidates per (quad round, wave)
   uint32_t woff[QMAX * PW];
-  uint32_t ru[4 * PW];
-  unsigned long long r64[PW];
   uint32_t wr[4 * PW];               // per-wave chunk reductions (max key, flags, legal count, min key)
   unsigned long long wg[PW];         // per-wave greedy keys
-  double rd[2 * PW];
   uint32_t coff[MAXCH + 1];          // candidate offsets of the row's chunks
-  FinHdr h;
   uint32_t bc[8];                    // broadcast words
   double bd[4];
+  // one-barrier block reductions: two slot sets, used alternately
+  uint32_t xu[2][4 * PW];
+  double xd[2][2 * PW];
+  unsigned long long xq[2][PW];
 };
 
 // ---------------------------------------------------------------------------
-// Block helpers for PT-thread workgroups (every thread participates).
+// Block reductions and scans for PT-thread workgroups, one barrier each.
+// Every thread makes the same sequence of calls; successive calls alternate
+// between two LDS slot sets (Blk::p), so a set is rewritten only after a
+// later call's barrier has passed every reader of its previous contents.
 __device__ __forceinline__ uint32_t lane_() { return threadIdx.x & 63u; }
 __device__ __forceinline__ uint32_t wave_() { return threadIdx.x >> 6; }
-
-// Inclusive scan of u32 in thread order; *total receives the block total.
-__device__ __forceinline__ uint32_t bscan_u32(uint32_t v, Lds& S, uint32_t* total) {
+struct Blk {
+  uint32_t p = 0u;
+};
+// The finisher's width: a row whose candidate list is short is finished by
+// one wave (the others end once the list is in LDS), with no cross-wave
+// reductions; a long list keeps every wave.  nb histogram bins (nbb bits),
+// bpt per thread.
+struct Fw {
+  uint32_t nt, nw, nb, nbb, bpt;
+};
+constexpr uint32_t BPT_MAX = 8;
+constexpr uint32_t SHORT_LIST = 512;   // lists up to this length take one wave
+__device__ __forceinline__ uint32_t red_sum_u32(uint32_t v, Lds& S, Blk& B, uint32_t nw) {
+  v = wave_sum_u32(v);
+  if (lane_() == 0u) S.xu[B.p][wave_()] = v;
+  bar();
+  uint32_t s = 0u;
+  for (uint32_t i = 0; i < nw; ++i) s += S.xu[B.p][i];
+  B.p ^= 1u;
+  return s;
+}
+__device__ __forceinline__ uint32_t red_or_u32(uint32_t v, Lds& S, Blk& B, uint32_t nw) {
+  v = wave_or_u32(v);
+  if (lane_() == 0u) S.xu[B.p][wave_()] = v;
+  bar();
+  uint32_t s = 0u;
+  for (uint32_t i = 0; i < nw; ++i) s |= S.xu[B.p][i];
+  B.p ^= 1u;
+  return s;
+}
+__device__ __forceinline__ uint32_t red_min_u32(uint32_t v, Lds& S, Blk& B, uint32_t nw) {
+  v = ~wave_max_u32(~v);
+  if (lane_() == 0u) S.xu[B.p][wave_()] = v;
+  bar();
+  uint32_t s = NONE;
+  for (uint32_t i = 0; i < nw; ++i) s = min(s, S.xu[B.p][i]);
+  B.p ^= 1u;
+  return s;
+}
+__device__ __forceinline__ double red_sum_f64(double v, Lds& S, Blk& B, uint32_t nw) {
+  v = wave_sum_f64(v);
+  if (lane_() == 0u) S.xd[B.p][wave_()] = v;
+  bar();
+  double s = 0.0;
+  for (uint32_t i = 0; i < nw; ++i) s += S.xd[B.p][i];
+  B.p ^= 1u;
+  return s;
+}
+// The block sum of `sum` and the minimum of nonnegative `mn` (f64 bit
+// patterns of nonnegative values order as u64), in one barrier.
+__device__ __forceinline__ void red_sum_minpos_f64(double sum, double mn, Lds& S, Blk& B, double* osum, double* omin,
+                                                   uint32_t nw) {
+  sum = wave_sum_f64(sum);
+  const unsigned long long m = ~wave_max_u64(~__builtin_bit_cast(unsigned long long, mn));
+  if (lane_() == 0u) {
+    S.xd[B.p][wave_()] = sum;
+    S.xq[B.p][wave_()] = m;
+  }
+  bar();
+  double s = 0.0;
+  unsigned long long r = ~0ull;
+  for (uint32_t i = 0; i < nw; ++i) {
+    s += S.xd[B.p][i];
+    r = min(r, S.xq[B.p][i]);
+  }
+  B.p ^= 1u;
+  *osum = s;
+  *omin = __builtin_bit_cast(double, r);
+}
+// Inclusive scans in thread order (f64: the lane tree, then the waves in
+// order); *total receives the block total.
+__device__ __forceinline__ uint32_t scan_u32(uint32_t v, Lds& S, Blk& B, uint32_t* total, uint32_t nw) {
   const uint32_t inc = wave_scan_u32(v);
-  if (lane_() == 63u) S.ru[wave_()] = inc;
+  if (lane_() == 63u) S.xu[B.p][wave_()] = inc;
   bar();
   uint32_t before = 0u, all = 0u;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const uint32_t r = S.ru[i];
-    before += (uint32_t)i < wave_() ? r : 0u;
+  for (uint32_t i = 0; i < nw; ++i) {
+    const uint32_t r = S.xu[B.p][i];
+    before += i < wave_() ? r : 0u;
     all += r;
   }
-  bar();
+  B.p ^= 1u;
   *total = all;
   return before + inc;
 }
-// Inclusive scan of f64 in thread order (waves in order after the lane tree).
-__device__ __forceinline__ double bscan_f64(double v, Lds& S, double* total) {
+__device__ __forceinline__ double scan_f64(double v, Lds& S, Blk& B, double* total, uint32_t nw) {
   const double inc = wave_scan_f64(v);
-  if (lane_() == 63u) S.rd[wave_()] = inc;
+  if (lane_() == 63u) S.xd[B.p][wave_()] = inc;
   bar();
   double before = 0.0, all = 0.0;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) {
-    const double r = S.rd[i];
-    if ((uint32_t)i < wave_()) before += r;
+  for (uint32_t i = 0; i < nw; ++i) {
+    const double r = S.xd[B.p][i];
+    if (i < wave_()) before += r;
     all += r;
   }
-  bar();
+  B.p ^= 1u;
   *total = all;
   return before + inc;
-}
-__device__ __forceinline__ double bsum_f64(double v, Lds& S) {
-  double tot;
-  (void)bscan_f64(v, S, &tot);
-  return tot;
-}
-__device__ __forceinline__ uint32_t bsum_u32(uint32_t v, Lds& S) {
-  uint32_t tot;
-  (void)bscan_u32(v, S, &tot);
-  return tot;
-}
-__device__ __forceinline__ uint32_t bmin_u32(uint32_t v, Lds& S) {
-  v = ~wave_max_u32(~v);
-  if (lane_() == 0u) S.ru[wave_()] = v;
-  bar();
-  uint32_t m = NONE;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) m = min(m, S.ru[i]);
-  bar();
-  return m;
-}
-// Minimum of nonnegative f64 values (their bit patterns order as u64).
-__device__ __forceinline__ double bmin_pos_f64(double v, Lds& S) {
-  const unsigned long long m = ~wave_max_u64(~__builtin_bit_cast(unsigned long long, v));
-  if (lane_() == 0u) S.r64[wave_()] = m;
-  bar();
-  unsigned long long r = ~0ull;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) r = min(r, S.r64[i]);
-  bar();
-  return __builtin_bit_cast(double, r);
-}
-__device__ __forceinline__ uint32_t bor_u32(uint32_t v, Lds& S) {
-  v = wave_or_u32(v);
-  if (lane_() == 0u) S.ru[wave_()] = v;
-  bar();
-  uint32_t m = 0u;
-#pragma unroll
-  for (int i = 0; i < PW; ++i) m |= S.ru[i];
-  bar();
-  return m;
 }
 
 // ---------------------------------------------------------------------------
@@ -190,8 +221,7 @@ struct Cfg {
   int32_t err;
   bool greedy, uerr;
 };
-// Row-uniform values moved to scalar registers (the compiler cannot prove
-// the parameter arrays read-only, so it loads them into vector registers).
+// Row-uniform values moved to scalar registers.
 __device__ __forceinline__ uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
 __device__ __forceinline__ float uni(float v) { return __uint_as_float(uni(__float_as_uint(v))); }
 __device__ __forceinline__ double uni(double v) {
@@ -222,6 +252,8 @@ __device__ __forceinline__ Cfg load_cfg(const Args& A, uint32_t row) {
   c.uerr = !c.greedy && !(isfinite(c.u) && c.u >= 0.0 && c.u < 1.0);
   c.inv_rep = uni(1.0 / (double)c.rep);
   c.invT = uni(c.greedy ? 0.0 : 1.0 / c.T);
+  c.L_mp = -INFINITY;
+  c.L_nuc = -INFINITY;
   return c;
 }
 
@@ -258,12 +290,12 @@ __device__ __forceinline__ double seg_w(float l, float ref, double invT) {
 // The row finisher.  Runs on the last-arriving chunk workgroup of the row.
 // ===========================================================================
 
-// The row's working candidate list (token-ID order): compacted into LDS
-// when it fits, else read in place from the chunks' global lists.
+// The row's working candidate list (token-ID order): in LDS when it fits,
+// with each entry's weight, else read in place from the chunks' global lists.
 struct Work {
   uint32_t n;
   bool lds;
-  float thr;   // entries below thr are not candidates (the global lists hold some)
+  float thr;   // entries below thr are not candidates (the lists hold some)
 };
 
 __device__ __forceinline__ void wget(const Args& A, const Lds& S, uint32_t row, const Work& W, uint32_t i, float* l,
@@ -282,15 +314,104 @@ __device__ __forceinline__ void wget(const Args& A, const Lds& S, uint32_t row, 
   *l = __uint_as_float(e.x);
   *id = e.y;
 }
+// entry i's weight exp((l - M) / T): cached in LDS, else evaluated
+__device__ __forceinline__ double wgt(const Lds& S, const Work& W, uint32_t i, float l, double Md, double invT) {
+  return W.lds ? S.u.f.cw[i] : exp_neg(((double)l - Md) * invT);
+}
+
+// Passes over the working list.  For an LDS list every thread's entries are
+// loaded together first (at most RMAX per thread), so a pass costs one LDS
+// round trip rather than one per entry; a global list is walked in place.
+// each(): entries t, t + nt, ...; each_range(): the contiguous [i0, i1).
+// fn(i, l, id, w) receives the entry and its weight (cached in LDS, else
+// evaluated only when `need_w`).
+constexpr uint32_t RMAX = 8;    // 8 x 64 >= SHORT_LIST and 8 x PT >= NCL
+constexpr uint32_t RBATCH = 4;  // entries loaded together (register budget)
+template <bool need_w, typename Fn>
+__device__ __forceinline__ void each(const Args& A, const Lds& S, uint32_t row, const Work& W, const Fw& F, double Md,
+                                     double invT, Fn fn) {
+  const uint32_t t = threadIdx.x;
+  if (W.lds) {
+#pragma unroll
+    for (uint32_t r0 = 0; r0 < RMAX; r0 += RBATCH) {
+      if (t + r0 * F.nt >= W.n) break;
+      float l[RBATCH];
+      uint32_t id[RBATCH];
+      double wv[RBATCH];
+#pragma unroll
+      for (uint32_t r = 0; r < RBATCH; ++r) {
+        const uint32_t i = t + (r0 + r) * F.nt;
+        l[r] = 0.0f;
+        id[r] = 0u;
+        wv[r] = 0.0;
+        if (i < W.n) {
+          l[r] = S.u.f.cl[i];
+          id[r] = S.u.f.cid[i];
+          if (need_w) wv[r] = S.u.f.cw[i];
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < RBATCH; ++r) {
+        const uint32_t i = t + (r0 + r) * F.nt;
+        if (i < W.n) fn(i, l[r], id[r], wv[r]);
+      }
+    }
+  } else {
+    for (uint32_t i = t; i < W.n; i += F.nt) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      fn(i, l, id, need_w ? exp_neg(((double)l - Md) * invT) : 0.0);
+    }
+  }
+}
+template <bool need_w, typename Fn>
+__device__ __forceinline__ void each_range(const Args& A, const Lds& S, uint32_t row, const Work& W, uint32_t i0,
+                                           uint32_t i1, double Md, double invT, Fn fn) {
+  if (W.lds) {
+#pragma unroll
+    for (uint32_t r0 = 0; r0 < RMAX; r0 += RBATCH) {
+      if (i0 + r0 >= i1) break;
+      float l[RBATCH];
+      uint32_t id[RBATCH];
+      double wv[RBATCH];
+#pragma unroll
+      for (uint32_t r = 0; r < RBATCH; ++r) {
+        const uint32_t i = i0 + r0 + r;
+        l[r] = 0.0f;
+        id[r] = 0u;
+        wv[r] = 0.0;
+        if (i < i1) {
+          l[r] = S.u.f.cl[i];
+          id[r] = S.u.f.cid[i];
+          if (need_w) wv[r] = S.u.f.cw[i];
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < RBATCH; ++r) {
+        const uint32_t i = i0 + r0 + r;
+        if (i < i1) fn(i, l[r], id[r], wv[r]);
+      }
+    }
+  } else {
+    for (uint32_t i = i0; i < i1; ++i) {
+      float l;
+      uint32_t id;
+      wget(A, S, row, W, i, &l, &id);
+      fn(i, l, id, need_w ? exp_neg(((double)l - Md) * invT) : 0.0);
+    }
+  }
+}
 
 // Copies the entries of the chunks' global lists that satisfy keep(l, id)
-// into LDS, in token-ID order (each thread a contiguous range, then a block
-// scan).  Returns the count; the caller checks it fits beforehand.
+// into LDS with their weights, in token-ID order (each thread a contiguous
+// range, then a block scan).  Returns the count; the caller checks it fits.
 template <typename Keep>
-__device__ __forceinline__ uint32_t compact(const Args& A, Lds& S, uint32_t row, uint32_t N, Keep keep) {
+__device__ __forceinline__ uint32_t compact(const Args& A, Lds& S, Blk& B, const Fw& F, uint32_t row, uint32_t N, Keep keep,
+                                            double Md, double invT) {
   const uint32_t t = threadIdx.x;
   const Work G{N, false, -INFINITY};
-  const uint32_t R = (N + PT - 1u) / PT, i0 = min(N, t * R), i1 = min(N, i0 + R);
+  const uint32_t R = (N + F.nt - 1u) / F.nt, i0 = min(N, t * R), i1 = min(N, i0 + R);
   uint32_t mine = 0u;
   for (uint32_t i = i0; i < i1; ++i) {
     float l;
@@ -299,7 +420,7 @@ __device__ __forceinline__ uint32_t compact(const Args& A, Lds& S, uint32_t row,
     mine += keep(l, id) ? 1u : 0u;
   }
   uint32_t tot;
-  uint32_t p = bscan_u32(mine, S, &tot) - mine;
+  uint32_t p = scan_u32(mine, S, B, &tot, F.nw) - mine;
   for (uint32_t i = i0; i < i1; ++i) {
     float l;
     uint32_t id;
@@ -307,6 +428,50 @@ __device__ __forceinline__ uint32_t compact(const Args& A, Lds& S, uint32_t row,
     if (keep(l, id) && p < NCL) {
       S.u.f.cl[p] = l;
       S.u.f.cid[p] = id;
+      S.u.f.cw[p] = exp_neg(((double)l - Md) * invT);
+      ++p;
+    }
+  }
+  bar();
+  return tot;
+}
+
+// Keeps the LDS working list's entries with keep(l, id), in order, in place:
+// every thread reads its contiguous share into registers before any write.
+// Full width only (F.nt = PT).
+template <typename Keep>
+__device__ __forceinline__ uint32_t compact_lds(Lds& S, Blk& B, const Fw& F, const Work& W, Keep keep) {
+  const uint32_t t = threadIdx.x;
+  constexpr uint32_t RM = (NCL + PT - 1u) / PT;
+  const uint32_t R = (W.n + F.nt - 1u) / F.nt, i0 = min(W.n, t * R);
+  float l[RM];
+  uint32_t id[RM];
+  double wv[RM];
+  uint32_t km = 0u, mine = 0u;
+#pragma unroll
+  for (uint32_t r = 0; r < RM; ++r) {
+    const uint32_t i = i0 + r;
+    l[r] = -INFINITY;
+    id[r] = 0u;
+    wv[r] = 0.0;
+    if (r < R && i < W.n) {
+      l[r] = S.u.f.cl[i];
+      id[r] = S.u.f.cid[i];
+      wv[r] = S.u.f.cw[i];
+      if (l[r] >= W.thr && keep(l[r], id[r])) {
+        km |= 1u << r;
+        ++mine;
+      }
+    }
+  }
+  uint32_t tot;
+  uint32_t p = scan_u32(mine, S, B, &tot, F.nw) - mine;   // (its barrier also ends every read)
+#pragma unroll
+  for (uint32_t r = 0; r < RM; ++r) {
+    if ((km >> r) & 1u) {
+      S.u.f.cl[p] = l[r];
+      S.u.f.cid[p] = id[r];
+      S.u.f.cw[p] = wv[r];
       ++p;
     }
   }
@@ -330,65 +495,75 @@ __device__ __forceinline__ bool better(uint32_t ka, uint32_t ia, uint32_t kb, ui
 // (member(l, id)), finds the first member at which the running measure
 // reaches `need`.  The measure is 1 per member (MASS = false: the need-th
 // member) or its weight exp((l - M) / T) (MASS = true: the first member whose
-// inclusive running mass is >= need).  Bins of d = Mkey - key, refined 11 bits
-// at a time; a bin of at most 64 members is finished on one wave; equal keys
-// are taken in ID order.  Outputs the member's key and id, the running
+// inclusive running mass is >= need).  Bins of d = Mkey - key, refined F.nbb
+// bits at a time; a bin of at most 64 members is finished on one wave; equal
+// keys are taken in ID order.  Outputs the member's key and id, the running
 // measure before it (*before) and its own (*wself).  *found = false when the
 // members' total stays below `need` (*before then holds that total).
-template <bool MASS, typename Mem>
-__device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, const Work& W, Mem member,
+template <bool MASS, typename Memb>
+__device__ __forceinline__ void crossing(const Args& A, Lds& S, Blk& B, const Fw& F, uint32_t row, const Work& W,
+                                         Memb member,
                                          uint32_t Mkey, double Md, double invT, uint32_t dmax, double need,
                                          bool* found, uint32_t* kout, uint32_t* iout, double* before,
                                          double* wself) {
   const uint32_t t = threadIdx.x;
   uint32_t lo = 0;
-  int sh = 32 - __builtin_clz(dmax | 1u) - NBB;
+  int sh = 32 - __builtin_clz(dmax | 1u) - (int)F.nbb;
   if (sh < 0) sh = 0;
   double cum = 0.0;   // measure of the members before the current range
   for (;;) {
-    for (uint32_t b = t; b < (uint32_t)NB; b += PT) {
+    for (uint32_t b = t; b < F.nb; b += F.nt) {
       S.u.f.bc[b] = 0u;
       if (MASS) S.u.f.bm[b] = 0.0;
     }
-    if (t == 0) S.u.f.nmem = 0u;
+    if (t == 0) {
+      S.u.f.nmem = 0u;
+      S.bc[0] = NONE;
+    }
     bar();
-    const uint32_t span = sh >= 32 - NBB ? 0xffffffffu : (((uint32_t)NB << sh) - 1u);
-    for (uint32_t i = t; i < W.n; i += PT) {
-      float l;
-      uint32_t id;
-      wget(A, S, row, W, i, &l, &id);
-      if (!(l >= W.thr) || !member(l, id)) continue;
+    const uint32_t span = sh >= 32 - (int)F.nbb ? 0xffffffffu : ((F.nb << sh) - 1u);
+    each<MASS>(A, S, row, W, F, Md, invT, [&](uint32_t, float l, uint32_t id, double wv) {
+      if (!(l >= W.thr) || !member(l, id)) return;
       const uint32_t d = Mkey - okey(l);
-      if (d < lo || d - lo > span) continue;
+      if (d < lo || d - lo > span) return;
       const uint32_t b = (d - lo) >> sh;
       atomicAdd(&S.u.f.bc[b], 1u);
-      if (MASS) atomicAdd(&S.u.f.bm[b], exp_neg(((double)l - Md) * invT));
-    }
+      if (MASS) atomicAdd(&S.u.f.bm[b], wv);
+    });
     bar();
-    // thread t owns bins 4t .. 4t+3 (descending value order)
-    double m4[4];
-    uint32_t c4[4];
-    double msum = 0.0;
+    // thread t owns bins bpt t .. bpt t + bpt - 1 (descending value order)
+    uint32_t c4[BPT_MAX], csum = 0u;
+    double m4[BPT_MAX], msum = 0.0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = S.u.f.bc[4u * t + (uint32_t)q];
-      m4[q] = MASS ? S.u.f.bm[4u * t + (uint32_t)q] : (double)c4[q];
+    for (int q = 0; q < (int)BPT_MAX; ++q) {
+      c4[q] = 0u;
+      m4[q] = 0.0;
+      if (q < (int)F.bpt) {
+        c4[q] = S.u.f.bc[F.bpt * t + (uint32_t)q];
+        m4[q] = MASS ? S.u.f.bm[F.bpt * t + (uint32_t)q] : (double)c4[q];
+      }
+      csum += c4[q];
       msum += m4[q];
     }
-    double tot;
-    const double incl = bscan_f64(msum, S, &tot);
-    if (t == 0) S.bc[0] = NONE;
-    bar();
+    double incl, tot;
+    if (MASS) {
+      incl = scan_f64(msum, S, B, &tot, F.nw);
+    } else {
+      uint32_t tu;
+      incl = (double)scan_u32(csum, S, B, &tu, F.nw);
+      tot = (double)tu;
+    }
     const double tb = cum + (incl - msum);
     if (tb < need && cum + incl >= need) {
       double r = tb;
+      bool done = false;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (r + m4[q] >= need) {
-          S.bc[0] = 4u * t + (uint32_t)q;
+      for (int q = 0; q < (int)BPT_MAX; ++q) {
+        if (!done && q < (int)F.bpt && r + m4[q] >= need) {
+          S.bc[0] = F.bpt * t + (uint32_t)q;
           S.bc[1] = c4[q];
           S.bd[0] = r;
-          break;
+          done = true;
         }
         r += m4[q];
       }
@@ -399,53 +574,58 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
       *found = false;
       *before = cum + tot;
       *wself = 0.0;
-      bar();
       return;
     }
     const uint32_t bcnt = S.bc[1];
     cum = S.bd[0];
     lo += bstar << sh;
-    bar();
     if (bcnt <= 64u) {
       const uint32_t bspan = sh >= 32 ? 0xffffffffu : ((1u << sh) - 1u);
-      for (uint32_t i = t; i < W.n; i += PT) {
-        float l;
-        uint32_t id;
-        wget(A, S, row, W, i, &l, &id);
-        if (!(l >= W.thr) || !member(l, id)) continue;
+      each<MASS>(A, S, row, W, F, Md, invT, [&](uint32_t, float l, uint32_t id, double wv) {
+        if (!(l >= W.thr) || !member(l, id)) return;
         const uint32_t d = Mkey - okey(l);
-        if (d < lo || d - lo > bspan) continue;
+        if (d < lo || d - lo > bspan) return;
         const uint32_t p = atomicAdd(&S.u.f.nmem, 1u);
         if (p < 64u) {
-          S.u.f.mkey[p] = okey(l);
-          S.u.f.mid[p] = id;
-          S.u.f.mw[p] = MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
+          Mem e;
+          e.key = okey(l);
+          e.id = id;
+          e.w = MASS ? wv : 1.0;
+          S.u.f.mem[p] = e;
         }
-      }
+      });
       bar();
       if (t < 64u) {
         const uint32_t n = min(S.u.f.nmem, 64u);
-        uint32_t mk = 0u, mi = NONE;
-        double mw = 0.0;
-        if (t < n) { mk = S.u.f.mkey[t]; mi = S.u.f.mid[t]; mw = S.u.f.mw[t]; }
+        Mem me;
+        me.key = 0u;
+        me.id = NONE;
+        me.w = 0.0;
+        if (t < n) me = S.u.f.mem[t];
+        // the measure of the bin's members before this one
         double bef = 0.0;
-        for (uint32_t j = 0; j < n; ++j)
-          if (t < n && better(S.u.f.mkey[j], S.u.f.mid[j], mk, mi)) bef += S.u.f.mw[j];
-        const uint64_t hm = ballot(t < n && cum + bef < need && cum + bef + mw >= need);
+        for (uint32_t j = 0; j < n; ++j) {
+          const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)j);
+          const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)j);
+          const double wj = rd_lane(me.w, j);
+          if (better(kj, ij, me.key, me.id)) bef += wj;
+        }
+        const uint64_t hm = ballot(t < n && cum + bef < need && cum + bef + me.w >= need);
         if (hm) {
           if (t == (uint32_t)__builtin_ctzll(hm)) {
-            S.bc[2] = mk;
-            S.bc[3] = mi;
+            S.bc[2] = me.key;
+            S.bc[3] = me.id;
             S.bd[1] = cum + bef;
-            S.bd[2] = mw;
+            S.bd[2] = me.w;
             S.bc[4] = 1u;
           }
-        } else if (t == 0u) {
-          double all = cum;
-          for (uint32_t j = 0; j < n; ++j) all += S.u.f.mw[j];
-          S.bc[4] = 0u;
-          S.bd[1] = all;
-          S.bd[2] = 0.0;
+        } else {
+          const double all = cum + wave_sum_f64(t < n ? me.w : 0.0);
+          if (t == 0u) {
+            S.bc[4] = 0u;
+            S.bd[1] = all;
+            S.bd[2] = 0.0;
+          }
         }
       }
       bar();
@@ -454,37 +634,30 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
       *iout = S.bc[3];
       *before = S.bd[1];
       *wself = S.bd[2];
-      bar();
       return;
     }
     if (sh == 0) break;
-    sh = sh > NBB ? sh - NBB : 0;
+    sh = sh > (int)F.nbb ? sh - (int)F.nbb : 0;
   }
   // equal keys (Mkey - lo) in ID order: contiguous ranges and a block scan
   const uint32_t kk = Mkey - lo;
-  const uint32_t R = (W.n + PT - 1u) / PT, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
+  const uint32_t R = (W.n + F.nt - 1u) / F.nt, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
   double mine = 0.0;
-  for (uint32_t i = i0; i < i1; ++i) {
-    float l;
-    uint32_t id;
-    wget(A, S, row, W, i, &l, &id);
-    if (l >= W.thr && member(l, id) && okey(l) == kk) mine += MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
-  }
+  each_range<MASS>(A, S, row, W, i0, i1, Md, invT, [&](uint32_t, float l, uint32_t id, double wv) {
+    if (l >= W.thr && member(l, id) && okey(l) == kk) mine += MASS ? wv : 1.0;
+  });
   double tot;
-  const double incl = bscan_f64(mine, S, &tot);
+  const double incl = scan_f64(mine, S, B, &tot, F.nw);
   double r = cum + incl - mine;
   uint32_t best = NONE;
   double bb = 0.0, bw = 0.0;
-  for (uint32_t i = i0; i < i1 && best == NONE; ++i) {
-    float l;
-    uint32_t id;
-    wget(A, S, row, W, i, &l, &id);
-    if (!(l >= W.thr) || !member(l, id) || okey(l) != kk) continue;
-    const double m = MASS ? exp_neg(((double)l - Md) * invT) : 1.0;
+  each_range<MASS>(A, S, row, W, i0, i1, Md, invT, [&](uint32_t, float l, uint32_t id, double wv) {
+    if (best != NONE || !(l >= W.thr) || !member(l, id) || okey(l) != kk) return;
+    const double m = MASS ? wv : 1.0;
     if (r < need && r + m >= need) { best = id; bb = r; bw = m; }
     r += m;
-  }
-  const uint32_t win = bmin_u32(best, S);
+  });
+  const uint32_t win = red_min_u32(best, S, B, F.nw);
   if (win != NONE && best == win) {
     S.bd[1] = bb;
     S.bd[2] = bw;
@@ -495,7 +668,6 @@ __device__ __forceinline__ void crossing(const Args& A, Lds& S, uint32_t row, co
   *iout = win;
   *before = win != NONE ? S.bd[1] : cum + tot;
   *wself = win != NONE ? S.bd[2] : 0.0;
-  bar();
 }
 
 // Writes one row's outputs.
@@ -507,87 +679,118 @@ __device__ __forceinline__ void put_row(const Args& A, uint32_t row, int32_t sta
   if (A.kept_count) A.kept_count[row] = kept;
 }
 
-// The inverse-CDF draw over the working list's kept entries (kept(l, id)),
+// The inverse-CDF draw over the working list's kept entries (kept(l, id, w)),
 // token-ID order, and the row's outputs.  `unc` carries an earlier
-// uncertain decision (status 1).
-template <typename Kept>
-__device__ __forceinline__ void draw_row(const Args& A, Lds& S, const Cfg& cf, uint32_t row, const Work& W,
-                                         Kept kept, double Md, bool unc) {
-  const uint32_t t = threadIdx.x;
-  const uint32_t R = (W.n + PT - 1u) / PT, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
+// uncertain decision; closep(l, id) marks an entry whose min-p decision could
+// fall either way (status 1 as well).
+template <typename Kept, typename Close>
+__device__ __forceinline__ void draw_row(const Args& A, Lds& S, Blk& B, const Fw& F, const Cfg& cf, uint32_t row,
+                                         const Work& W,
+                                         Kept kept, Close closep, double Md, bool unc) {
+  const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
+  const uint32_t R = (W.n + F.nt - 1u) / F.nt, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
   const uint32_t kwords = (A.V + 31u) / 32u;
-  uint32_t nk = 0u, bad = 0u, n1 = 0u;
+  uint32_t nk = 0u, n1 = 0u, mink = NONE, close = 0u;
   double mass = 0.0;
-  for (uint32_t i = i0; i < i1; ++i) {
-    float l;
-    uint32_t id;
-    wget(A, S, row, W, i, &l, &id);
-    if (!(l >= W.thr) || !kept(l, id)) continue;
+  each_range<true>(A, S, row, W, i0, i1, Md, cf.invT, [&](uint32_t, float l, uint32_t id, double wv) {
+    if (!(l >= W.thr)) return;
+    if (closep(l, id)) close = 1u;
+    if (!kept(l, id, wv)) return;
     ++nk;
     n1 += (double)l == Md ? 1u : 0u;
-    if (!isfinite(((double)l - Md) / cf.T)) bad = 1u;
-    mass += exp_neg(((double)l - Md) * cf.invT);
+    mink = min(mink, okey(l));
+    mass += wv;
     if (A.kept_bits) atomicOr(A.kept_bits + (uint64_t)row * kwords + (id >> 5), 1u << (id & 31u));
-  }
-  const uint32_t nkept = bsum_u32(nk, S);
-  const uint32_t nones = bsum_u32(n1, S);
-  if (bor_u32(bad, S)) {
-    // sample_categorical's shifted_logit check over the kept set
-    if (t == 0) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
-    return;
-  }
-  if (A.nodraw) {
-    if (t == 0) put_row(A, row, unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_OK, -1, 0.0, nkept);
-    return;
-  }
-  double Ssum;
-  const double incl = bscan_f64(mass, S, &Ssum);
-  const double target = cf.u * Ssum;
-  // every kept weight exactly 1 (ties at the maximum): the sums are small
-  // integers on both sides and target is the same product, so the
-  // comparisons are exact
-  const double E = nones == nkept ? 0.0 : 2.0 * sum_err(Ssum, (double)nkept) + U53 * target;
-  double r = incl - mass;
-  uint32_t hit = NONE, last = NONE, hid = NONE, lid = NONE;
-  double hb = 0.0, ha = 0.0;
-  float hl = 0.0f, ll = 0.0f;
-  for (uint32_t i = i0; i < i1; ++i) {
-    float l;
-    uint32_t id;
-    wget(A, S, row, W, i, &l, &id);
-    if (!(l >= W.thr) || !kept(l, id)) continue;
-    const double wv = exp_neg(((double)l - Md) * cf.invT);
-    if (hit == NONE && target < r + wv) { hit = i; hb = r; ha = r + wv; hl = l; hid = id; }
-    if (wv > 0.0) { last = i; ll = l; lid = id; }
-    r += wv;
-  }
-  uint32_t win = bmin_u32(hit, S);
-  const bool fallback = win == NONE;
-  if (fallback) win = ~bmin_u32(~last, S);   // target past every running mass (rounding)
-  if (win != NONE && ((!fallback && hit == win) || (fallback && last == win))) {
-    S.bc[5] = fallback ? lid : hid;
-    S.bd[3] = ((double)(fallback ? ll : hl) - Md) / cf.T - log(Ssum);
-    S.bc[6] = (!fallback && target - hb >= E && ha - target > E) ? 1u : 0u;
-  }
-  bar();
-  if (t == 0) {
-    if (win == NONE) put_row(A, row, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u);
-    else put_row(A, row, (S.bc[6] && !unc) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)S.bc[5], S.bd[3], nkept);
+  });
+  // counts, smallest kept key, the close flag and the mass scan: one barrier
+  const uint32_t P = B.p;
+  {
+    const uint32_t a = wave_sum_u32(nk), b = wave_sum_u32(n1);
+    const uint32_t m = ~wave_max_u32(~mink), o = wave_or_u32(close);
+    const double inc = wave_scan_f64(mass);
+    if (L == 63u) {
+      S.xu[P][w] = a;
+      S.xu[P][PW + w] = b;
+      S.xu[P][2 * PW + w] = m;
+      S.xu[P][3 * PW + w] = o;
+      S.xd[P][w] = inc;
+    }
+    if (t == 0) {
+      S.bc[5] = NONE;
+      S.bc[6] = 0u;
+    }
+    bar();
+    uint32_t nkept = 0u, nones = 0u, mk = NONE, cl = 0u;
+    double before = 0.0, Ssum = 0.0;
+#pragma unroll
+    for (uint32_t i = 0; i < F.nw; ++i) {
+      nkept += S.xu[P][i];
+      nones += S.xu[P][PW + i];
+      mk = min(mk, S.xu[P][2 * PW + i]);
+      cl |= S.xu[P][3 * PW + i];
+      const double r = S.xd[P][i];
+      if (i < w) before += r;
+      Ssum += r;
+    }
+    B.p ^= 1u;
+    if (cl) unc = true;
+    // sample_categorical's shifted_logit check over the kept set: the
+    // smallest kept value has the largest shift
+    if (nkept && !isfinite(((double)okey_value(mk) - Md) / cf.T)) {
+      if (t == 0) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+      return;
+    }
+    if (A.nodraw) {
+      if (t == 0) put_row(A, row, unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_OK, -1, 0.0, nkept);
+      return;
+    }
+    const double target = cf.u * Ssum;
+    // every kept weight exactly 1 (ties at the maximum): the sums are small
+    // integers on both sides and target is the same product, so the
+    // comparisons are exact
+    const double E = nones == nkept ? 0.0 : 2.0 * sum_err(Ssum, (double)nkept) + U53 * target;
+    double r = before + inc - mass;
+    uint32_t hit = NONE, last = NONE, hid = NONE, lid = NONE;
+    double hb = 0.0, ha = 0.0;
+    float hl = 0.0f, ll = 0.0f;
+    each_range<true>(A, S, row, W, i0, i1, Md, cf.invT, [&](uint32_t i, float l, uint32_t id, double wv) {
+      if (!(l >= W.thr) || !kept(l, id, wv)) return;
+      if (hit == NONE && target < r + wv) { hit = i; hb = r; ha = r + wv; hl = l; hid = id; }
+      if (wv > 0.0) { last = i; ll = l; lid = id; }
+      r += wv;
+    });
+    if (hit != NONE) atomicMin(&S.bc[5], hit);
+    if (last != NONE) atomicMax(&S.bc[6], last + 1u);
+    bar();
+    const uint32_t win = S.bc[5], lwin = S.bc[6];
+    // the winning entry's thread writes the row; past every running mass
+    // (rounding) the last positive-weight entry is taken, uncertified
+    if (win != NONE) {
+      if (hit == win) {
+        const bool cert = target - hb >= E && ha - target > E;
+        put_row(A, row, (cert && !unc) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)hid,
+                ((double)hl - Md) / cf.T - log(Ssum), nkept);
+      }
+    } else if (lwin != 0u) {
+      if (last == lwin - 1u) put_row(A, row, MXS_ROW_UNCERTIFIED, (int32_t)lid, ((double)ll - Md) / cf.T - log(Ssum), nkept);
+    } else if (t == 0) {
+      put_row(A, row, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u);
+    }
   }
 }
 
 // Keep-all rows: the draw walks the row's 256-token segment masses, then
 // re-derives the crossing segment's weights exactly.
 template <typename In>
-__device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, const Cfg& cf, uint32_t row, uint32_t Mkey,
-                                                 uint32_t nl) {
+__device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, Blk& B, const Fw& F, const Cfg& cf, uint32_t row,
+                                                 uint32_t Mkey, uint32_t nl) {
   const uint32_t t = threadIdx.x, L = lane_();
   const double Md = (double)okey_value(Mkey);
   const uint32_t nseg = A.C * (uint32_t)NSEG;
   const Seg* sg = A.s.seg + (uint64_t)row * A.s.cm * NSEG;
   // segment s = c NSEG + j PW + w covers chunk c's tokens [4 (j PT + w 64), + 256);
   // thread t sums segments [t R, t R + R)
-  const uint32_t R = (nseg + PT - 1u) / PT, s0 = min(nseg, t * R), s1 = min(nseg, s0 + R);
+  const uint32_t R = (nseg + F.nt - 1u) / F.nt, s0 = min(nseg, t * R), s1 = min(nseg, s0 + R);
   auto segmass = [&](uint32_t s) {
     const uint32_t c = s / NSEG, j = (s - c * NSEG) / PW;
     if (j >= A.per) return 0.0;
@@ -596,8 +799,12 @@ __device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, const Cf
   };
   double mine = 0.0;
   for (uint32_t s = s0; s < s1; ++s) mine += segmass(s);
+  if (t == 0) {
+    S.bc[5] = NONE;
+    S.bc[6] = 0u;
+  }
   double Ssum;
-  const double incl = bscan_f64(mine, S, &Ssum);
+  const double incl = scan_f64(mine, S, B, &Ssum, F.nw);
   const double target = cf.u * Ssum;
   // each weight differs from the reference's by a few ulp (two exp
   // evaluations, two extra roundings); both sides' summation orders
@@ -611,17 +818,19 @@ __device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, const Cf
     if (m > 0.0) { ls = s; lb = r; }
     r += m;
   }
-  uint32_t seg = bmin_u32(hs, S);
-  const bool fallback = seg == NONE;
-  if (fallback) seg = ~bmin_u32(~ls, S);
-  if ((!fallback && hs == seg) || (fallback && ls == seg)) S.bd[0] = fallback ? lb : hb;
+  if (hs != NONE) atomicMin(&S.bc[5], hs);
+  if (ls != NONE) atomicMax(&S.bc[6], ls + 1u);
   if (t < 256u) S.u.f.segtab[t] = 0u;
+  bar();
+  const bool fallback = S.bc[5] == NONE;
+  const uint32_t seg = fallback ? S.bc[6] - 1u : S.bc[5];
+  if ((!fallback && hs == seg) || (fallback && ls == seg)) S.bd[0] = fallback ? lb : hb;
   bar();
   const double sbefore = S.bd[0];
   const uint32_t c = seg / NSEG, rr = seg - c * NSEG, j = rr / PW, wv = rr - j * PW;
   const uint32_t c0 = c * A.CH, cend = min(c0 + A.CH, A.V);
   const uint32_t sbase = c0 + 4u * (j * PT + wv * 64u);
-  for (uint32_t i = t; i < cf.hlen; i += PT) {
+  for (uint32_t i = t; i < cf.hlen; i += F.nt) {
     const uint32_t id = A.hids[cf.h0 + i];
     if (id - sbase < 256u) atomicAdd(&S.u.f.segtab[id - sbase], 1u);
   }
@@ -690,58 +899,494 @@ __device__ __forceinline__ void keepall_segments(const Args& A, Lds& S, const Cf
   if (src == NONE && L == 0u) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, nl);
 }
 
+// Rows with a min-p cut: every kept token is a member at or above the cut
+// (a prefix of the descending order), so past the top-k mass the decision
+// only involves those survivors.  With at most 64 of them, one wave finishes
+// the row: lane j holds survivor j (token order), the running mass before
+// each in descending order comes from the other lanes, the top-p crossing is
+// the lane where it reaches `target` (E = Ea, plus Eb unless the crossing
+// sits on the maximum's plateau), and the draw scans the kept lanes.  A
+// crossing past every survivor keeps them all.  Returns false (nothing
+// written) when there are more than 64 survivors.
+template <typename Memb, typename Ok, typename Near>
+__device__ __forceinline__ bool minp_tail(const Args& A, Lds& S, Blk& B, const Fw& F, const Cfg& cf, uint32_t row,
+                                          const Work& W, Memb member, Ok ok, Near nearp, uint32_t Mkey, double Md,
+                                          double target, double Ea, double Eb) {
+  const uint32_t t = threadIdx.x, L = lane_();
+  const uint32_t R = (W.n + F.nt - 1u) / F.nt, i0 = min(W.n, t * R), i1 = min(W.n, i0 + R);
+  uint32_t mine = 0u, near = 0u;
+  each_range<false>(A, S, row, W, i0, i1, Md, cf.invT, [&](uint32_t, float l, uint32_t id, double) {
+    if (!(l >= W.thr) || !member(l, id)) return;
+    if (nearp(l)) near = 1u;
+    if (ok(l)) ++mine;
+  });
+  // survivors (low 16 bits) and near-cut members (high bits) in one scan
+  uint32_t tot;
+  const uint32_t v = mine | (near << 16);
+  const uint32_t p0 = (scan_u32(v, S, B, &tot, F.nw) - v) & 0xffffu;
+  const uint32_t n = tot & 0xffffu;
+  if (n > 64u) return false;
+  uint32_t p = p0;
+  each_range<true>(A, S, row, W, i0, i1, Md, cf.invT, [&](uint32_t, float l, uint32_t id, double wv) {
+    if (!(l >= W.thr) || !member(l, id) || !ok(l)) return;
+    Mem e;
+    e.key = okey(l);
+    e.id = id;
+    e.w = wv;
+    S.u.f.mem[p++] = e;
+  });
+  bar();
+  if (t >= 64u) return true;
+  Mem me;
+  me.key = 0u;
+  me.id = NONE;
+  me.w = 0.0;
+  if (L < n) me = S.u.f.mem[L];
+  // the survivors' mass before this one in the reference's descending order
+  double bef = 0.0;
+  for (uint32_t j = 0; j < n; ++j) {
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)j);
+    const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)j);
+    const double wj = rd_lane(me.w, j);
+    if (better(kj, ij, me.key, me.id)) bef += wj;
+  }
+  bool unc = (tot >> 16) != 0u;
+  bool kept;
+  const uint64_t hm = ballot(L < n && bef < target && bef + me.w >= target);
+  if (hm) {
+    const uint32_t c = (uint32_t)__builtin_ctzll(hm);
+    const uint32_t ck = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)c);
+    const uint32_t ci = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)c);
+    const double b2 = rd_lane(bef, c), w2 = rd_lane(me.w, c);
+    const double E = Ea + (ck == Mkey ? 0.0 : Eb);
+    if (!(target - b2 > E && b2 + w2 - target >= E)) unc = true;
+    kept = L < n && !better(ck, ci, me.key, me.id);
+  } else {
+    // the crossing lies past every survivor: all of them are kept
+    const double covered = wave_sum_f64(L < n ? me.w : 0.0);
+    if (!(covered < target - (Ea + Eb))) unc = true;
+    kept = L < n;
+  }
+  const float lv = okey_value(me.key);
+  const uint64_t km = ballot(kept);
+  const uint32_t nkept = (uint32_t)__builtin_popcountll(km);
+  const uint32_t nones = (uint32_t)__builtin_popcountll(ballot(kept && (double)lv == Md));
+  // sample_categorical's shifted_logit check: the smallest kept value
+  const uint32_t mk = ~wave_max_u32(kept ? ~me.key : 0u);
+  if (nkept && !isfinite(((double)okey_value(mk) - Md) / cf.T)) {
+    if (L == 0u) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+    return true;
+  }
+  if (kept && A.kept_bits) {
+    const uint32_t kwords = (A.V + 31u) / 32u;
+    atomicOr(A.kept_bits + (uint64_t)row * kwords + (me.id >> 5), 1u << (me.id & 31u));
+  }
+  if (A.nodraw) {
+    if (L == 0u) put_row(A, row, unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_OK, -1, 0.0, nkept);
+    return true;
+  }
+  // the inverse-CDF draw over the kept lanes, token order
+  const double wk = kept ? me.w : 0.0;
+  const double incl = wave_scan_f64(wk);
+  const double Ssum = rd_lane(incl, 63u);
+  const double td = cf.u * Ssum;
+  const double Ed = nones == nkept ? 0.0 : 2.0 * sum_err(Ssum, (double)nkept) + U53 * td;
+  const uint64_t hh = ballot(kept && td < incl);
+  if (hh) {
+    if (L == (uint32_t)__builtin_ctzll(hh)) {
+      const double hb = incl - wk;
+      const bool cert = td - hb >= Ed && incl - td > Ed;
+      put_row(A, row, (cert && !unc) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)me.id,
+              ((double)lv - Md) / cf.T - log(Ssum), nkept);
+    }
+  } else {
+    // past every running mass (rounding): the last positive-weight kept lane
+    const uint64_t pm = ballot(kept && wk > 0.0);
+    if (pm) {
+      if (L == 63u - (uint32_t)__builtin_clzll(pm))
+        put_row(A, row, MXS_ROW_UNCERTIFIED, (int32_t)me.id, ((double)lv - Md) / cf.T - log(Ssum), nkept);
+    } else if (L == 0u) {
+      put_row(A, row, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u);
+    }
+  }
+  return true;
+}
+
+constexpr uint32_t PD = 4;   // candidate entries each finisher thread prefetches
+
+// The register finisher, for a row with a min-p cut whose candidates all sit
+// in the threads' prefetched registers (entry q of thread t: chunk mc, slot
+// mo + q SPC).  Top-k rows first find the k-th candidate in the reference's
+// descending order (histogram rounds over d = Mkey - key on the entries in
+// registers, the final bin of at most 64 ranked on one wave) and the top-k
+// mass; then the survivors of the min-p cut (at most 64) go to one wave,
+// which takes the top-p crossing among them, the kept set and the draw in
+// token order, with the same certification as the general path.  Returns
+// false, having written nothing, when a bin of more than 64 equal keys or
+// more than 64 survivors needs the general path.
+__device__ __forceinline__ bool finish_regs(const Args& A, Lds& S, Blk& B, const Cfg& cf, uint32_t row,
+                                            const uint2 (&pre)[PD], uint32_t ev, uint32_t mc, uint32_t mo,
+                                            uint32_t SPC, uint32_t myoff, bool kact, uint32_t Mkey, double Md,
+                                            float thr, uint32_t N, uint32_t nl, bool complete, double total0,
+                                            double terr0) {
+  const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
+  (void)mc;
+  float el[PD];
+  uint32_t ek[PD], eid[PD];
+  double ew[PD];
+  uint32_t cand = 0u;   // bit q: entry q is a candidate (exists and >= thr)
+#pragma unroll
+  for (uint32_t q = 0; q < PD; ++q) {
+    el[q] = __uint_as_float(pre[q].x);
+    eid[q] = pre[q].y;
+    ek[q] = okey(el[q]);
+    ew[q] = 0.0;
+    if (((ev >> q) & 1u) && el[q] >= thr) cand |= 1u << q;
+  }
+  // min-p, as the general path decides it
+  const double L_mp = cf.L_mp;
+  const double mp_p = L_mp * cf.T;
+  const double mp_m = fabs(mp_p) * 0x1p-49 + 1e-300;
+  const double mp_c = fabs(mp_p) * 0x1p-47 + 1e-300;
+  auto minp_ok = [&](float l) {
+    const double y = (double)l - Md;
+    if (y >= mp_p + mp_m) return true;
+    if (y <= mp_p - mp_m) return false;
+    return y / cf.T >= L_mp;
+  };
+  auto minp_close = [&](float l) {
+    if (cf.min_p >= 1.0) return false;
+    const double y = (double)l - Md;
+    if (fabs(y - mp_p) > mp_c) return false;
+    return fabs(y / cf.T - L_mp) <= 4.0 * U53 * fabs(L_mp);
+  };
+  uint32_t memb = cand;     // the decision's members: the top-k for a top-k row
+  bool weighed = false;     // ew[] holds the members' weights
+  double target = INFINITY, Ea = 0.0, Eb = 0.0;
+  if (kact) {
+    // ---- the k-th candidate: histogram rounds, 12 bits of d at a time
+    uint32_t need = cf.k, lo = 0u;
+    const uint32_t dmax = Mkey - okey(thr);
+    int sh = 32 - __builtin_clz(dmax | 1u) - NBB;
+    if (sh < 0) sh = 0;
+    uint32_t kk = 0u, ki = NONE;
+    for (;;) {
+#pragma unroll
+      for (uint32_t b = 0; b < 4u; ++b) S.u.f.bc[4u * t + b] = 0u;
+      if (t == 0) S.bc[0] = NONE;
+      bar();
+      const uint32_t span = sh >= 32 - NBB ? 0xffffffffu : (((uint32_t)NB << sh) - 1u);
+#pragma unroll
+      for (uint32_t q = 0; q < PD; ++q) {
+        const uint32_t d = Mkey - ek[q];
+        if (((cand >> q) & 1u) && d >= lo && d - lo <= span) atomicAdd(&S.u.f.bc[(d - lo) >> sh], 1u);
+      }
+      bar();
+      uint32_t c4[4], csum = 0u;
+#pragma unroll
+      for (uint32_t b = 0; b < 4u; ++b) {
+        c4[b] = S.u.f.bc[4u * t + b];
+        csum += c4[b];
+      }
+      uint32_t tot;
+      const uint32_t incl = scan_u32(csum, S, B, &tot, PW);
+      if (incl - csum < need && incl >= need) {
+        uint32_t r = incl - csum;
+#pragma unroll
+        for (uint32_t b = 0; b < 4u; ++b) {
+          if (r < need && r + c4[b] >= need) {
+            S.bc[0] = 4u * t + b;
+            S.bc[1] = c4[b];
+            S.bc[2] = r;
+          }
+          r += c4[b];
+        }
+      }
+      bar();
+      const uint32_t bstar = S.bc[0];
+      if (bstar == NONE) {   // fewer candidates than k: the candidate bound failed
+        if (t == 0) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, 0u);
+        return true;
+      }
+      const uint32_t bcnt = S.bc[1];
+      need -= S.bc[2];
+      lo += bstar << sh;
+      if (bcnt <= 64u || sh == 0) {
+        if (bcnt > 64u) return false;   // more than 64 equal keys
+        const uint32_t bspan = sh >= 32 ? 0xffffffffu : ((1u << sh) - 1u);
+        uint32_t inb = 0u, nm = 0u;
+#pragma unroll
+        for (uint32_t q = 0; q < PD; ++q) {
+          const uint32_t d = Mkey - ek[q];
+          if (((cand >> q) & 1u) && d >= lo && d - lo <= bspan) {
+            inb |= 1u << q;
+            ++nm;
+          }
+        }
+        uint32_t tot2;
+        uint32_t p = scan_u32(nm, S, B, &tot2, PW) - nm;
+#pragma unroll
+        for (uint32_t q = 0; q < PD; ++q) {
+          if ((inb >> q) & 1u) {
+            Mem e;
+            e.key = ek[q];
+            e.id = eid[q];
+            e.w = 0.0;
+            S.u.f.mem[p++] = e;
+          }
+        }
+        bar();
+        if (w == 0u) {
+          Mem me;
+          me.key = 0u;
+          me.id = NONE;
+          me.w = 0.0;
+          if (L < tot2) me = S.u.f.mem[L];
+          uint32_t rank = 0u;
+          for (uint32_t j = 0; j < tot2; ++j) {
+            const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)j);
+            const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)j);
+            rank += better(kj, ij, me.key, me.id) ? 1u : 0u;
+          }
+          if (L < tot2 && rank == need - 1u) {
+            S.bc[3] = me.key;
+            S.bc[4] = me.id;
+          }
+        }
+        bar();
+        kk = S.bc[3];
+        ki = S.bc[4];
+        break;
+      }
+      sh = sh > NBB ? sh - NBB : 0;
+    }
+    // ---- the top-k members and their mass
+    memb = 0u;
+    double km = 0.0, wmin = 1.0;
+#pragma unroll
+    for (uint32_t q = 0; q < PD; ++q) {
+      if (((cand >> q) & 1u) && (ek[q] > kk || (ek[q] == kk && eid[q] <= ki))) {
+        memb |= 1u << q;
+        ew[q] = exp_neg(((double)el[q] - Md) * cf.invT);
+        km += ew[q];
+        wmin = fmin(wmin, ew[q]);
+      }
+    }
+    weighed = true;
+    double kept;
+    red_sum_minpos_f64(km, wmin, S, B, &kept, &wmin, PW);
+    // every top-k token tied at the maximum: kept is exactly k on both sides
+    const bool kones = kk == Mkey;
+    const double Ekept = kones ? 0.0 : sum_err(kept, (double)cf.k);
+    target = cf.top_p * kept;
+    Ea = cf.top_p * Ekept + (kones ? 0.0 : U53 * target);
+    Eb = Ekept;
+  } else if (cf.top_p < 1.0) {
+    double total = total0, terr = terr0;
+    bool tones = false;
+    if (complete) {
+      // every legal token is a candidate: the total from the candidates
+      double tm = 0.0;
+      uint32_t n1 = 0u;
+#pragma unroll
+      for (uint32_t q = 0; q < PD; ++q) {
+        if ((cand >> q) & 1u) {
+          ew[q] = exp_neg(((double)el[q] - Md) * cf.invT);
+          tm += ew[q];
+          n1 += (double)el[q] == Md ? 1u : 0u;
+        }
+      }
+      weighed = true;
+      total = red_sum_f64(tm, S, B, PW);
+      terr = sum_err(total, (double)nl);
+      tones = red_sum_u32(n1, S, B, PW) == nl;   // every weight 1: the total is exactly nl
+    }
+    target = cf.top_p * total;
+    Ea = tones ? 0.0 : cf.top_p * terr + U53 * target;
+    Eb = sum_err(total, (double)N);
+  }
+  // ---- the survivors of the min-p cut, and members within its rounding band
+  uint32_t surv = 0u, ns = 0u, near = 0u;
+#pragma unroll
+  for (uint32_t q = 0; q < PD; ++q) {
+    if ((memb >> q) & 1u) {
+      if (minp_close(el[q])) near = 1u;
+      if (minp_ok(el[q])) {
+        surv |= 1u << q;
+        ++ns;
+        if (!weighed) ew[q] = exp_neg(((double)el[q] - Md) * cf.invT);
+      }
+    }
+  }
+  uint32_t tot;
+  const uint32_t v = ns | (near << 16);
+  uint32_t p = (scan_u32(v, S, B, &tot, PW) - v) & 0xffffu;
+  const uint32_t n = tot & 0xffffu;
+  if (n > 64u) return false;
+#pragma unroll
+  for (uint32_t q = 0; q < PD; ++q) {
+    if ((surv >> q) & 1u) {
+      Mem e;
+      e.key = ek[q];
+      e.id = eid[q];
+      e.w = ew[q];
+      S.u.f.mem[p] = e;
+      S.u.f.mix[p] = myoff + mo + q * SPC;
+      ++p;
+    }
+  }
+  bar();
+  if (w != 0u) return true;
+  // ---- one wave: lane j holds survivor j
+  Mem me;
+  me.key = 0u;
+  me.id = NONE;
+  me.w = 0.0;
+  uint32_t mix = NONE;
+  if (L < n) {
+    me = S.u.f.mem[L];
+    mix = S.u.f.mix[L];
+  }
+  // the mass before each survivor in the descending order, and its place in
+  // token order
+  double bef = 0.0;
+  uint32_t trank = 0u;
+  for (uint32_t j = 0; j < n; ++j) {
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)j);
+    const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)j);
+    const uint32_t xj = (uint32_t)__builtin_amdgcn_readlane((int)mix, (int)j);
+    const double wj = rd_lane(me.w, j);
+    if (better(kj, ij, me.key, me.id)) bef += wj;
+    trank += xj < mix ? 1u : 0u;
+  }
+  bool unc = (tot >> 16) != 0u;
+  bool kept;
+  const uint64_t hm = ballot(L < n && bef < target && bef + me.w >= target);
+  if (hm) {
+    const uint32_t c = (uint32_t)__builtin_ctzll(hm);
+    const uint32_t ck = (uint32_t)__builtin_amdgcn_readlane((int)me.key, (int)c);
+    const uint32_t ci = (uint32_t)__builtin_amdgcn_readlane((int)me.id, (int)c);
+    const double b2 = rd_lane(bef, c), w2 = rd_lane(me.w, c);
+    const double E = Ea + (ck == Mkey ? 0.0 : Eb);
+    if (!(target - b2 > E && b2 + w2 - target >= E)) unc = true;
+    kept = L < n && !better(ck, ci, me.key, me.id);
+  } else {
+    // the crossing lies past every survivor (or there is no top-p): all kept
+    const double covered = wave_sum_f64(L < n ? me.w : 0.0);
+    if (!(covered < target - (Ea + Eb))) unc = true;
+    kept = L < n;
+  }
+  // to token order
+  if (L < n) {
+    S.u.f.dmem[trank] = me;
+    S.u.f.dkf[trank] = kept ? 1u : 0u;
+  }
+  bar();   // (this wave alone is left)
+  Mem d;
+  d.key = 0u;
+  d.id = NONE;
+  d.w = 0.0;
+  bool dk = false;
+  if (L < n) {
+    d = S.u.f.dmem[L];
+    dk = S.u.f.dkf[L] != 0u;
+  }
+  const float lv = okey_value(d.key);
+  const uint32_t nkept = (uint32_t)__builtin_popcountll(ballot(dk));
+  const uint32_t nones = (uint32_t)__builtin_popcountll(ballot(dk && (double)lv == Md));
+  // sample_categorical's shifted_logit check: the smallest kept value
+  const uint32_t mk = ~wave_max_u32(dk ? ~d.key : 0u);
+  if (nkept && !isfinite(((double)okey_value(mk) - Md) / cf.T)) {
+    if (L == 0u) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
+    return true;
+  }
+  if (dk && A.kept_bits) {
+    const uint32_t kwords = (A.V + 31u) / 32u;
+    atomicOr(A.kept_bits + (uint64_t)row * kwords + (d.id >> 5), 1u << (d.id & 31u));
+  }
+  if (A.nodraw) {
+    if (L == 0u) put_row(A, row, unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_OK, -1, 0.0, nkept);
+    return true;
+  }
+  // the inverse-CDF draw over the kept lanes, token order
+  const double wk = dk ? d.w : 0.0;
+  const double incl = wave_scan_f64(wk);
+  const double Ssum = rd_lane(incl, 63u);
+  const double td = cf.u * Ssum;
+  const double Ed = nones == nkept ? 0.0 : 2.0 * sum_err(Ssum, (double)nkept) + U53 * td;
+  const uint64_t hh = ballot(dk && td < incl);
+  if (hh) {
+    if (L == (uint32_t)__builtin_ctzll(hh)) {
+      const double hb = incl - wk;
+      const bool cert = td - hb >= Ed && incl - td > Ed;
+      put_row(A, row, (cert && !unc) ? MXS_ROW_OK : MXS_ROW_UNCERTIFIED, (int32_t)d.id,
+              ((double)lv - Md) / cf.T - log(Ssum), nkept);
+    }
+  } else {
+    // past every running mass (rounding): the last positive-weight kept lane
+    const uint64_t pm = ballot(dk && wk > 0.0);
+    if (pm) {
+      if (L == 63u - (uint32_t)__builtin_clzll(pm))
+        put_row(A, row, MXS_ROW_UNCERTIFIED, (int32_t)d.id, ((double)lv - Md) / cf.T - log(Ssum), nkept);
+    } else if (L == 0u) {
+      put_row(A, row, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u);
+    }
+  }
+  return true;
+}
+
 template <typename In>
 __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf, uint32_t row) {
   const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
   const uint32_t C = A.C;
+  Blk B;
   stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 0u);
-  // ---- header: wave 0 merges the chunk statistics, lane q <-> chunk q
-  if (w == 0u) {
-    Stat s{};
-    s.thr = -INFINITY;
-    s.minkey = NONE;
-    if (L < C) s = A.s.stat[(uint64_t)row * A.s.cm + L];
-    const uint32_t Mkey = wave_max_u32(s.maxkey);
-    const uint32_t mink = ~wave_max_u32(~s.minkey);
-    const uint32_t fl = wave_or_u32(s.flags);
-    const uint32_t nl = wave_sum_u32(s.nlegal);
-    const unsigned long long g =
-        wave_max_u64(s.gkey ? (((unsigned long long)s.gkey << 32) | (unsigned long long)(~s.gid)) : 0ull);
-    const uint32_t nc = s.ncand;
-    const uint32_t inc = wave_scan_u32(nc);
-    if (L < C) S.coff[L] = inc - nc;
-    const uint32_t N = bcast63(inc);
-    if (L == 0u) S.coff[C] = N;
-    const uint32_t tk = wave_max_u32(L < C ? okey(s.thr) : 0u);
-    const uint32_t notall = wave_or_u32(L < C && s.ncand != s.nlegal ? 1u : 0u);
-    // chunk masses rescaled to the row maximum
-    const double Md = (double)okey_value(Mkey);
-    double rm = 0.0, re = 0.0;
-    if (L < C && s.maxkey && s.mass > 0.0) {
-      const double f = exp_neg(((double)okey_value(s.maxkey) - Md) * cf.invT);
-      rm = s.mass * f;
-      re = s.mass_err * f + rm * 8.0 * U53;
-    }
-    const double tot = wave_sum_f64(rm);
-    const double terr = wave_sum_f64(re) + tot * 80.0 * U53;
-    if (L == 0u) {
-      S.h.Mkey = Mkey;
-      S.h.flags = fl;
-      S.h.nl = nl;
-      S.h.N = N;
-      S.h.thrkey = tk;
-      S.h.complete = notall ? 0u : 1u;
-      S.h.gid = g ? ~(uint32_t)g : NONE;
-      S.h.mink = mink;
-      S.h.total = tot;
-      S.h.terr = terr;
-    }
+  // ---- one round trip: each wave's lane c reads chunk c's statistics, and
+  // each thread the first entry of its share of a chunk's candidate list
+  // (SPC threads per chunk; entries past the chunk's count are ignored)
+  Stat s{};
+  s.thr = -INFINITY;
+  s.minkey = NONE;
+  if (L < C) s = A.s.stat[(uint64_t)row * A.s.cm + L];
+  // thread t reads chunk mc's entries mo, mo + SPC, ... (PD of them; never
+  // past the chunk's CH slots)
+  const uint32_t SPC = PT / C;
+  const uint32_t mc = t / SPC, mo = t - mc * SPC;
+  uint2 pre[PD];
+#pragma unroll
+  for (uint32_t q = 0; q < PD; ++q) {
+    const uint32_t o = mo + q * SPC;
+    pre[q] = make_uint2(0u, 0u);
+    if (mc < C && o < A.CH) pre[q] = A.s.cand[(uint64_t)row * A.s.cand_stride + (uint64_t)mc * A.CH + o];
   }
-  bar();
-  stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 2u);
-  const uint32_t Mkey = S.h.Mkey, fl = S.h.flags, nl = S.h.nl, N = S.h.N;
-  const float thr = okey_value(S.h.thrkey);
-  const bool complete = S.h.complete != 0u;
+  // ---- the header, on every wave
+  const uint32_t Mkey = wave_max_u32(s.maxkey);
+  const uint32_t mink = ~wave_max_u32(~s.minkey);
+  const uint32_t fl = wave_or_u32(s.flags);
+  const uint32_t nl = wave_sum_u32(s.nlegal);
+  const unsigned long long gk =
+      wave_max_u64(s.gkey ? (((unsigned long long)s.gkey << 32) | (unsigned long long)(~s.gid)) : 0ull);
+  const uint32_t nc = s.ncand;
+  const uint32_t inc = wave_scan_u32(nc);
+  const uint32_t coffL = inc - nc;
+  const uint32_t N = bcast63(inc);
+  const uint32_t thrkey = wave_max_u32(L < C ? okey(s.thr) : 0u);
+  const bool complete = wave_or_u32(L < C && s.ncand != s.nlegal ? 1u : 0u) == 0u;
+  const double Md = (double)okey_value(Mkey);
+  double rm = 0.0, re = 0.0;
+  if (L < C && s.maxkey && s.mass > 0.0) {
+    // chunk masses rescaled to the row maximum
+    const double f = exp_neg(((double)okey_value(s.maxkey) - Md) * cf.invT);
+    rm = s.mass * f;
+    re = s.mass_err * f + rm * 8.0 * U53;
+  }
+  const double total0 = wave_sum_f64(rm);
+  const double terr0 = wave_sum_f64(re) + total0 * 80.0 * U53;
+  const float thr = okey_value(thrkey);
+  if (w == 0u) {
+    if (L < C) S.coff[L] = coffL;
+    if (L == 0u) S.coff[C] = N;
+  }
   if (t == 0) {
     A.s.sync[(uint64_t)row * SYNC] = 0u;
     A.s.sync[(uint64_t)row * SYNC + 1u] = 0u;
@@ -759,14 +1404,16 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
   const uint32_t kwords = (A.V + 31u) / 32u;
   if (cf.greedy) {
     if (t == 0) {
-      const uint32_t id = S.h.gid;
+      const uint32_t id = gk ? ~(uint32_t)gk : NONE;
       put_row(A, row, MXS_ROW_OK, (int32_t)id, 0.0, 1u);
       if (A.kept_bits) atomicOr(A.kept_bits + (uint64_t)row * kwords + (id >> 5), 1u << (id & 31u));
     }
     return;
   }
   const bool kact = cf.k > 0u && cf.k < nl;
-  const double Md = (double)okey_value(Mkey);
+  // the finisher's width: one wave for a short candidate list
+  const Fw Ffull{(uint32_t)PT, (uint32_t)PW, (uint32_t)NB, (uint32_t)NBB, 4u};
+  const Fw F = N <= SHORT_LIST ? Fw{64u, 1u, 512u, 9u, 8u} : Ffull;
   if (!kact && cf.top_p >= 1.0 && cf.min_p == 0.0 && !complete) {
     // keep-all without a complete candidate list
     if (A.nodraw) {
@@ -775,77 +1422,140 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     }
     // the reference's legal_shifted_sum checks every legal token's shifted
     // logit; the smallest overflows first
-    if (S.h.mink != NONE && !isfinite(((double)okey_value(S.h.mink) - Md) / cf.T)) {
+    if (mink != NONE && !isfinite(((double)okey_value(mink) - Md) / cf.T)) {
       if (t == 0) put_row(A, row, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u);
       return;
     }
-    keepall_segments<In>(A, S, cf, row, Mkey, nl);
+    bar();   // S.coff is written
+    keepall_segments<In>(A, S, B, Ffull, cf, row, Mkey, nl);
     return;
   }
-  // ---- the working candidate list
+  // ---- this thread's prefetched entries: value, id, index in token order
+  const uint32_t myn = (uint32_t)__shfl((int)nc, (int)(mc < C ? mc : 0u), 64);
+  const uint32_t myoff = (uint32_t)__shfl((int)coffL, (int)(mc < C ? mc : 0u), 64);
+  uint32_t ev = 0u;   // bit q: prefetched entry q exists
+#pragma unroll
+  for (uint32_t q = 0; q < PD; ++q)
+    if (mc < C && mo + q * SPC < myn) ev |= 1u << q;
+  // every entry of every chunk is in some thread's registers
+  const bool all_pre = wave_or_u32(L < C && nc > PD * SPC ? 1u : 0u) == 0u;
+  if (all_pre && cf.min_p > 0.0 && (cf.top_p < 1.0 || !kact) &&
+      finish_regs(A, S, B, cf, row, pre, ev, mc, mo, SPC, myoff, kact, Mkey, Md, thr, N, nl, complete, total0, terr0))
+    return;
+  // ---- the working candidate list: in LDS with its weights when it fits
   Work W{N, false, thr};
   uint32_t dmax = Mkey - okey(thr);
-  if (kact && N > NCL) {
-    // stream the global lists once: the bin holding the k-th member bounds it
-    int sh = 32 - __builtin_clz(dmax | 1u) - NBB;
-    if (sh < 0) sh = 0;
-    for (uint32_t b = t; b < (uint32_t)NB; b += PT) S.u.f.bc[b] = 0u;
-    bar();
-    for (uint32_t i = t; i < N; i += PT) {
-      float l;
-      uint32_t id;
-      wget(A, S, row, W, i, &l, &id);
-      if (l >= thr) atomicAdd(&S.u.f.bc[(Mkey - okey(l)) >> sh], 1u);
+  if (N <= NCL) {
+    // this thread's chunk offset (lane mc of the wave's scan)
+    const uint32_t off = (uint32_t)__shfl((int)coffL, (int)(mc < C ? mc : 0u), 64);
+    const uint32_t cnt = (uint32_t)__shfl((int)nc, (int)(mc < C ? mc : 0u), 64);
+    // weights now for rows without a top-k; top-k rows weigh their members later
+    auto place = [&](uint32_t p, uint2 e) {
+      const float l = __uint_as_float(e.x);
+      S.u.f.cl[p] = l;
+      S.u.f.cid[p] = e.y;
+      if (!kact) S.u.f.cw[p] = l >= thr ? exp_neg(((double)l - Md) * cf.invT) : 0.0;
+    };
+#pragma unroll
+    for (uint32_t q = 0; q < PD; ++q)
+      if ((ev >> q) & 1u) place(off + mo + q * SPC, pre[q]);
+    // entries past each chunk's first PD SPC: every load in flight, then placed
+    if (!all_pre) {
+      bar();   // S.coff is written
+      constexpr uint32_t RMAX = (NCL + PT - 1u) / PT;
+      uint2 e[RMAX];
+      uint32_t at[RMAX];
+#pragma unroll
+      for (uint32_t r = 0; r < RMAX; ++r) {
+        const uint32_t i = t + r * PT;
+        at[r] = NONE;
+        e[r] = make_uint2(0u, 0u);
+        if (i < N) {
+          uint32_t lo = 0, hi = C;   // the last chunk c with coff[c] <= i
+          while (hi - lo > 1u) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (S.coff[mid] <= i) lo = mid; else hi = mid;
+          }
+          const uint32_t o = i - S.coff[lo];
+          if (o >= PD * SPC) {
+            at[r] = i;
+            e[r] = A.s.cand[(uint64_t)row * A.s.cand_stride + (uint64_t)lo * A.CH + o];
+          }
+        }
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < RMAX; ++r)
+        if (at[r] != NONE) place(at[r], e[r]);
     }
     bar();
-    uint32_t c4[4], cs = 0u;
+    W = Work{N, true, thr};
+    if (w >= F.nw) return;   // the finisher's waves go on alone
+  } else {
+    bar();   // S.coff is written
+    if (w >= F.nw) return;
+    if (kact) {
+      // stream the global lists once: the bin holding the k-th member bounds it
+      int sh = 32 - __builtin_clz(dmax | 1u) - (int)F.nbb;
+      if (sh < 0) sh = 0;
+      for (uint32_t b = t; b < F.nb; b += F.nt) S.u.f.bc[b] = 0u;
+      if (t == 0) S.bc[0] = NONE;
+      bar();
+      for (uint32_t i = t; i < N; i += F.nt) {
+        float l;
+        uint32_t id;
+        wget(A, S, row, W, i, &l, &id);
+        if (l >= thr) atomicAdd(&S.u.f.bc[(Mkey - okey(l)) >> sh], 1u);
+      }
+      bar();
+      uint32_t c4[BPT_MAX], cs = 0u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      c4[q] = S.u.f.bc[4u * t + (uint32_t)q];
-      cs += c4[q];
-    }
-    uint32_t tot;
-    const uint32_t inc = bscan_u32(cs, S, &tot);
-    if (t == 0) S.bc[0] = NONE;
-    bar();
-    if (inc - cs < cf.k && inc >= cf.k) {
-      uint32_t r = inc - cs;
+      for (int q = 0; q < (int)F.bpt; ++q) {
+        c4[q] = S.u.f.bc[F.bpt * t + (uint32_t)q];
+        cs += c4[q];
+      }
+      uint32_t tot;
+      const uint32_t incs = scan_u32(cs, S, B, &tot, F.nw);
+      if (incs - cs < cf.k && incs >= cf.k) {
+        uint32_t r = incs - cs;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (r < cf.k && r + c4[q] >= cf.k) { S.bc[0] = 4u * t + (uint32_t)q; S.bc[1] = r + c4[q]; }
-        r += c4[q];
+        for (int q = 0; q < (int)F.bpt; ++q) {
+          if (r < cf.k && r + c4[q] >= cf.k) { S.bc[0] = F.bpt * t + (uint32_t)q; S.bc[1] = r + c4[q]; }
+          r += c4[q];
+        }
+      }
+      bar();
+      if (S.bc[0] != NONE && S.bc[1] <= NCL) {
+        const uint32_t dlim = ((S.bc[0] + 1u) << sh) - 1u;
+        const uint32_t n = compact(A, S, B, F, row, N, [&](float l, uint32_t) { return l >= thr && Mkey - okey(l) <= dlim; },
+                                   Md, cf.invT);
+        W = Work{n, true, thr};
+        dmax = dlim;
       }
     }
-    bar();
-    if (S.bc[0] != NONE && S.bc[1] <= NCL) {
-      const uint32_t dlim = ((S.bc[0] + 1u) << sh) - 1u;
-      const uint32_t n = compact(A, S, row, N, [&](float l, uint32_t) { return l >= thr && Mkey - okey(l) <= dlim; });
-      W = Work{n, true, thr};
-      dmax = dlim;
-    }
-  } else if (N <= NCL) {
-    const uint32_t n = compact(A, S, row, N, [&](float l, uint32_t) { return l >= thr; });
-    W = Work{n, true, thr};
   }
   stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 3u);
   bool unc = false;
   const double L_mp = cf.L_mp;
-  auto minp_ok = [&](float l) { return cf.min_p <= 0.0 || ((double)l - Md) / cf.T >= L_mp; };
+  // min-p: the reference keeps l when (l - M) / T >= ln(min_p) (f64).  The
+  // division is taken only within a relative 2^-49 of the boundary
+  // y = ln(min_p) T: further out the rounded quotient cannot reach across.
+  const double mp_p = L_mp * cf.T;
+  const double mp_m = fabs(mp_p) * 0x1p-49 + 1e-300;
+  auto minp_ok = [&](float l) {
+    if (cf.min_p <= 0.0) return true;
+    const double y = (double)l - Md;
+    if (y >= mp_p + mp_m) return true;
+    if (y <= mp_p - mp_m) return false;
+    return y / cf.T >= L_mp;
+  };
   // a shifted logit within an ulp of ln(min_p) could fall on either side of
-  // the reference's logarithm
+  // the reference's logarithm (only possible within 2^-47 of the boundary)
+  const double mp_c = fabs(mp_p) * 0x1p-47 + 1e-300;
   auto minp_close = [&](float l) {
     if (cf.min_p <= 0.0 || cf.min_p >= 1.0) return false;
-    return fabs(((double)l - Md) / cf.T - L_mp) <= 4.0 * U53 * fabs(L_mp);
-  };
-  auto any_close = [&](auto member) {
-    uint32_t close = 0u;
-    for (uint32_t i = t; i < W.n; i += PT) {
-      float l;
-      uint32_t id;
-      wget(A, S, row, W, i, &l, &id);
-      if (l >= W.thr && member(l, id) && minp_close(l)) close = 1u;
-    }
-    return bor_u32(close, S) != 0u;
+    const double y = (double)l - Md;
+    if (fabs(y - mp_p) > mp_c) return false;
+    return fabs(y / cf.T - L_mp) <= 4.0 * U53 * fabs(L_mp);
   };
   if (kact) {
     // ---- top-k: the k-th member, the kept mass, the nucleus cut
@@ -853,7 +1563,7 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
     uint32_t kk, ki;
     double bef, wsf;
     auto all = [&](float, uint32_t) { return true; };
-    crossing<false>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, (double)cf.k, &f1, &kk, &ki, &bef, &wsf);
+    crossing<false>(A, S, B, F, row, W, all, Mkey, Md, cf.invT, dmax, (double)cf.k, &f1, &kk, &ki, &bef, &wsf);
     stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 4u);
     if (!f1) {   // fewer candidates than k: the candidate bound failed
       if (t == 0) put_row(A, row, MXS_ROW_UNCERTIFIED, -1, 0.0, 0u);
@@ -863,30 +1573,40 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
       const uint32_t key = okey(l);
       return key > kk || (key == kk && id <= ki);
     };
+    // a long list shrinks to the top-k members before the passes below
+    if (W.lds && F.nt == (uint32_t)PT && W.n > 2u * cf.k && W.n > SHORT_LIST) {
+      W.n = compact_lds(S, B, F, W, inK);
+      dmax = Mkey - kk;
+    }
+    // the top-k members' weights (an LDS list caches them for the passes below)
     double km = 0.0, wmin = 1.0;
-    for (uint32_t i = t; i < W.n; i += PT) {
-      float l;
-      uint32_t id;
-      wget(A, S, row, W, i, &l, &id);
+    each<false>(A, S, row, W, F, Md, cf.invT, [&](uint32_t i, float l, uint32_t id, double) {
       if (l >= W.thr && inK(l, id)) {
         const double wv = exp_neg(((double)l - Md) * cf.invT);
+        if (W.lds) S.u.f.cw[i] = wv;
         km += wv;
         wmin = fmin(wmin, wv);
       }
-    }
-    const double kept = bsum_f64(km, S);
-    wmin = bmin_pos_f64(wmin, S);
+    });
+    double kept;
+    red_sum_minpos_f64(km, wmin, S, B, &kept, &wmin, F.nw);
     stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 5u);
     // every top-k token tied at the maximum: kept is exactly k on both sides
     const bool kones = kk == Mkey;
     const double Ekept = kones ? 0.0 : sum_err(kept, (double)cf.k);
+    if (cf.min_p > 0.0 && cf.top_p < 1.0 && W.lds) {
+      const double target = cf.top_p * kept;
+      if (minp_tail(A, S, B, F, cf, row, W, inK, minp_ok, minp_close, Mkey, Md, target,
+                    cf.top_p * Ekept + (kones ? 0.0 : U53 * target), Ekept))
+        return;
+    }
     uint32_t ck = kk, ci = ki;
     double habs = -1.0, hlo = 0.0, hhi = 0.0;   // top_p = 1: weights at or below habs are absorbed
     if (cf.top_p < 1.0) {
       const double target = cf.top_p * kept;
       bool f2;
       double b2, w2;
-      crossing<true>(A, S, row, W, inK, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+      crossing<true>(A, S, B, F, row, W, inK, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
       stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 6u);
       // running masses inside the maximum's plateau are exact integers
       const double Ec = ck == Mkey ? 0.0 : Ekept;
@@ -912,29 +1632,22 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
       hhi = ldexp(1.0, e2) - kept <= Ekept ? 2.0 * h : h;
       if (!(wmin > hhi * (1.0 + 4.0 * U53))) habs = h;
     }
-    auto keptf = [&](float l, uint32_t id) {
+    auto keptf = [&](float l, uint32_t id, double wv) {
       const uint32_t key = okey(l);
       if (!(key > ck || (key == ck && id <= ci))) return false;
-      if (habs >= 0.0 && !(exp_neg(((double)l - Md) * cf.invT) > habs)) return false;
+      if (habs >= 0.0 && !(wv > habs)) return false;
       return minp_ok(l);
     };
     if (habs >= 0.0) {
       // a weight within its rounding of habs could fall on either side
       uint32_t close = 0u;
-      for (uint32_t i = t; i < W.n; i += PT) {
-        float l;
-        uint32_t id;
-        wget(A, S, row, W, i, &l, &id);
-        if (l >= W.thr && inK(l, id)) {
-          const double wv = exp_neg(((double)l - Md) * cf.invT);
-          if (wv >= hlo * (1.0 - 4.0 * U53) && wv <= hhi * (1.0 + 4.0 * U53)) close = 1u;
-        }
-      }
-      if (bor_u32(close, S)) unc = true;
+      each<true>(A, S, row, W, F, Md, cf.invT, [&](uint32_t, float l, uint32_t id, double wv) {
+        if (l >= W.thr && inK(l, id) && wv >= hlo * (1.0 - 4.0 * U53) && wv <= hhi * (1.0 + 4.0 * U53)) close = 1u;
+      });
+      if (red_or_u32(close, S, B, F.nw)) unc = true;
     }
-    if (any_close(inK)) unc = true;
     stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 7u);
-    draw_row(A, S, cf, row, W, keptf, Md, unc);
+    draw_row(A, S, B, F, cf, row, W, keptf, [&](float l, uint32_t id) { return inK(l, id) && minp_close(l); }, Md, unc);
     return;
   }
   // ---- no top-k: nucleus (top_p < 1), min-p only, or keep-all (complete list)
@@ -942,30 +1655,31 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
   bool reached = true;
   uint32_t ck = 0u, ci = NONE;
   if (cf.top_p < 1.0) {
-    double total = S.h.total, terr = S.h.terr;
+    double total = total0, terr = terr0;
     bool tones = false;
     if (complete) {
       // every legal token is a candidate: the total from the candidates
       double tm = 0.0;
       uint32_t n1 = 0u;
-      for (uint32_t i = t; i < W.n; i += PT) {
-        float l;
-        uint32_t id;
-        wget(A, S, row, W, i, &l, &id);
+      each<true>(A, S, row, W, F, Md, cf.invT, [&](uint32_t, float l, uint32_t, double wv) {
         if (l >= W.thr) {
-          tm += exp_neg(((double)l - Md) * cf.invT);
+          tm += wv;
           n1 += (double)l == Md ? 1u : 0u;
         }
-      }
-      total = bsum_f64(tm, S);
+      });
+      total = red_sum_f64(tm, S, B, F.nw);
       terr = sum_err(total, (double)nl);
-      tones = bsum_u32(n1, S) == nl;   // every weight 1: the total is exactly nl
+      tones = red_sum_u32(n1, S, B, F.nw) == nl;   // every weight 1: the total is exactly nl
     }
     const double target = cf.top_p * total;
+    if (cf.min_p > 0.0 && W.lds &&
+        minp_tail(A, S, B, F, cf, row, W, all, minp_ok, minp_close, Mkey, Md, target,
+                  tones ? 0.0 : cf.top_p * terr + U53 * target, sum_err(total, (double)N)))
+      return;
     bool f2;
     double b2, w2;
     stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 5u);
-    crossing<true>(A, S, row, W, all, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
+    crossing<true>(A, S, B, F, row, W, all, Mkey, Md, cf.invT, dmax, target, &f2, &ck, &ci, &b2, &w2);
     stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 6u);
     // running masses inside the maximum's plateau are exact integers; a
     // complete list tied at the maximum has an exact total
@@ -980,17 +1694,19 @@ __device__ __forceinline__ void finish_row(const Args& A, Lds& S, const Cfg& cf,
       unc = true;
     }
   }
+  if (cf.top_p >= 1.0 && cf.min_p > 0.0 && W.lds &&
+      minp_tail(A, S, B, F, cf, row, W, all, minp_ok, minp_close, Mkey, Md, INFINITY, 0.0, 0.0))
+    return;
   const bool cut = cf.top_p < 1.0 && reached;
-  auto keptf = [&](float l, uint32_t id) {
+  auto keptf = [&](float l, uint32_t id, double) {
     if (cut) {
       const uint32_t key = okey(l);
       if (!(key > ck || (key == ck && id <= ci))) return false;
     }
     return minp_ok(l);
   };
-  if (any_close(all)) unc = true;
   stamp(A, row, MXS_DEBUG_TIMING_SLOTS - 1u, 7u);
-  draw_row(A, S, cf, row, W, keptf, Md, unc);
+  draw_row(A, S, B, F, cf, row, W, keptf, [&](float l, uint32_t) { return minp_close(l); }, Md, unc);
 }
 
 // ===========================================================================
@@ -1011,6 +1727,7 @@ template <typename In>
 __global__ __launch_bounds__(PT) void pick_kernel(Args A) {
   __shared__ Lds S;
   using Q = Quad<In>;
+  Blk Bc;
   const uint32_t t = threadIdx.x, w = wave_(), L = lane_();
   // XCD-aware mapping: workgroup g runs on XCD g mod 8; a row's chunks share
   // one XCD (and its L2), rows r = 8 ri + ((x - ri) mod 8)
@@ -1469,7 +2186,7 @@ __global__ __launch_bounds__(PT) void pick_kernel(Args A) {
       hs += h4[q];
     }
     uint32_t tot;
-    const uint32_t inc = bscan_u32(hs, S, &tot);
+    const uint32_t inc = scan_u32(hs, S, Bc, &tot, PW);
     if (inc - hs < k && inc >= k) {
       uint32_t r = inc - hs;
 #pragma unroll
@@ -1592,8 +2309,8 @@ __global__ __launch_bounds__(PT) void pick_kernel(Args A) {
       b = ((double)meb * 2.1 * (double)U24 + (double)ms * (4.0 + (double)mn) * 1.01 * (double)U24 + (double)mex +
            (double)mn * 1.1754943508222875e-38) * gsc * 1.001 + sm * 4.0 * U53;
     }
-    cmass = bsum_f64(sm, S);
-    cerr = bsum_f64(b, S) + cmass * 16.0 * U53;
+    cmass = red_sum_f64(sm, S, Bc, PW);
+    cerr = red_sum_f64(b, S, Bc, PW) + cmass * 16.0 * U53;
   }
 
   // ---- statistics, then arrive

@@ -348,6 +348,16 @@ __device__ __forceinline__ double sum_bound(double s, uint32_t n, double term_ul
   return (2.0 * (double)n + term_ulps + 4.0) * U * s * 1.0001 + 1e-300;
 }
 
+// top_p = 1 under a top-k: the reference's running f64 sum over the top-k
+// weights (descending) stops at its first value equal to the kept mass, so
+// weights too small to move the sum (at or below 2.3e-16 of it) may be cut.
+// Only members at or above the min-p cut are kept, and each such member's
+// weight is at least min_p (to within rounding): when min_p clears that
+// stall level, the cut cannot reach a kept member.
+__device__ __forceinline__ bool minp_above_stall(const RowCfg& c, double esum) {
+  return c.min_p > 0.0 && c.min_p * (1.0 - 1e-12) > 2.3e-16 * esum;
+}
+
 // ---------------------------------------------------------------------------
 // Finisher state shared by its phases.
 struct FinCtx {
@@ -444,7 +454,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
   double theta = 0.0, theta_err = 0.0;
   if (X.k_path) {
     if (c.top_p >= 1.0) {
-      if (!(wmin > 2.3e-16 * esum)) uncert = true;
+      if (!minp_above_stall(c, esum) && !(wmin > 2.3e-16 * esum)) uncert = true;
     } else {
       cut = true;
       theta = c.top_p * esum;
@@ -684,7 +694,7 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
     if (c.top_p >= 1.0) {
       // covered reaches kept only at E's last token when every weight is
       // large enough to change the running f64 sum; otherwise replay.
-      replay = !(wmin > 2.3e-16 * esum);
+      replay = !minp_above_stall(c, esum) && !(wmin > 2.3e-16 * esum);
     } else {
       theta_set = true;
       theta = c.top_p * esum;
@@ -1058,7 +1068,7 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
           wk = b < wk ? b : wk;
         }
       const double wmin = __builtin_bit_cast(double, Gr::min_u64(wk, F));
-      if (!(wmin > 2.3e-16 * esum)) return false;   // the running sum may stall: replay
+      if (!minp_above_stall(c, esum) && !(wmin > 2.3e-16 * esum)) return false;   // the running sum may stall: replay
     } else {
       theta_set = true;
       theta = c.top_p * esum;
@@ -1430,7 +1440,7 @@ __device__ __forceinline__ bool wave_finish(const FinCtx& X, FinSmem& F) {
     if (c.top_p >= 1.0) {
       // the running sum may stall before reaching the total: the general path replays it
       const double wm = __builtin_bit_cast(double, ~wave_max_u64(~wmin));
-      if (!(wm > 2.3e-16 * esum)) return false;
+      if (!minp_above_stall(c, esum) && !(wm > 2.3e-16 * esum)) return false;
     } else {
       theta_set = true;
       theta = c.top_p * esum;
@@ -1757,7 +1767,7 @@ __device__ __forceinline__ bool sel_theta(const FinCtx& X, const SelSums& Q, boo
   if (X.k_path) {
     if (c.top_p >= 1.0) {
       // the running sum may stall before reaching the total
-      if (!(Q.wlo > 2.3e-16 * (Q.esum + Q.esum_err))) return false;
+      if (!minp_above_stall(c, Q.esum + Q.esum_err) && !(Q.wlo > 2.3e-16 * (Q.esum + Q.esum_err))) return false;
     } else {
       *set = true;
       *theta = c.top_p * Q.esum;
@@ -2978,7 +2988,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     if constexpr (MODE == M_MINP) {
       // this wave's maximum goes to the row's exchange word right away
       if (lane() == 0)
-        __hip_atomic_fetch_max(A.w.rowx + row, ((unsigned long long)A.epoch << 32) | kmax, __ATOMIC_RELAXED,
+        __hip_atomic_fetch_max(A.w.rowx + (uint64_t)row * ROWX_STRIDE, ((unsigned long long)A.epoch << 32) | kmax, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint32_t wf = wave_or_u32(my_flags) | (nf ? (uint32_t)F_NONFINITE : 0u);
@@ -3066,7 +3076,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     // logarithm's error, T * 2^-24 absolute, is not covered by a margin
     // relative to the logits when they and T ln(min_p) are near 0).
     emit = true;
-    const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long cur = __hip_atomic_load(A.w.rowx + (uint64_t)row * ROWX_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t xkey = maxkey;
     if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
     xkey = (uint32_t)__builtin_amdgcn_readfirstlane((int)xkey);
@@ -3249,18 +3259,24 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
   }
   stamp(A, row, chunk, 2);
   if constexpr (XD) {
-    // The row's last chunk to finish becomes its finisher: the barrier waits
-    // for every wave's device-scope stores, then one relaxed device-scope
-    // count per chunk.
+    // The row's last chunk to finish becomes its finisher.  Every thread's
+    // device-scope stores happen before the workgroup barrier, which happens
+    // before thread 0's release on the row counter; the last arriver's
+    // acquire fence, then the barrier, order its workgroup's loads after all
+    // of the row's stores.
     __syncthreads();
     uint32_t last = 0;
     if (tid == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
+      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
-      if (last) st_dev(&A.w.ctr[row], 0u);
+      if (last) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        st_dev(ctr, 0u);
+      }
       S.xkey = last;
     }
-    lds_barrier();
+    __syncthreads();
     last = S.xkey;
     lds_barrier();   // the finisher's LDS overlays the chunk's
     if (!last) return;
@@ -3661,7 +3677,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
       minp_x = true;
       if (tid == 0) {
         const unsigned long long old = __hip_atomic_fetch_max(
-            A.w.rowx + row, ((unsigned long long)A.epoch << 32) | maxkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            A.w.rowx + (uint64_t)row * ROWX_STRIDE, ((unsigned long long)A.epoch << 32) | maxkey, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if ((uint32_t)(old >> 32) == A.epoch) xkey = max(xkey, (uint32_t)old);
       }
     } else if (mode == M_ALL) {
@@ -3747,7 +3763,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
   if (minp_x) {
     // the largest chunk maximum of the row published by now
     if (tid == 0) {
-      const unsigned long long cur = __hip_atomic_load(A.w.rowx + row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long cur = __hip_atomic_load(A.w.rowx + (uint64_t)row * ROWX_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
       S.xkey = xkey;
     }
@@ -3860,18 +3876,21 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
   }
   stamp(A, row, chunk, 2);
   if constexpr (XD) {
-    // The row's last chunk to finish becomes its finisher.  The barrier
-    // waits for every wave's device-scope stores; then one relaxed
-    // device-scope count per chunk.
+    // The row's last chunk to finish becomes its finisher (release on the
+    // row counter after the barrier, acquire by the last arriver, as above).
     __syncthreads();
     uint32_t last = 0;
     if (tid == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&A.w.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
+      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
-      if (last) st_dev(&A.w.ctr[row], 0u);
+      if (last) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        st_dev(ctr, 0u);
+      }
       S.xkey = last;
     }
-    lds_barrier();
+    __syncthreads();
     last = S.xkey;
     lds_barrier();   // the finisher's LDS overlays the chunk's
     if (!last) return;
@@ -4081,14 +4100,14 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   hipSetDevice(device);
   const size_t rv = (size_t)max_rows * max_vocab;
   hipError_t e = hipSuccess;
-  e = e ? e : hipMalloc(&ctx->work.ctr, (size_t)max_rows * sizeof(uint32_t));
-  e = e ? e : hipMalloc(&ctx->work.rowx, (size_t)max_rows * sizeof(unsigned long long));
+  e = e ? e : hipMalloc(&ctx->work.ctr, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->work.rowx, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
   e = e ? e : hipMalloc(&ctx->work.stat, (size_t)max_rows * mxs::MAXC * sizeof(mxs::ChunkStat));
   e = e ? e : hipMalloc(&ctx->work.cand_l, rv * sizeof(float));
   e = e ? e : hipMalloc(&ctx->work.cand_id, rv * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
-  e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * sizeof(unsigned long long));
-  e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
+  e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   {
     // Two kernels unless MXS_SAMPLER_FUSED=1 (one kernel whose last chunk
     // per row finishes the row; it measured no faster on config 2).
