@@ -1,15 +1,15 @@
 // mx_sampler.hip -- MI355X (gfx950) token sampler: kernels and the C ABI of
 // include/mx_sampler.h.
 //
-// One mxs_sample call is two kernels on one stream.  sample_kernel splits
-// each logit row into C chunks of at most CHUNK_MAX tokens; one 1024-thread
-// workgroup streams a chunk from HBM once into registers (16-byte loads,
-// coalesced), applies logit bias and penalties from an LDS count table, the
-// grammar mask and the finite check, reduces the chunk's statistics and
-// writes a compact, token-ID-ordered candidate list.  finish_kernel runs one
-// workgroup per row after it (the kernel boundary orders the two): it merges
-// the chunk statistics and candidates and decides top-k, top-p, min-p and
-// the inverse-CDF draw in f64.  Decisions the reference makes with
+// One mxs_sample call is one kernel.  sample_kernel splits each logit row
+// into C chunks of at most CHUNK_MAX tokens; one 1024-thread workgroup
+// streams a chunk from HBM once into registers (16-byte loads, coalesced),
+// applies logit bias and penalties from an LDS count table, the grammar mask
+// and the finite check, reduces the chunk's statistics and writes a compact,
+// token-ID-ordered candidate list with device-scope stores.  The row's last
+// chunk to arrive on the row counter (release by every chunk, acquire by the
+// last) becomes the row finisher: it merges the chunk statistics and
+// candidates and decides top-k, top-p, min-p and the inverse-CDF draw in f64.  Decisions the reference makes with
 // sequential f64 sums are taken from parallel sums only when a rigorous
 // error bound certifies them; otherwise the finisher replays the
 // reference's sequential order, or reports the row uncertified.
@@ -379,7 +379,6 @@ struct FinCtx {
   uint32_t nwords;
   uint64_t* timing;    // phase timestamps (diagnostics), null when off
   const double* etab;  // exp_neg's tables in LDS
-  bool xdev;           // candidates were written by workgroups of this launch: device-scope reads
 };
 
 // Finisher phase timestamp k (slot MAXC of the row's timing record).
@@ -398,12 +397,12 @@ __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, ui
 __device__ __forceinline__ float cand_l(const FinCtx& X, const FinSmem& F, uint32_t j) {
   if (X.lds_c) return F.cl[j];
   const float* p = &X.cand_l[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
-  return X.xdev ? ld_dev(p) : *p;
+  return ld_dev(p);
 }
 __device__ __forceinline__ uint32_t cand_id(const FinCtx& X, const FinSmem& F, uint32_t j) {
   if (X.lds_c) return F.cid[j];
   const uint32_t* p = &X.cand_id[cand_pos_of(F, X.C, X.rbase, X.CH, j)];
-  return X.xdev ? ld_dev(p) : *p;
+  return ld_dev(p);
 }
 __device__ __forceinline__ bool member(const FinCtx& X, float l, uint32_t id) {
   if (X.k_path) {
@@ -1672,7 +1671,6 @@ struct FinLoads {
   ChunkStat v;
 };
 static_assert(SR % 2 == 0, "slot pairs");
-template <bool XD>
 __device__ __forceinline__ void fin_issue(const SampleArgs& A, uint32_t row, FinLoads& P) {
   const uint32_t C = A.C, V = A.b.vocab, CH = A.CH;
   uint32_t sq, sj;
@@ -1688,16 +1686,16 @@ __device__ __forceinline__ void fin_issue(const SampleArgs& A, uint32_t row, Fin
     float2 lv = make_float2(0.0f, 0.0f);
     uint2 iv = make_uint2(0u, 0u);
     if (pairs && slot + 1u < lim) {
-      lv = xget<XD>(reinterpret_cast<const float2*>(&A.w.cand_l[base + u]));
-      iv = xget<XD>(reinterpret_cast<const uint2*>(&A.w.cand_id[base + u]));
+      lv = ld_dev(reinterpret_cast<const float2*>(&A.w.cand_l[base + u]));
+      iv = ld_dev(reinterpret_cast<const uint2*>(&A.w.cand_id[base + u]));
     } else {
       if (slot < lim) {
-        lv.x = xget<XD>(&A.w.cand_l[base + u]);
-        iv.x = xget<XD>(&A.w.cand_id[base + u]);
+        lv.x = ld_dev(&A.w.cand_l[base + u]);
+        iv.x = ld_dev(&A.w.cand_id[base + u]);
       }
       if (slot + 1u < lim) {
-        lv.y = xget<XD>(&A.w.cand_l[base + u + 1]);
-        iv.y = xget<XD>(&A.w.cand_id[base + u + 1]);
+        lv.y = ld_dev(&A.w.cand_l[base + u + 1]);
+        iv.y = ld_dev(&A.w.cand_id[base + u + 1]);
       }
     }
     P.l[u] = lv.x; P.l[u + 1] = lv.y;
@@ -1708,16 +1706,16 @@ __device__ __forceinline__ void fin_issue(const SampleArgs& A, uint32_t row, Fin
   v.minkey = NONE; v.thr = 0.0f; v.mass = 0.0; v.mass_err = 0.0;
   if (wave() < 2u && lane() < C) {   // wave 0: the header; wave 1: the chunk masses
     const ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC + lane()];
-    v.maxkey = xget<XD>(&st->maxkey);
-    v.gbest_id = xget<XD>(&st->gbest_id);
-    v.gbest_val = xget<XD>(&st->gbest_val);
-    v.nlegal = xget<XD>(&st->nlegal);
-    v.ncand = xget<XD>(&st->ncand);
-    v.flags = xget<XD>(&st->flags);
-    v.mass = xget<XD>(&st->mass);
-    v.mass_err = xget<XD>(&st->mass_err);
-    v.minkey = xget<XD>(&st->minkey);
-    v.thr = xget<XD>(&st->thr);
+    v.maxkey = ld_dev(&st->maxkey);
+    v.gbest_id = ld_dev(&st->gbest_id);
+    v.gbest_val = ld_dev(&st->gbest_val);
+    v.nlegal = ld_dev(&st->nlegal);
+    v.ncand = ld_dev(&st->ncand);
+    v.flags = ld_dev(&st->flags);
+    v.mass = ld_dev(&st->mass);
+    v.mass_err = ld_dev(&st->mass_err);
+    v.minkey = ld_dev(&st->minkey);
+    v.thr = ld_dev(&st->thr);
   }
 }
 
@@ -2363,7 +2361,7 @@ __device__ __forceinline__ void keepall_bits(const SampleArgs& A, uint32_t row, 
   }
 }
 
-template <typename In, bool XD>
+template <typename In>
 __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
                            uint64_t rbase, double invT, const FinLoads& P) {
   const mxs_batch& b = A.b;
@@ -2441,7 +2439,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
   X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
-  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab; X.xdev = XD;
+  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab;
   if (err) {
     write_result(X, err, -1, 0.0, 0u);
     if (kbits)
@@ -2472,7 +2470,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     double part = 0.0;
     for (uint32_t s = tid; s < nseg; s += FT) {
       const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-      if (F.st[q].nlegal) part += xget<XD>(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
+      if (F.st[q].nlegal) part += ld_dev(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
     }
     const double total = block_sum<double>(part, F.red_d);
     const double target = c.u * total;
@@ -2487,7 +2485,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       double w = 0.0;
       if (s < nseg) {
         const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-        if (F.st[q].nlegal) w = xget<XD>(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
+        if (F.st[q].nlegal) w = ld_dev(&A.w.seg[((uint64_t)row * MAXC + q) * PER_MAX * NW + r]) * F.cscale[q];
       }
       double tot;
       const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
@@ -2650,8 +2648,8 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
         const uint32_t local = j - F.coff[qj];
         if (local >= cov) {
           const uint64_t pos = rbase + (uint64_t)qj * A.CH + local;
-          lv[u] = xget<XD>(&A.w.cand_l[pos]);
-          iv[u] = xget<XD>(&A.w.cand_id[pos]);
+          lv[u] = ld_dev(&A.w.cand_l[pos]);
+          iv[u] = ld_dev(&A.w.cand_id[pos]);
           need |= 1u << u;
         }
       }
@@ -2782,17 +2780,12 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
 
 // ---------------------------------------------------------------------------
 // The sampling kernel.
-// Fused mode: the chunk pass and the row finisher share the workgroup's
-// LDS (the finisher starts after the chunk is published).
+// The chunk pass and the row finisher share the workgroup's LDS (the
+// finisher starts after the chunk is published).
 union alignas(16) FusedSmem {
   ChunkSmem s;
   FinSmem f;
 };
-template <bool XD>
-struct KernelSmem { using T = ChunkSmem; };
-template <>
-struct KernelSmem<true> { using T = FusedSmem; };
-__device__ __forceinline__ ChunkSmem& chunk_smem(ChunkSmem& s) { return s; }
 __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 
 // ---------------------------------------------------------------------------
@@ -2814,8 +2807,8 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 //   - each wave publishes its maximum to the row's exchange word as soon as
 //     its pass 1 ends, so the min-p threshold sees the other chunks' maxima
 //     as early as possible.
-template <typename In, uint32_t MODE, bool HIST, bool XD>
-__device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelSmem<XD>::T& U, const RowCfg& c,
+template <typename In, uint32_t MODE, bool HIST>
+__device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                            const uint32_t row, const uint32_t chunk, const uint32_t c0,
                                            const uint32_t c1, const uint32_t hn) {
   ChunkSmem& S = chunk_smem(U);
@@ -3221,8 +3214,8 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
                 sti[off] = e0 + (uint32_t)e;
               } else {
                 const uint64_t pos = cbase + off;
-                xput<XD>(&A.w.cand_l[pos], lv[i][e]);
-                xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+                st_dev(&A.w.cand_l[pos], lv[i][e]);
+                st_dev(&A.w.cand_id[pos], e0 + (uint32_t)e);
               }
               ++off;
             }
@@ -3233,8 +3226,8 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     if (staged) {
       lds_barrier();
       for (uint32_t j = tid; j < ncand; j += NT) {
-        xput<XD>(&A.w.cand_l[cbase + j], stl[j]);
-        xput<XD>(&A.w.cand_id[cbase + j], sti[j]);
+        st_dev(&A.w.cand_l[cbase + j], stl[j]);
+        st_dev(&A.w.cand_id[cbase + j], sti[j]);
       }
     }
   }
@@ -3246,19 +3239,19 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     if constexpr (MODE == M_GREEDY)
       for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
     ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
-    xput<XD>(&st.maxkey, nleg ? maxkey : 0u);
-    xput<XD>(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
-    xput<XD>(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
-    xput<XD>(&st.nlegal, nleg);
-    xput<XD>(&st.ncand, ncand);
-    xput<XD>(&st.flags, cflags);
-    xput<XD>(&st.mass, mass);
-    xput<XD>(&st.mass_err, mass_err);
-    xput<XD>(&st.minkey, 0u);
-    xput<XD>(&st.thr, thr);
+    st_dev(&st.maxkey, nleg ? maxkey : 0u);
+    st_dev(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
+    st_dev(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
+    st_dev(&st.nlegal, nleg);
+    st_dev(&st.ncand, ncand);
+    st_dev(&st.flags, cflags);
+    st_dev(&st.mass, mass);
+    st_dev(&st.mass_err, mass_err);
+    st_dev(&st.minkey, 0u);
+    st_dev(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
-  if constexpr (XD) {
+  {
     // The row's last chunk to finish becomes its finisher.  Every thread's
     // device-scope stores happen before the workgroup barrier, which happens
     // before thread 0's release on the row counter; the last arriver's
@@ -3282,20 +3275,20 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, typename KernelS
     if (!last) return;
     stamp(A, row, MAXC, 0);
     FinLoads P;
-    fin_issue<true>(A, row, P);
-    finish_row<In, true>(A, U.f, c, row, MODE, (uint64_t)row * V, invT, P);
+    fin_issue(A, row, P);
+    finish_row<In>(A, U.f, c, row, MODE, (uint64_t)row * V, invT, P);
     stamp(A, row, MAXC, 7);
   }
 }
 
 // The general chunk body: every row the lean body does not cover (grammar
 // masks, logit bias, long histories, parameter errors, the all-candidates
-// and keep-all modes) and every row of the fused mode.  The kernel has
+// and keep-all modes).  The kernel has
 // already read the row's parameters (c).  The kernel's own load of the
 // first slice is not passed in (it would stay live across both bodies): the
 // general body issues its slices itself.
-template <typename In, bool XD>
-__device__ __forceinline__ void chunk_general(const SampleArgs& A, typename KernelSmem<XD>::T& U, const RowCfg& c,
+template <typename In>
+__device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                               const uint32_t row, const uint32_t chunk) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
@@ -3748,7 +3741,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
           m0 += sw;
           if (mode == M_KEEPALL) {
             const double ws = wave_sum_f64(sw);
-            if (lane() == 0) xput<XD>(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
+            if (lane() == 0) st_dev(&A.w.seg[(((uint64_t)row * MAXC + chunk) * PER_MAX + i) * NW + wave()], ws);
           }
         }
       } else if (lane() == 0 && emit) {
@@ -3846,8 +3839,8 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
         for (int e = 0; e < 4; ++e) {
           if (em[e]) {
             const uint64_t pos = cbase + off;
-            xput<XD>(&A.w.cand_l[pos], lv[i][e]);
-            xput<XD>(&A.w.cand_id[pos], e0 + (uint32_t)e);
+            st_dev(&A.w.cand_l[pos], lv[i][e]);
+            st_dev(&A.w.cand_id[pos], e0 + (uint32_t)e);
             ++off;
           }
         }
@@ -3863,19 +3856,19 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
     if (want_arg)
       for (int w = 0; w < NW; ++w) garg = garg > S.wp[w].arg ? garg : S.wp[w].arg;
     ChunkStat& st = A.w.stat[(uint64_t)row * MAXC + chunk];
-    xput<XD>(&st.maxkey, nleg ? maxkey : 0u);
-    xput<XD>(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
-    xput<XD>(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
-    xput<XD>(&st.nlegal, nleg);
-    xput<XD>(&st.ncand, ncand);
-    xput<XD>(&st.flags, cflags);
-    xput<XD>(&st.mass, mass);
-    xput<XD>(&st.mass_err, mass_err);
-    xput<XD>(&st.minkey, minkey);
-    xput<XD>(&st.thr, thr);
+    st_dev(&st.maxkey, nleg ? maxkey : 0u);
+    st_dev(&st.gbest_id, garg ? ~(uint32_t)garg : NONE);
+    st_dev(&st.gbest_val, garg ? okey_value((uint32_t)(garg >> 32)) : 0.0f);
+    st_dev(&st.nlegal, nleg);
+    st_dev(&st.ncand, ncand);
+    st_dev(&st.flags, cflags);
+    st_dev(&st.mass, mass);
+    st_dev(&st.mass_err, mass_err);
+    st_dev(&st.minkey, minkey);
+    st_dev(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
-  if constexpr (XD) {
+  {
     // The row's last chunk to finish becomes its finisher (release on the
     // row counter after the barrier, acquire by the last arriver, as above).
     __syncthreads();
@@ -3896,8 +3889,8 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
     if (!last) return;
     stamp(A, row, MAXC, 0);
     FinLoads P;
-    fin_issue<true>(A, row, P);
-    finish_row<In, true>(A, U.f, c, row, mode, rbase, invT, P);
+    fin_issue(A, row, P);
+    finish_row<In>(A, U.f, c, row, mode, rbase, invT, P);
     stamp(A, row, MAXC, 7);
   }
 }
@@ -3907,13 +3900,13 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, typename Kern
 // first slice goes out before the row's parameters arrive; rows the lean
 // body covers then issue the history ids and the rest of the stream and run
 // it, the others run the general body (which issues its own loads).
-template <typename In, bool XD>
+template <typename In>
 __global__ __launch_bounds__(NT) void sample_kernel(
     SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
     const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
     const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
     const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
-  __shared__ __align__(16) typename KernelSmem<XD>::T U;
+  __shared__ __align__(16) FusedSmem U;
   const mxs_batch& b = A.b;
   const uint32_t xcd = blockIdx.x & 7u;
   const uint32_t chunk = blockIdx.x >> 3;
@@ -3931,44 +3924,18 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
       if (hn) {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true, XD>(A, U, c, row, chunk, c0, c1, hn);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true, XD>(A, U, c, row, chunk, c0, c1, hn);
-        else chunk_fast<In, M_MINP, true, XD>(A, U, c, row, chunk, c0, c1, hn);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn);
+        else chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn);
       } else {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
-        else chunk_fast<In, M_MINP, false, XD>(A, U, c, row, chunk, c0, c1, 0u);
+        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u);
+        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u);
+        else chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u);
       }
       return;
     }
   }
-  chunk_general<In, XD>(A, U, c, row, chunk);
-}
-
-// ---------------------------------------------------------------------------
-// The row finisher: one workgroup per row, launched after the chunk kernel
-// on the same stream (the kernel boundary makes every chunk's statistics and
-// candidates visible).  Row r runs as workgroup r, on XCD r mod 8, the XCD
-// that ran the row's chunks.
-template <typename In>
-__global__ __launch_bounds__(FT) void finish_kernel(
-    SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
-    const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
-    const float* __restrict__ p_pres, const float* __restrict__ p_freq, const double* __restrict__ p_uniform,
-    const uint32_t* __restrict__ p_hoff, const uint32_t* __restrict__ p_boff) {
-  __shared__ __align__(16) FinSmem F;
-  const uint32_t row = blockIdx.x;   // the grid holds exactly one workgroup per row
-  // the statistics and candidate loads go out before the parameter loads
-  // are waited for
-  FinLoads P;
-  fin_issue<false>(A, row, P);
-  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
-                            p_boff, row);
-  const uint32_t mode = chunk_mode(c, A.b.vocab);
-  const double invT = c.greedy ? 0.0 : 1.0 / c.T;
-  stamp(A, row, MAXC, 0);
-  finish_row<In, false>(A, F, c, row, mode, (uint64_t)row * A.b.vocab, invT, P);
-  stamp(A, row, MAXC, 7);
+  chunk_general<In>(A, U, c, row, chunk);
 }
 
 }  // namespace mxs
@@ -3980,7 +3947,6 @@ __global__ __launch_bounds__(FT) void finish_kernel(
 namespace mxs {
 
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw) {
-  if (ctx && ctx->use_pick) return pick_launch(ctx, b, o, nodraw);
   if (!ctx || !b || !o) return MXS_EINVAL;
   if (b->rows == 0) return MXS_OK;
   if (!b->logits || !b->temperature || !o->token || !o->status) return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
@@ -4026,26 +3992,13 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
-  // Split (default): the chunk pass, then the row finisher as a second
-  // kernel (stream order makes the chunk results visible).  Fused: one
-  // kernel; each row's last chunk finishes the row, the chunks' results
-  // handed over through device-scope stores and a per-row counter.
+  // One kernel: each row's last chunk to finish decides the row.
 #define MXS_ARGS A, b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets
-  if (!ctx->split) {
-    if (b->dtype == MXS_F32)
-      hipLaunchKernelGGL((mxs::sample_kernel<float, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    else
-      hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-  } else if (b->dtype == MXS_F32) {
-    hipLaunchKernelGGL((mxs::sample_kernel<float, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<float>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
-  } else {
-    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-    if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
-    hipLaunchKernelGGL(mxs::finish_kernel<uint16_t>, dim3(b->rows), dim3(mxs::FT), 0, ctx->stream, MXS_ARGS);
-  }
+  if (b->dtype == MXS_F32)
+    hipLaunchKernelGGL((mxs::sample_kernel<float>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+  else
+    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+  if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
 #undef MXS_ARGS
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
@@ -4108,29 +4061,6 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
-  {
-    // Two kernels unless MXS_SAMPLER_FUSED=1 (one kernel whose last chunk
-    // per row finishes the row; it measured no faster on config 2).
-    const char* fz = getenv("MXS_SAMPLER_FUSED");
-    ctx->split = !(fz && fz[0] == '1');
-  }
-  {
-    const char* pz = getenv("MXS_SAMPLER_PICK");
-    ctx->use_pick = pz && pz[0] == '1';
-  }
-  {
-    const mxs::pk::Layout ly = mxs::pk::layout(max_vocab);
-    mxs::pk::Scratch& P = ctx->pick;
-    P.cm = ly.C;
-    P.cand_stride = (uint64_t)max_vocab + 32u * ly.C + 32u;
-    P.gtab_stride = ((uint64_t)max_vocab + 8u) & ~(uint64_t)3u;
-    e = e ? e : hipMalloc(&P.sync, (size_t)max_rows * mxs::pk::SYNC * sizeof(uint32_t));
-    e = e ? e : hipMemset(P.sync, 0, (size_t)max_rows * mxs::pk::SYNC * sizeof(uint32_t));
-    e = e ? e : hipMalloc(&P.stat, (size_t)max_rows * P.cm * sizeof(mxs::pk::Stat));
-    e = e ? e : hipMalloc(&P.cand, (size_t)max_rows * P.cand_stride * sizeof(uint2));
-    e = e ? e : hipMalloc(&P.seg, (size_t)max_rows * P.cm * mxs::pk::NSEG * sizeof(mxs::pk::Seg));
-    e = e ? e : hipMalloc(&P.gtab, (size_t)max_rows * P.gtab_stride * sizeof(uint32_t));
-  }
   e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
@@ -4197,11 +4127,6 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->race_ctr);
   hipFree(ctx->race_scratch);
   hipFree(ctx->race_kept);
-  hipFree(ctx->pick.sync);
-  hipFree(ctx->pick.stat);
-  hipFree(ctx->pick.cand);
-  hipFree(ctx->pick.seg);
-  hipFree(ctx->pick.gtab);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;

@@ -8,7 +8,6 @@
 #include <string>
 
 #include "../../include/mx_sampler.h"
-#include "mxs_pick.h"
 
 namespace mxs {
 
@@ -25,9 +24,6 @@ constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 // mxs_sample's launch; `nodraw` makes keep-all rows skip the inverse-CDF
 // draw (token -1, status 0, the kept set still written).
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
-// The single-kernel pick (mx_sample.hip); `nodraw` skips the inverse-CDF
-// draw on every row (token -1, status certifies the kept set).
-int pick_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
 
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
@@ -68,11 +64,8 @@ struct mxs_ctx {
   float* d_zero_f32 = nullptr;
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
-  hipEvent_t split_event = nullptr;   // recorded between the chunk kernel and the finisher (diagnostics)
+  hipEvent_t split_event = nullptr;   // recorded after mxs_sample's kernel (diagnostics)
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
-  bool split = true;                  // the row finisher as a second kernel (else fused: MXS_SAMPLER_FUSED=1)
-  bool use_pick = false;              // mxs_sample runs the single-kernel pick (MXS_SAMPLER_PICK=1)
-  mxs::pk::Scratch pick{};            // the single-kernel pick's scratch
   // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
   uint32_t* topn_ctr = nullptr;
   void* topn_scratch = nullptr;

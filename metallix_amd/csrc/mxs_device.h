@@ -66,16 +66,6 @@ __device__ __forceinline__ uint2 ld_dev(const uint2* p) {
 __device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Stores and loads of data one workgroup hands to another within a launch
-// (X = true: device-scope, as above) or to a later launch (X = false: plain).
-template <bool X, typename T>
-__device__ __forceinline__ void xput(T* p, T v) {
-  if constexpr (X) st_dev(p, v); else *p = v;
-}
-template <bool X, typename T>
-__device__ __forceinline__ T xget(const T* p) {
-  if constexpr (X) return ld_dev(p); else return *p;
-}
 // Waits until this lane's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
