@@ -1,22 +1,27 @@
 """Benchmark: sampled rows/s of the HIP token sampler on one MI355X.
 
-Workload (the metric's configuration): B=64 rows x
-V=151936 f32 logits drawn N(0, 2^2) with 1-50 peaks per row, per-row
-temperature U[0.3, 1.5], top_k in {0, 20, 50, 1000}, top_p U[0.5, 1),
+Default workload (the metric's configuration):
+B=64 rows x V=151936 f32 logits drawn N(0, 2^2) with 1-50 peaks per row,
+per-row temperature U[0.3, 1.5], top_k in {0, 20, 50, 1000}, top_p U[0.5, 1),
 min_p 0.05, presence 0.5 / frequency 0.3 / repetition 1.1 over 2048-token
 Zipf(1.1) histories, one seeded uniform per row.  One step = one full
-pipeline pass (penalties + top-k + top-p + min-p + draw) over the batch.
+pipeline pass (penalties + top-k + top-p + min-p + draw) over the batch: one
+mxs_sample call, which is one kernel launch (sample_kernel).
 
-Inputs are resident in HBM before timing starts.  The logits rotate over 8
-copies (311 MB, more than the 256 MB Infinity Cache) so every step streams
-its logits from HBM rather than from the cache.  The CPU baseline is the C
-restatement of the reference sampler (oracle/) timed on this host on a
-bounded sample of the same rows.
+`--config N` times the other configurations of BASELINE.json instead
+(1: one Qwen3 row, stochastic; 3: 32 bf16 rows under grammar masks; 4:
+256 x 262144 f32 rows, a pick plus the top-20 log-softmax per row; 5:
+speculative verification of 16 rows with 4 drafted tokens each).
+
+Inputs are resident in HBM before timing starts.  The logits rotate over
+enough copies (at least 300 MB, more than the 256 MB Infinity Cache) that
+every step streams its logits from HBM rather than from the cache.  The CPU
+baseline is the C restatement of the reference sampler (oracle/) timed on
+this host on a bounded sample of the same rows.
 """
 from __future__ import annotations
 
 import argparse
-import ctypes
 import json
 import os
 import sys
@@ -28,59 +33,226 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "sampled rows/s at B=64,V=151936 fp32; achieved HBM GB/s vs MI355X peak"
 HBM_PEAK_GBS = 8000.0
-NBUF = 8
+ROTATE_BYTES = 300 << 20
+OUT_BYTES_PER_ROW = 4 + 8 + 4 + 4       # token, sampling_logprob, status, kept_count
+TOPN = 20
 
 
-def algorithmic_bytes(b) -> int:
-    """Compulsory bytes of one pass: inputs read once, required outputs written once."""
-    n = b.logits.nbytes                                  # 38,895,616
-    n += b.history_ids.nbytes + b.history_offsets.nbytes  # 524,288 + 260
-    n += b.rows * (8 + 4 + 8 + 8 + 4 + 4 + 4 + 8)        # T, top_k, top_p, min_p, rep, pres, freq, u
-    n += b.rows * (4 + 8 + 4)                            # token, sampling_logprob, status
-    return n
+def nbytes(t) -> int:
+    return 0 if t is None else t.numel() * t.element_size()
 
 
-def cpu_baseline(b, seconds: float):
+def sample_bytes(logits, kw) -> int:
+    """Compulsory bytes of one mxs_sample call: the V logits of every row
+    and every per-row input read once, the outputs written once."""
+    rows, V = logits.shape[0], kw["vocab"]
+    n = rows * V * logits.element_size()
+    for k, v in kw.items():
+        if isinstance(v, tuple):
+            n += sum(nbytes(t) for t in v)
+        elif hasattr(v, "element_size"):
+            n += nbytes(v)
+    return n + rows * OUT_BYTES_PER_ROW
+
+
+def topn_bytes(logits, V, n) -> int:
+    """mxs_logsoftmax_topn: the logits once; ids i32 + logprobs f64 for n
+    per row, maximum and log-normaliser f64, status i32."""
+    rows = logits.shape[0]
+    return rows * V * logits.element_size() + rows * (n * 12 + 8 + 8 + 4)
+
+
+def spec_bytes(d) -> int:
+    """mxs_spec_verify: target and draft logits once, the per-row inputs,
+    the outputs (tokens [rows, K+1], count, accepted, status)."""
+    rows, k1, _ = d["target"].shape
+    n = nbytes(d["target"]) + nbytes(d["draft"]) + nbytes(d["draft_tokens"]) + nbytes(d["temperature"])
+    n += nbytes(d["accept_u"]) + nbytes(d["resample_u"]) + nbytes(d["bonus_u"])
+    return n + rows * k1 * 4 + rows * 12
+
+
+def rotation(per_copy: int) -> int:
+    return max(2, min(1024, -(-ROTATE_BYTES // max(per_copy, 1))))
+
+
+class Call:
+    """One API call of a step: `fn(i)` queues it on the sampler's stream
+    against input copy i; `bytes_` are its algorithmic bytes."""
+
+    def __init__(self, name, kernels, fn, bytes_):
+        self.name, self.kernels, self.fn, self.bytes_ = name, kernels, fn, bytes_
+
+
+def build_workload(cfg, torch, Sampler, synth, to_device):
+    """Returns (description, rows per step, sampler, [Call], check(), batch
+    or dict for the CPU baseline)."""
+    if cfg == 5:
+        d = synth.config5()
+        rows, k1, V = d["target"].shape
+        dev = "cuda"
+        T = lambda a, dt=None: torch.from_numpy(a if dt is None else a.astype(dt)).to(dev)
+        tgt0, drf0 = T(d["target"]), T(d["draft"])
+        per = nbytes(tgt0) + nbytes(drf0)
+        nb = rotation(per)
+        tgts = [tgt0] + [tgt0.clone() for _ in range(nb - 1)]
+        drfs = [drf0] + [drf0.clone() for _ in range(nb - 1)]
+        dt = T(d["draft_tokens"])
+        temp, ua, ur, ub = T(d["temperature"]), T(d["accept_u"]), T(d["resample_u"]), T(d["bonus_u"])
+        stream = torch.cuda.Stream()
+        s = Sampler(max_rows=rows, max_vocab=V, stream=stream)
+        res = {}
+
+        def spec(i):
+            res["out"] = s.spec_verify(tgts[i % nb], drfs[i % nb], dt, temp, ua, ur, ub)
+
+        dd = dict(target=tgt0, draft=drf0, draft_tokens=dt, temperature=temp, accept_u=ua,
+                  resample_u=ur, bonus_u=ub)
+        calls = [Call("mxs_spec_verify", "spec_pass1<true> + spec_pass2<true>", spec, spec_bytes(dd))]
+
+        def check():
+            st = res["out"][3].cpu().numpy()
+            assert (st >= 0).all(), f"row errors in the benchmark batch: {st}"
+            return int((st == 1).sum())
+
+        desc = (f"cfg5: speculative verify, {rows} rows x draft {k1 - 1} x V={V} f32 target + draft, "
+                f"accept min(1,p/q), residual resample, bonus draw; inputs rotated over {nb} HBM copies")
+        return desc, rows, s, calls, check, d, stream
+
+    b = {1: synth.config1, 2: synth.config2, 3: synth.config3, 4: synth.config4}[cfg]()
+    logits, kw = to_device(torch, b)
+    nb = rotation(nbytes(logits))
+    bufs = [logits] + [logits.clone() for _ in range(nb - 1)]
+    stream = torch.cuda.Stream()
+    s = Sampler(max_rows=b.rows, max_vocab=b.vocab, stream=stream)
+    with torch.cuda.stream(stream):
+        launch = s.launcher(bufs[0], **kw)
+    calls = [Call("mxs_sample", "sample_kernel", lambda i: launch(bufs[i % nb]), sample_bytes(logits, kw))]
+    res = {}
+    if cfg == 1:   # config 1 also runs greedy (temperature 0) on the same logits
+        gkw = dict(kw)
+        gkw["temperature"] = torch.zeros_like(kw["temperature"])
+        with torch.cuda.stream(stream):
+            glaunch = s.launcher(bufs[0], **gkw)
+        calls.append(Call("mxs_sample greedy", "sample_kernel", lambda i: glaunch(bufs[i % nb]),
+                          sample_bytes(logits, gkw)))
+        res["greedy"] = glaunch
+    if cfg == 4:
+        def topn(i):
+            res["topn"] = s.logsoftmax_topn(bufs[i % nb], TOPN, vocab=b.vocab)
+
+        calls.append(Call("mxs_logsoftmax_topn", "topn_kernel", topn, topn_bytes(logits, b.vocab, TOPN)))
+
+    def check():
+        st = launch.out.status.cpu().numpy()
+        assert (st >= 0).all(), f"row errors in the benchmark batch: {st}"
+        unc = int((st == 1).sum())
+        if "greedy" in res:
+            g = res["greedy"].out.status.cpu().numpy()
+            assert (g == 0).all(), f"greedy row errors: {g}"
+        if "topn" in res:
+            t = res["topn"][4].cpu().numpy()
+            assert (t >= 0).all(), f"row errors in the top-n batch: {t}"
+        return unc
+
+    descs = {
+        1: "cfg1: 1 x V=151936 f32, T 0.7, top_k 20, top_p 0.8, repetition 1.05 over 512 ids, inverse-CDF draw",
+        2: "cfg2: B=64 x V=151936 f32, penalties + top-k {0,20,50,1000} + top-p U[.5,1) + min-p .05 + "
+           "inverse-CDF draw",
+        3: "cfg3: 32 x V=151936 bf16, packed u32 grammar masks (0.5-5% legal), T 1, top_p .95, draw",
+        4: "cfg4: 256 x V=262144 f32, T 1, top_k 64, top_p .95, draw; plus log-softmax top-20 per row",
+    }
+    desc = descs[cfg] + f"; logits rotated over {nb} HBM copies"
+    return desc, b.rows, s, calls, check, b, stream
+
+
+def cpu_baseline(cfg, data, seconds: float):
     """Times the oracle (the reference sampler restated in C) on this host."""
     import numpy as np
     from oracle import oracle
 
     oracle.lib()
+
+    if cfg == 5:
+        def one_pass():
+            d = data
+            for r in range(d["target"].shape[0]):
+                oracle.spec_verify_row(d["target"][r], d["draft"][r], d["draft_tokens"][r], float(d["temperature"][r]),
+                                       d["accept_u"][r], d["resample_u"][r], float(d["bonus_u"][r]))
+            return d["target"].shape[0]
+    elif cfg == 4:
+        def one_pass():
+            b = data
+            rows = range(0, 8)
+            oracle.sample_batch(b, rows=rows)
+            for r in rows:
+                oracle.token_logprob_top(b.logits[r], TOPN)
+            return len(rows)
+    else:
+        def one_pass():
+            oracle.sample_batch(data)
+            return data.rows
+
     rows_done, t0 = 0, time.perf_counter()
     while time.perf_counter() - t0 < seconds:
-        oracle.sample_batch(b)
-        rows_done += b.rows
+        rows_done += one_pass()
     single = rows_done / (time.perf_counter() - t0)
-    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
-    rows_mt, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 2:
-        oracle.sample_batch_threads(b, threads)
-        rows_mt += b.rows
-    multi = rows_mt / (time.perf_counter() - t0)
-    cpu = "unknown"
+    out = {
+        "value": round(single, 2), "unit": "rows/s", "cores": 1, "kind": "port",
+        "sample": f"{rows_done} rows of the same cfg{cfg} inputs (1 thread, rows serial, {seconds:.0f} s)",
+    }
+    if cfg in (2, 3):
+        threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+        rows_mt, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 2:
+            oracle.sample_batch_threads(data, threads)
+            rows_mt += data.rows
+        out["multi_thread"] = {"value": round(rows_mt / (time.perf_counter() - t0), 2), "cores": threads,
+                               "sample": f"{rows_mt} rows"}
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
+                out["cpu"] = line.split(":", 1)[1].strip()
                 break
     except OSError:
         pass
-    return {
-        "value": round(single, 2), "unit": "rows/s", "cores": 1, "kind": "port",
-        "sample": f"{rows_done} rows of the same cfg2 batch (1 thread, rows serial, {seconds:.0f} s)",
-        "multi_thread": {"value": round(multi, 2), "cores": threads, "sample": f"{rows_mt} rows"},
-        "cpu": cpu,
-    }
+    return out
 
 
-def committed_traffic():
-    p = ROOT / "profiles" / "sample_kernel_cfg2_traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("hbm_bytes_per_launch")
-        except Exception:
-            return None
-    return None
+def committed_traffic(cfg):
+    """HBM bytes per dispatch from the committed counter summary (FETCH_SIZE
+    and WRITE_SIZE passes scaled by a plain copy's readings)."""
+    p = ROOT / "profiles" / "hbm_traffic.json"
+    try:
+        return json.loads(p.read_text()).get(f"cfg{cfg}", {})
+    except Exception:
+        return {}
+
+
+def time_steps(torch, stream, calls, steps, warmup):
+    """Back-to-back steps bracketed by events on the sampler's stream; then,
+    for each call of the step, K back-to-back calls of that call alone, also
+    bracketed by events on that stream (its mean launch duration: with one
+    kernel per call the GPU runs that kernel back to back)."""
+    def timed(fns):
+        t_begin = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            t_begin.record(stream)
+            for i in range(steps):
+                for f in fns:
+                    f(i)
+            t_end.record(stream)
+        torch.cuda.synchronize()
+        return t_begin.elapsed_time(t_end) / steps
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            for c in calls:
+                c.fn(i)
+    ms_per_step = timed([c.fn for c in calls])
+    per_call = [ms_per_step] if len(calls) == 1 else [timed([c.fn]) for c in calls]
+    return ms_per_step, per_call
 
 
 def main():
@@ -88,9 +260,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE.json configuration to time (2 = the metric's)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
-    ap.add_argument("--race", action="store_true", help="also time race-v2 picks (mxs_sample_race)")
+    ap.add_argument("--race", action="store_true", help="also time race-v2 picks (mxs_sample_race, config 2)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device copies (scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -99,7 +273,6 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
     import torch
 
     if args.copy_calibration:
@@ -118,64 +291,27 @@ def main():
     from helpers import to_device
 
     assert torch.cuda.is_available(), "bench.py needs the GPU"
-    b = synth.config2()
-    logits, kw = to_device(torch, b)
-    bufs = [logits] + [logits.clone() for _ in range(NBUF - 1)]
-    stream = torch.cuda.Stream()
-    s = Sampler(max_rows=b.rows, max_vocab=b.vocab, stream=stream)
-    with torch.cuda.stream(stream):
-        launch = s.launcher(bufs[0], **kw)
-        out = launch.out
-        for i in range(args.warmup):
-            launch(bufs[i % NBUF])
-    torch.cuda.synchronize()
-    # Timed region: K back-to-back steps on the sampler's stream, bracketed by
-    # events on that stream; a second pair per launch gives kernel durations.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    t_begin = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        t_begin.record(stream)
-        for i in range(args.steps):
-            launch(bufs[i % NBUF])
-        t_end.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t_begin.elapsed_time(t_end)
-    # Kernel durations: a separate pass with events around each launch and
-    # one the library records between its two kernels (the chunk pass,
-    # sample_kernel, and the row finisher, finish_kernel).
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    with torch.cuda.stream(stream):
-        for i in range(args.steps):
-            mids[i].record(stream)   # creates the underlying hipEvent_t
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for i in range(args.steps):
-            starts[i].record(stream)
-            s.lib.mxs_debug_set_split_event(s.ctx, ctypes.c_void_p(mids[i].cuda_event))
-            launch(bufs[i % NBUF])
-            ends[i].record(stream)
-    s.lib.mxs_debug_set_split_event(s.ctx, None)
-    torch.cuda.synchronize()
-    chunk = sorted(st.elapsed_time(md) for st, md in zip(starts, mids))
-    fin = sorted(md.elapsed_time(en) for md, en in zip(mids, ends))
-    per = sorted(st.elapsed_time(en) for st, en in zip(starts, ends))
-    kern_ms = float(np.mean(chunk))
-    status = out.status.cpu().numpy()
-    assert (status >= 0).all(), f"row errors in the benchmark batch: {status}"
+    cfg = args.config
+    desc, rows, s, calls, check, data, stream = build_workload(cfg, torch, Sampler, synth, to_device)
+    ms_per_step, per_call = time_steps(torch, stream, calls, args.steps, args.warmup)
+    uncertified = check()
 
-    ms_per_step = total_ms / args.steps
-    rows_per_s = b.rows / (ms_per_step / 1e3)
-    bytes_ = algorithmic_bytes(b)
-    # the chunk pass streams every input byte: its rate against HBM peak
-    achieved = bytes_ / (kern_ms / 1e3) / 1e9
-    step_gbs = bytes_ / (ms_per_step / 1e3) / 1e9
+    traffic = committed_traffic(cfg)
+    kernels = []
+    for c, mean_ms in zip(calls, per_call):
+        gbs = c.bytes_ / (mean_ms / 1e3) / 1e9
+        kernels.append({
+            "call": c.name, "kernels": c.kernels, "algorithmic_bytes": c.bytes_,
+            "ms_mean": round(mean_ms, 6),
+            "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic.get(c.name),
+        })
+    dom = max(kernels, key=lambda k: k["ms_mean"])
+    step_bytes = sum(c.bytes_ for c in calls)
     props = torch.cuda.get_device_properties(0)
     res = {
-        "metric": METRIC,
-        "value": round(rows_per_s, 1),
+        "metric": METRIC if cfg == 2 else f"sampled rows/s, config {cfg}; achieved HBM GB/s vs MI355X peak",
+        "value": round(rows / (ms_per_step / 1e3), 1),
         "unit": "rows/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -184,51 +320,49 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32 logits, f64 sampling math",
-        "data": "synthetic (seeded SplitMix64, BASELINE config 2)",
-        "config": {
-            "workload": "cfg2: B=64 x V=151936 f32, penalties + top-k {0,20,50,1000} + top-p U[.5,1) + "
-                        "min-p .05 + inverse-CDF draw; logits rotated over 8 HBM copies",
-            "rows": b.rows, "vocab": b.vocab, "history": 2048,
-        },
+        "dtype": ("bf16" if cfg == 3 else "f32") + " logits, f64 sampling math",
+        "data": f"synthetic (seeded SplitMix64, BASELINE config {cfg})",
+        "config": {"workload": desc, "rows": rows},
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "achieved": dom["achieved_gbs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": committed_traffic(),
-            "kernel": "sample_kernel<float>",
-            "algorithmic_bytes": bytes_,
-            "kernel_ms_mean": round(kern_ms, 6),
-            "kernel_ms_median": round(chunk[len(chunk) // 2], 6),
-            "finish_kernel_ms_mean": round(float(np.mean(fin)), 6),
-            "pipeline_ms_mean": round(float(np.mean(per)), 6),
-            "pipeline_gbs": round(bytes_ / (float(np.mean(per)) / 1e3) / 1e9, 1),
-            "step_gbs": round(step_gbs, 1),
+            "frac": dom["frac"],
+            "traffic": dom["traffic"],
+            "kernel": dom["kernels"],
+            "algorithmic_bytes": dom["algorithmic_bytes"],
+            "kernel_ms_mean": dom["ms_mean"],
+            "step_gbs": round(step_bytes / (ms_per_step / 1e3) / 1e9, 1),
+            "step_frac": round(step_bytes / (ms_per_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
             "device": props.name,
         },
+        "calls": kernels,
+        "uncertified_rows": uncertified,
     }
-    if args.race:
-        res["race"] = race_bench(torch, s, stream, bufs, kw, b, args.steps, args.warmup)
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(b, args.cpu_seconds)
-    else:
-        res["cpu_baseline"] = None
+    if args.race and cfg == 2:
+        res["race"] = race_bench(torch, s, stream, data, args.steps, args.warmup)
+    res["cpu_baseline"] = None if args.no_cpu else cpu_baseline(cfg, data, args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 
-def race_bench(torch, s, stream, bufs, kw, b, steps, warmup):
-    """race-v2 picks (mxs_sample_race) on the same resident config-2 logits:
-    the batch's own rules (a kept set of 1 to ~600 tokens per row), and every
-    row a whole-row race (top_k 0, top_p 1, min_p 0: the race kernel scores
-    all V tokens).  Time per call, back to back, from events on the stream."""
+def race_bench(torch, s, stream, b, steps, warmup):
+    """race-v2 picks (mxs_sample_race) on resident config-2 logits: the
+    batch's own rules (a kept set of 1 to ~600 tokens per row), and every row
+    a whole-row race (top_k 0, top_p 1, min_p 0: the race kernel scores all V
+    tokens).  Time per call, back to back, from events on the stream."""
     import numpy as np
 
     from metallix_amd import synth
 
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import to_device
+
+    logits, kw = to_device(torch, b)
+    nb = rotation(nbytes(logits))
+    bufs = [logits] + [logits.clone() for _ in range(nb - 1)]
     st = synth.Stream(0x72616365)
-    dev = bufs[0].device
+    dev = logits.device
     race = (torch.from_numpy(st.u64(b.rows).view(np.int64)).to(dev),
             None, torch.from_numpy(np.arange(b.rows, dtype=np.int32)).to(dev))
     whole = dict(kw)
@@ -240,13 +374,13 @@ def race_bench(torch, s, stream, bufs, kw, b, steps, warmup):
         with torch.cuda.stream(stream):
             launch = s.launcher(bufs[0], race=race, **args_)
             for i in range(warmup):
-                launch(bufs[i % NBUF])
+                launch(bufs[i % nb])
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
             e0.record(stream)
             for i in range(steps):
-                launch(bufs[i % NBUF])
+                launch(bufs[i % nb])
             e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps

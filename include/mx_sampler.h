@@ -164,11 +164,6 @@ int mxs_sync(mxs_ctx* ctx);
  * the row finisher at slot MXS_DEBUG_TIMING_SLOTS - 1.  NULL disables. */
 #define MXS_DEBUG_TIMING_SLOTS 65
 int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer);
-/* Diagnostics (no reference counterpart): when `hip_event` (a hipEvent_t) is
- * non-null, mxs_sample records it on the context's stream between its two
- * kernels (the chunk pass and the row finisher), so a caller can time each
- * kernel with events.  NULL disables. */
-int mxs_debug_set_split_event(mxs_ctx* ctx, void* hip_event);
 const char* mxs_last_error(const mxs_ctx* ctx);
 const char* mxs_status_string(int32_t status);
 int mxs_abi_version(void);

@@ -3998,7 +3998,6 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
     hipLaunchKernelGGL((mxs::sample_kernel<float>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
   else
     hipLaunchKernelGGL((mxs::sample_kernel<uint16_t>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-  if (ctx->split_event) hipEventRecord(ctx->split_event, ctx->stream);
 #undef MXS_ARGS
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
@@ -4141,12 +4140,6 @@ int mxs_set_stream(mxs_ctx* ctx, void* stream) {
 int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer) {
   if (!ctx) return MXS_EINVAL;
   ctx->timing = (uint64_t*)device_buffer;
-  return MXS_OK;
-}
-
-int mxs_debug_set_split_event(mxs_ctx* ctx, void* hip_event) {
-  if (!ctx) return MXS_EINVAL;
-  ctx->split_event = (hipEvent_t)hip_event;
   return MXS_OK;
 }
 

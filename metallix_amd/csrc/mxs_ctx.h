@@ -64,7 +64,6 @@ struct mxs_ctx {
   float* d_zero_f32 = nullptr;
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
-  hipEvent_t split_event = nullptr;   // recorded after mxs_sample's kernel (diagnostics)
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
   // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
   uint32_t* topn_ctr = nullptr;
