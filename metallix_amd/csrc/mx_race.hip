@@ -78,7 +78,7 @@ struct RaceArgs {
   int32_t* token;
   double* logprob;          // may be null
   int32_t* status;
-  uint32_t* ctr;            // per-row arrival counters (zero between calls)
+  uint32_t* ctr;            // per-row arrival counters, CTR_STRIDE words apart (zero between calls)
   RaceStat* stat;           // rows x C
 };
 
@@ -306,17 +306,24 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     st_dev(&p->lbest, t.l);
     st_dev(&p->id, t.id);
     st_dev(&p->flags, flags | (any ? RF_ANY : 0u));
+    // The chunk's record is this thread's own device-scope stores: they
+    // complete before the increment (the ordering argument of arrive_last),
+    // and the last arriver's acquire fence precedes the merge's loads.
     wait_mem();
-    const uint32_t prev = __hip_atomic_fetch_add(&A.ctr[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S.last = prev == A.C - 1u ? 1u : 0u;
+    uint32_t* ctr = A.ctr + (uint64_t)row * CTR_STRIDE;
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = prev + 1u == A.C ? 1u : 0u;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      st_dev(ctr, 0u);
+    }
+    S.last = last;
   }
   __syncthreads();
   if (!S.last || wave() != 0) return;
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the merge's loads stay after the arrival
   // ---- the row's last chunk: wave 0 merges the chunks' records, lane q
   // taking chunks q, q + 64, ... (all loads in flight at once) ------------
   const uint32_t ln = lane();
-  if (ln == 0) st_dev(&A.ctr[row], 0u);
   const RaceStat* rs = &A.stat[(uint64_t)row * A.C];
   uint32_t rf = 0u;
   float M = -INFINITY;

@@ -84,7 +84,7 @@ struct SampleArgs {
   uint32_t CH;         // tokens per chunk (multiple of 4)
   uint64_t* timing;    // optional phase timestamps (diagnostics), see mxs_debug_set_timing
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
-  uint32_t epoch;      // this call's tag for Work::rowx (never 0)
+  uint32_t epoch;      // this call's tag for Work::rowx (never 0; the row's last chunk also clears its word)
   uint32_t nodraw;     // keep-all rows skip the inverse-CDF draw (race-v2 calls)
 };
 
@@ -3252,20 +3252,25 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
   }
   stamp(A, row, chunk, 2);
   {
-    // The row's last chunk to finish becomes its finisher.  Every thread's
-    // device-scope stores happen before the workgroup barrier, which happens
-    // before thread 0's release on the row counter; the last arriver's
-    // acquire fence, then the barrier, order its workgroup's loads after all
-    // of the row's stores.
+    // The row's last chunk to finish becomes its finisher.  Every wave
+    // waits for its own device-scope stores to complete before the
+    // workgroup barrier, which comes before thread 0's increment of the row
+    // counter; the last arriver's acquire fence, then the barrier, order its
+    // workgroup's loads after all of the row's stores (the ordering argument
+    // of arrive_last: a relaxed increment, no L2 write-back per arrival).
+    wait_mem();
     __syncthreads();
     uint32_t last = 0;
     if (tid == 0) {
       uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
-      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
       if (last) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         st_dev(ctr, 0u);
+        // every chunk's exchange update precedes its arrival: clear the
+        // row's word so no value outlives this call
+        st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
       }
       S.xkey = last;
     }
@@ -3869,17 +3874,22 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
   }
   stamp(A, row, chunk, 2);
   {
-    // The row's last chunk to finish becomes its finisher (release on the
-    // row counter after the barrier, acquire by the last arriver, as above).
+    // The row's last chunk to finish becomes its finisher (stores complete,
+    // barrier, relaxed increment of the row counter, acquire by the last
+    // arriver, as above).
+    wait_mem();
     __syncthreads();
     uint32_t last = 0;
     if (tid == 0) {
       uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
-      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
       if (last) {
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         st_dev(ctr, 0u);
+        // every chunk's exchange update precedes its arrival: clear the
+        // row's word so no value outlives this call
+        st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
       }
       S.xkey = last;
     }
@@ -4025,7 +4035,7 @@ const char* mxs_status_string(int32_t s) {
     case MXS_ROW_INVALID_TOP_P: return "nucleus sampling requires top_p in (0, 1]";
     case MXS_ROW_INVALID_MIN_P: return "min_p must be in [0, 1]";
     case MXS_ROW_INVALID_PENALTY: return "repetition penalty must be finite and positive; presence and frequency finite";
-    case MXS_ROW_INVALID_HISTORY: return "history token IDs must be below the vocabulary (at most 65535 per row)";
+    case MXS_ROW_INVALID_HISTORY: return "history token IDs must be below the vocabulary";
     case MXS_ROW_INVALID_BIAS: return "logit bias IDs must be strictly increasing, below the vocabulary, with finite values";
     case MXS_ROW_TOKEN_OUT_OF_RANGE: return "drafted token outside the vocabulary";
     case MXS_ROW_PROBABILITIES: return "invalid probability vectors";
@@ -4060,14 +4070,14 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
-  e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * sizeof(uint32_t));
-  e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
-  e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
-  e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->spec_scratch, mxs::spec_scratch_bytes(max_rows));
-  e = e ? e : hipMalloc(&ctx->race_ctr, (size_t)max_rows * sizeof(uint32_t));
-  e = e ? e : hipMemset(ctx->race_ctr, 0, (size_t)max_rows * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->race_ctr, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
+  e = e ? e : hipMemset(ctx->race_ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->race_scratch, mxs::race_scratch_bytes(max_rows, max_vocab));
   e = e ? e : hipMalloc(&ctx->race_kept, (size_t)max_rows * ((max_vocab + 31u) / 32u) * sizeof(uint32_t));
   const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;

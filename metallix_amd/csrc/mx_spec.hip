@@ -69,8 +69,8 @@ struct SpecArgs {
   int32_t* out_count;
   int32_t* out_accepted;
   int32_t* status;
-  uint32_t* ctr1;                     // [rows * (SPEC_KMAX + 1)]
-  uint32_t* ctr2;                     // [rows]
+  uint32_t* ctr1;                     // [rows * (SPEC_KMAX + 1)], CTR_STRIDE words apart
+  uint32_t* ctr2;                     // [rows], CTR_STRIDE words apart
   SpecStat* stat;                     // [rows * (SPEC_KMAX + 1) * SMAXC]
   SpecPos* pos;                       // [rows * (SPEC_KMAX + 1)]
   double* seg;                        // [rows * SMAXC * SSEG]
@@ -201,15 +201,7 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     st_dev(&st->tsum, tsum);
     st_dev(&st->dsum, dsum);
   }
-  wait_mem();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t slot = row * (SPEC_KMAX + 1) + j;
-    const uint32_t prev = __hip_atomic_fetch_add(&A.ctr1[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S.s_u[0] = (prev == A.C - 1u) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!S.s_u[0]) return;
+  if (!arrive_last(&A.ctr1[(row * (SPEC_KMAX + 1) + j) * CTR_STRIDE], A.C, &S.s_u[0])) return;
 
   // ---- the position's verdict (one thread does the arithmetic) -------------
   const uint32_t slot = row * (SPEC_KMAX + 1) + j;
@@ -227,7 +219,6 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
   }
   __syncthreads();
   if (tid != 0) return;
-  st_dev(&A.ctr1[slot], 0u);
   uint32_t fl = 0;
   float Mt = -INFINITY, Md = -INFINITY, Mn = INFINITY;
   for (uint32_t q = 0; q < C; ++q) {
@@ -389,17 +380,9 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
       if (lane() == 0) st_dev(&A.seg[((uint64_t)row * SMAXC + chunk) * SSEG + i * NW + wave()], ws);
     }
   }
-  wait_mem();
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&A.ctr2[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    S.s_u[0] = (prev == A.C - 1u) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!S.s_u[0]) return;
+  if (!arrive_last(&A.ctr2[row * CTR_STRIDE], A.C, &S.s_u[0])) return;
 
   // ---- the row's last chunk: outputs and the draw ---------------------------
-  if (tid == 0) st_dev(&A.ctr2[row], 0u);
   int32_t* ot = A.out_tokens + (uint64_t)row * (K + 1u);
   for (uint32_t j = tid; j <= K; j += NT) ot[j] = (j < pl.r) ? A.tok[(uint64_t)row * K + j] : -1;
   if (pl.err) {
@@ -578,7 +561,7 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   A.out_accepted = out_accepted;
   A.status = status;
   A.ctr1 = ctx->spec_ctr;
-  A.ctr2 = ctx->spec_ctr + (size_t)ctx->max_rows * (SPEC_KMAX + 1);
+  A.ctr2 = ctx->spec_ctr + (size_t)ctx->max_rows * (SPEC_KMAX + 1) * CTR_STRIDE;
   char* base = reinterpret_cast<char*>(ctx->spec_scratch);
   const size_t pairs = (size_t)ctx->max_rows * (SPEC_KMAX + 1);
   A.stat = reinterpret_cast<SpecStat*>(base);

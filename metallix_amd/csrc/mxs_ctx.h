@@ -34,13 +34,14 @@ constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8)
 
 // Rows' counters and exchange words sit on their own 128-byte lines, so the
 // atomics of different rows do not queue on one line.
-constexpr uint32_t CTR_STRIDE = 32;    // u32 words per row of Work::ctr
+constexpr uint32_t CTR_STRIDE = 32;    // u32 words between arrival counters (one 128-byte line each)
 constexpr uint32_t ROWX_STRIDE = 16;   // u64 words per row of Work::rowx
 
 // Device scratch of mxs_sample, sized for the context's limits.
 struct Work {
-  uint32_t* ctr;              // [max_rows * CTR_STRIDE] chunks of the row done (fused mode; the row's last chunk resets it)
-  unsigned long long* rowx;   // [max_rows * ROWX_STRIDE] (call epoch << 32) | largest chunk-maximum key published so far
+  uint32_t* ctr;              // [max_rows * CTR_STRIDE] chunks of the row done (the row's last chunk resets it)
+  unsigned long long* rowx;   // [max_rows * ROWX_STRIDE] (call epoch << 32) | largest chunk-maximum key published so far;
+                              // the row's last chunk clears it, so an entry never outlives its call
   ChunkStat* stat;            // [max_rows * MAXC]
   float* cand_l;              // [max_rows * max_vocab]
   uint32_t* cand_id;          // [max_rows * max_vocab]

@@ -68,6 +68,40 @@ __device__ __forceinline__ void st_dev(unsigned long long* p, unsigned long long
 }
 // Waits until this lane's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_mem() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Arrival of one workgroup on a counter shared by the `total` workgroups
+// that split one unit of work (a row, a row position).  Returns true in every
+// thread of the last workgroup to arrive, which also returns the counter to
+// zero for the next launch.  `flag` is a word of LDS.
+//
+// Ordering.  Everything the workgroups exchange is written with the
+// device-scope stores above (st_dev: scope bits sc1, written through to the
+// level every XCD reads) and read with the device-scope loads (ld_dev).  Each
+// wave waits for its own stores to complete (s_waitcnt vmcnt(0): complete
+// means performed at device scope), the workgroup barrier puts every wave's
+// wait before thread 0's increment, and the last arriver issues its loads
+// only after its increment returned the final count, that is after every
+// other workgroup's increment, each issued after that workgroup's stores had
+// completed.  The increment itself is relaxed: a release increment would add
+// a write-back of the XCD's whole L2 (buffer_wbl2) per arrival, which the
+// device-scope stores do not need (measured: +25 us per config-4 pick with
+// 1792 arrivals, +250 us per config-4 top-n with 8192).  The last arriver
+// still takes an acquire fence (a cache invalidate, cheap) before its loads.
+__device__ __forceinline__ bool arrive_last(uint32_t* ctr, uint32_t total, uint32_t* flag) {
+  wait_mem();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = prev + 1u == total ? 1u : 0u;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    *flag = last;
+  }
+  __syncthreads();
+  return *flag != 0u;
+}
 // Workgroup barrier for LDS traffic: waits for this wave's LDS (and scalar)
 // operations only.  __syncthreads() also drains every outstanding global
 // load and store first, which would stall the chunk phase until its whole
@@ -374,6 +408,13 @@ __device__ __forceinline__ double block_incl_scan_f64(double v, double* slot /* 
 
 constexpr int NBR = 2048;                 // radix-select bins (11 bits)
 
+// LDS word of histogram bin b.  Lane j of a wave owns the 32 bins
+// [NBR - 32 (j + 1), NBR - 32 j) and reads them as eight 4-bin groups; the
+// groups are stored transposed (group g of owner o at word 256 g + 4 o), so
+// the 64 lanes' 16-byte reads of one group index are consecutive and the
+// bin search is free of bank conflicts.
+__device__ __forceinline__ uint32_t hpos(uint32_t b) { return ((b & 31u) >> 2) * 256u + (b >> 5) * 4u + (b & 3u); }
+
 // The k-th largest (k >= 1) of the active 32-bit keys the workgroup's
 // threads hold (up to R each; bit r of `act` marks key[r] active), by three
 // radix passes (11, 11 and 10 bits) over LDS histograms; *above receives how
@@ -383,6 +424,7 @@ template <int R>
 __device__ __forceinline__ uint32_t block_kth_largest(const uint32_t (&key)[R], uint64_t act, uint32_t k, uint32_t* hist,
                                       uint32_t* above) {
   uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
+  const uint32_t own = 4u * (63u - lane());   // this lane's word within a group row
 #pragma unroll
   for (int p = 0; p < 3; ++p) {
     const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
@@ -390,103 +432,35 @@ __device__ __forceinline__ uint32_t block_kth_largest(const uint32_t (&key)[R], 
     uint32_t* h = hist + p * NBR;
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      if (((act >> r) & 1ull) && (key[r] & pmask) == prefix) atomicAdd(&h[(key[r] >> sh) & dmask], 1u);
+      if (((act >> r) & 1ull) && (key[r] & pmask) == prefix) atomicAdd(&h[hpos((key[r] >> sh) & dmask)], 1u);
     lds_barrier();
-    // Every wave finds the bin itself.  Lane j owns bins
-    // [NBR - 32 (j + 1), NBR - 32 j), visited from the highest.
+    // Every wave finds the bin itself, each lane over its own 32 bins from
+    // the highest (group 7 down to group 0).
     const uint32_t hi = (uint32_t)NBR - 32u * lane();
+    uint32_t c[32];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&h[(uint32_t)(7 - g) * 256u + own]);
+      c[4 * g + 0] = v.w; c[4 * g + 1] = v.z; c[4 * g + 2] = v.y; c[4 * g + 3] = v.x;
+    }
     uint32_t s = 0;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 4u * (uint32_t)(q + 1)]);
-      s += v.x + v.y + v.z + v.w;
-    }
+    for (int q = 0; q < 32; ++q) s += c[q];
     const uint32_t inc = wave_scan_u32(s);
     const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
     if (!reach) break;   // fewer than k active keys: the caller's contract is broken
     const uint32_t L = (uint32_t)__builtin_ctzll(reach);
-    // the crossing bin inside lane L's range (every lane walks its own,
-    // 16 bins at a time from vector reads)
+    // the crossing bin inside lane L's range (every lane walks its own)
     uint32_t run = inc - s, bin = hi - 1u, before = run;
     bool found = false;
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      uint32_t c[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 16u * (uint32_t)half - 4u * (uint32_t)(q + 1)]);
-        c[4 * q + 0] = v.w; c[4 * q + 1] = v.z; c[4 * q + 2] = v.y; c[4 * q + 3] = v.x;
+    for (int q = 0; q < 32; ++q) {
+      if (!found && run + c[q] >= need) {
+        found = true;
+        bin = hi - 1u - (uint32_t)q;
+        before = run;
       }
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (!found && run + c[q] >= need) {
-          found = true;
-          bin = hi - 1u - 16u * (uint32_t)half - (uint32_t)q;
-          before = run;
-        }
-        run += c[q];
-      }
-    }
-    const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
-    const uint32_t cnt_above = (uint32_t)__builtin_amdgcn_readlane((int)before, (int)L);
-    need -= cnt_above;
-    abv += cnt_above;
-    prefix |= b << sh;
-    pmask |= dmask << sh;
-  }
-  *above = abv;
-  return prefix;
-}
-
-
-
-// As block_kth_largest, for keys fetched on demand: get(r) returns this
-// thread's r-th key, for r < R with bit r of `act` set (R <= 64).
-template <typename Get>
-__device__ __forceinline__ uint32_t block_kth_largest_fn(Get get, uint32_t R, uint64_t act, uint32_t k,
-                                                          uint32_t* hist, uint32_t* above) {
-  uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
-    const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
-    uint32_t* h = hist + p * NBR;
-    for (uint32_t r = 0; r < R; ++r) {
-      if (!((act >> r) & 1ull)) continue;
-      const uint32_t key = get(r);
-      if ((key & pmask) == prefix) atomicAdd(&h[(key >> sh) & dmask], 1u);
-    }
-    lds_barrier();
-    const uint32_t hi = (uint32_t)NBR - 32u * lane();
-    uint32_t s = 0;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 4u * (uint32_t)(q + 1)]);
-      s += v.x + v.y + v.z + v.w;
-    }
-    const uint32_t inc = wave_scan_u32(s);
-    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
-    if (!reach) break;
-    const uint32_t L = (uint32_t)__builtin_ctzll(reach);
-    uint32_t run = inc - s, bin = hi - 1u, before = run;
-    bool found = false;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      uint32_t c[16];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint4 v = *reinterpret_cast<const uint4*>(&h[hi - 16u * (uint32_t)half - 4u * (uint32_t)(q + 1)]);
-        c[4 * q + 0] = v.w; c[4 * q + 1] = v.z; c[4 * q + 2] = v.y; c[4 * q + 3] = v.x;
-      }
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (!found && run + c[q] >= need) {
-          found = true;
-          bin = hi - 1u - 16u * (uint32_t)half - (uint32_t)q;
-          before = run;
-        }
-        run += c[q];
-      }
+      run += c[q];
     }
     const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)bin, (int)L);
     const uint32_t cnt_above = (uint32_t)__builtin_amdgcn_readlane((int)before, (int)L);

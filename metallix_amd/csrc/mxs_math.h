@@ -91,4 +91,33 @@ MXS_HD double exp_neg_t(double x, const double* tab_hi, const double* tab_lo) {
 }
 MXS_HD double exp_neg(double x) { return exp_neg_t(x, kExp2Tab, kExp2TabLo); }
 
+// exp(x) for x <= 0 in f64 without tables (for loops over registers, where
+// table gathers would be hoisted and held): x = n ln2 + r, |r| <= ln2 / 2
+// (Cody-Waite reduction with a 32-bit high part of ln2, so n * hi is exact
+// for |n| < 2^21), degree-13 Taylor polynomial for e^r (truncation below
+// 5e-18 relative), scaled by 2^n.  Within 2 ulp of glibc's exp (checked in
+// tests).  Returns 0 below -746 and for -inf.
+MXS_HD double exp_neg_p(double x) {
+  if (!(x > -746.0)) return 0.0;
+  const double kLn2Hi = 0.6931471803691238;       // ln 2, low 21 bits of the significand clear
+  const double kLn2Lo = 1.9082149292705877e-10;   // ln 2 - kLn2Hi
+  const double t = rint(x * 1.4426950408889634);
+  double r = fma(-t, kLn2Hi, x);
+  r = fma(-t, kLn2Lo, r);
+  double p = 1.0 / 6227020800.0;                  // 1/13!
+  p = fma(p, r, 1.0 / 479001600.0);
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  return ldexp(fma(p, r, 1.0), (int)t);
+}
+
 }  // namespace mxs
