@@ -8,7 +8,7 @@
 // f64(l) - maximum - log_normalizer.  The caller over-selects top + 8 and
 // filters unspellable IDs, as the reference does.
 //
-// One launch: each row is split into C chunks of TCH tokens, one 256-thread
+// Two launches.  The chunk pass: each row is split into C chunks of TCH tokens, one 256-thread
 // workgroup per chunk (small register and LDS footprints, so several
 // workgroups share a CU and their streams overlap).  A chunk streams its
 // logits once and reduces its maximum and its f64 sum of exp(l - chunk
@@ -17,10 +17,11 @@
 // token at least that large), the largest over the waves.  The tokens at or
 // above it (about n to 2n of 8192 on ordinary rows) are ranked exactly by
 // counting, in (total_cmp descending, ID ascending) order.  A chunk whose
-// threshold admits more than TWCAP tokens in one wave (near-ties) takes an exact radix
-// select over its registers instead.  The last chunk of the row to arrive
-// merges the C sorted lists (by binary search ranks, in rounds of at most
-// TMCAP entries) and the C (maximum, sum) pairs.
+// threshold admits more than TWCAP tokens in one wave (near-ties) takes an
+// exact radix select instead.  The merge, one workgroup per row, merges the C sorted lists (the entries at or above the largest last
+// entry of a full list, ranked by counting) and the C (maximum, sum) pairs;
+// the launch boundary orders the chunk pass's stores before the merge's
+// loads, so the chunk workgroups exit without waiting on an arrival counter.
 
 #include <hip/hip_runtime.h>
 
@@ -42,7 +43,6 @@ constexpr uint32_t TSL = TNT * 4;         // tokens per slice (one quad per thre
 constexpr uint32_t TCH = TSL * TQ;        // tokens per chunk (8192)
 constexpr int TMAXC = 320;                // chunks per row (vocab <= 320 * 8192)
 constexpr uint32_t TWCAP = 256;           // candidate slots per wave
-constexpr uint32_t TMCAP = 2048;          // list entries one merge round holds
 
 struct TopnStat {
   float maxv;          // chunk maximum (NaN ignored)
@@ -61,52 +61,33 @@ struct TopnArgs {
   double* maximum;
   double* lognorm;
   int32_t* status;
-  uint32_t* ctr;                // [rows] arrival counters, CTR_STRIDE words apart
   TopnStat* stat;               // [rows * C]
   unsigned long long* list;     // [rows * C * n], (okey << 32) | ~id, descending
 };
 
 struct alignas(16) TopnSmem {
   union {
-    alignas(16) uint32_t hist[3][NBR];               // exact select: three radix passes
+    alignas(16) uint32_t hist[NBR];                  // exact select (one radix pass at a time)
     unsigned long long cand[TNW * TWCAP];            // threshold candidates, per-wave regions
-    unsigned long long ent[TMCAP];                   // merge round
   } u;
-  unsigned long long top[TOPN_MAX];                  // the chunk's list / the merge's running list
-  double etab[128];                                  // 2^(j/64) and its low parts
-  TopnStat st[TMAXC];
-  uint32_t lo[TMAXC + 2];                            // merge: list boundaries within ent
+  unsigned long long top[TOPN_MAX];                  // the exact select's list
+  double etab[128];                                  // 2^(j/64) and its low parts (exp_neg_t)
   uint32_t wcnt[TQ * TNW];
+  uint32_t wkept[TNW];
   uint32_t red_u[3][TNW];
+  float red_f[TNW];
   double red_d[TNW];
-  unsigned long long red64[TNW];
-  uint32_t s_cnt, s_last, s_n;
+  uint32_t s_cnt;
 };
 
 __device__ __forceinline__ unsigned long long entry_key(uint32_t k, uint32_t id) {
   return ((unsigned long long)k << 32) | (unsigned long long)(~id);
 }
 
-// Entries of the sorted (descending) list ent[b, e) larger than x.
-__device__ __forceinline__ uint32_t count_above(const unsigned long long* ent, uint32_t b, uint32_t e,
-                                                unsigned long long x) {
-  uint32_t lo = b, hi = e;
-  while (lo < hi) {
-    const uint32_t md = (lo + hi) >> 1;
-    if (ent[md] > x) lo = md + 1u; else hi = md;
-  }
-  return lo - b;
-}
-
-// A chunk's exact top `take` (near-ties: the threshold admitted too many
-// tokens): radix select over the chunk, reloaded, with ties at the k-th key
-// taken in token-ID order; the list goes out sorted.
 template <typename In>
-__device__ __noinline__ void exact_list(const TopnArgs& A, TopnSmem& S, const In* src, uint32_t row, uint32_t chunk,
-                                        uint32_t c0, uint32_t c1, uint32_t take) {
+__device__ __noinline__ void exact_list(unsigned long long* list, TopnSmem& S, const In* src, uint32_t c0, uint32_t c1,
+                                        uint32_t take) {
   const uint32_t tid = threadIdx.x;
-  for (uint32_t t = tid; t < 3u * NBR / 4u; t += TNT)
-    reinterpret_cast<uint4*>(&S.u.hist[0][0])[t] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) S.s_cnt = 0u;
   uint32_t keys[TQ * 4];
   uint64_t act = 0;
@@ -122,7 +103,7 @@ __device__ __noinline__ void exact_list(const TopnArgs& A, TopnSmem& S, const In
   }
   lds_barrier();
   uint32_t above = 0;
-  const uint32_t kth = block_kth_largest<TQ * 4>(keys, act, take, &S.u.hist[0][0], &above);
+  const uint32_t kth = block_kth_largest<TQ * 4>(keys, act, take, S.u.hist, &above);
   // keys above kth go straight in; ties at kth in token-ID order
   const uint32_t need_t = take - above;
   for (int j = 0; j < TQ * 4; ++j) {
@@ -172,12 +153,12 @@ __device__ __noinline__ void exact_list(const TopnArgs& A, TopnSmem& S, const In
     const unsigned long long mine = lane() < take ? S.top[lane()] : 0ull;
     uint32_t rank = 0;
     for (uint32_t j = 0; j < take; ++j) rank += S.top[j] > mine ? 1u : 0u;
-    if (lane() < take) st_dev(&A.list[((uint64_t)row * A.C + chunk) * A.n + rank], mine);
+    if (lane() < take) st_dev(&list[rank], mine);
   }
 }
 
 template <typename In>
-__global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
+__global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
   __shared__ TopnSmem S;
   const uint32_t tid = threadIdx.x;
   const uint32_t xcd = blockIdx.x & 7u;
@@ -189,35 +170,51 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
   const uint32_t c1 = min(V, c0 + TCH);
   const In* src = reinterpret_cast<const In*>(A.logits) + (uint64_t)row * A.stride;
 
-  // the exp tables first: their loads complete ahead of the stream's
+  // Token (q, e) of this thread is c0 + q TSL + 4 tid + e: one base register
+  // and immediate offsets.  Out-of-range tokens (the row's last chunk) read
+  // as -inf; a row with a real -inf is non-finite and takes no list.
+  const uint32_t len = c1 - c0;
+  const uint32_t tb = c0 + tid * 4u;
   const double tab = tid < 128u ? (tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u]) : 0.0;
   typename Quad<In>::Raw raw[TQ];
 #pragma unroll
   for (int q = 0; q < TQ; ++q) {
-    const uint32_t e0 = c0 + (uint32_t)q * TSL + tid * 4u;
-    raw[q] = Quad<In>::load(src + (e0 < c1 ? e0 : c0));
+    const uint32_t off = (uint32_t)q * TSL + tid * 4u;
+    raw[q] = Quad<In>::load(src + c0 + (off < len ? off : 0u));
   }
+
   if (tid < 128u) S.etab[tid] = tab;
 
   // ---- pass 1: maximum, finite check, lane maxima ---------------------------
   float x[TQ][4];
   float t1 = -INFINITY;
   bool nf = false;
+  if (len == TCH) {
 #pragma unroll
-  for (int q = 0; q < TQ; ++q) {
-    float v[4];
-    Quad<In>::unpack(raw[q], v);
-    const uint32_t e0 = c0 + (uint32_t)q * TSL + tid * 4u;
+    for (int q = 0; q < TQ; ++q) {
+      Quad<In>::unpack(raw[q], x[q]);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool inr = e0 + (uint32_t)e < c1;
-      x[q][e] = inr ? v[e] : -INFINITY;
-      nf |= inr && !__builtin_isfinite(v[e]);
-      t1 = fmaxf(t1, x[q][e]);
+      for (int e = 0; e < 4; ++e) {
+        nf |= !__builtin_isfinite(x[q][e]);
+        t1 = fmaxf(t1, x[q][e]);
+      }
+    }
+  } else {
+    const int rem = (int)len - (int)(tid * 4u);   // tokens of the chunk from this thread's first on
+#pragma unroll
+    for (int q = 0; q < TQ; ++q) {
+      float v[4];
+      Quad<In>::unpack(raw[q], v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool inr = q * (int)TSL + e < rem;
+        x[q][e] = inr ? v[e] : -INFINITY;
+        nf |= inr && !__builtin_isfinite(v[e]);
+        t1 = fmaxf(t1, x[q][e]);
+      }
     }
   }
   const uint32_t n = A.n;
-  const uint32_t len = c1 - c0;
   const uint32_t take = min(n, len);
   // This wave's take-th largest lane maximum: `take` lanes hold a token at
   // least that large, so the chunk's take-th largest token is too (0 when
@@ -239,29 +236,30 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
   double part = 0.0;
   if (take > 0u) {
     unsigned long long* wc = S.u.cand + wave() * TWCAP;
+    // (a float compare: a superset of key >= wthr, never an out-of-range
+    // -inf; the ranking filters by key)
+    const float fthr = okey_value(max(wthr, okey(-INFINITY) + 1u));
 #pragma unroll
     for (int q = 0; q < TQ; ++q) {
-      const uint32_t e0 = c0 + (uint32_t)q * TSL + tid * 4u;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t key = okey(x[q][e]);
-        const bool c = e0 + (uint32_t)e < c1 && key >= wthr;
+        const bool c = x[q][e] >= fthr;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(c);
         if (bal) {
           const uint32_t at = woff + lanes_below(bal);
-          if (c && at < TWCAP) wc[at] = entry_key(key, e0 + (uint32_t)e);
+          if (c && at < TWCAP) wc[at] = entry_key(okey(x[q][e]), tb + (uint32_t)(q * TSL + e));
           woff += (uint32_t)__builtin_popcountll(bal);
         }
       }
     }
   }
-  lds_barrier();   // the exp tables are in LDS
+  lds_barrier();   // the exp tables
   if (t1 > -INFINITY) {
     const double tm = (double)t1;
 #pragma unroll
     for (int q = 0; q < TQ; ++q)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part += exp_neg_p((double)x[q][e] - tm);   // -inf -> 0
+      for (int e = 0; e < 4; ++e) part += exp_neg_t((double)x[q][e] - tm, S.etab, S.etab + 64);   // -inf -> 0
   }
   {
     const uint32_t kmax = wave_max_u32(lk);
@@ -294,18 +292,44 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
     part = wave_sum_f64(part);
     if (lane() == 0) S.red_d[wave()] = part;
     if (take > 0u && !over) {
-      // ---- rank the candidates at or above the block threshold by counting
-      // (keys are distinct; candidates below it never outrank one above it)
-      for (uint32_t j = tid; j < ncand; j += TNT) {
+      // ---- the candidates at or above the block threshold: each wave
+      // compacts its own region in place, then they are ranked by counting
+      // (keys are distinct).
+      {
+        const uint32_t wn = S.wcnt[wave()];
+        unsigned long long* wc = S.u.cand + wave() * TWCAP;
+        unsigned long long ev[TWCAP / 64];
+        bool keep[TWCAP / 64];
+#pragma unroll
+        for (int i = 0; i < (int)(TWCAP / 64); ++i) {
+          const uint32_t k = lane() + 64u * (uint32_t)i;
+          ev[i] = k < wn ? wc[k] : 0ull;
+          keep[i] = k < wn && (uint32_t)(ev[i] >> 32) >= lthr;
+        }
+        uint32_t mk = 0;
+#pragma unroll
+        for (int i = 0; i < (int)(TWCAP / 64); ++i) {
+          const uint64_t b = __builtin_amdgcn_ballot_w64(keep[i]);
+          if (keep[i]) wc[mk + lanes_below(b)] = ev[i];
+          mk += (uint32_t)__builtin_popcountll(b);
+        }
+        if (lane() == 0) S.wkept[wave()] = mk;
+      }
+      lds_barrier();
+      uint32_t kb[TNW + 1];
+      kb[0] = 0;
+#pragma unroll
+      for (int w = 0; w < TNW; ++w) kb[w + 1] = kb[w] + S.wkept[w];
+      for (uint32_t j = tid; j < kb[TNW]; j += TNT) {
         uint32_t w = 0;
 #pragma unroll
-        for (int i = 1; i < TNW; ++i) w += j >= wb[i] ? 1u : 0u;
-        const unsigned long long mine = S.u.cand[w * TWCAP + (j - wb[w])];
-        if ((uint32_t)(mine >> 32) < lthr) continue;
+        for (int i = 1; i < TNW; ++i) w += j >= kb[i] ? 1u : 0u;
+        const unsigned long long mine = S.u.cand[w * TWCAP + (j - kb[w])];
         uint32_t rank = 0;
+#pragma unroll
         for (int v = 0; v < TNW; ++v) {
           const unsigned long long* cw = S.u.cand + v * TWCAP;
-          const uint32_t cn = S.wcnt[v];
+          const uint32_t cn = kb[v + 1] - kb[v];
           for (uint32_t i = 0; i < cn; ++i) rank += cw[i] > mine ? 1u : 0u;
         }
         if (rank < take) st_dev(&A.list[((uint64_t)row * A.C + chunk) * n + rank], mine);
@@ -313,7 +337,7 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
       listed = take;
     } else if (take > 0u) {
       __syncthreads();   // the histograms overlay the candidate slots
-      exact_list<In>(A, S, src, row, chunk, c0, c1, take);
+      exact_list<In>(A.list + ((uint64_t)row * A.C + chunk) * n, S, src, c0, c1, take);
       listed = take;
     }
     lds_barrier();
@@ -327,27 +351,123 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
     st_dev(&st->count, listed);
     st_dev(&st->sum, sum);
   }
-  if (!arrive_last(A.ctr + (uint64_t)row * CTR_STRIDE, A.C, &S.s_last)) return;
+}
 
-  // ---- the row's last chunk: merge ------------------------------------------
-  const uint32_t C = A.C;
-  for (uint32_t q = tid; q < C; q += TNT) {
-    const TopnStat* st = &A.stat[(uint64_t)row * C + q];
-    TopnStat v;
-    v.maxv = ld_dev(&st->maxv);
-    v.flags = ld_dev(&st->flags);
-    v.count = ld_dev(&st->count);
-    v.sum = ld_dev(&st->sum);
-    S.st[q] = v;
+// ---------------------------------------------------------------------------
+// The merge: one workgroup per row, after the chunk pass (the launch boundary
+// orders the chunks' stores before its loads).  Every chunk of a row without
+// non-finite logits lists min(n, its length) entries, sorted.  A list of n
+// entries has n at or above its last, so entries below the largest such
+// last entry (thr) cannot rank below n.  The entries at or above thr (about
+// n to 2n on ordinary rows) are collected, in rounds of at most MGRP lists
+// with the running top n, and ranked by counting.
+constexpr uint32_t MDCAP = 2048;                  // collected entries a round selects from
+struct alignas(16) MergeSmem {
+  unsigned long long dense[MDCAP];
+  unsigned long long tie[MDCAP];
+  alignas(16) uint32_t hist[NBR];
+  unsigned long long sel[TOPN_MAX];
+  unsigned long long top[TOPN_MAX];
+  uint32_t red_u[2][TNW];
+  double red_d[TNW];
+  unsigned long long red64[TNW];
+  uint32_t s_m, s_sel, s_tie;
+};
+
+// The `want` largest of S.dense[0, m) (distinct keys, want <= m, want <=
+// TOPN_MAX) into S.top[0, want), sorted descending: a radix select of the
+// want-th largest high word (the f32 key), the entries above it, and the
+// ties at it by counting on the full key.
+__device__ __forceinline__ void top_of_dense(MergeSmem& S, uint32_t m, uint32_t want) {
+  const uint32_t tid = threadIdx.x;
+  constexpr int RM = (int)(MDCAP / TNT);
+  if (tid == 0) { S.s_sel = 0u; S.s_tie = 0u; }
+  if (want < m) {
+    uint32_t keys[RM];
+    uint64_t act = 0;
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      const uint32_t j = tid + (uint32_t)i * TNT;
+      keys[i] = j < m ? (uint32_t)(S.dense[j] >> 32) : 0u;
+      if (j < m) act |= 1ull << i;
+    }
+    uint32_t above = 0;
+    const uint32_t kth = block_kth_largest<RM>(keys, act, want, S.hist, &above);
+#pragma unroll
+    for (int i = 0; i < RM; ++i) {
+      if (!((act >> i) & 1ull)) continue;
+      const unsigned long long e = S.dense[tid + (uint32_t)i * TNT];
+      if (keys[i] > kth) S.sel[atomicAdd(&S.s_sel, 1u)] = e;
+      else if (keys[i] == kth) S.tie[atomicAdd(&S.s_tie, 1u)] = e;
+    }
+    __syncthreads();
+    const uint32_t need = want - above, t = S.s_tie;
+    for (uint32_t j = tid; j < t; j += TNT) {
+      const unsigned long long e = S.tie[j];
+      uint32_t r = 0;
+      if (t > need)
+        for (uint32_t i = 0; i < t; ++i) r += S.tie[i] > e ? 1u : 0u;
+      if (r < need) S.sel[above + (t > need ? r : j)] = e;
+    }
+  } else {
+    for (uint32_t j = tid; j < m; j += TNT) S.sel[j] = S.dense[j];
   }
   __syncthreads();
-  uint32_t rflags = 0;
-  float M32 = -INFINITY;
-  for (uint32_t q = 0; q < C; ++q) {
-    rflags |= S.st[q].flags;
-    M32 = fmaxf(M32, S.st[q].maxv);
+  if (wave() == 0) {   // sort the selection by counting
+    const unsigned long long e = lane() < want ? S.sel[lane()] : 0ull;
+    uint32_t r = 0;
+    for (uint32_t i = 0; i < want; ++i) r += S.sel[i] > e ? 1u : 0u;
+    if (lane() < want) S.top[r] = e;
   }
-  if (rflags) {
+  __syncthreads();
+}
+
+__global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
+  __shared__ MergeSmem S;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t row = blockIdx.x;
+  const uint32_t V = A.V, n = A.n;
+  const uint32_t C = A.C;
+  const unsigned long long* lists = A.list + (uint64_t)row * C * n;
+  auto cnt_of = [&](uint32_t q) { return min(n, min(TCH, V - q * TCH)); };
+  // chunk statistics and the last entry of each full list (chunks tid, tid + TNT)
+  float cm[2];
+  double cs[2];
+  uint32_t fl = 0;
+  float mx = -INFINITY;
+  unsigned long long tl = 0ull;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t q = tid + (uint32_t)i * TNT;
+    cm[i] = -INFINITY;
+    cs[i] = 0.0;
+    if (q < C) {
+      const TopnStat* st = &A.stat[(uint64_t)row * C + q];
+      cm[i] = ld_dev(&st->maxv);
+      cs[i] = ld_dev(&st->sum);
+      fl |= ld_dev(&st->flags);
+      mx = fmaxf(mx, cm[i]);
+      if (n > 0 && cnt_of(q) == n)
+        tl = max(tl, __builtin_bit_cast(unsigned long long,
+                                        ld_dev(reinterpret_cast<const double*>(&lists[(uint64_t)q * n + n - 1u]))));
+    }
+  }
+  {
+    const uint32_t wf = wave_or_u32(fl);
+    const uint32_t wm = wave_max_u32(okey(mx));
+    tl = wave_max_u64(tl);
+    if (lane() == 0) { S.red_u[0][wave()] = wf; S.red_u[1][wave()] = wm; S.red64[wave()] = tl; }
+  }
+  __syncthreads();
+  uint32_t rflags = 0, mkey = 0;
+  unsigned long long thr = 0ull;
+#pragma unroll
+  for (int w = 0; w < TNW; ++w) {
+    rflags |= S.red_u[0][w];
+    mkey = max(mkey, S.red_u[1][w]);
+    thr = max(thr, S.red64[w]);
+  }
+  if (rflags) {   // a non-finite logit (the chunks wrote no lists)
     for (uint32_t j = tid; j < n; j += TNT) {
       A.ids[(uint64_t)row * n + j] = -1;
       A.logprobs[(uint64_t)row * n + j] = __builtin_nan("");
@@ -359,73 +479,40 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
     }
     return;
   }
-  const double M = (double)M32;
+  const double M = (double)okey_value(mkey);
   double rpart = 0.0;
-  for (uint32_t q = tid; q < C; q += TNT)
-    if (S.st[q].sum > 0.0) rpart += S.st[q].sum * exp_neg_t((double)S.st[q].maxv - M, S.etab, S.etab + 64);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    if (cs[i] > 0.0) rpart += cs[i] * exp_neg_p((double)cm[i] - M);
   rpart = wave_sum_f64(rpart);
   if (lane() == 0) S.red_d[wave()] = rpart;
-  // Merge rounds: the running list (sorted, at most n entries) and as many
-  // whole chunk lists as fit in TMCAP entries; each entry's rank is its
-  // place in its own list plus, per other list, the entries larger than it.
-  const uint32_t nout = min(n, V);
   uint32_t nrun = 0;
-  uint32_t q0 = 0;
   if (n > 0) {
-    while (q0 < C) {
-      if (tid == 0) {
-        uint32_t at = nrun, q = q0, k = 1;
-        S.lo[0] = 0u;
-        S.lo[1] = nrun;
-        while (q < C && at + S.st[q].count <= TMCAP) {
-          at += S.st[q].count;
-          S.lo[++k] = at;
-          ++q;
-        }
-        S.s_n = q;   // chunks q0 .. q - 1 join this round
+    const uint32_t grp = (MDCAP - TOPN_MAX) / n;          // lists per round
+    const uint32_t mg = ((1u << 20) + n - 1u) / n;        // j / n == (j * mg) >> 20 for j < 2^14
+    for (uint32_t q0 = 0; q0 < C; q0 += grp) {
+      const uint32_t q1 = min(C, q0 + grp);
+      if (tid == 0) S.s_m = 0u;
+      __syncthreads();
+      // the running top n (all at or above thr are kept) and this round's
+      // entries at or above thr
+      for (uint32_t j = tid; j < nrun; j += TNT) {
+        const unsigned long long e = S.top[j];
+        if (e >= thr) S.dense[atomicAdd(&S.s_m, 1u)] = e;
+      }
+      const uint32_t span = (q1 - q0) * n;
+      for (uint32_t j = tid; j < span; j += TNT) {
+        const uint32_t l = (j * mg) >> 20;
+        const uint32_t pos = j - l * n;
+        if (pos >= cnt_of(q0 + l)) continue;
+        const unsigned long long e = __builtin_bit_cast(
+            unsigned long long, ld_dev(reinterpret_cast<const double*>(&lists[(uint64_t)(q0 + l) * n + pos])));
+        if (e >= thr) S.dense[atomicAdd(&S.s_m, 1u)] = e;
       }
       __syncthreads();
-      const uint32_t q1 = S.s_n;
-      const uint32_t nl = q1 - q0 + 1u;   // lists: the running list, then the chunks
-      const uint32_t total = S.lo[nl];
-      for (uint32_t j = tid; j < total; j += TNT) {
-        unsigned long long v;
-        if (j < nrun) {
-          v = S.top[j];
-        } else {
-          uint32_t l = 1;
-          while (S.lo[l + 1] <= j) ++l;
-          const uint32_t q = q0 + l - 1u;
-          v = __builtin_bit_cast(unsigned long long,
-                                 ld_dev(reinterpret_cast<const double*>(&A.list[((uint64_t)row * C + q) * n + (j - S.lo[l])])));
-        }
-        S.u.ent[j] = v;
-      }
-      __syncthreads();
-      // A list of n entries has n at or above its last: entries below the
-      // largest such last entry cannot rank below n.
-      unsigned long long tl = 0ull;
-      for (uint32_t l = tid; l < nl; l += TNT)
-        if (S.lo[l + 1] - S.lo[l] >= n) tl = max(tl, S.u.ent[S.lo[l] + n - 1u]);
-      tl = wave_max_u64(tl);
-      if (lane() == 0) S.red64[wave()] = tl;
-      __syncthreads();
-      unsigned long long thr = 0ull;
-#pragma unroll
-      for (int w = 0; w < TNW; ++w) thr = max(thr, S.red64[w]);
-      for (uint32_t j = tid; j < total; j += TNT) {
-        const unsigned long long e = S.u.ent[j];
-        if (e < thr) continue;
-        uint32_t l = 0;
-        while (S.lo[l + 1] <= j) ++l;
-        uint32_t rank = j - S.lo[l];
-        for (uint32_t r = 0; r < nl; ++r)
-          if (r != l) rank += count_above(S.u.ent, S.lo[r], S.lo[r + 1], e);
-        if (rank < n) S.top[rank] = e;
-      }
-      nrun = min(n, total);
-      q0 = q1;
-      __syncthreads();
+      const uint32_t m = S.s_m;
+      nrun = min(n, m);
+      top_of_dense(S, m, nrun);   // the new running top, in order
     }
   }
   __syncthreads();
@@ -433,6 +520,7 @@ __global__ __launch_bounds__(TNT, 4) void topn_kernel(TopnArgs A) {
 #pragma unroll
   for (int w = 0; w < TNW; ++w) Ssum += S.red_d[w];
   const double ln = log(Ssum);
+  const uint32_t nout = min(n, V);
   for (uint32_t j = tid; j < n; j += TNT) {
     if (j < nout && j < nrun) {
       const unsigned long long e = S.top[j];
@@ -480,7 +568,6 @@ extern "C" int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dty
   A.maximum = maximum;
   A.lognorm = log_normalizer;
   A.status = status;
-  A.ctr = ctx->topn_ctr;
   A.stat = reinterpret_cast<mxs::TopnStat*>(ctx->topn_scratch);
   A.list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ctx->topn_scratch) +
                                                  (size_t)ctx->max_rows * mxs::TMAXC * sizeof(mxs::TopnStat));
@@ -492,6 +579,7 @@ extern "C" int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dty
     hipLaunchKernelGGL(mxs::topn_kernel<float>, grid, dim3(mxs::TNT), 0, ctx->stream, A);
   else
     hipLaunchKernelGGL(mxs::topn_kernel<uint16_t>, grid, dim3(mxs::TNT), 0, ctx->stream, A);
+  hipLaunchKernelGGL(mxs::topn_merge_kernel, dim3(rows), dim3(mxs::TNT), 0, ctx->stream, A);
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "topn_kernel launch");

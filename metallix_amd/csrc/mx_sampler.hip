@@ -4070,8 +4070,6 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
   e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
-  e = e ? e : hipMalloc(&ctx->topn_ctr, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
-  e = e ? e : hipMemset(ctx->topn_ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
   e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
@@ -4129,7 +4127,6 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->d_one_f32);
   hipFree(ctx->d_zero_f32);
   hipFree(ctx->d_mask_ones);
-  hipFree(ctx->topn_ctr);
   hipFree(ctx->topn_scratch);
   hipFree(ctx->spec_ctr);
   hipFree(ctx->spec_scratch);

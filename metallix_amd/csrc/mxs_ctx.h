@@ -66,8 +66,7 @@ struct mxs_ctx {
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
-  // mxs_logsoftmax_topn: per-row arrival counters and per-chunk results
-  uint32_t* topn_ctr = nullptr;
+  // mxs_logsoftmax_topn: per-chunk results
   void* topn_scratch = nullptr;
   // mxs_spec_verify: per-position arrival counters and per-chunk results
   uint32_t* spec_ctr = nullptr;

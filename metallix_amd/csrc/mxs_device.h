@@ -417,19 +417,23 @@ __device__ __forceinline__ uint32_t hpos(uint32_t b) { return ((b & 31u) >> 2) *
 
 // The k-th largest (k >= 1) of the active 32-bit keys the workgroup's
 // threads hold (up to R each; bit r of `act` marks key[r] active), by three
-// radix passes (11, 11 and 10 bits) over LDS histograms; *above receives how
-// many active keys are larger.  Needs at least k active keys and three
-// zeroed NBR-word histograms, which it leaves dirty.
+// radix passes (11, 11 and 10 bits) over one NBR-word LDS histogram, which it
+// clears before each pass; *above receives how many active keys are larger.
+// Needs at least k active keys.
 template <int R>
 __device__ __forceinline__ uint32_t block_kth_largest(const uint32_t (&key)[R], uint64_t act, uint32_t k, uint32_t* hist,
                                       uint32_t* above) {
   uint32_t prefix = 0, pmask = 0, need = k, abv = 0;
   const uint32_t own = 4u * (63u - lane());   // this lane's word within a group row
-#pragma unroll
+#pragma unroll 1
   for (int p = 0; p < 3; ++p) {
     const int sh = p == 0 ? 21 : (p == 1 ? 10 : 0);
     const uint32_t dmask = p == 2 ? 0x3ffu : 0x7ffu;
-    uint32_t* h = hist + p * NBR;
+    uint32_t* h = hist;
+    __syncthreads();   // every wave has finished reading the previous pass's counts
+    for (uint32_t t = threadIdx.x; t < (uint32_t)NBR / 4u; t += blockDim.x)
+      reinterpret_cast<uint4*>(h)[t] = make_uint4(0u, 0u, 0u, 0u);
+    lds_barrier();
 #pragma unroll
     for (int r = 0; r < R; ++r)
       if (((act >> r) & 1ull) && (key[r] & pmask) == prefix) atomicAdd(&h[hpos((key[r] >> sh) & dmask)], 1u);
