@@ -157,6 +157,22 @@ int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const float* draft
                     const double* accept_uniform, const double* resample_uniform,
                     const double* bonus_uniform, int32_t* out_tokens, int32_t* out_count,
                     int32_t* out_accepted, int32_t* status);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): mxs_logsoftmax_topn without a context.  The kernels run
+ * on `stream` (a hipStream_t; NULL = the default stream) on the current
+ * device, with their per-chunk statistics and lists in a device array the
+ * library holds per GPU until the process ends: rows * ceil(vocab / 8192) *
+ * (24 + 8 n) bytes must fit in MXS_TOPN_STATIC_BYTES (MXS_EINVAL otherwise).
+ * Calls on one GPU share that array, so calls that overlap in time on one
+ * GPU (other streams, other threads) race; calls in order on one stream do
+ * not.  Allocates nothing.  mxs_last_error(NULL) reads this thread's last
+ * error message. */
+#define MXS_TOPN_STATIC_BYTES (8u << 20)
+int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int32_t dtype, uint32_t rows,
+                                uint32_t vocab, uint64_t row_stride, uint32_t n, int32_t* ids,
+                                double* logprobs, double* maximum, double* log_normalizer,
+                                int32_t* status);
 int mxs_sync(mxs_ctx* ctx);
 /* Diagnostics (no reference counterpart): when `device_buffer` is non-null,
  * mxs_sample records 100 MHz wall-clock stamps at fixed phase boundaries:

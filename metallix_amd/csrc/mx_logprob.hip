@@ -28,6 +28,9 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+#include <string>
+
 #include "../../include/mx_sampler.h"
 #include "mxs_ctx.h"
 #include "mxs_device.h"
@@ -541,22 +544,30 @@ __global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
 
 }  // namespace mxs
 
-extern "C" int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dtype, uint32_t rows, uint32_t vocab,
-                                   uint64_t row_stride, uint32_t n, int32_t* ids, double* logprobs, double* maximum,
-                                   double* log_normalizer, int32_t* status) {
-  if (!ctx) return MXS_EINVAL;
-  if (rows == 0) return MXS_OK;
+namespace mxs {
+
+// Argument checks shared by both entry points (nullptr: accepted).
+static const char* topn_check(const void* logits, int32_t dtype, uint32_t vocab, uint64_t row_stride, uint32_t n,
+                              const int32_t* ids, const double* logprobs, const double* maximum,
+                              const double* log_normalizer, const int32_t* status) {
   if (!logits || !maximum || !log_normalizer || !status || (n > 0 && (!ids || !logprobs)))
-    return fail(ctx, MXS_EINVAL, "logits, maximum, log_normalizer and status are required (ids and logprobs when n > 0)");
-  if (rows > ctx->max_rows || vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
-  if (vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
-  if (n > mxs::TOPN_MAX) return fail(ctx, MXS_EINVAL, "n must be at most 64");
-  if (dtype != MXS_F32 && dtype != MXS_BF16) return fail(ctx, MXS_EINVAL, "dtype must be MXS_F32 or MXS_BF16");
-  if (row_stride < vocab || (row_stride & 3u)) return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");
-  if (((uintptr_t)logits) % (dtype == MXS_F32 ? 16u : 8u)) return fail(ctx, MXS_EINVAL, "logits must be 16-byte (f32) or 8-byte (bf16) aligned");
-  const uint32_t C = (vocab + mxs::TCH - 1u) / mxs::TCH;
-  if (C > (uint32_t)mxs::TMAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
-  mxs::TopnArgs A;
+    return "logits, maximum, log_normalizer and status are required (ids and logprobs when n > 0)";
+  if (vocab == 0) return "vocab must be positive";
+  if (n > TOPN_MAX) return "n must be at most 64";
+  if (dtype != MXS_F32 && dtype != MXS_BF16) return "dtype must be MXS_F32 or MXS_BF16";
+  if (row_stride < vocab || (row_stride & 3u)) return "row_stride must be >= vocab and a multiple of 4";
+  if (((uintptr_t)logits) % (dtype == MXS_F32 ? 16u : 8u)) return "logits must be 16-byte (f32) or 8-byte (bf16) aligned";
+  if ((vocab + TCH - 1u) / TCH > (uint32_t)TMAXC) return "vocab too large for the chunk layout";
+  return nullptr;
+}
+
+// Queues the chunk pass and the merge on `stream` (current device) with the
+// per-chunk statistics and lists at `stat` and `list`.
+static hipError_t topn_launch(hipStream_t stream, const void* logits, int32_t dtype, uint32_t rows, uint32_t vocab,
+                              uint64_t row_stride, uint32_t n, int32_t* ids, double* logprobs, double* maximum,
+                              double* log_normalizer, int32_t* status, TopnStat* stat, unsigned long long* list) {
+  const uint32_t C = (vocab + TCH - 1u) / TCH;
+  TopnArgs A;
   A.logits = logits;
   A.stride = row_stride;
   A.rows = rows;
@@ -568,27 +579,98 @@ extern "C" int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dty
   A.maximum = maximum;
   A.lognorm = log_normalizer;
   A.status = status;
-  A.stat = reinterpret_cast<mxs::TopnStat*>(ctx->topn_scratch);
-  A.list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ctx->topn_scratch) +
-                                                 (size_t)ctx->max_rows * mxs::TMAXC * sizeof(mxs::TopnStat));
+  A.stat = stat;
+  A.list = list;
   const dim3 grid(8u * C, (rows + 7u) / 8u);
-  int prev = 0;
-  hipGetDevice(&prev);
-  if (prev != ctx->device) hipSetDevice(ctx->device);
   if (dtype == MXS_F32)
-    hipLaunchKernelGGL(mxs::topn_kernel<float>, grid, dim3(mxs::TNT), 0, ctx->stream, A);
+    hipLaunchKernelGGL(topn_kernel<float>, grid, dim3(TNT), 0, stream, A);
   else
-    hipLaunchKernelGGL(mxs::topn_kernel<uint16_t>, grid, dim3(mxs::TNT), 0, ctx->stream, A);
-  hipLaunchKernelGGL(mxs::topn_merge_kernel, dim3(rows), dim3(mxs::TNT), 0, ctx->stream, A);
-  hipError_t e = hipGetLastError();
-  if (prev != ctx->device) hipSetDevice(prev);
-  if (e != hipSuccess) return hip_fail(ctx, e, "topn_kernel launch");
-  return MXS_OK;
+    hipLaunchKernelGGL(topn_kernel<uint16_t>, grid, dim3(TNT), 0, stream, A);
+  hipLaunchKernelGGL(topn_merge_kernel, dim3(rows), dim3(TNT), 0, stream, A);
+  return hipGetLastError();
 }
 
-namespace mxs {
 // Scratch bytes the context allocates for mxs_logsoftmax_topn.
 size_t topn_scratch_bytes(uint32_t max_rows) {
   return (size_t)max_rows * TMAXC * (sizeof(TopnStat) + TOPN_MAX * sizeof(unsigned long long));
 }
+
+// ---------------------------------------------------------------------------
+// mxs_logsoftmax_topn_noalloc: the per-chunk statistics and lists live in a
+// device array of the library (one copy per GPU, held until the process
+// ends).  Its device address is looked up once per device, with that device
+// current, and kept; host code passes that address, never the array's name
+// (a host-side stand-in).  Calls on one GPU share the array.
+static __device__ __align__(256) unsigned char scratch[MXS_TOPN_STATIC_BYTES];
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES];
+static thread_local std::string g_noalloc_error;
+
+static int noalloc_fail(int code, const std::string& msg) {
+  g_noalloc_error = msg;
+  return code;
+}
+
+static int scratch_of_device(int dev, void** out) {
+  if (dev < 0 || dev >= MAX_DEVICES) return noalloc_fail(MXS_ENODEV, "device index beyond the library's table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return noalloc_fail(MXS_EHIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MXS_OK;
+}
+
+const char* noalloc_last_error() { return g_noalloc_error.empty() ? nullptr : g_noalloc_error.c_str(); }
+
 }  // namespace mxs
+
+extern "C" int mxs_logsoftmax_topn(mxs_ctx* ctx, const void* logits, int32_t dtype, uint32_t rows, uint32_t vocab,
+                                   uint64_t row_stride, uint32_t n, int32_t* ids, double* logprobs, double* maximum,
+                                   double* log_normalizer, int32_t* status) {
+  if (!ctx) return MXS_EINVAL;
+  if (rows == 0) return MXS_OK;
+  if (const char* m = mxs::topn_check(logits, dtype, vocab, row_stride, n, ids, logprobs, maximum, log_normalizer, status))
+    return fail(ctx, MXS_EINVAL, m);
+  if (rows > ctx->max_rows || vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
+  auto* stat = reinterpret_cast<mxs::TopnStat*>(ctx->topn_scratch);
+  auto* list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ctx->topn_scratch) +
+                                                     (size_t)ctx->max_rows * mxs::TMAXC * sizeof(mxs::TopnStat));
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  const hipError_t e = mxs::topn_launch(ctx->stream, logits, dtype, rows, vocab, row_stride, n, ids, logprobs, maximum,
+                                        log_normalizer, status, stat, list);
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "topn launch");
+  return MXS_OK;
+}
+
+extern "C" int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int32_t dtype, uint32_t rows,
+                                           uint32_t vocab, uint64_t row_stride, uint32_t n, int32_t* ids,
+                                           double* logprobs, double* maximum, double* log_normalizer,
+                                           int32_t* status) {
+  if (rows == 0) return MXS_OK;
+  if (const char* m = mxs::topn_check(logits, dtype, vocab, row_stride, n, ids, logprobs, maximum, log_normalizer, status))
+    return mxs::noalloc_fail(MXS_EINVAL, m);
+  const uint64_t pairs = (uint64_t)rows * ((vocab + mxs::TCH - 1u) / mxs::TCH);
+  const uint64_t stat_bytes = (pairs * sizeof(mxs::TopnStat) + 255u) & ~(uint64_t)255u;
+  if (stat_bytes + pairs * n * sizeof(unsigned long long) > (uint64_t)MXS_TOPN_STATIC_BYTES)
+    return mxs::noalloc_fail(MXS_EINVAL, "rows * ceil(vocab / 8192) * (24 + 8 n) bytes exceed MXS_TOPN_STATIC_BYTES");
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return mxs::noalloc_fail(MXS_ENODEV, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  void* base = nullptr;
+  if (int rc = mxs::scratch_of_device(dev, &base)) return rc;
+  auto* stat = reinterpret_cast<mxs::TopnStat*>(base);
+  auto* list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(base) + stat_bytes);
+  e = mxs::topn_launch((hipStream_t)stream, logits, dtype, rows, vocab, row_stride, n, ids, logprobs, maximum,
+                       log_normalizer, status, stat, list);
+  if (e != hipSuccess) return mxs::noalloc_fail(MXS_EHIP, std::string("topn launch: ") + hipGetErrorString(e));
+  return MXS_OK;
+}

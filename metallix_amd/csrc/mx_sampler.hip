@@ -4157,7 +4157,11 @@ int mxs_sync(mxs_ctx* ctx) {
   return MXS_OK;
 }
 
-const char* mxs_last_error(const mxs_ctx* ctx) { return ctx ? ctx->last_error.c_str() : "null context"; }
+const char* mxs_last_error(const mxs_ctx* ctx) {
+  if (ctx) return ctx->last_error.c_str();
+  const char* m = mxs::noalloc_last_error();   // the context-free entry point's
+  return m ? m : "null context";
+}
 
 int mxs_sample(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o) { return mxs::sample_launch(ctx, b, o, false); }
 

@@ -28,6 +28,7 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);
+const char* noalloc_last_error();   // this thread's last mxs_logsoftmax_topn_noalloc error, or nullptr
 size_t spec_scratch_bytes(uint32_t max_rows);
 size_t race_scratch_bytes(uint32_t max_rows, uint32_t max_vocab);
 constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8), one per row

@@ -78,6 +78,8 @@ PROTOTYPES = {
                                        ctypes.POINTER(MxsOut)]),
     "mxs_logsoftmax_topn": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
                                            ctypes.c_uint64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _vp]),
+    "mxs_logsoftmax_topn_noalloc": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32,
+                                                   ctypes.c_uint64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "mxs_spec_verify": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mxs_sync": (ctypes.c_int, [_vp]),

@@ -40,3 +40,12 @@ def test_create_rejects_bad_arguments_without_a_device():
     assert lib.mxs_create(0, None, 0, 10, ctypes.byref(ctx)) == -1
     assert lib.mxs_create(0, None, 1, 0, ctypes.byref(ctx)) == -1
     assert lib.mxs_create(0, None, 1, 10, None) == -1
+
+
+def test_noalloc_topn_rejects_bad_arguments_without_a_device():
+    from metallix_amd import sampler
+
+    lib = sampler.load_library()
+    # null logits: rejected by the argument checks, before any HIP call
+    assert lib.mxs_logsoftmax_topn_noalloc(None, None, 0, 4, 100, 100, 5, None, None, None, None, None) == -1
+    assert b"required" in lib.mxs_last_error(None)
