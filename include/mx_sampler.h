@@ -110,7 +110,9 @@ typedef struct {
   const uint32_t* history_ids;
   const uint32_t* bias_offsets;   /* rows + 1 offsets into bias_ids/bias_values; NULL => none */
   const uint32_t* bias_ids;       /* strictly increasing within a row */
-  const float* bias_values;
+  const float* bias_values;       /* finite, or -INFINITY: the token is suppressed, its adjusted
+                                     logit f32::MIN (ChatFormat::suppress,
+                                     crates/core/chat-format/src/lib.rs:771-780) */
   const uint32_t* mask_words;     /* rows x mask_stride u32 words, bit b of word w <-> token 32w+b; NULL => none */
   uint64_t mask_stride;           /* words between row masks; >= ceil(vocab / 32) */
   uint32_t tokenizer_vocab;       /* with a mask: tokens at or past it are never legal */

@@ -266,6 +266,9 @@ __device__ __forceinline__ RowCfg load_cfg(const double* __restrict__ temperatur
   return c;
 }
 
+// A bias value is finite, or -inf (the token is suppressed: f32::MIN).
+__device__ __forceinline__ bool bias_ok(float v) { return v == v && v != INFINITY; }
+
 // Error precedence after the parameter checks: history ids, bias entries,
 // uniform, non-finite adjusted logit, empty support.
 __device__ __forceinline__ int32_t combine_errors(const RowCfg& c, uint32_t flags, uint32_t nlegal) {
@@ -3393,13 +3396,13 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
       for (uint32_t j = tid; j < bn; j += NT) {
         const uint32_t id = S.bids[j];
         const uint32_t prev = j == 0 ? 0u : S.bids[j - 1];
-        if (id >= V || !isfinite(S.bvals[j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+        if (id >= V || !bias_ok(S.bvals[j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
       }
     } else {
       for (uint32_t j = tid; j < bn; j += NT) {
         const uint32_t id = b.bias_ids[c.bb + j];
         const uint32_t prev = j == 0 ? 0u : b.bias_ids[c.bb + j - 1];
-        if (id >= V || !isfinite(b.bias_values[c.bb + j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
+        if (id >= V || !bias_ok(b.bias_values[c.bb + j]) || (j > 0 && prev >= id)) my_flags |= F_BIAS;
       }
     }
   }
@@ -4036,7 +4039,7 @@ const char* mxs_status_string(int32_t s) {
     case MXS_ROW_INVALID_MIN_P: return "min_p must be in [0, 1]";
     case MXS_ROW_INVALID_PENALTY: return "repetition penalty must be finite and positive; presence and frequency finite";
     case MXS_ROW_INVALID_HISTORY: return "history token IDs must be below the vocabulary";
-    case MXS_ROW_INVALID_BIAS: return "logit bias IDs must be strictly increasing, below the vocabulary, with finite values";
+    case MXS_ROW_INVALID_BIAS: return "logit bias IDs must be strictly increasing, below the vocabulary, with finite values (or -inf: suppressed)";
     case MXS_ROW_TOKEN_OUT_OF_RANGE: return "drafted token outside the vocabulary";
     case MXS_ROW_PROBABILITIES: return "invalid probability vectors";
     default: return "unknown status";

@@ -303,9 +303,11 @@ __device__ __forceinline__ float vmax(float a, float b) {
 // Logit-bias and penalty stage for one token (BUILD-DEFINED semantics, f32,
 // every operation rounded separately): bias, then for a token seen cnt > 0
 // times the repetition penalty once (l < 0 ? l * rep : l / rep), then
-// - cnt * freq, then - pres.
+// - cnt * freq, then - pres.  A bias of -inf suppresses the token (f32::MIN,
+// as bias_and_penalize).
 __device__ __forceinline__ float penalize_logit(float l, uint32_t cnt, bool has_bias, float bias, float rep,
                                                 float pres, float freq) {
+  if (has_bias && bias == -INFINITY) return kF32Min;
   if (has_bias) l = l + bias;
   if (cnt) {
     l = l < 0.0f ? l * rep : l / rep;

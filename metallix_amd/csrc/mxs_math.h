@@ -48,13 +48,19 @@ MXS_HD float okey_value(uint32_t k) {
 // f32 division on the host over random and edge-case operands.
 MXS_HD float div_by_recip(float l, double inv_r) { return (float)((double)l * inv_r); }
 
+// The lowest finite f32 (Rust's f32::MIN): a suppressed token's logit.
+constexpr float kF32Min = -0x1.fffffep+127f;
+
 // Logit bias and penalties for one token, every step rounded to f32 in this
 // order: l + bias (when the token has a bias entry), then for a token seen
 // `cnt` > 0 times in the history: repetition (l < 0 ? l * rep : l / rep),
 // minus cnt * frequency, minus presence.  `tv` packs cnt in bits 0-30 and
-// "has a bias entry" in bit 31.
+// "has a bias entry" in bit 31.  A bias entry of -inf suppresses the token:
+// its adjusted logit is f32::MIN whatever the penalties
+// (ChatFormat::suppress, crates/core/chat-format/src/lib.rs:771-780).
 MXS_HD float bias_and_penalize(float l, uint32_t tv, float bias, float rep, double inv_rep, float freq,
                                float pres) {
+  if ((tv >> 31) && bias == -INFINITY) return kF32Min;
   const uint32_t cnt = tv & 0x7fffffffu;
   const float a = (tv >> 31) ? l + bias : l;
   const float r = a < 0.0f ? a * rep : div_by_recip(a, inv_rep);

@@ -112,6 +112,37 @@ def load_library(path: Optional[Path] = None):
     return lib
 
 
+def with_suppression(rows: int, suppress_ids, bias_offsets=None, bias_ids=None, bias_values=None):
+    """Host-side CSR for the sampler's bias stage with the checkpoint's
+    suppressed tokens merged in (ChatFormat::suppress,
+    crates/core/chat-format/src/lib.rs:761-780): every row gets a -inf entry
+    for each id of `suppress_ids` (ids are per checkpoint, the same for every
+    row), which the sampler turns into an adjusted logit of f32::MIN.  A
+    suppressed id keeps no bias of its own.  Returns numpy (offsets u32[rows
+    + 1], ids u32, values f32), ids strictly increasing within a row."""
+    import numpy as np
+
+    sup = np.unique(np.asarray(suppress_ids, dtype=np.uint32))
+    offs, ids, vals = [0], [], []
+    for r in range(rows):
+        if bias_offsets is not None:
+            b0, b1 = int(bias_offsets[r]), int(bias_offsets[r + 1])
+            bi = np.asarray(bias_ids[b0:b1], dtype=np.uint32)
+            bv = np.asarray(bias_values[b0:b1], dtype=np.float32)
+            keep = ~np.isin(bi, sup)
+            bi, bv = bi[keep], bv[keep]
+        else:
+            bi, bv = np.zeros(0, np.uint32), np.zeros(0, np.float32)
+        ri = np.concatenate([bi, sup])
+        rv = np.concatenate([bv, np.full(sup.size, -np.inf, dtype=np.float32)])
+        order = np.argsort(ri, kind="stable")
+        ids.append(ri[order])
+        vals.append(rv[order])
+        offs.append(offs[-1] + ri.size)
+    return (np.asarray(offs, dtype=np.uint32), np.concatenate(ids).astype(np.uint32),
+            np.concatenate(vals).astype(np.float32))
+
+
 def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
@@ -251,6 +282,48 @@ class Sampler:
 
         launch.out = out
         return launch
+
+    def verify_point_mass(self, logits, draft, temperature, uniform, *, stop_ids=(), **rule):
+        """Point-mass speculative verification on device picks (A9): the
+        walk of accept_and_roll_back (crates/core/engine/src/speculative.rs:
+        318-347, as accept_verified exposes it for device picks) over S
+        sequences of K + 1 scored positions.  `logits` [S * (K + 1), V] on
+        the device, sequence-major; `draft` host ints [S, K]; `temperature`,
+        `uniform` and the other rule tensors of `sample` are per row (row i
+        of a sequence carries uniform_ahead(i), crates/app/cli/src/
+        qwen_forward.rs:283-292).  Every row is picked in one mxs_sample
+        call; on the host each sequence keeps picks in order until one
+        leaves the draft, is a stop token, or is the bonus row.  Returns, per
+        sequence, dict(emitted, accepted, stopped, status): status is 0, or
+        the first non-zero row status among the settled rows (1: the host
+        settles that row, as TokenPicker does, chat_turn.rs:348-358)."""
+        import numpy as np
+
+        draft = np.asarray(draft)
+        S, K = draft.shape
+        assert logits.shape[0] == S * (K + 1), "logits rows must be S * (K + 1)"
+        out = self.sample(logits, temperature, uniform=uniform, **rule)
+        self.sync()
+        tok = out.token.cpu().numpy().reshape(S, K + 1)
+        st = out.status.cpu().numpy().reshape(S, K + 1)
+        stops = set(int(t) for t in stop_ids)
+        res = []
+        for s_ in range(S):
+            emitted, accepted, stopped, status = [], 0, False, 0
+            for i in range(K + 1):
+                if status == 0 and st[s_, i] != 0:
+                    status = int(st[s_, i])
+                t = int(tok[s_, i])
+                emitted.append(t)
+                matches = i < K and int(draft[s_, i]) == t
+                accepted += int(matches)
+                if t in stops:
+                    stopped = True
+                    break
+                if not matches:
+                    break
+            res.append(dict(emitted=emitted, accepted=accepted, stopped=stopped, status=status))
+        return res
 
     def logsoftmax_topn(self, logits, n: int, *, vocab: Optional[int] = None):
         """Queues the T=1 log-softmax of every row with its n most likely IDs

@@ -19,6 +19,7 @@
  */
 #include "mx_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -589,7 +590,10 @@ float orc_bf16_to_f32(uint16_t h) {
  *     l = l - presence
  * repetition follows the Hugging Face RepetitionPenaltyLogitsProcessor
  * (applied once per distinct token); frequency and presence follow OpenAI's
- * definitions. */
+ * definitions.  A bias value of -inf suppresses its token: the adjusted
+ * logit is f32::MIN after everything else, as ChatFormat::suppress writes it
+ * (crates/core/chat-format/src/lib.rs:771-780; the reference has no bias or
+ * penalties, so there suppression is exactly "logit = f32::MIN"). */
 int orc_adjust_logits(const float* logits, size_t n, const orc_row_params* p, float* adjusted) {
   if (!(isfinite(p->repetition) && p->repetition > 0.0f) || !isfinite(p->presence) ||
       !isfinite(p->frequency))
@@ -597,11 +601,13 @@ int orc_adjust_logits(const float* logits, size_t n, const orc_row_params* p, fl
   for (size_t j = 0; j < p->history_len; ++j)
     if (p->history[j] >= n) return ORC_INVALID_HISTORY;
   for (size_t j = 0; j < p->bias_len; ++j) {
-    if (p->bias_ids[j] >= n || !isfinite(p->bias_values[j])) return ORC_INVALID_BIAS;
+    const float v = p->bias_values[j];
+    if (p->bias_ids[j] >= n || isnan(v) || v == INFINITY) return ORC_INVALID_BIAS;
     if (j > 0 && p->bias_ids[j] <= p->bias_ids[j - 1]) return ORC_INVALID_BIAS;
   }
   memcpy(adjusted, logits, n * sizeof(float));
   for (size_t j = 0; j < p->bias_len; ++j) {
+    if (p->bias_values[j] == -INFINITY) continue;   /* suppressed: set below */
     volatile float sum = adjusted[p->bias_ids[j]] + p->bias_values[j];
     adjusted[p->bias_ids[j]] = sum;
   }
@@ -621,6 +627,8 @@ int orc_adjust_logits(const float* logits, size_t n, const orc_row_params* p, fl
     }
     free(counts);
   }
+  for (size_t j = 0; j < p->bias_len; ++j)
+    if (p->bias_values[j] == -INFINITY) adjusted[p->bias_ids[j]] = -FLT_MAX;
   return ORC_OK;
 }
 

@@ -38,7 +38,7 @@ enum {
   ORC_INVALID_MIN_P = -9,      /* BUILD-DEFINED: min_p outside [0, 1] */
   ORC_INVALID_PENALTY = -10,   /* BUILD-DEFINED: repetition <= 0 or non-finite penalty */
   ORC_INVALID_HISTORY = -11,   /* BUILD-DEFINED: history id >= vocabulary */
-  ORC_INVALID_BIAS = -12,      /* BUILD-DEFINED: bias id >= vocabulary, ids not increasing, non-finite bias */
+  ORC_INVALID_BIAS = -12,      /* BUILD-DEFINED: bias id >= vocabulary, ids not increasing, NaN or +inf bias */
   ORC_TOKEN_OUT_OF_RANGE = -13,/* speculative: drafted token outside the row */
   ORC_PROBABILITIES = -14,     /* speculative: invalid probability vectors */
 };

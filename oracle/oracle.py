@@ -311,3 +311,62 @@ def spec_verify_row(target, draft, draft_tokens, temperature, accept_u, resample
     st = lib().orc_spec_verify_row(_p(t), _p(d), _sz(V), _sz(k), _p(toks), _dbl(temperature), _p(ua), _p(ur),
                                    _dbl(bonus_u), _p(out), ctypes.byref(cnt), ctypes.byref(acc))
     return st, out, cnt.value, acc.value
+
+
+# ---- point-mass verify walk (A9) ---------------------------------------------
+def accept_and_roll_back(draft, pick_at):
+    """The acceptance walk of speculative decoding
+    (crates/core/engine/src/speculative.rs:318-347): rows 0..=len(draft) are
+    settled in order by pick_at(i) -> (token, stop); a row's token is
+    emitted, counts as accepted when it equals draft[i], and the walk ends
+    after a stop token, after the first row that leaves the draft, or after
+    the bonus row (index len(draft)).  Returns (emitted, accepted, stopped);
+    rows after the end are never settled."""
+    emitted, accepted, stopped = [], 0, False
+    for index in range(len(draft) + 1):
+        token, stop = pick_at(index)
+        emitted.append(int(token))
+        matches = index < len(draft) and int(draft[index]) == int(token)
+        if matches:
+            accepted += 1
+        if stop:
+            stopped = True
+            break
+        if not matches:
+            break
+    return emitted, accepted, stopped
+
+
+def point_mass_verify(rows_logits, draft, uniforms, stop_ids=(), **rule):
+    """The walk over rows settled by the row sampler (sample_row with the
+    row's uniform: uniform_ahead(i), crates/app/cli/src/qwen_forward.rs:
+    283-292, as the device verify reads it).  Returns (emitted, accepted,
+    stopped, statuses of the settled rows)."""
+    stops = set(int(t) for t in stop_ids)
+    statuses = []
+
+    def pick_at(i):
+        r = sample_row(rows_logits[i], uniform=float(uniforms[i]), **rule)
+        statuses.append(r["status"])
+        return r["token"], r["token"] in stops
+
+    emitted, accepted, stopped = accept_and_roll_back(draft, pick_at)
+    return emitted, accepted, stopped, statuses
+
+
+class SplitMix64:
+    """SplitMix64 (the reference tests' Rng, speculative/tests.rs:128-149)."""
+
+    def __init__(self, seed: int):
+        self.state = seed & 0xFFFFFFFFFFFFFFFF
+
+    def next_u64(self) -> int:
+        m = 0xFFFFFFFFFFFFFFFF
+        self.state = (self.state + 0x9E3779B97F4A7C15) & m
+        z = self.state
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+        return z ^ (z >> 31)
+
+    def uniform(self) -> float:
+        return (self.next_u64() >> 11) / float(1 << 53)

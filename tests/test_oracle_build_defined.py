@@ -140,3 +140,47 @@ def test_build_defined_error_precedence(orc):
     y[5] = 3e38
     assert orc.sample_row(y, temperature=1.0, uniform=0.5, bias_ids=[5], bias_values=[3e38])["status"] == -6
     assert s(uniform=1.0) == -5
+
+
+def test_suppression_is_the_reference_f32_min_write(orc):
+    """A bias entry of -inf (suppression) must give what the reference's
+    ChatFormat::suppress gives: the logit written as f32::MIN before the
+    pick (crates/core/chat-format/src/lib.rs:771-780), here checked on rows
+    without other bias or penalties against the oracle run on the rewritten
+    row, for sampling, greedy and top-k/top-p rules; with penalties and a
+    bias on the same row, the suppressed tokens still read f32::MIN."""
+    fmin = np.float32(-3.4028234663852886e38)
+    for seed in range(30):
+        x, rng = row(300 + seed, n=96)
+        sup = np.unique(rng.integers(0, 96, int(rng.integers(1, 12))))
+        if seed % 3 == 0:
+            sup = np.unique(np.concatenate([sup, [int(np.argmax(x))]]))   # the argmax is suppressed
+        y = x.copy()
+        y[sup] = fmin
+        T = [0.0, 0.7, 1.3][seed % 3]
+        kw = dict(temperature=T, top_p=float(rng.uniform(0.5, 1.0)), top_k=int(rng.choice([0, 5, 40])),
+                  uniform=float(rng.random()))
+        a = orc.sample_row(x, bias_ids=sup, bias_values=np.full(sup.size, -np.inf, np.float32), **kw)
+        b = orc.sample_row(y, **kw)
+        for k in ("status", "token", "sampling_logprob", "kept_count"):
+            assert a[k] == b[k], (seed, k, a[k], b[k])
+        assert np.array_equal(a["adjusted"].view(np.uint32), y.view(np.uint32))
+        assert np.array_equal(a["kept"], b["kept"])
+    # every token suppressed: all logits equal f32::MIN; greedy takes ID 0
+    x, rng = row(7, n=50)
+    allids = np.arange(50)
+    g = orc.sample_row(x, temperature=0.0, bias_ids=allids, bias_values=np.full(50, -np.inf, np.float32))
+    assert g["status"] == 0 and g["token"] == 0
+    # with penalties and a bias elsewhere: suppressed ids read f32::MIN, the rest as before
+    r = orc.sample_row(x, temperature=1.0, uniform=0.3, repetition=1.3, presence=0.2, frequency=0.1,
+                       history=[3, 3, 4, 9], bias_ids=[3, 4, 20], bias_values=[-np.inf, 0.5, -np.inf])
+    q = orc.sample_row(x, temperature=1.0, uniform=0.3, repetition=1.3, presence=0.2, frequency=0.1,
+                       history=[3, 3, 4, 9], bias_ids=[4], bias_values=[0.5])
+    assert r["status"] == 0
+    assert r["adjusted"][3] == fmin and r["adjusted"][20] == fmin
+    other = np.setdiff1d(np.arange(50), [3, 20])
+    assert np.array_equal(r["adjusted"][other].view(np.uint32), q["adjusted"][other].view(np.uint32))
+    # +inf and NaN bias values stay invalid
+    for bad in (np.inf, np.nan):
+        z = orc.sample_row(x, temperature=1.0, uniform=0.3, bias_ids=[1], bias_values=[bad])
+        assert z["status"] == -12   # ORC_INVALID_BIAS

@@ -271,3 +271,92 @@ def test_law_check_sees_a_wrong_bonus_row(orc):
     the bonus drawn from target row 0 instead of row K it fails."""
     chi = law_chi(orc, 6000, 21, bonus_row=0)
     assert chi > 160.0, chi
+
+
+# ---- A9: the point-mass verify walk (accept_and_roll_back) --------------------
+TOY_VOCAB, TOY_PROMPT = 3, [0, 2, 1]   # speculative/tests.rs:14-15
+
+
+def toy_logits(context):
+    """speculative/tests.rs:37-52: the toy model's next-token row."""
+    last = context[-1] if context else 0
+    before = context[-2] if len(context) >= 2 else 0
+    n = len(context)
+    return np.array([np.float32(np.float32((last * 7 + before * 3 + t * 5 + n) % 11) * np.float32(0.37))
+                     - (np.float32(0.8) if t == last else np.float32(0.0)) for t in range(TOY_VOCAB)],
+                    dtype=np.float32)
+
+
+def toy_sample(orc, row, uniform):
+    st, tok, _ = orc.sample_categorical(row, None, 0.9, uniform)
+    assert st == 0
+    return tok
+
+
+def test_walk_stops_at_a_stop_token(orc):
+    """speculative/tests.rs:608-631: picks 1, 2, 0 over draft [1, 2, 2] with
+    token 2 stopping: emitted [1, 2], 2 accepted, stopped, and the third row
+    is never settled."""
+    picks = iter([1, 2, 0])
+    settled = []
+
+    def pick_at(i):
+        settled.append(i)
+        t = next(picks)
+        return t, t == 2
+
+    emitted, accepted, stopped = orc.accept_and_roll_back([1, 2, 2], pick_at)
+    assert (emitted, accepted, stopped) == ([1, 2], 2, True)
+    assert settled == [0, 1]
+
+
+def test_walk_rejection_positions_and_bonus(orc):
+    for k in range(0, 5):
+        draft = list(range(10, 10 + k))
+        for diverge in range(k + 1):   # diverge == k: every draft accepted, the bonus row ends it
+            def pick_at(i, diverge=diverge, draft=draft):
+                return (draft[i] if i < diverge else 99), False
+            emitted, accepted, stopped = orc.accept_and_roll_back(draft, pick_at)
+            assert accepted == diverge and not stopped
+            assert emitted == draft[:diverge] + [99]
+
+
+def test_pre_drawn_row_uniforms_reproduce_plain_sampling(orc):
+    """speculative/tests.rs:271-321 on the oracle: speculative decoding of the
+    toy model whose rows carry pre-drawn uniforms (row i reads i draws ahead,
+    one draw committed per settled row) emits exactly what plain sampling
+    emits, for random drafts that reject at every position."""
+    Rng = orc.SplitMix64
+
+    def decode_plain(seed, length=24):
+        rng = Rng(seed)
+        ctx = list(TOY_PROMPT)
+        out = []
+        while len(out) < length:
+            t = toy_sample(orc, toy_logits(ctx), rng.uniform())
+            out.append(t)
+            ctx.append(t)
+        return out
+
+    for seed in range(20):
+        expected = decode_plain(seed)
+        stream = Rng(seed)
+        draft_rng = Rng(seed ^ 0xABCD)
+        out = [toy_sample(orc, toy_logits(TOY_PROMPT), stream.uniform())]
+        rejected = 0
+        while len(out) < 24:
+            limit = 24 - len(out) - 1
+            k = min(draft_rng.next_u64() % 4, limit)
+            proposal = [int((draft_rng.next_u64() % 1024) % TOY_VOCAB) for _ in range(k)]
+            ctx = TOY_PROMPT + out
+            rows = [toy_logits(ctx + proposal[:i]) for i in range(k + 1)]
+            peek = Rng(stream.state)
+            ahead = [peek.uniform() for _ in range(k + 1)]
+            emitted, accepted, stopped, _ = orc.point_mass_verify(rows, proposal, ahead, temperature=0.9)
+            for _ in emitted:
+                stream.uniform()   # one committed draw per settled row
+            rejected += int(0 < accepted < k)
+            out.extend(emitted)
+        assert out == expected, f"seed {seed}"
+        if seed == 0:
+            assert rejected > 0

@@ -283,3 +283,45 @@ def test_keepall_rows_with_history_and_bias(torch_mod, sampler, orc):
     b.bias_offsets = np.array(offs, dtype=np.uint32)
     b.bias_values = (3.0 * (s.uniform(len(b.bias_ids)) - 0.5)).astype(np.float32)
     check(torch_mod, sampler, orc, b)
+
+
+def test_suppressed_tokens(torch_mod, sampler, orc):
+    """A7: the checkpoint's suppress list (ChatFormat::suppress,
+    crates/core/chat-format/src/lib.rs:761-780), given to the device as -inf
+    bias entries merged with the row's own bias (with_suppression): the
+    suppressed tokens' adjusted logits are f32::MIN and the picks match the
+    oracle's.  Rows cover greedy with its argmax suppressed, top-k / top-p /
+    min-p rules, penalties, a row whose peaks are all suppressed, and
+    config-3-style masked bf16 rows."""
+    from metallix_amd import synth
+    from metallix_amd.sampler import with_suppression
+
+    b = synth.config2(rows=24)
+    b.name = "suppress-cfg2"
+    rng = np.random.default_rng(761)
+    sup = np.unique(np.concatenate([rng.integers(0, b.vocab, 40), np.argmax(b.logits, axis=1)[:6]]))
+    b.temperature[::5] = 0.0                      # greedy rows: several argmaxes are suppressed
+    own_ids = [np.unique(rng.integers(0, b.vocab, 8)).astype(np.uint32) for _ in range(b.rows)]
+    own_off = np.concatenate([[0], np.cumsum([len(i) for i in own_ids])]).astype(np.uint32)
+    own_val = (rng.standard_normal(int(own_off[-1])) * 2.0).astype(np.float32)
+    b.bias_offsets, b.bias_ids, b.bias_values = with_suppression(b.rows, sup, own_off, np.concatenate(own_ids),
+                                                                 own_val)
+    gpu, ref = check(torch_mod, sampler, orc, b)
+    assert (gpu["status"] == 0).all()
+    assert (gpu["adjusted"][:, sup] == np.float32(-3.4028234663852886e38)).all()
+    assert not np.isin(gpu["token"], sup).any()
+
+    # every peak of one row suppressed, at T 1 over a small vocabulary
+    x = np.full((4, 512), -2.0, dtype=np.float32)
+    x[:, 100:110] = 9.0
+    c = synth.Batch(name="suppress-peaks", logits=x, temperature=np.ones(4), uniform=rng.random(4),
+                    top_k=np.array([0, 5, 0, 1], dtype=np.uint32), top_p=np.array([0.9, 1.0, 1.0, 1.0]))
+    c.bias_offsets, c.bias_ids, c.bias_values = with_suppression(4, np.arange(100, 110))
+    gpu, ref = check(torch_mod, sampler, orc, c)
+    assert not np.isin(gpu["token"], np.arange(100, 110)).any()
+
+    # masked bf16 rows (the grammar path) with suppression
+    d = synth.config3(rows=8)
+    d.name = "suppress-masked"
+    d.bias_offsets, d.bias_ids, d.bias_values = with_suppression(d.rows, rng.integers(0, d.vocab, 300))
+    check(torch_mod, sampler, orc, d)

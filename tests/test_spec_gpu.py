@@ -127,3 +127,79 @@ def test_error_matrix(torch_mod, sampler, orc):
     d["bonus_u"][7] = -0.5                       # invalid bonus uniform
     d["accept_u"][7, :] = 0.0
     run(torch_mod, sampler, orc, d, "errors")
+
+
+# ---- A9: point-mass verify on device picks -------------------------------------
+def test_point_mass_verify_toy_model_reproduces_plain_sampling(torch_mod, sampler, orc):
+    """speculative/tests.rs:271-321 with device picks: the toy model's rows
+    (V = 3) are verified by one mxs_sample call per step (row i carries the
+    uniform i draws ahead), and the emitted sequence equals plain sampling of
+    the oracle with the same stream, for random drafts."""
+    import test_oracle_spec as toy
+
+    torch = torch_mod
+    Rng = orc.SplitMix64
+    for seed in range(6):
+        rng = Rng(seed)
+        ctx, expected = list(toy.TOY_PROMPT), []
+        while len(expected) < 24:
+            t = toy.toy_sample(orc, toy.toy_logits(ctx), rng.uniform())
+            expected.append(t)
+            ctx.append(t)
+        stream = Rng(seed)
+        draft_rng = Rng(seed ^ 0xABCD)
+        out = [toy.toy_sample(orc, toy.toy_logits(toy.TOY_PROMPT), stream.uniform())]
+        while len(out) < 24:
+            limit = 24 - len(out) - 1
+            k = int(min(draft_rng.next_u64() % 4, limit))
+            proposal = [int((draft_rng.next_u64() % 1024) % toy.TOY_VOCAB) for _ in range(k)]
+            rows = np.stack([toy.toy_logits(toy.TOY_PROMPT + out + proposal[:i]) for i in range(k + 1)])
+            peek = Rng(stream.state)
+            ahead = np.array([peek.uniform() for _ in range(k + 1)])
+            logits = torch.zeros((k + 1, 4), dtype=torch.float32, device="cuda")
+            logits[:, :3] = torch.from_numpy(rows).to("cuda")
+            res = sampler.verify_point_mass(
+                logits, np.array([proposal], dtype=np.int64).reshape(1, k),
+                torch.full((k + 1,), 0.9, dtype=torch.float64, device="cuda"),
+                torch.from_numpy(ahead).to("cuda"), vocab=3)[0]
+            assert res["status"] == 0
+            for _ in res["emitted"]:
+                stream.uniform()
+            out.extend(res["emitted"])
+        assert out == expected, f"seed {seed}"
+
+
+def test_point_mass_verify_matches_the_oracle_walk(torch_mod, sampler, orc):
+    """Sequences of 5 scored positions at V = 151936 under config 2's rules:
+    drafts follow the oracle's picks for a random number of positions and
+    then leave them (or not at all: the bonus row), some with a stop token
+    inside the draft; the device walk's emitted tokens, acceptance count and
+    stop flag equal the oracle walk's."""
+    from metallix_amd import synth
+
+    torch = torch_mod
+    S, K = 12, 4
+    b = synth.config2(rows=S * (K + 1))
+    rng = np.random.default_rng(347)
+    ref_tok = orc.sample_batch(b)["token"].reshape(S, K + 1)
+    draft = np.zeros((S, K), dtype=np.int64)
+    stop_ids = set()
+    for s in range(S):
+        d = int(rng.integers(0, K + 1))      # positions that follow the picks
+        draft[s, :d] = ref_tok[s, :d]
+        if d < K:
+            draft[s, d:] = (ref_tok[s, d:K] + 1 + rng.integers(0, 100, K - d)) % b.vocab
+        if s % 4 == 3 and d > 1:
+            stop_ids.add(int(ref_tok[s, 1]))
+    from helpers import to_device
+
+    logits, kw = to_device(torch, b)
+    temp, uni = kw.pop("temperature"), kw.pop("uniform")
+    got = sampler.verify_point_mass(logits, draft, temp, uni, stop_ids=stop_ids, **kw)
+    for s in range(S):
+        # the oracle walk over the oracle's per-row picks (same rows, rules and uniforms)
+        picks = ref_tok[s]
+        e_ref, a_ref, st_ref = orc.accept_and_roll_back(draft[s], lambda i: (picks[i], int(picks[i]) in stop_ids))
+        assert got[s]["status"] == 0, (s, got[s])
+        assert got[s]["emitted"] == e_ref, (s, got[s], e_ref)
+        assert got[s]["accepted"] == a_ref and got[s]["stopped"] == st_ref
