@@ -182,6 +182,22 @@ int mxs_sync(mxs_ctx* ctx);
  * the row finisher at slot MXS_DEBUG_TIMING_SLOTS - 1.  NULL disables. */
 #define MXS_DEBUG_TIMING_SLOTS 65
 int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer);
+/* Diagnostics (no reference counterpart): when `device_buffer` (int32
+ * [rows]) is non-null, mxs_sample writes the finisher path each row took. */
+enum {
+  MXS_PATH_ERROR = 1,          /* a row error status */
+  MXS_PATH_GREEDY = 2,         /* temperature 0: the chunks' argmax */
+  MXS_PATH_KEEPALL = 3,        /* every legal token kept: draw by segment masses */
+  MXS_PATH_KEEPALL_RACE = 4,   /* the same rows under race-v2 (no draw) */
+  MXS_PATH_SELECT = 5,         /* candidates in registers: the selection finisher */
+  MXS_PATH_WAVE = 6,           /* few candidates: one wave */
+  MXS_PATH_FAST = 7,           /* the k head or min-p set in LDS */
+  MXS_PATH_EXACT = 8,          /* working set in LDS, the nucleus certified without a sort */
+  MXS_PATH_EXACT_SORTED = 9,   /* ... the crossing inside the min-p prefix: that prefix sorted */
+  MXS_PATH_EXACT_REPLAY = 10,  /* ... an uncertain crossing: the reference's sums replayed */
+  MXS_PATH_LARGE = 11          /* working set beyond LDS: mass-weighted radix select */
+};
+int mxs_debug_set_paths(mxs_ctx* ctx, void* device_buffer);
 const char* mxs_last_error(const mxs_ctx* ctx);
 const char* mxs_status_string(int32_t status);
 int mxs_abi_version(void);

@@ -83,6 +83,7 @@ struct SampleArgs {
   uint32_t per;        // quads per thread per chunk (<= PER_MAX)
   uint32_t CH;         // tokens per chunk (multiple of 4)
   uint64_t* timing;    // optional phase timestamps (diagnostics), see mxs_debug_set_timing
+  int32_t* paths;      // optional finisher path per row (diagnostics), see mxs_debug_set_paths
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
   uint32_t epoch;      // this call's tag for Work::rowx (never 0; the row's last chunk also clears its word)
   uint32_t nodraw;     // keep-all rows skip the inverse-CDF draw (race-v2 calls)
@@ -131,6 +132,7 @@ struct alignas(16) ChunkSmem {
   WavePart wp[NW];
   WavePart wq[NW];
   uint32_t xkey;                       // min-p rows: the exchanged row-maximum lower bound
+  double etab[128];                    // exp_neg's tables (f64 weights of keep-all and top-p-only rows)
 };
 // The row finisher runs 1024 threads: its candidate phase keeps at most
 // CCAP / FT = 8 candidates per thread; sets of at most 256 E tokens are
@@ -381,8 +383,15 @@ struct FinCtx {
   uint32_t* kbits;
   uint32_t nwords;
   uint64_t* timing;    // phase timestamps (diagnostics), null when off
+  int32_t* paths;      // finisher path per row (diagnostics), null when off
   const double* etab;  // exp_neg's tables in LDS
 };
+
+// The finisher path a row took (MXS_PATH_*, diagnostics); a later call on
+// the same row overwrites an earlier one.
+__device__ __forceinline__ void fpath(const FinCtx& X, int32_t p) {
+  if (X.paths && threadIdx.x == 0) X.paths[X.row] = p;
+}
 
 // Finisher phase timestamp k (slot MAXC of the row's timing record).
 __device__ __forceinline__ void fstamp(const FinCtx& X, uint32_t k) {
@@ -435,7 +444,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
   const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
-  auto weight = [&](float l) { return exp_neg(((double)l - X.M) / c.T); };
+  auto weight = [&](float l) { return exp_neg_t(((double)l - X.M) / c.T, X.etab, X.etab + 64); };
   bool uncert = false;
   double wpart = 0.0, wmin = INFINITY;
   for (uint32_t j = tid; j < n; j += FT) {
@@ -450,6 +459,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
   wmin = -block_max<double>(-wmin, F.red_d);
   double total = X.total, total_err = X.total_err;
   if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
+  fstamp(X, 4);
 
   uint32_t tau = 0, id_cut = NONE;
   bool cut = false;
@@ -573,6 +583,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
     }
   }
 
+  fstamp(X, 5);
   // kept = member, inside the cut, and (unless E is the min-p set already)
   // at or above ln(min_p); the draw walks kept tokens in ID order.
   const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
@@ -592,7 +603,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
     double s;
     const bool k = kept(l, cand_id(X, F, j), &s);
     if (apply_minp && fabs(s - X.L) < X.Lclose) close = 1;
-    if (k) { kpart += exp_neg(s); ++kn; if (!isfinite(s)) bad = 1; }
+    if (k) { kpart += exp_neg_t(s, X.etab, X.etab + 64); ++kn; if (!isfinite(s)) bad = 1; }
   }
   if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
   if (block_max<uint32_t>(close, F.red_u)) uncert = true;
@@ -602,6 +613,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
   const double derr = sum_bound(S, nkept + 64u, 8.0);
   if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
   __syncthreads();
+  fstamp(X, 6);
   double run = 0.0;
   for (uint32_t base = 0; base < n; base += FT) {
     const uint32_t j = base + tid;
@@ -610,7 +622,7 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
     if (j < n) {
       const float l = cand_l(X, F, j);
       id = cand_id(X, F, j);
-      if (kept(l, id, &s)) w = exp_neg(s);
+      if (kept(l, id, &s)) w = exp_neg_t(s, X.etab, X.etab + 64);
     }
     double tot;
     const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
@@ -669,7 +681,7 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
   uint32_t pn = 0, close = 0;
   for (uint32_t t = tid; t < ne; t += FT) {
     const double s = ((double)el(t) - X.M) / c.T;
-    const double w = exp_neg(s);
+    const double w = exp_neg_t(s, X.etab, X.etab + 64);
     F.u.e.ew[t] = w;
     epart += w;
     wmin = fmin(wmin, w);
@@ -709,6 +721,7 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
   }
   if (theta_set && !(psum + sum_bound(psum, np_, 8.0) < theta - theta_err)) {
     // The crossing lies inside P: sort P and find the first prefix reaching theta.
+    fpath(X, MXS_PATH_EXACT_SORTED);
     if (tid == 0) F.s_u[8] = 0u;
     __syncthreads();
     for (uint32_t t = tid; t < ne; t += FT) {
@@ -756,6 +769,7 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
   }
   if (replay) {
     // Sort all of E and replay the reference's sequential f64 sums.
+    fpath(X, MXS_PATH_EXACT_REPLAY);
     for (uint32_t t = tid; t < ne; t += FT)
       F.u.e.skey[t] = ((unsigned long long)okey(el(t)) << 32) | (unsigned long long)(0xffffffffu - t);
     __syncthreads();
@@ -2442,14 +2456,16 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
   X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
-  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.etab = F.etab;
+  X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.paths = A.paths; X.etab = F.etab;
   if (err) {
+    fpath(X, MXS_PATH_ERROR);
     write_result(X, err, -1, 0.0, 0u);
     if (kbits)
       for (uint32_t q = tid; q < nwords; q += FT) kbits[q] = 0u;
     return;
   }
   if (mode == M_GREEDY) {
+    fpath(X, MXS_PATH_GREEDY);
     write_result(X, 0, (int32_t)bi, 0.0, 1u);
     if (kbits)
       for (uint32_t q = tid; q < nwords; q += FT) kbits[q] = (q == (bi >> 5)) ? (1u << (bi & 31u)) : 0u;
@@ -2464,10 +2480,12 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       if (F.st[q].nlegal && F.st[q].minkey < mink) mink = F.st[q].minkey;
     if (!isfinite(((double)okey_value(mink) - M) / c.T)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
     if (A.nodraw) {   // race-v2: the kept set is every legal token; the race kernel picks
+      fpath(X, MXS_PATH_KEEPALL_RACE);
       write_result(X, 0, -1, 0.0, nlegal);
       keepall_bits(A, row, kbits, nwords, V);
       return;
     }
+    fpath(X, MXS_PATH_KEEPALL);
     const uint32_t segs_per_chunk = A.per * NW;   // the chunk kernel's 256-token (slice, wave) segments
     const uint32_t nseg = C * segs_per_chunk;
     double part = 0.0;
@@ -2539,7 +2557,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
           float l;
           bool lg;
           rederive_token<In>(A, c, row, id, scnt[lane() * 4u + (uint32_t)e], &l, &lg);
-          if (lg) { sh[e] = ((double)l - M) / c.T; wl[e] = exp_neg(sh[e]); }
+          if (lg) { sh[e] = ((double)l - M) / c.T; wl[e] = exp_neg_t(sh[e], F.etab, F.etab + 64); }
         }
         lsum += wl[e];
       }
@@ -2621,6 +2639,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   // rows whose candidates all sit in the register slots: the selection finisher
   if ((mode == M_TOPK || mode == M_MINP) && ncand > 0u && C <= (uint32_t)FW && F.hdr.qmax <= cov) {
     if (finish_sel(X, F, P, sq, sj)) {
+      fpath(X, MXS_PATH_SELECT);
       stamp(A, row, MAXC, 2);
       return;
     }
@@ -2673,12 +2692,14 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     }
     lds_barrier();
     if (F.s_u[15]) {
+      fpath(X, MXS_PATH_WAVE);
       stamp(A, row, MAXC, 2);
       return;
     }
     lds_barrier();   // wave 0's LDS scratch is reused below
   }
   if (mode != M_KEEPALL && finish_fast(X, F)) {
+    fpath(X, MXS_PATH_FAST);
     stamp(A, row, MAXC, 2);
     return;
   }
@@ -2774,8 +2795,10 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   mp_close = block_max<uint32_t>(mp_close ? 1u : 0u, F.red_u) != 0u;
   stamp(A, row, MAXC, 3);
   if (ne <= (uint32_t)ECAP && X.lds_c) {
+    fpath(X, MXS_PATH_EXACT);
     finish_exact(X, F, ne, mp_close);
   } else {
+    fpath(X, MXS_PATH_LARGE);
     finish_large(X, F, ne);
     if (mp_close && tid == 0 && A.o.status[row] == 0) A.o.status[row] = MXS_ROW_UNCERTIFIED;
   }
@@ -3349,6 +3372,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
 #pragma unroll
     for (int r = 0; r < MCAP / NT; ++r) mreg[r] = mp[min((uint32_t)r * NT + tid, nmw - 1u)];
   }
+  const double etab_v = tid < 128u ? (tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u]) : 0.0;
 #pragma unroll
   for (int i = 1; i < PER_MAX; ++i) {
     const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
@@ -3358,6 +3382,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
 #pragma unroll
     for (int r = 0; r < HCAP / NT; ++r) S.hids[r * NT + tid] = hreg[r];
   }
+  if (tid < 128u) S.etab[tid] = etab_v;
   if (stage_b) {
 #pragma unroll
     for (int r = 0; r < BCAP / NT; ++r) { S.bids[r * NT + tid] = breg[r]; S.bvals[r * NT + tid] = vreg[r]; }
@@ -3745,7 +3770,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
           double sw = 0.0;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            sw += ((qb >> e) & 1u) ? exp_neg(((double)lv[i][e] - md) * invT) : 0.0;
+            sw += ((qb >> e) & 1u) ? exp_neg_t(((double)lv[i][e] - md) * invT, S.etab, S.etab + 64) : 0.0;
           m0 += sw;
           if (mode == M_KEEPALL) {
             const double ws = wave_sum_f64(sw);
@@ -3977,6 +4002,7 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   A.o = *o;
   A.w = ctx->work;
   A.timing = ctx->timing;
+  A.paths = ctx->paths;
   if (++ctx->epoch == 0u) ctx->epoch = 1u;   // 0 is the zeroed scratch's tag
   A.epoch = ctx->epoch;
   A.nodraw = nodraw ? 1u : 0u;
@@ -4144,6 +4170,12 @@ int mxs_destroy(mxs_ctx* ctx) {
 int mxs_set_stream(mxs_ctx* ctx, void* stream) {
   if (!ctx) return MXS_EINVAL;
   ctx->stream = (hipStream_t)stream;
+  return MXS_OK;
+}
+
+int mxs_debug_set_paths(mxs_ctx* ctx, void* device_buffer) {
+  if (!ctx) return MXS_EINVAL;
+  ctx->paths = (int32_t*)device_buffer;
   return MXS_OK;
 }
 

@@ -66,6 +66,7 @@ struct mxs_ctx {
   float* d_zero_f32 = nullptr;
   uint32_t* d_mask_ones = nullptr;
   uint64_t* timing = nullptr;
+  int32_t* paths = nullptr;             // finisher path per row (diagnostics)
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
   // mxs_logsoftmax_topn: per-chunk results
   void* topn_scratch = nullptr;

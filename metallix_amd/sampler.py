@@ -84,6 +84,7 @@ PROTOTYPES = {
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mxs_sync": (ctypes.c_int, [_vp]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
+    "mxs_debug_set_paths": (ctypes.c_int, [_vp, _vp]),
     "mxs_last_error": (ctypes.c_char_p, [_vp]),
 }
 

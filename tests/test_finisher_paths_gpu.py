@@ -1,0 +1,148 @@
+"""Every finisher path of mxs_sample, reached at V = 151936 and checked
+against the oracle.  mxs_debug_set_paths records the path each row took
+(MXS_PATH_* of include/mx_sampler.h); one batch holds a row built for each
+path, and the test asserts both the path and parity (statuses, adjusted
+logits, kept sets and tokens bit-exact, logprobs within 1e-5).  The
+reference's counterparts are the row-level rules the paths implement:
+greedy_token (chat_generation.rs:2213-2231), nucleus_mask
+(qwen_forward.rs:474-549) and sample_categorical (sampling.rs:56-158)."""
+import sys
+
+import numpy as np
+import pytest
+
+from helpers import compare, run_gpu, to_device
+
+pytestmark = pytest.mark.gpu
+
+V = 151936
+PATHS = {"ERROR": 1, "GREEDY": 2, "KEEPALL": 3, "KEEPALL_RACE": 4, "SELECT": 5, "WAVE": 6, "FAST": 7,
+         "EXACT": 8, "EXACT_SORTED": 9, "EXACT_REPLAY": 10, "LARGE": 11}
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+@pytest.fixture(scope="module")
+def sampler(torch_mod):
+    from metallix_amd import Sampler
+
+    s = Sampler(max_rows=64, max_vocab=V)
+    yield s
+    s.close()
+
+
+def path_batch():
+    """One row per path: (expected path, logits, T, top_k, top_p, min_p)."""
+    from metallix_amd.synth import Batch
+
+    rng = np.random.default_rng(2365)
+    rows = []
+
+    def noise(scale=1.0, shift=0.0):
+        return (rng.standard_normal(V) * scale + shift).astype(np.float32)
+
+    def crowd(n, base=5.0, step=1e-6, floor=-40.0):
+        """n near-equal logits base - i step at random ids, the rest at floor."""
+        x = np.full(V, floor, dtype=np.float32)
+        ids = rng.choice(V, n, replace=False)
+        x[ids] = (base - step * np.arange(n)).astype(np.float32)
+        return x
+
+    peaked = noise(2.0)
+    peaked[rng.choice(V, 20, replace=False)] += 8.0
+    rows.append(("ERROR", peaked.copy(), -1.0, 20, 0.9, 0.0))          # invalid temperature
+    rows.append(("GREEDY", peaked.copy(), 0.0, 0, 1.0, 0.0))
+    rows.append(("KEEPALL", noise(2.0), 0.9, 0, 1.0, 0.0))
+    rows.append(("SELECT", peaked.copy(), 0.7, 20, 0.8, 0.0))
+    # a grammar-masked row (mask below) with 60 legal tokens, top-p only
+    rows.append(("WAVE", noise(1.0), 1.0, 0, 0.9, 0.0))
+    rows.append(("FAST", crowd(3000, step=1e-3), 1.0, 0, 1.0, 0.01))   # a min-p set of 3000
+    def groups(*spec, floor=-40.0):
+        """(count, value) groups of equal logits at random ids, the rest at floor."""
+        x = np.full(V, floor, dtype=np.float32)
+        ids = rng.choice(V, sum(n for n, _ in spec), replace=False)
+        at = 0
+        for n, v in spec:
+            x[ids[at:at + n]] = np.float32(v)
+            at += n
+        return x
+
+    # 300 logits at 5.0 over 7000 at 4.9, k 500: every chunk emits more
+    # candidates than its register slots, and the k-th key is one of 7000
+    # equal keys (the LDS select gives up; the radix select finds the head)
+    two = groups((300, 5.0), (7000, 4.9))
+    rows.append(("EXACT", two.copy(), 1.0, 500, 1.0, 0.0))
+    rows.append(("EXACT_SORTED", two.copy(), 1.0, 500, 0.5, 0.0))
+    # 7000 equal logits, a head of 1200 and top_p 0.5: the nucleus ends
+    # exactly on a token boundary, which only the reference's own
+    # sequential sums settle
+    rows.append(("EXACT_REPLAY", groups((7000, 5.0)), 1.0, 1200, 0.5, 0.0))
+    rows.append(("LARGE", crowd(10000, step=1e-4), 1.0, 0, 0.7, 0.0))
+    names = [r[0] for r in rows]
+    words = (V + 31) // 32
+    mask = np.full((len(rows), words), 0xFFFFFFFF, dtype=np.uint32)
+    w = names.index("WAVE")
+    mask[w] = 0
+    legal = rng.choice(V, 60, replace=False)
+    np.bitwise_or.at(mask[w], legal // 32, (np.uint32(1) << (legal % 32).astype(np.uint32)))
+    b = Batch(name="finisher-paths", logits=np.stack([r[1] for r in rows]),
+              temperature=np.array([r[2] for r in rows]), uniform=rng.random(len(rows)),
+              top_k=np.array([r[3] for r in rows], dtype=np.uint32), top_p=np.array([r[4] for r in rows]),
+              min_p=np.array([r[5] for r in rows]), mask_words=mask, tokenizer_vocab=V)
+    return names, b
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_every_finisher_path(torch_mod, sampler, orc):
+    torch = torch_mod
+    names, b = path_batch()
+    say(f"case finisher-paths: rows {b.rows} vocab {b.vocab}")
+    buf = torch.zeros(b.rows, dtype=torch.int32, device="cuda")
+    sampler.lib.mxs_debug_set_paths(sampler.ctx, buf.data_ptr())
+    try:
+        gpu = run_gpu(torch, sampler, b)
+    finally:
+        sampler.lib.mxs_debug_set_paths(sampler.ctx, None)
+    got = buf.cpu().numpy()
+    inv = {v: k for k, v in PATHS.items()}
+    wrong = [(n, inv.get(int(p), int(p))) for n, p in zip(names, got) if PATHS[n] != int(p)]
+    assert not wrong, f"rows took other paths: {wrong}"
+    ref = orc.sample_batch(b, debug=True)
+    compare(b, gpu, ref, allow_uncertified=1)
+    # an uncertified row may only be the large-set row (f32 chunk masses)
+    unc = [names[r] for r in np.nonzero(gpu["status"] == 1)[0]]
+    assert set(unc) <= {"LARGE"}, unc
+
+    # the keep-all row under race-v2: the finisher keeps every token, no draw
+    from test_race_gpu import oracle_race, race_keys
+
+    keys = race_keys(b.rows, 3)
+    logits, kw = to_device(torch, b)
+    dev = logits.device
+    race = (torch.from_numpy(keys[0].view(np.int64)).to(dev), torch.from_numpy(keys[1].view(np.int32)).to(dev),
+            torch.from_numpy(keys[2].view(np.int32)).to(dev))
+    sampler.lib.mxs_debug_set_paths(sampler.ctx, buf.data_ptr())
+    try:
+        out = sampler.sample(logits, race=race, **kw)
+        torch.cuda.synchronize()
+    finally:
+        sampler.lib.mxs_debug_set_paths(sampler.ctx, None)
+    got = buf.cpu().numpy()
+    assert got[names.index("KEEPALL")] == PATHS["KEEPALL_RACE"]
+    rref = oracle_race(orc, b, keys)
+    tok = out.token.cpu().numpy()
+    st = out.status.cpu().numpy()
+    for r in range(b.rows):
+        if st[r] == 0 and names[r] != "LARGE":
+            assert tok[r] == rref["token"][r], (names[r], tok[r], rref["token"][r])
