@@ -77,6 +77,7 @@ struct SpecArgs {
 };
 
 struct SpecSmem {
+  double etab[128];                   // exp_neg's tables
   SpecStat st[SMAXC];
   SpecPos ps[SPEC_KMAX + 1];
   uint32_t red_u[4][NW];
@@ -127,6 +128,7 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
   const bool tok_T = temperature_ok(T);
   const double invT = tok_T ? 1.0 / T : 0.0;
 
+  if (tid < 128u) S.etab[tid] = tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u];
   float tv[SP][4], dv[SP][4];
 #pragma unroll
   for (int i = 0; i < SP; ++i) {
@@ -182,8 +184,8 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     for (int i = 0; i < SP; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pt += exp_neg(((double)tv[i][e] - mtd) * invT);
-        if (has_draft) pd += exp_neg(((double)dv[i][e] - mdd) * invT);
+        pt += exp_neg_t(((double)tv[i][e] - mtd) * invT, S.etab, S.etab + 64);
+        if (has_draft) pd += exp_neg_t(((double)dv[i][e] - mdd) * invT, S.etab, S.etab + 64);
       }
     pt = wave_sum_f64(pt);
     pd = wave_sum_f64(pd);
@@ -319,10 +321,11 @@ __device__ Plan row_plan(const SpecPos* ps, uint32_t K) {
 // Weight of token i in the distribution drawn at the plan's position:
 // the residual max(0, t_i / sum t - q_i / sum q), or the target weight t_i
 // for the bonus draw.
-__device__ __forceinline__ double draw_weight(bool bonus, float t, float q, const SpecPos& P, double invT) {
-  const double wt = exp_neg(((double)t - (double)P.mt) * invT);
+__device__ __forceinline__ double draw_weight(bool bonus, float t, float q, const SpecPos& P, double invT,
+                                              const double* etab) {
+  const double wt = exp_neg_t(((double)t - (double)P.mt) * invT, etab, etab + 64);
   if (bonus) return wt;
-  const double wq = exp_neg(((double)q - (double)P.md) * invT);
+  const double wq = exp_neg_t(((double)q - (double)P.md) * invT, etab, etab + 64);
   return fmax(wt / P.tt - wq / P.td, 0.0);
 }
 
@@ -338,6 +341,7 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= A.rows) return;
   const uint32_t K = A.K, V = A.V;
+  if (tid < 128u) S.etab[tid] = tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u];
   for (uint32_t j = tid; j <= K; j += NT) {
     const SpecPos* src = &A.pos[row * (SPEC_KMAX + 1) + j];
     SpecPos P;
@@ -374,7 +378,7 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
         if (!bonus) load_quad<ALIGNED>(dp, es, c1, q);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (e0 + (uint32_t)e < c1) s += draw_weight(bonus, t[e], q[e], P, invT);
+          if (e0 + (uint32_t)e < c1) s += draw_weight(bonus, t[e], q[e], P, invT, S.etab);
       }
       const double ws = wave_sum_f64(s);
       if (lane() == 0) st_dev(&A.seg[((uint64_t)row * SMAXC + chunk) * SSEG + i * NW + wave()], ws);
@@ -468,7 +472,7 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const uint32_t id = id0 + (uint32_t)e;
-        wl[e] = id < qc1 ? draw_weight(bonus, tp[id], bonus ? 0.0f : dp[id], P, invT) : 0.0;
+        wl[e] = id < qc1 ? draw_weight(bonus, tp[id], bonus ? 0.0f : dp[id], P, invT, S.etab) : 0.0;
         lsum += wl[e];
       }
       double inc = lsum;
