@@ -35,7 +35,7 @@ METRIC = "sampled rows/s at B=64,V=151936 fp32; achieved HBM GB/s vs MI355X peak
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 300 << 20
 OUT_BYTES_PER_ROW = 4 + 8 + 4 + 4       # token, sampling_logprob, status, kept_count
-TOPN = 20
+TOPN = 28                               # the top 20 logprobs plus the reference's 8 spares (chat_turn.rs:506-563)
 
 
 def nbytes(t) -> int:
@@ -140,7 +140,8 @@ def build_workload(cfg, torch, Sampler, synth, to_device):
         def topn(i):
             res["topn"] = s.logsoftmax_topn(bufs[i % nb], TOPN, vocab=b.vocab)
 
-        calls.append(Call("mxs_logsoftmax_topn", "topn_kernel", topn, topn_bytes(logits, b.vocab, TOPN)))
+        calls.append(Call("mxs_logsoftmax_topn", "topn_kernel + topn_merge_kernel", topn,
+                          topn_bytes(logits, b.vocab, TOPN)))
 
     def check():
         st = launch.out.status.cpu().numpy()
