@@ -54,6 +54,10 @@ constexpr int BCAP = 2 * NT;              // bias entries staged in LDS
 // mask words of one chunk (CHUNK_MAX / 32 + 2), rounded up to whole
 // 1024-word rounds of the LDS staging, which writes every lane's slot
 constexpr int MCAP = ((CHUNK_MAX / 32 + 2 + NT - 1) / NT) * NT;
+#ifndef MXS_LA
+#define MXS_LA 3
+#endif
+constexpr int LA = MXS_LA;                // slices in flight ahead of pass 1 (lean chunk body)
 static_assert(HCAP % NT == 0 && BCAP % NT == 0 && MCAP % NT == 0,
               "LDS staging copies whole 1024-entry rounds");
 static_assert(HB == NT, "one histogram bin per thread");
@@ -2437,7 +2441,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     const double ms = P.v.mass, me = P.v.mass_err;
     const uint32_t mkey = wave_max_u32(nlg ? mxk : 0u);
     const double Mw = (double)okey_value(mkey);
-    const double cs = nlg ? exp_neg(((double)okey_value(mxk) - Mw) * invT) : 0.0;
+    const double cs = nlg ? exp_neg_p(((double)okey_value(mxk) - Mw) * invT) : 0.0;
     const double t = wave_sum_f64(ms * cs), te = wave_sum_f64(me * cs);
     const uint32_t nl = wave_sum_u32(nlg);
     if (qa) F.cscale[q] = cs;
@@ -2834,7 +2838,7 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 //     its pass 1 ends, so the min-p threshold sees the other chunks' maxima
 //     as early as possible.
 template <typename In, uint32_t MODE, bool HIST>
-__device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
+__device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                            const uint32_t row, const uint32_t chunk, const uint32_t c0,
                                            const uint32_t c1, const uint32_t hn) {
   ChunkSmem& S = chunk_smem(U);
@@ -2858,18 +2862,31 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
 #pragma unroll
     for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
   }
+  // The slices stream through a window of LA loads in flight per wave: slice
+  // i + LA is issued as slice i is processed.  A wave issues in order, and a
+  // load waits at issue while the CU's memory pipeline is full, so issuing
+  // every slice up front would hold each wave at its last load until most
+  // of the chunk had arrived, with pass 1 only starting after it.
   typename Quad<In>::Raw raw[PER_MAX];
-  {
-    const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
+  const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
+  auto issue = [&](int i) {
+    const uint32_t e0 = c0k + (uint32_t)i * SLICE + tid * 4u;
+    raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0k));
+  };
 #pragma unroll
-    for (int i = 0; i < PER_MAX; ++i) {
-      const uint32_t e0 = c0k + (uint32_t)i * SLICE + tid * 4u;
-      raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0k));
-    }
-  }
+  for (int i = 0; i < LA; ++i)
+    if (i < (int)A.per) issue(i);
   const uint32_t clen = c1 - c0;
   const double invT = MODE == M_GREEDY ? 0.0 : 1.0 / c.T;
   uint32_t my_flags = 0;
+  // T ln(min_p) for the min-p threshold, computed while the loads are in
+  // flight (the empty asm keeps the f64 logarithm here instead of on the
+  // path after the chunk reduction)
+  double tlnmp = 0.0;
+  if constexpr (MODE == M_MINP) {
+    tlnmp = c.T * log(c.min_p);
+    __asm__ volatile("" : "+v"(tlnmp));
+  }
 
   // ---- the chunk's history count table (u16 per token) -------------------
   if constexpr (HIST) {
@@ -2912,6 +2929,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
 #pragma unroll
   for (int i = 0; i < PER_MAX; ++i) {
     qm[i] = -INFINITY;
+    if (i + LA < PER_MAX && i + LA < (int)A.per) issue(i + LA);
     if (i < (int)A.per) {
       const uint32_t sbase = c0 + (uint32_t)i * SLICE;
       const uint32_t e0 = sbase + tid * 4u;
@@ -3002,13 +3020,17 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
 
   // ---- chunk statistics: one block reduction ------------------------------
   const uint32_t nleg = clen;   // no mask: every token of the chunk is legal
+  unsigned long long xprev = 0ull;   // min-p rows: the exchange word before this wave's update (lane 0)
   {
     const uint32_t kmax = wave_max_u32(okey(MODE == M_GREEDY ? gv : t1));
     if constexpr (MODE == M_MINP) {
-      // this wave's maximum goes to the row's exchange word right away
+      // this wave's maximum goes to the row's exchange word right away; the
+      // value it replaces (the other chunks' maxima published so far)
+      // returns while the workgroup reduces, and feeds the threshold
       if (lane() == 0)
-        __hip_atomic_fetch_max(A.w.rowx + (uint64_t)row * ROWX_STRIDE, ((unsigned long long)A.epoch << 32) | kmax, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+        xprev = __hip_atomic_fetch_max(A.w.rowx + (uint64_t)row * ROWX_STRIDE,
+                                       ((unsigned long long)A.epoch << 32) | kmax, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
     }
     const uint32_t wf = wave_or_u32(my_flags) | (nf ? (uint32_t)F_NONFINITE : 0u);
     unsigned long long arg = 0ull;
@@ -3095,12 +3117,11 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
     // logarithm's error, T * 2^-24 absolute, is not covered by a margin
     // relative to the logits when they and T ln(min_p) are near 0).
     emit = true;
-    const unsigned long long cur = __hip_atomic_load(A.w.rowx + (uint64_t)row * ROWX_STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    uint32_t xkey = maxkey;
-    if ((uint32_t)(cur >> 32) == A.epoch) xkey = max(xkey, (uint32_t)cur);
-    xkey = (uint32_t)__builtin_amdgcn_readfirstlane((int)xkey);
+    const uint32_t xhi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(xprev >> 32));
+    const uint32_t xlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)xprev);
+    const uint32_t xkey = xhi == A.epoch ? max(maxkey, xlo) : maxkey;
     const float mx = okey_value(xkey);
-    const double lim_d = (double)mx + c.T * log(c.min_p);
+    const double lim_d = (double)mx + tlnmp;
     thr = (float)lim_d - (fabsf((float)lim_d) + fabsf(mx)) * 1e-5f - 1e-30f;
   }
   uint32_t cnt_i[PER_MAX];
@@ -3303,12 +3324,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
     __syncthreads();
     last = S.xkey;
     lds_barrier();   // the finisher's LDS overlays the chunk's
-    if (!last) return;
-    stamp(A, row, MAXC, 0);
-    FinLoads P;
-    fin_issue(A, row, P);
-    finish_row<In>(A, U.f, c, row, MODE, (uint64_t)row * V, invT, P);
-    stamp(A, row, MAXC, 7);
+    return last != 0u;
   }
 }
 
@@ -3319,7 +3335,7 @@ __device__ __forceinline__ void chunk_fast(const SampleArgs& A, FusedSmem& U, co
 // first slice is not passed in (it would stay live across both bodies): the
 // general body issues its slices itself.
 template <typename In>
-__device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
+__device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                               const uint32_t row, const uint32_t chunk) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
@@ -3924,12 +3940,7 @@ __device__ __forceinline__ void chunk_general(const SampleArgs& A, FusedSmem& U,
     __syncthreads();
     last = S.xkey;
     lds_barrier();   // the finisher's LDS overlays the chunk's
-    if (!last) return;
-    stamp(A, row, MAXC, 0);
-    FinLoads P;
-    fin_issue(A, row, P);
-    finish_row<In>(A, U.f, c, row, mode, rbase, invT, P);
-    stamp(A, row, MAXC, 7);
+    return last != 0u;
   }
 }
 
@@ -3956,24 +3967,35 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
                             p_boff, row);
   const uint32_t mode = chunk_mode(c, V);
+  bool last;
   {
     const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
     if (!c.err && A.masked == 0u && bn == 0u && hn <= (uint32_t)HCAP &&
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
       if (hn) {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn);
-        else chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn);
+        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn);
+        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn);
+        else last = chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn);
       } else {
-        if (mode == M_GREEDY) chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u);
-        else if (mode == M_TOPK) chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u);
-        else chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u);
+        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u);
+        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u);
+        else last = chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u);
       }
-      return;
+    } else {
+      last = chunk_general<In>(A, U, c, row, chunk);
     }
   }
-  chunk_general<In>(A, U, c, row, chunk);
+  // The row finisher: one copy for every chunk body.  The finisher runs once
+  // per row, mostly down code no other wave of the workgroup has run, so its
+  // instruction fetches miss the instruction cache; one shared copy keeps the
+  // kernel's code (and the lines every row's finisher fetches) small.
+  if (!last) return;
+  stamp(A, row, MAXC, 0);
+  FinLoads P;
+  fin_issue(A, row, P);
+  finish_row<In>(A, U.f, c, row, mode, (uint64_t)row * V, c.greedy ? 0.0 : 1.0 / c.T, P);
+  stamp(A, row, MAXC, 7);
 }
 
 }  // namespace mxs
