@@ -195,7 +195,8 @@ enum {
   MXS_PATH_EXACT = 8,          /* working set in LDS, the nucleus certified without a sort */
   MXS_PATH_EXACT_SORTED = 9,   /* ... the crossing inside the min-p prefix: that prefix sorted */
   MXS_PATH_EXACT_REPLAY = 10,  /* ... an uncertain crossing: the reference's sums replayed */
-  MXS_PATH_LARGE = 11          /* working set beyond LDS: mass-weighted radix select */
+  MXS_PATH_LARGE = 11,         /* working set beyond LDS: mass-weighted radix select */
+  MXS_PATH_SHORT = 12          /* top-k <= 64 or min-p rows, at most 512 candidates: one wave, one E member per lane */
 };
 int mxs_debug_set_paths(mxs_ctx* ctx, void* device_buffer);
 const char* mxs_last_error(const mxs_ctx* ctx);

@@ -2362,6 +2362,163 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
 }
 
 // ---------------------------------------------------------------------------
+// The short one-wave finisher: top-k rows with k <= 64 and min-p rows, at
+// most WR * 64 candidates (lane l holds candidates WR l .. WR l + WR - 1 from
+// LDS, so lane order is token-ID order) and a working set E of at most 64
+// members.  It makes wave_finish's decisions with far fewer dependent steps,
+// which is what a single wave's finish time is made of:
+//   - E (the top-k head, or the min-p set) is compacted to one member per
+//     lane in token-ID order; each lane then takes one exact f64 shifted
+//     logit (the reference's division) and one weight;
+//   - the nucleus cut needs the mass ahead of each member of P (E with the
+//     min-p test) in (key desc, ID asc) order: each lane sums the weights of
+//     the P members ranked before it, one ballot-driven pass over P, instead
+//     of a sort;
+//   - the draw is sel_draw_wave (one inclusive scan in token-ID order).
+// Every decision carries the same certificate as elsewhere: a margin inside
+// the bound returns false having written nothing, and the row goes on to
+// the other finishers (which replay it where needed).
+__device__ __forceinline__ bool finish_w1(const FinCtx& X, FinSmem& F) {
+  const RowCfg& c = X.c;
+  const uint32_t n = X.ncand, ln = lane(), j0 = ln * (uint32_t)WR;
+  if (n == 0u || n > (uint32_t)(WR * 64)) return false;
+  float lv[WR];
+  uint32_t key[WR];
+  uint32_t act = 0;
+  {
+    const float4 a0 = *reinterpret_cast<const float4*>(&F.cl[j0]);
+    const float4 a1 = *reinterpret_cast<const float4*>(&F.cl[j0 + 4u]);
+    lv[0] = a0.x; lv[1] = a0.y; lv[2] = a0.z; lv[3] = a0.w;
+    lv[4] = a1.x; lv[5] = a1.y; lv[6] = a1.z; lv[7] = a1.w;
+  }
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    const bool a = j0 + (uint32_t)r < n;
+    act |= a ? 1u << r : 0u;
+    key[r] = a ? okey(lv[r]) : 0u;
+  }
+  // ---- E: the top-k head (key above kappa, then the lowest-ID ties) or the
+  // min-p set (the f32 logit decides away from the threshold, the exact
+  // shifted logit near it)
+  uint32_t inE = 0;
+  bool unc = false;
+  if (X.k_path) {
+    if (c.k > 64u || c.k > n) return false;
+    uint32_t kappa, above;
+    if (!wave_kth(F.eidx, key, act, c.k, &kappa, &above)) return false;
+    const uint32_t need_t = c.k - above;
+    uint32_t tie = 0;
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      inE |= ((act >> r) & 1u) && key[r] > kappa ? 1u << r : 0u;
+      tie |= ((act >> r) & 1u) && key[r] == kappa ? 1u << r : 0u;
+    }
+    const uint32_t tc = (uint32_t)__builtin_popcount(tie);
+    uint32_t t = wave_scan_u32(tc) - tc;
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if ((tie >> r) & 1u) { if (t < need_t) inE |= 1u << r; ++t; }
+  } else {
+    const float Mf = (float)X.M;
+    const float lthr = Mf + (float)(c.T * X.L);
+    const float band = 1e-5f * (fabsf(Mf) + fabsf((float)(c.T * X.L))) + 1e-30f;
+    const bool lfin = __builtin_isfinite(lthr + band) && __builtin_isfinite(lthr - band);
+    const float lhi = lfin ? lthr + band : INFINITY, llo = lfin ? lthr - band : -INFINITY;
+#pragma unroll
+    for (int r = 0; r < WR; ++r) {
+      if (!((act >> r) & 1u)) continue;
+      bool in = lv[r] >= lhi;
+      if (lv[r] >= llo && lv[r] < lhi) {
+        const double sd = ((double)lv[r] - X.M) / c.T;
+        in = sd >= X.L;
+        if (fabs(sd - X.L) < X.Lclose) unc = true;
+      }
+      inE |= in ? 1u << r : 0u;
+    }
+  }
+  // ---- E compacted to lanes in token-ID order --------------------------------
+  const uint32_t ec = (uint32_t)__builtin_popcount(inE);
+  const uint32_t einc = wave_scan_u32(ec);
+  const uint32_t ne = bcast63(einc);
+  if (ne == 0u || ne > 64u) return false;
+  uint32_t* ek = F.eidx + 256;   // past wave_kth's histogram
+  uint32_t* ep = ek + 64;
+  {
+    uint32_t at = einc - ec;
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if ((inE >> r) & 1u) { ek[at] = key[r]; ep[at] = j0 + (uint32_t)r; ++at; }
+  }
+  wave_lds_sync();
+  const bool mine = ln < ne;
+  const uint32_t mk = mine ? ek[ln] : 0u, mp = mine ? ep[ln] : 0u;
+  const float ml = mine ? F.cl[mp] : 0.0f;
+  const uint32_t mid = mine ? F.cid[mp] : NONE;
+  const double s = mine ? ((double)ml - X.M) / c.T : 0.0;
+  const double w = mine ? exp_neg_t(s, X.etab, X.etab + 64) : 0.0;
+  // P: E with the min-p test (top-k rows; E already is the min-p set otherwise)
+  bool inp = mine;
+  if (mine && X.k_path && c.min_p > 0.0) {
+    inp = s >= X.L;
+    if (fabs(s - X.L) < X.Lclose) unc = true;
+  }
+  const uint64_t pmask = __builtin_amdgcn_ballot_w64(inp);
+  const uint32_t np = (uint32_t)__builtin_popcountll(pmask);
+  const double esum = wave_sum_f64(w);
+  const double psum = wave_sum_f64(inp ? w : 0.0);
+  unc = __builtin_amdgcn_ballot_w64(unc) != 0ull;
+
+  // ---- the nucleus cut --------------------------------------------------------
+  bool theta_set = false;
+  double theta = 0.0, theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      // the running sum may stall before reaching the total: the other paths replay it
+      const unsigned long long wb = mine ? __builtin_bit_cast(unsigned long long, w) : ~0ull;
+      const double wm = __builtin_bit_cast(double, ~wave_max_u64(~wb));
+      if (!minp_above_stall(c, esum) && !(wm > 2.3e-16 * esum)) return false;
+    } else {
+      theta_set = true;
+      theta = c.top_p * esum;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
+    }
+  } else if (c.top_p < 1.0) {
+    // the reference walks the tokens whose weight reaches 1e-9 of the total:
+    // every min-p member must clear that level
+    if (!(c.min_p * (1.0 - 1e-12) > 1e-9 * (X.total + X.total_err) * (1.0 + 1e-12))) return false;
+    theta_set = true;
+    theta = c.top_p * X.total;
+    theta_err = c.top_p * X.total_err + U * theta;
+  }
+  bool kept = inp;
+  if (theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) {
+    // The nucleus can end inside P: each member takes the mass of the P
+    // members ranked before it; the reference keeps a member whose running
+    // sum before it is still below theta.
+    double pre = 0.0;
+    uint32_t rank = 0;
+    uint64_t m = pmask;
+    while (m) {
+      const uint32_t j = (uint32_t)__builtin_ctzll(m);
+      m &= m - 1ull;
+      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)j);
+      const uint32_t pj = (uint32_t)__builtin_amdgcn_readlane((int)mp, (int)j);
+      const double wj = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, w), j));
+      const bool ahead = kj > mk || (kj == mk && pj < mp);
+      pre += ahead ? wj : 0.0;
+      rank += ahead ? 1u : 0u;
+    }
+    const double ep_ = sum_bound(pre, rank + 1u, 8.0);
+    const bool in_c = pre + ep_ < theta - theta_err;    // certainly before the cut
+    const bool out_c = pre - ep_ >= theta + theta_err;  // certainly after it
+    if (__builtin_amdgcn_ballot_w64(inp && !in_c && !out_c)) return false;
+    kept = inp && in_c;
+  }
+  sel_draw_wave(X, kept, w, s, mid, unc);
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // The row finisher.  Runs in the last chunk workgroup of a row, after every
 // chunk published its statistics and candidates.
 // The kept set of a keep-all row: every legal token.
@@ -2640,18 +2797,10 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   X.kappa = 0;
   X.id_tie = NONE;
 
-  // rows whose candidates all sit in the register slots: the selection finisher
-  if ((mode == M_TOPK || mode == M_MINP) && ncand > 0u && C <= (uint32_t)FW && F.hdr.qmax <= cov) {
-    if (finish_sel(X, F, P, sq, sj)) {
-      fpath(X, MXS_PATH_SELECT);
-      stamp(A, row, MAXC, 2);
-      return;
-    }
-  }
   // One bulk load of every candidate into LDS, all loads in flight at once.
   // Candidate j lives in chunk q's region at j - coff[q]; j grows with u,
   // so each thread walks the chunk offsets once.
-  if (X.lds_c) {
+  auto bulk_load = [&]() {
     // the register slots first (every chunk's first cov candidates)
     {
       const uint32_t nq = sq < C ? F.st[sq].ncand : 0u;
@@ -2686,7 +2835,34 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       if ((need >> u) & 1u) { F.cl[j] = lv[u]; F.cid[j] = iv[u]; }
     }
     lds_barrier();
+  };
+  // short rows first: the one-wave finisher
+  bool loaded = false;
+  if (((mode == M_TOPK && c.k <= 64u) || mode == M_MINP) && ncand > 0u && ncand <= (uint32_t)(WR * 64) &&
+      X.lds_c) {
+    bulk_load();
+    loaded = true;
+    if (wave() == 0) {
+      const bool ok = finish_w1(X, F);
+      if (lane() == 0) F.s_u[15] = ok ? 1u : 0u;
+    }
+    lds_barrier();
+    if (F.s_u[15]) {
+      fpath(X, MXS_PATH_SHORT);
+      stamp(A, row, MAXC, 2);
+      return;
+    }
+    lds_barrier();   // wave 0's LDS scratch is reused below
   }
+  // rows whose candidates all sit in the register slots: the selection finisher
+  if ((mode == M_TOPK || mode == M_MINP) && ncand > 0u && C <= (uint32_t)FW && F.hdr.qmax <= cov) {
+    if (finish_sel(X, F, P, sq, sj)) {
+      fpath(X, MXS_PATH_SELECT);
+      stamp(A, row, MAXC, 2);
+      return;
+    }
+  }
+  if (X.lds_c && !loaded) bulk_load();
   stamp(A, row, MAXC, 1);
   if (mode != M_KEEPALL && X.lds_c && ncand <= (uint32_t)(WR * 64)) {
     // at most WR * 64 candidates: one wave finishes the row

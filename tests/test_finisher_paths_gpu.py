@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 V = 151936
 PATHS = {"ERROR": 1, "GREEDY": 2, "KEEPALL": 3, "KEEPALL_RACE": 4, "SELECT": 5, "WAVE": 6, "FAST": 7,
-         "EXACT": 8, "EXACT_SORTED": 9, "EXACT_REPLAY": 10, "LARGE": 11}
+         "EXACT": 8, "EXACT_SORTED": 9, "EXACT_REPLAY": 10, "LARGE": 11, "SHORT": 12}
 
 
 @pytest.fixture(scope="module")
@@ -60,7 +60,8 @@ def path_batch():
     rows.append(("ERROR", peaked.copy(), -1.0, 20, 0.9, 0.0))          # invalid temperature
     rows.append(("GREEDY", peaked.copy(), 0.0, 0, 1.0, 0.0))
     rows.append(("KEEPALL", noise(2.0), 0.9, 0, 1.0, 0.0))
-    rows.append(("SELECT", peaked.copy(), 0.7, 20, 0.8, 0.0))
+    rows.append(("SHORT", peaked.copy(), 0.7, 20, 0.8, 0.0))
+    rows.append(("SELECT", peaked.copy(), 0.7, 100, 0.8, 0.0))     # k above the one-wave finisher's 64
     # a grammar-masked row (mask below) with 60 legal tokens, top-p only
     rows.append(("WAVE", noise(1.0), 1.0, 0, 0.9, 0.0))
     rows.append(("FAST", crowd(3000, step=1e-3), 1.0, 0, 1.0, 0.01))   # a min-p set of 3000
