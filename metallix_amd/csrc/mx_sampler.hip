@@ -3049,9 +3049,11 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     const uint32_t e0 = c0k + (uint32_t)i * SLICE + tid * 4u;
     raw[i] = Quad<In>::load(src + (e0 < c1 ? e0 : c0k));
   };
+  // (every thread issues all PER_MAX slices, past the chunk re-reading its
+  // first quad, so each wave's count of loads in flight is known at compile
+  // time and every wait is exact)
 #pragma unroll
-  for (int i = 0; i < LA; ++i)
-    if (i < (int)A.per) issue(i);
+  for (int i = 0; i < LA; ++i) issue(i);
   const uint32_t clen = c1 - c0;
   const double invT = MODE == M_GREEDY ? 0.0 : 1.0 / c.T;
   uint32_t my_flags = 0;
@@ -3065,6 +3067,19 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   }
 
   // ---- the chunk's history count table (u16 per token) -------------------
+  // Penalties in this body never raise a logit (repetition >= 1, frequency
+  // and presence >= 0; other rows take the general body), and they touch
+  // few tokens.  Pass 1 leaves every penalised token out of the statistics
+  // (-inf), and the thread whose count-table increment came first for a
+  // token (its owner) computes the token's adjusted logit from its own load
+  // of the logit and adds it back; the candidate pass swaps the adjusted
+  // logit in where a slice can hold a candidate (a penalised logit at or
+  // above a threshold was at or above it before the penalty).  The owner
+  // leaves the adjusted logit in pvals and marks the token's table entry
+  // 0x8000 | slot.
+  uint32_t own = 0;              // bit r: this thread owns history entry r's token
+  float hraw[HCAP / NT];         // the owned tokens' logits
+  float* pvals = reinterpret_cast<float*>(S.hids);   // HCAP adjusted logits by slot (the lean body stages no history)
   if constexpr (HIST) {
     const uint32_t n4 = A.per * (SLICE / 8);   // uint4 words covering per slices
     for (uint32_t t = tid; t < n4; t += NT) reinterpret_cast<uint4*>(S.t.ct)[t] = make_uint4(0u, 0u, 0u, 0u);
@@ -3079,9 +3094,17 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
         const uint32_t id = hreg[r];
         if (id >= V) my_flags |= F_HIST;
         const uint32_t t = id - c0;
-        if (t < clen) atomicAdd(&S.t.ct[t >> 1], 1u << ((t & 1u) * 16u));
+        if (t < clen) {
+          const uint32_t sh = (t & 1u) * 16u;
+          const uint32_t old = atomicAdd(&S.t.ct[t >> 1], 1u << sh);
+          if (((old >> sh) & 0xffffu) == 0u) own |= 1u << r;
+        }
       }
     }
+    // every thread issues its HCAP / NT loads (a non-owner re-reads the
+    // chunk's first token): a fixed count of loads in flight per wave
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) hraw[r] = Quad<In>::one(src + (((own >> r) & 1u) ? hreg[r] : c0k));
     lds_barrier();
   }
   stamp(A, row, chunk, 3);
@@ -3102,10 +3125,11 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   // and add per slice.
   float mrun = -FLT_MAX;
   float acc = 0.0f, eacc = 0.0f;
+  uint32_t pq = 0;   // bit i: this thread's quad of slice i holds a penalised token
 #pragma unroll
   for (int i = 0; i < PER_MAX; ++i) {
     qm[i] = -INFINITY;
-    if (i + LA < PER_MAX && i + LA < (int)A.per) issue(i + LA);
+    if (i + LA < PER_MAX) issue(i + LA);
     if (i < (int)A.per) {
       const uint32_t sbase = c0 + (uint32_t)i * SLICE;
       const uint32_t e0 = sbase + tid * 4u;
@@ -3113,17 +3137,15 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
       const uint32_t rb = full ? 0xfu : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
       float x[4];
       Quad<In>::unpack(raw[i], x);
+      // xe: the logits the statistics see (penalised tokens left out)
+      float xe[4] = {x[0], x[1], x[2], x[3]};
       if constexpr (HIST) {
-        // Penalised tokens are rare: only an element position where some
-        // lane of the wave holds a count runs the penalty arithmetic.
         const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
-        if (__builtin_amdgcn_ballot_w64((cw.x | cw.y) != 0u)) {
-          const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (__builtin_amdgcn_ballot_w64(h[e] != 0u))
-              x[e] = h[e] ? bias_and_penalize(x[e], h[e], 0.0f, c.rep, inv_rep, c.freq, c.pres) : x[e];
-        }
+        xe[0] = (cw.x & 0xffffu) ? -INFINITY : x[0];
+        xe[1] = (cw.x >> 16) ? -INFINITY : x[1];
+        xe[2] = (cw.y & 0xffffu) ? -INFINITY : x[2];
+        xe[3] = (cw.y >> 16) ? -INFINITY : x[3];
+        pq |= (cw.x | cw.y) ? 1u << i : 0u;
       }
       if (A.o.adjusted) {
 #pragma unroll
@@ -3139,33 +3161,38 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
           const bool inr = (rb >> e) & 1u;
           nf |= __builtin_amdgcn_ballot_w64(inr && !__builtin_isfinite(x[e]));
           x[e] = inr ? x[e] : -INFINITY;
+          xe[e] = inr ? xe[e] : -INFINITY;
         }
       }
       if constexpr (MODE == M_GREEDY) {
         // IEEE >, first index wins (ids grow with e and i in this thread)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const bool g = x[e] > gv;
-          gv = g ? x[e] : gv;
+          const bool g = xe[e] > gv;
+          gv = g ? xe[e] : gv;
           gi = g ? e0 + (uint32_t)e : gi;
         }
       } else {
+        // qm: the slice screen of the candidate pass (raw logits: a superset);
+        // qe: the statistics' quad maximum
         qm[i] = vmax(vmax3(x[0], x[1], x[2]), x[3]);
+        const float qe = HIST ? vmax(vmax3(xe[0], xe[1], xe[2]), xe[3]) : qm[i];
         if (top2) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) { t2 = vmed3(t1, t2, x[e]); t1 = vmax(t1, x[e]); }
+          for (int e = 0; e < 4; ++e) { t2 = vmed3(t1, t2, xe[e]); t1 = vmax(t1, xe[e]); }
         } else {
-          t1 = vmax(t1, qm[i]);
+          t1 = vmax(t1, qe);
         }
         if (do_mass) {
-          const float mnew = vmax(mrun, qm[i]);
+          const float mnew = vmax(mrun, qe);
           const float ys = (mrun - mnew) * c2;                 // <= 0
           const float s = __builtin_amdgcn_exp2f(ys);
           float sw = 0.0f, ew = 0.0f;
           if (full) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float y = (x[e] - mnew) * c2;
+              // a left-out token (-inf) weighs 0 with a finite exponent
+              const float y = HIST ? vmax((xe[e] - mnew) * c2, -200.0f) : (xe[e] - mnew) * c2;
               const float w = __builtin_amdgcn_exp2f(y);
               sw += w;
               ew = __builtin_fmaf(w, -y, ew);
@@ -3174,7 +3201,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const bool inr = (rb >> e) & 1u;
-              const float y = (x[e] - mnew) * c2;
+              const float y = HIST ? vmax((xe[e] - mnew) * c2, -200.0f) : (xe[e] - mnew) * c2;
               const float w = inr ? __builtin_amdgcn_exp2f(y) : 0.0f;
               sw += w;
               ew = inr ? __builtin_fmaf(w, -y, ew) : ew;
@@ -3190,6 +3217,49 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) lv[i][e] = x[e];
+    }
+  }
+  if constexpr (HIST) {
+    // The owners' adjusted logits join the statistics (their loads landed
+    // with the slices), go to pvals and mark their table entries.  Pass 1
+    // wrote the penalised tokens' raw logits to the adjusted output: those
+    // writes complete before the owners overwrite them.
+    if (A.o.adjusted) {
+      wait_mem();
+      __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) {
+      if (!((own >> r) & 1u)) continue;
+      const uint32_t id = hreg[r], t = id - c0, sh = (t & 1u) * 16u;
+      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0xffffu;
+      const float pv = bias_and_penalize(hraw[r], cnt, 0.0f, c.rep, inv_rep, c.freq, c.pres);
+      if (!__builtin_isfinite(pv)) my_flags |= F_NONFINITE;
+      if (A.o.adjusted) A.o.adjusted[(uint64_t)row * V + id] = pv;
+      const uint32_t slot = (uint32_t)r * NT + tid;
+      pvals[slot] = pv;
+      reinterpret_cast<uint16_t*>(S.t.ct)[t] = (uint16_t)(0x8000u | slot);
+      if constexpr (MODE == M_GREEDY) {
+        if (better(pv, id, gv, gi)) { gv = pv; gi = id; }
+      } else {
+        if (top2) {
+          t2 = vmed3(t1, t2, pv);
+          t1 = vmax(t1, pv);
+        } else {
+          t1 = vmax(t1, pv);
+        }
+        if (do_mass) {   // one more online step
+          const float mnew = vmax(mrun, pv);
+          const float ys = (mrun - mnew) * c2;
+          const float sc = __builtin_amdgcn_exp2f(ys);
+          const float y = vmax((pv - mnew) * c2, -200.0f);
+          const float w = __builtin_amdgcn_exp2f(y);
+          const bool live = acc > 0.0f;
+          eacc = live ? __builtin_fmaf(__builtin_fmaf(acc, -ys, eacc), sc, w * -y) : w * -y;
+          acc = live ? __builtin_fmaf(acc, sc, w) : w;
+          mrun = mnew;
+        }
+      }
     }
   }
   stamp(A, row, chunk, 6);
@@ -3312,6 +3382,18 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
         // screen the slice on the quad maxima first
         uint32_t cnt = 0;
         if (__builtin_amdgcn_ballot_w64(qm[i] >= thr)) {
+          if (HIST && __builtin_amdgcn_ballot_w64(((pq >> i) & 1u) && qm[i] >= thr)) {
+            // a penalised token can only be a candidate if its raw logit is
+            // (penalties never raise a logit): then its owner's adjusted
+            // logit comes in
+            if (((pq >> i) & 1u) && qm[i] >= thr) {
+              const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
+              const uint32_t h[4] = {cw.x & 0xffffu, cw.x >> 16, cw.y & 0xffffu, cw.y >> 16};
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (h[e] && lv[i][e] >= thr) lv[i][e] = pvals[h[e] & 0xfffu];
+            }
+          }
           if (thr_fin) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -3357,7 +3439,9 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     // relative; a term's exponent and the rescale exponents applied to it
     // telescope to its distance from the chunk maximum), + n 2^-120 for
     // weights and factors below 2^-126, + 2^-40 S for the f64 sums.
-    mass_err = 1.01 * (0x1p-22 * S0 * (double)(A.per + 3u) + (double)(A.per + 5u) * 0x1p-24 * S0 +
+    // (each owned history token is one more step)
+    const uint32_t steps = A.per + (HIST ? (uint32_t)(HCAP / NT) : 0u);
+    mass_err = 1.01 * (0x1p-22 * S0 * (double)(steps + 3u) + (double)(steps + 5u) * 0x1p-24 * S0 +
                        0.6931471805599453 * 3.0001 * 0x1p-24 * E0) +
                (double)nleg * 0x1p-120 + 0x1p-40 * S0;
   }
@@ -4146,7 +4230,9 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   bool last;
   {
     const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
+    // (the lean body's penalties never raise a logit: others take the general body)
     if (!c.err && A.masked == 0u && bn == 0u && hn <= (uint32_t)HCAP &&
+        (hn == 0u || (c.rep >= 1.0f && c.freq >= 0.0f && c.pres >= 0.0f)) &&
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
       if (hn) {
