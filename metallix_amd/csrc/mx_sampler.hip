@@ -2362,6 +2362,346 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
 }
 
 // ---------------------------------------------------------------------------
+// finish_large for candidates cached in LDS (n <= FT * FR): each thread
+// holds a contiguous range of R = ceil(n / FT) candidates in registers, with
+// its shifted logits and weights computed once, so every later pass is one
+// loop over registers and each prefix is one block scan (the draw's scan in
+// token-ID order included) instead of one block scan per FT candidates.
+// The decisions and certificates are finish_large's.
+__device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint32_t ne) {
+  const RowCfg& c = X.c;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n = X.ncand;
+  const uint32_t R = (n + FT - 1u) / FT, j0 = tid * R;
+  uint32_t kv[FR];
+  double sv[FR], wv[FR];
+  uint32_t have = 0, mem = 0;
+  bool uncert = false;
+  double wpart = 0.0, wmin = INFINITY;
+  // The shifted logit decides membership (min-p rows) and the min-p test:
+  // there it is the reference's quotient.  Otherwise it only feeds weights,
+  // and the product with 1/T (within 2 ulp of the quotient) moves a weight
+  // by at most w |s| 2^-51 <= 2^-51 / e, inside the bounds' allowance for
+  // every prefix from the top (each holds the maximum, weight 1).
+  const bool exact_s = X.mode == M_MINP || (c.min_p > 0.0 && X.mode != M_MINP);
+  const double invT = 1.0 / c.T;
+  float lmin = INFINITY;   // the smallest member logit
+#pragma unroll
+  for (int r = 0; r < FR; ++r) {
+    kv[r] = 0u;
+    sv[r] = 0.0;
+    wv[r] = 0.0;
+    if ((uint32_t)r < R && j0 + (uint32_t)r < n) {
+      const float l = F.cl[j0 + r];
+      const uint32_t id = F.cid[j0 + r];
+      const uint32_t key = okey(l);
+      const double sh = exact_s ? ((double)l - X.M) / c.T : ((double)l - X.M) * invT;
+      kv[r] = key;
+      sv[r] = sh;
+      have |= 1u << r;
+      const bool m = X.k_path ? (key > X.kappa || (key == X.kappa && id <= X.id_tie))
+                              : (X.mode == M_MINP ? sh >= X.L : true);
+      if (m) {
+        mem |= 1u << r;
+        const double w = exp_neg_t(sh, X.etab, X.etab + 64);
+        wv[r] = w;
+        wpart += w;
+        wmin = fmin(wmin, w);
+        lmin = fminf(lmin, l);
+      }
+    }
+  }
+  const double esum = block_sum<double>(wpart, F.red_d);
+  wmin = -block_max<double>(-wmin, F.red_d);
+  lmin = -block_max<float>(-lmin, F.red_f);
+  double total = X.total, total_err = X.total_err;
+  if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
+  fstamp(X, 4);
+
+  uint32_t tau = 0, id_cut = NONE;
+  bool cut = false;
+  double theta = 0.0, theta_err = 0.0;
+  if (X.k_path) {
+    if (c.top_p >= 1.0) {
+      if (!minp_above_stall(c, esum) && !(wmin > 2.3e-16 * esum)) uncert = true;
+    } else {
+      cut = true;
+      theta = c.top_p * esum;
+      theta_err = c.top_p * sum_bound(esum, ne, 8.0) + U * theta;
+    }
+  } else if (c.top_p < 1.0) {
+    theta = c.top_p * total;
+    theta_err = c.top_p * total_err + U * theta;
+    cut = !(esum + sum_bound(esum, ne, 8.0) < theta - theta_err);
+  }
+  bool binned = false;
+  if (cut) {
+    // One mass histogram on NB value bins (bin 0 holds the largest logits;
+    // a bin index never decreases as the logit decreases), its block scan,
+    // and the crossing bin's members ranked exactly by one wave: the cut
+    // member's (key, ID) in one pass.  More than 64 members in the
+    // crossing bin: the radix passes below.
+    const float Mf = (float)X.M;
+    const float span = Mf - lmin;
+    const float sc = span > 1e-30f ? (float)(NB - 1) / span : 0.0f;
+    for (uint32_t t = tid; t < (uint32_t)NB; t += FT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
+    if (tid == 0) { F.s_u[4] = NONE; F.s_u[6] = 0u; F.s_u[10] = 0u; }
+    __syncthreads();
+    uint32_t bins[FR];
+#pragma unroll
+    for (int r = 0; r < FR; ++r) {
+      bins[r] = 0u;
+      if ((mem >> r) & 1u) {
+        const float d = (Mf - okey_value(kv[r])) * sc;
+        bins[r] = d < (float)(NB - 1) ? (uint32_t)d : (uint32_t)(NB - 1);
+        atomicAdd(&F.u.h.hcnt[bins[r]], 1u);
+        atomicAdd(&F.u.h.hmass[bins[r]], wv[r]);
+      }
+    }
+    __syncthreads();
+    const uint32_t b0 = BPT * tid;   // this thread's bins, in descending value order
+    double msum = 0.0;
+    uint32_t nsum = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < BPT; ++i) { msum += F.u.h.hmass[b0 + i]; nsum += F.u.h.hcnt[b0 + i]; }
+    double mtot, mexc;
+    uint32_t ntot;
+    const double minc = block_scan_pair<double>(msum, F.red_d, &mexc, &mtot);
+    const uint32_t nexc = block_scan_incl<uint32_t>(nsum, F.red_u, &ntot) - nsum;
+    {
+      double lo = mexc;
+      uint32_t nlo = nexc;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) {
+        const double mh = F.u.h.hmass[b0 + i];
+        const uint32_t nh = F.u.h.hcnt[b0 + i];
+        const double hi = i + 1 == BPT ? minc : lo + mh;
+        if (nh && lo < theta && theta <= hi) { F.s_u[4] = b0 + i; F.s_u[5] = nlo; F.s_d[4] = lo; }
+        lo = hi;
+        nlo += nh;
+      }
+    }
+    __syncthreads();
+    const uint32_t bstar = F.s_u[4];
+    if (bstar != NONE) {
+#pragma unroll
+      for (int r = 0; r < FR; ++r)
+        if (((mem >> r) & 1u) && bins[r] == bstar) {
+          const uint32_t at = atomicAdd(&F.s_u[10], 1u);
+          if (at < 64u) { F.u.h.hcnt[at] = kv[r]; F.eidx[at] = F.cid[j0 + r]; }
+        }
+    }
+    __syncthreads();
+    const uint32_t cm = F.s_u[10];
+    if (bstar != NONE && cm <= 64u) {
+      binned = true;
+      if (wave() == 0) {
+        // sort the members by (key desc, ID asc); each lane's weight from its key
+        const uint32_t ln = lane();
+        const bool mine = ln < cm;
+        const unsigned long long sk =
+            wave_sort_desc(mine ? ((unsigned long long)F.u.h.hcnt[ln] << 32) | (unsigned long long)(~F.eidx[ln]) : 0ull);
+        const bool live = ln < cm;   // sorted: the members occupy lanes 0 .. cm - 1
+        const uint32_t key = (uint32_t)(sk >> 32), id = ~(uint32_t)sk;
+        const double sh = exact_s ? ((double)okey_value(key) - X.M) / c.T : ((double)okey_value(key) - X.M) * invT;
+        const double w = live ? exp_neg_t(sh, X.etab, X.etab + 64) : 0.0;
+        const double above = F.s_d[4];
+        const uint32_t above_n = F.s_u[5];
+        const double cum = above + wave_scan_f64(w);   // after this member
+        const double prev = cum - w;
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(live && cum >= theta);
+        if (ln == 0) { F.s_u[3] = NONE; F.s_u[11] = NONE; F.s_u[7] = 1u; }
+        if (hit) {
+          const uint32_t i = (uint32_t)__builtin_ctzll(hit);
+          if (ln == i) {
+            const double e1 = sum_bound(cum, above_n + i + 65u, 8.0), e0 = sum_bound(prev, above_n + i + 64u, 8.0);
+            const bool cert = (i == 0u ? above + sum_bound(above, above_n + 64u, 8.0) < theta - theta_err
+                                       : prev + e0 < theta - theta_err) &&
+                              cum - e1 >= theta + theta_err;
+            F.s_u[3] = id;
+            F.s_u[11] = key;
+            F.s_u[7] = cert ? 0u : 1u;
+          }
+        }
+      }
+      __syncthreads();
+      if (F.s_u[11] == NONE) { cut = false; uncert = true; }
+      else { tau = F.s_u[11]; id_cut = F.s_u[3]; if (F.s_u[7]) uncert = true; }
+      __syncthreads();
+    }
+  }
+  if (cut && !binned) {
+    uint32_t prefix = 0, pmask = 0, above_n = 0;
+    double above = 0.0;
+    for (int pass = 0; pass < 3; ++pass) {
+      const int sh = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+      for (uint32_t t = tid; t < (uint32_t)NB; t += FT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < FR; ++r) {
+        if (((mem >> r) & 1u) && (kv[r] & pmask) == prefix) {
+          const uint32_t bin = (kv[r] >> sh) & (NB - 1);
+          atomicAdd(&F.u.h.hcnt[bin], 1u);
+          atomicAdd(&F.u.h.hmass[bin], wv[r]);
+        }
+      }
+      __syncthreads();
+      // as in finish_large: per-thread bin intervals tile the mass exactly
+      const uint32_t b0 = NB - 1 - BPT * tid;
+      double msum = 0.0;
+      uint32_t nsum = 0;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) { msum += F.u.h.hmass[b0 - i]; nsum += F.u.h.hcnt[b0 - i]; }
+      double mtot, mexc;
+      uint32_t ntot, nexc;
+      const double minc = above + block_scan_pair<double>(msum, F.red_d, &mexc, &mtot);
+      mexc += above;
+      nexc = above_n + block_scan_incl<uint32_t>(nsum, F.red_u, &ntot) - nsum;
+      if (tid == 0) { F.s_u[4] = NONE; F.s_u[6] = 0u; }
+      __syncthreads();
+      double lo = mexc;
+      uint32_t nlo = nexc;
+#pragma unroll
+      for (uint32_t i = 0; i < BPT; ++i) {
+        const double mh = F.u.h.hmass[b0 - i];
+        const uint32_t nh = F.u.h.hcnt[b0 - i];
+        const double hi = i + 1 == BPT ? minc : lo + mh;
+        if (nh && lo < theta && theta <= hi) {
+          F.s_u[4] = b0 - i; F.s_u[5] = nlo; F.s_d[4] = lo;
+          const double e0 = sum_bound(lo, nlo + 64u, 8.0);
+          const double e1 = sum_bound(hi, nlo + nh + 64u, 8.0);
+          if (!(lo + e0 < theta - theta_err) || !(hi - e1 >= theta + theta_err)) F.s_u[6] = 1u;
+        }
+        lo = hi;
+        nlo += nh;
+      }
+      __syncthreads();
+      const uint32_t bin = F.s_u[4];
+      const uint32_t amb = F.s_u[6];
+      const uint32_t an = F.s_u[5];
+      const double am = F.s_d[4];
+      __syncthreads();
+      if (bin == NONE) { cut = false; uncert = true; break; }
+      if (amb) uncert = true;
+      prefix |= bin << sh;
+      pmask |= (uint32_t)(NB - 1) << sh;
+      above = am;
+      above_n = an;
+    }
+    if (cut) {
+      tau = prefix;
+      const double wt = exp_neg_t(((double)okey_value(tau) - X.M) / c.T, X.etab, X.etab + 64);
+      if (tid == 0) {
+        uint32_t jn = 0;
+        double cov = above;
+        bool close = false;
+        for (uint32_t q = 0; q < (uint32_t)NB * 64u; ++q) {
+          cov += wt;
+          ++jn;
+          const double e = sum_bound(cov, above_n + jn + 64u, 8.0);
+          if (fabs(cov - theta) <= e + theta_err) close = true;
+          if (cov >= theta || !(wt > 0.0)) break;
+        }
+        F.s_u[6] = jn;
+        F.s_u[7] = close ? 1u : 0u;
+        F.s_u[3] = NONE;
+      }
+      __syncthreads();
+      const uint32_t jneed = F.s_u[6];
+      if (F.s_u[7]) uncert = true;
+      // the jneed-th member at tau in token-ID order (ranges are in ID order)
+      uint32_t tie = 0;
+#pragma unroll
+      for (int r = 0; r < FR; ++r) tie |= ((mem >> r) & 1u) && kv[r] == tau ? 1u << r : 0u;
+      uint32_t ttot;
+      uint32_t t = block_excl_scan_u32((uint32_t)__builtin_popcount(tie), F.sc_u[0], &ttot);
+#pragma unroll
+      for (int r = 0; r < FR; ++r)
+        if ((tie >> r) & 1u) { ++t; if (t == jneed) F.s_u[3] = F.cid[j0 + r]; }
+      __syncthreads();
+      id_cut = F.s_u[3];
+      if (id_cut == NONE) { id_cut = 0xfffffffeu; uncert = true; }
+      __syncthreads();
+    }
+  }
+
+  fstamp(X, 5);
+  // kept = member, inside the cut, and (unless E is the min-p set already)
+  // at or above ln(min_p); the draw walks kept tokens in ID order.
+  const bool apply_minp = c.min_p > 0.0 && X.mode != M_MINP;
+  uint32_t kept = 0, kn = 0, close = 0, bad = 0;
+  double kpart = 0.0;
+#pragma unroll
+  for (int r = 0; r < FR; ++r) {
+    if (!((have >> r) & 1u)) continue;
+    if (apply_minp && fabs(sv[r] - X.L) < X.Lclose) close = 1;
+    if (!((mem >> r) & 1u)) continue;
+    if (cut && !(kv[r] > tau || (kv[r] == tau && F.cid[j0 + r] <= id_cut))) continue;
+    if (apply_minp && !(sv[r] >= X.L)) continue;
+    kept |= 1u << r;
+    kpart += wv[r];
+    ++kn;
+    if (!isfinite(sv[r]) && !isfinite(((double)F.cl[j0 + r] - X.M) / c.T)) bad = 1;
+  }
+  if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+  if (block_max<uint32_t>(close, F.red_u)) uncert = true;
+  const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
+  if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
+  // the draw: one scan of the per-thread kept masses; the threads'
+  // intervals tile (0, S] exactly, and inside a thread the last positive
+  // weight's interval ends at the thread's inclusive prefix
+  double kexc, S;
+  const double kinc = block_scan_pair<double>(kpart, F.red_d, &kexc, &S);
+  const double target = c.u * S;
+  const double derr = sum_bound(S, nkept + 64u, 8.0);
+  fstamp(X, 6);
+  uint32_t lastw = 0;   // bit r: the last slot of this thread with a positive kept weight
+#pragma unroll
+  for (int r = 0; r < FR; ++r) if (((kept >> r) & 1u) && wv[r] > 0.0) lastw = 1u << r;
+  double run = kexc;
+#pragma unroll
+  for (int r = 0; r < FR; ++r) {
+    if (!((kept >> r) & 1u) || !(wv[r] > 0.0)) continue;
+    const double prev = run;
+    run = ((lastw >> r) & 1u) ? kinc : run + wv[r];
+    atomicMax(&F.s_u[1], j0 + (uint32_t)r + 1u);
+    if (target < run && !(target < prev)) {
+      F.s_u[0] = F.cid[j0 + r];
+      F.s_u[8] = kv[r];
+      F.s_d[0] = sv[r];
+      if (fabs(target - prev) <= derr || fabs(run - target) <= derr) F.s_u[2] = 1u;
+    }
+  }
+  __syncthreads();
+  uint32_t tok = F.s_u[0];
+  double shifted = F.s_d[0];
+  if (F.s_u[2]) uncert = true;
+  if (tok == NONE && F.s_u[1]) {
+    // rounding left the variate past the accumulated mass: last positive kept token
+    const uint32_t j = F.s_u[1] - 1u;
+    tok = F.cid[j];
+    shifted = ((double)F.cl[j] - X.M) / c.T;
+    uncert = true;
+  } else if (tok != NONE && !exact_s) {
+    // the output takes the reference's quotient
+    shifted = ((double)okey_value(F.s_u[8]) - X.M) / c.T;
+  }
+  __syncthreads();
+  if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
+  write_result(X, uncert ? MXS_ROW_UNCERTIFIED : 0, (int32_t)tok, shifted - log(S), nkept);
+  if (X.kbits) {
+    for (uint32_t q = tid; q < X.nwords; q += FT) X.kbits[q] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < FR; ++r)
+      if ((kept >> r) & 1u) {
+        const uint32_t id = F.cid[j0 + r];
+        atomicOr(&X.kbits[id >> 5], 1u << (id & 31u));
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // The short one-wave finisher: top-k rows with k <= 64 and min-p rows, at
 // most WR * 64 candidates (lane l holds candidates WR l .. WR l + WR - 1 from
 // LDS, so lane order is token-ID order) and a working set E of at most 64
@@ -2941,6 +3281,47 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   bool mp_close = false;
   if (tid == 0) F.s_u[7] = NONE;
   __syncthreads();
+  if (X.lds_c) {
+    // contiguous per-thread ranges of the cached candidates (ID order runs
+    // through the threads): one block scan for the ties, one for E
+    const uint32_t R = (ncand + FT - 1u) / FT, j0 = tid * R;
+    uint32_t inb = 0, tieb = 0;
+#pragma unroll
+    for (int r = 0; r < FR; ++r) {
+      const uint32_t j = j0 + (uint32_t)r;
+      if ((uint32_t)r < R && j < ncand) {
+        const float l = F.cl[j];
+        if (X.k_path) {
+          const uint32_t key = okey(l);
+          inb |= key > X.kappa ? 1u << r : 0u;
+          tieb |= key == X.kappa ? 1u << r : 0u;
+        } else if (mode == M_MINP) {
+          const double sd = ((double)l - M) / c.T;
+          inb |= sd >= L ? 1u << r : 0u;
+          if (fabs(sd - L) < X.Lclose) mp_close = true;
+        } else {
+          inb |= 1u << r;
+        }
+      }
+    }
+    if (X.k_path) {
+      uint32_t ttot;
+      uint32_t t = block_excl_scan_u32((uint32_t)__builtin_popcount(tieb), F.sc_u[0], &ttot);
+#pragma unroll
+      for (int r = 0; r < FR; ++r)
+        if ((tieb >> r) & 1u) {
+          ++t;
+          if (t <= ties_needed) inb |= 1u << r;
+          if (t == ties_needed) F.s_u[7] = F.cid[j0 + r];
+        }
+    }
+    uint32_t at = block_excl_scan_u32((uint32_t)__builtin_popcount(inb), F.sc_u[1], &ne);
+    if (ne <= (uint32_t)ECAP) {
+#pragma unroll
+      for (int r = 0; r < FR; ++r)
+        if ((inb >> r) & 1u) F.eidx[at++] = j0 + (uint32_t)r;
+    }
+  } else
   for (uint32_t base = 0; base < ncand; base += FT) {
     const uint32_t j = base + tid;
     bool in = false, tie = false;
@@ -2979,7 +3360,8 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     finish_exact(X, F, ne, mp_close);
   } else {
     fpath(X, MXS_PATH_LARGE);
-    finish_large(X, F, ne);
+    if (X.lds_c) finish_large_r(X, F, ne);
+    else finish_large(X, F, ne);
     if (mp_close && tid == 0 && A.o.status[row] == 0) A.o.status[row] = MXS_ROW_UNCERTIFIED;
   }
 }

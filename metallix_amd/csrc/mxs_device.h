@@ -110,95 +110,12 @@ __device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_waitcnt lgkm
 
 __device__ __forceinline__ uint32_t lane() { return threadIdx.x & 63; }
 __device__ __forceinline__ uint32_t wave() { return threadIdx.x >> 6; }
+// The block helpers are for NT-thread blocks, the size every kernel here
+// launches with (a compile-time count spares a kernel-argument load before
+// each use).
+__device__ __forceinline__ uint32_t nwaves() { return (uint32_t)NW; }
 __device__ __forceinline__ uint32_t lanes_below(uint64_t mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
-}
-
-// ---------------------------------------------------------------------------
-// Block-wide reductions and scans (all threads participate and receive the
-// result).  `red` is LDS scratch of at least NW elements of the type.
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-template <typename T>
-__device__ __forceinline__ T wave_max(T v) {
-  for (int o = 32; o > 0; o >>= 1) { T t = __shfl_xor(v, o); v = t > v ? t : v; }
-  return v;
-}
-// The block helpers below are for NT-thread blocks, the size every kernel
-// here launches with (a compile-time count spares a kernel-argument load
-// before each use).
-__device__ __forceinline__ uint32_t nwaves() { return (uint32_t)NW; }
-template <typename T>
-__device__ __forceinline__ T block_sum(T v, T* red) {
-  v = wave_sum(v);
-  if (lane() == 0) red[wave()] = v;
-  __syncthreads();
-  T s = red[0];
-#pragma unroll 1
-  for (uint32_t i = 1; i < nwaves(); ++i) s += red[i];
-  __syncthreads();
-  return s;
-}
-template <typename T>
-__device__ __forceinline__ T block_max(T v, T* red) {
-  v = wave_max(v);
-  if (lane() == 0) red[wave()] = v;
-  __syncthreads();
-  T s = red[0];
-#pragma unroll 1
-  for (uint32_t i = 1; i < nwaves(); ++i) s = red[i] > s ? red[i] : s;
-  __syncthreads();
-  return s;
-}
-// Inclusive scan in thread order; *total receives the block total.
-template <typename T>
-__device__ __forceinline__ T block_scan_incl(T v, T* red, T* total) {
-  const uint32_t l = lane();
-  for (int o = 1; o < 64; o <<= 1) {
-    T t = __shfl_up(v, o);
-    if (l >= (uint32_t)o) v += t;
-  }
-  if (l == 63) red[wave()] = v;
-  __syncthreads();
-  T before = T(0), all = T(0);
-#pragma unroll 1
-  for (uint32_t i = 0; i < nwaves(); ++i) {
-    T r = red[i];
-    if (i < wave()) before += r;
-    all += r;
-  }
-  __syncthreads();
-  *total = all;
-  return before + v;
-}
-// As block_scan_incl, and *excl receives the exclusive prefix computed so
-// that it is bit-identical to the previous thread's inclusive value: the
-// per-thread intervals (excl, incl] then tile (0, total] with no gap or
-// overlap even in floating point.
-template <typename T>
-__device__ __forceinline__ T block_scan_pair(T v, T* red, T* excl, T* total) {
-  const uint32_t l = lane();
-  for (int o = 1; o < 64; o <<= 1) {
-    T t = __shfl_up(v, o);
-    if (l >= (uint32_t)o) v += t;
-  }
-  T prev = __shfl_up(v, 1);
-  if (l == 63) red[wave()] = v;
-  __syncthreads();
-  T before = T(0), all = T(0);
-#pragma unroll 1
-  for (uint32_t i = 0; i < nwaves(); ++i) {
-    T r = red[i];
-    if (i < wave()) before += r;
-    all += r;
-  }
-  __syncthreads();
-  *total = all;
-  *excl = l == 0 ? before : before + prev;
-  return before + v;
 }
 
 // ---------------------------------------------------------------------------
@@ -406,6 +323,123 @@ __device__ __forceinline__ double block_incl_scan_f64(double v, double* slot /* 
   *total = __builtin_bit_cast(double, readlane64(wb, 63));
   const double before = wave() ? __builtin_bit_cast(double, readlane64(wb, wave() - 1)) : 0.0;
   return before + inc;
+}
+
+// ---------------------------------------------------------------------------
+// Block-wide reductions and scans for NT-thread blocks (all threads
+// participate and receive the result), on the DPP wave primitives: the
+// waves' results meet in `red` (LDS, at least NW elements of the type) and
+// one wave-wide pass combines them lane-parallel.
+template <int CTRL, int RM = 0xf>
+__device__ __forceinline__ unsigned long long dpp64o(unsigned long long old, unsigned long long v) {
+  const uint32_t lo = dpp<CTRL, RM>((uint32_t)old, (uint32_t)v);
+  const uint32_t hi = dpp<CTRL, RM>((uint32_t)(old >> 32), (uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ double bcast63(double v) {
+  return __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, v), 63));
+}
+__device__ __forceinline__ float bcast63(float v) { return __uint_as_float(bcast63(__float_as_uint(v))); }
+__device__ __forceinline__ double readlane_t(double v, uint32_t l) {
+  return __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, v), l));
+}
+__device__ __forceinline__ uint32_t readlane_t(uint32_t v, uint32_t l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, (int)l);
+}
+// f32 and f64 maxima: lanes with no source read -inf; `t > v ? t : v` as the
+// scalar code compares
+__device__ __forceinline__ float wave_max_f32(float v) {
+  const uint32_t ninf = 0xff800000u;
+  float t;
+  t = __uint_as_float(dpp<DPP_SHR1>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  t = __uint_as_float(dpp<DPP_SHR2>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  t = __uint_as_float(dpp<DPP_SHR4>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  t = __uint_as_float(dpp<DPP_SHR8>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  t = __uint_as_float(dpp<DPP_BC15, 0xa>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  t = __uint_as_float(dpp<DPP_BC31, 0xc>(ninf, __float_as_uint(v))); v = t > v ? t : v;
+  return bcast63(v);
+}
+__device__ __forceinline__ double wave_max_f64(double v) {
+  const unsigned long long ninf = 0xfff0000000000000ull;
+  double t;
+#define MXS_MAXSTEP(C, R) \
+  t = __builtin_bit_cast(double, dpp64o<C, R>(ninf, __builtin_bit_cast(unsigned long long, v))); v = t > v ? t : v;
+  MXS_MAXSTEP(DPP_SHR1, 0xf) MXS_MAXSTEP(DPP_SHR2, 0xf) MXS_MAXSTEP(DPP_SHR4, 0xf) MXS_MAXSTEP(DPP_SHR8, 0xf)
+  MXS_MAXSTEP(DPP_BC15, 0xa) MXS_MAXSTEP(DPP_BC31, 0xc)
+#undef MXS_MAXSTEP
+  return bcast63(v);
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += __uint_as_float(dpp<DPP_SHR1>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<DPP_SHR2>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<DPP_SHR4>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<DPP_SHR8>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<DPP_BC15, 0xa>(0u, __float_as_uint(v)));
+  v += __uint_as_float(dpp<DPP_BC31, 0xc>(0u, __float_as_uint(v)));
+  return bcast63(v);
+}
+__device__ __forceinline__ uint32_t wave_sum(uint32_t v) { return wave_sum_u32(v); }
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32(v); }
+__device__ __forceinline__ double wave_sum(double v) { return wave_sum_f64(v); }
+__device__ __forceinline__ uint32_t wave_max(uint32_t v) { return wave_max_u32(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_max_f32(v); }
+__device__ __forceinline__ double wave_max(double v) { return wave_max_f64(v); }
+__device__ __forceinline__ uint32_t wave_scan(uint32_t v) { return wave_scan_u32(v); }
+__device__ __forceinline__ double wave_scan(double v) { return wave_scan_f64(v); }
+template <typename T>
+__device__ __forceinline__ T max_identity() { return T(0); }
+template <>
+__device__ __forceinline__ float max_identity<float>() { return -INFINITY; }
+template <>
+__device__ __forceinline__ double max_identity<double>() { return -INFINITY; }
+
+template <typename T>
+__device__ __forceinline__ T block_sum(T v, T* red) {
+  v = wave_sum(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  const T s = wave_sum(lane() < nwaves() ? red[lane()] : T(0));
+  __syncthreads();
+  return s;
+}
+template <typename T>
+__device__ __forceinline__ T block_max(T v, T* red) {
+  v = wave_max(v);
+  if (lane() == 0) red[wave()] = v;
+  __syncthreads();
+  const T s = wave_max(lane() < nwaves() ? red[lane()] : max_identity<T>());
+  __syncthreads();
+  return s;
+}
+// Inclusive scan in thread order; *total receives the block total.
+template <typename T>
+__device__ __forceinline__ T block_scan_incl(T v, T* red, T* total) {
+  v = wave_scan(v);
+  if (lane() == 63) red[wave()] = v;
+  __syncthreads();
+  const T ws = wave_scan(lane() < nwaves() ? red[lane()] : T(0));
+  const T before = wave() ? readlane_t(ws, wave() - 1u) : T(0);
+  *total = readlane_t(ws, nwaves() - 1u);
+  __syncthreads();
+  return before + v;
+}
+// As block_scan_incl, and *excl receives the exclusive prefix computed so
+// that it is bit-identical to the previous thread's inclusive value: the
+// per-thread intervals (excl, incl] then tile (0, total] with no gap or
+// overlap even in floating point.
+template <typename T>
+__device__ __forceinline__ T block_scan_pair(T v, T* red, T* excl, T* total) {
+  const uint32_t l = lane();
+  v = wave_scan(v);
+  const T prev = __shfl_up(v, 1);
+  if (l == 63) red[wave()] = v;
+  __syncthreads();
+  const T ws = wave_scan(l < nwaves() ? red[l] : T(0));
+  const T before = wave() ? readlane_t(ws, wave() - 1u) : T(0);
+  *total = readlane_t(ws, nwaves() - 1u);
+  __syncthreads();
+  *excl = l == 0 ? before : before + prev;
+  return before + v;
 }
 
 constexpr int NBR = 2048;                 // radix-select bins (11 bits)
