@@ -3125,7 +3125,9 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   X.total = 0.0;
   X.total_err = 0.0;
   X.have_total = false;
-  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || mode == M_ALL || (mode == M_TOPK && A.masked))) {
+  // (an all-candidates row's working set is every legal token: its sum is
+  // the total)
+  if (c.top_p < 1.0 && !k_act && (mode == M_MINP || (mode == M_TOPK && A.masked))) {
     X.total = F.hdr.mass;
     X.total_err = F.hdr.mass_err;
     X.have_total = true;
@@ -4371,7 +4373,9 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
   stamp(A, row, chunk, 4);
   const bool mass32 = row_ok && nleg > 0 &&
                       ((mode == M_MINP && c.top_p < 1.0) || (mode == M_TOPK && masked_row));
-  const bool mass64 = row_ok && nleg > 0 && (mode == M_ALL || mode == M_KEEPALL);
+  // (all-candidates rows emit every legal token: the finisher's own f64
+  // sum over its working set is their row total, no chunk mass needed)
+  const bool mass64 = row_ok && nleg > 0 && mode == M_KEEPALL;
   uint32_t cnt_i[PER_MAX];
   double m0 = 0.0, m1 = 0.0;
   {
@@ -4426,9 +4430,29 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
           m1 += (double)ew;
         } else if (mass64) {
           double sw = 0.0;
+          if (masked_row) {
+            // legal tokens are sparse: the wave's legal logits of the slice
+            // are packed into its own 256-float stretch of the count table
+            // (dead after pass 1) and weighted one per lane, instead of an
+            // f64 weight per element position any lane holds
+            float* cb = reinterpret_cast<float*>(S.t.ct) + wave() * 256u;
+            uint32_t nb = 0;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            sw += ((qb >> e) & 1u) ? exp_neg_t(((double)lv[i][e] - md) * invT, S.etab, S.etab + 64) : 0.0;
+            for (int e = 0; e < 4; ++e) {
+              const bool lg = (qb >> e) & 1u;
+              const uint64_t bm = __builtin_amdgcn_ballot_w64(lg);
+              if (lg) cb[nb + lanes_below(bm)] = lv[i][e];
+              nb += (uint32_t)__builtin_popcountll(bm);
+            }
+            wave_lds_sync();
+            for (uint32_t k = lane(); k < nb; k += 64u)
+              sw += exp_neg_t(((double)cb[k] - md) * invT, S.etab, S.etab + 64);
+            wave_lds_sync();
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              sw += ((qb >> e) & 1u) ? exp_neg_t(((double)lv[i][e] - md) * invT, S.etab, S.etab + 64) : 0.0;
+          }
           m0 += sw;
           if (mode == M_KEEPALL) {
             const double ws = wave_sum_f64(sw);
