@@ -2496,31 +2496,36 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
     if (bstar != NONE && cm <= 64u) {
       binned = true;
       if (wave() == 0) {
-        // sort the members by (key desc, ID asc); each lane's weight from its key
+        // rank the members by (key desc, ID asc): each lane sums the weights
+        // of the members ahead of it (one pass over the members, no sort)
         const uint32_t ln = lane();
-        const bool mine = ln < cm;
-        const unsigned long long sk =
-            wave_sort_desc(mine ? ((unsigned long long)F.u.h.hcnt[ln] << 32) | (unsigned long long)(~F.eidx[ln]) : 0ull);
-        const bool live = ln < cm;   // sorted: the members occupy lanes 0 .. cm - 1
-        const uint32_t key = (uint32_t)(sk >> 32), id = ~(uint32_t)sk;
+        const bool live = ln < cm;
+        const uint32_t key = live ? F.u.h.hcnt[ln] : 0u, id = live ? F.eidx[ln] : NONE;
         const double sh = exact_s ? ((double)okey_value(key) - X.M) / c.T : ((double)okey_value(key) - X.M) * invT;
         const double w = live ? exp_neg_t(sh, X.etab, X.etab + 64) : 0.0;
+        double pre = 0.0;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < cm; ++j) {
+          const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)key, (int)j);
+          const uint32_t ij = (uint32_t)__builtin_amdgcn_readlane((int)id, (int)j);
+          const double wj = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, w), j));
+          const bool ahead = kj > key || (kj == key && ij < id);
+          pre += ahead ? wj : 0.0;
+          rank += ahead ? 1u : 0u;
+        }
         const double above = F.s_d[4];
         const uint32_t above_n = F.s_u[5];
-        const double cum = above + wave_scan_f64(w);   // after this member
-        const double prev = cum - w;
-        const uint64_t hit = __builtin_amdgcn_ballot_w64(live && cum >= theta);
+        const double prev = above + pre, cum = prev + w;   // before and after this member
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(live && prev < theta && theta <= cum);
         if (ln == 0) { F.s_u[3] = NONE; F.s_u[11] = NONE; F.s_u[7] = 1u; }
         if (hit) {
           const uint32_t i = (uint32_t)__builtin_ctzll(hit);
           if (ln == i) {
-            const double e1 = sum_bound(cum, above_n + i + 65u, 8.0), e0 = sum_bound(prev, above_n + i + 64u, 8.0);
-            const bool cert = (i == 0u ? above + sum_bound(above, above_n + 64u, 8.0) < theta - theta_err
-                                       : prev + e0 < theta - theta_err) &&
-                              cum - e1 >= theta + theta_err;
+            const double e1 = sum_bound(cum, above_n + rank + 65u, 8.0), e0 = sum_bound(prev, above_n + rank + 64u, 8.0);
+            const bool cert = prev + e0 < theta - theta_err && cum - e1 >= theta + theta_err;
             F.s_u[3] = id;
             F.s_u[11] = key;
-            F.s_u[7] = cert ? 0u : 1u;
+            F.s_u[7] = cert && __builtin_popcountll(hit) == 1 ? 0u : 1u;
           }
         }
       }
