@@ -58,6 +58,7 @@ constexpr int MCAP = ((CHUNK_MAX / 32 + 2 + NT - 1) / NT) * NT;
 #define MXS_LA 3
 #endif
 constexpr int LA = MXS_LA;                // slices in flight ahead of pass 1 (lean chunk body)
+constexpr uint32_t WIDE_NCAND = 2048;     // a min-p chunk past this many candidates sums its mass in f64
 static_assert(HCAP % NT == 0 && BCAP % NT == 0 && MCAP % NT == 0,
               "LDS staging copies whole 1024-entry rounds");
 static_assert(HB == NT, "one histogram bin per thread");
@@ -3849,6 +3850,41 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     const uint32_t s1 = (uint32_t)__builtin_amdgcn_readlane((int)i1, 63);
     const uint32_t s2 = (uint32_t)__builtin_amdgcn_readlane((int)i2, 63);
     ncand = s0 + s1 + s2;
+    if constexpr (MODE == M_MINP) {
+      if (do_mass && row_ok && ncand > WIDE_NCAND) {
+        // A wide min-p set: its nucleus cut can fall between tokens that
+        // each carry about 1e-5 of the row mass, finer than the f32 mass's
+        // bound, so the chunk mass is summed again from f64 weights relative
+        // to the chunk maximum (penalised tokens by their owners; the count
+        // table, still intact here, marks them).
+        double part = 0.0;
+#pragma unroll
+        for (int i = 0; i < PER_MAX; ++i) {
+          if (i < (int)A.per) {
+            uint32_t skip = 0;
+            if constexpr (HIST) {
+              if ((pq >> i) & 1u) {
+                const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
+                skip = ((cw.x & 0xffffu) ? 1u : 0u) | ((cw.x >> 16) ? 2u : 0u) | ((cw.y & 0xffffu) ? 4u : 0u) |
+                       ((cw.y >> 16) ? 8u : 0u);
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (!((skip >> e) & 1u)) part += exp_neg_p(((double)lv[i][e] - md) * invT);
+          }
+        }
+        if constexpr (HIST) {
+#pragma unroll
+          for (int r = 0; r < HCAP / NT; ++r)
+            if ((own >> r) & 1u) part += exp_neg_p(((double)pvals[(uint32_t)r * NT + tid] - md) * invT);
+        }
+        mass = block_sum<double>(part, reinterpret_cast<double*>(S.wq));
+        // 2 ulp per weight plus the sums (sum_bound), and the rounding of
+        // (l - m) / T as a product (at most 3 ulp of it: w |x| 3 2^-53 <= 3 2^-53 / e)
+        mass_err = sum_bound(mass, nleg + (uint32_t)NT, 8.0) + 3.0 * 0.37 * (double)nleg * mxs::U;
+      }
+    }
     const uint32_t x0 = i0 - v0, x1 = i1 - v1 + s0, x2 = i2 - v2 + s0 + s1;
     const uint64_t cbase = (uint64_t)row * V + c0;
     // Candidates are staged in LDS (the count table is dead by now) and then

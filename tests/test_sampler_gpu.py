@@ -227,19 +227,51 @@ def selection_batch(seed, rows, V):
 
 @pytest.mark.parametrize("seed", [1, 2])
 def test_selection_finisher_mix(torch_mod, sampler, orc, seed):
-    """Parity over the selection finisher's range.  Rows whose nucleus holds
-    more than 8192 tokens (min_p 0.001 at high temperature) take the
-    large-set path, whose nucleus cut rests on the chunk pass's f32 row mass
-    (error bound about 5e-6 of the total): there a cut that falls within
-    the bound of a token boundary is flagged uncertified, and only there."""
+    """Parity over the selection finisher's range, every row certified.
+    Rows whose nucleus holds more than 8192 tokens (min_p 0.001 at high
+    temperature) take the large-set path; their nucleus cut rests on the
+    row mass, which the chunks sum from f64 weights once a chunk holds more
+    than 2048 min-p candidates (an f32 mass's bound, about 5e-6 of the
+    total, is coarser than one token's share there)."""
     b = selection_batch(seed, 64, 151936)
     say(f"case {b.name}: rows {b.rows} vocab {b.vocab}")
     ref = orc.sample_batch(b, debug=True)
     gpu = run_gpu(torch_mod, sampler, b)
     wide = np.asarray(ref["kept"]).sum(axis=1) > 8192
     unc = np.asarray(gpu["status"]) == 1
-    assert not (unc & ~wide).any(), f"uncertified outside the wide-nucleus rows: {np.nonzero(unc & ~wide)[0]}"
-    compare(b, gpu, ref, allow_uncertified=int(wide.sum()))
+    say(f"wide rows {int(wide.sum())}, uncertified {int(unc.sum())}")
+    assert wide.any()
+    compare(b, gpu, ref)
+
+
+def test_wide_min_p_nuclei_certified(torch_mod, sampler, orc):
+    """Rows whose min-p set is most of the vocabulary (min_p 0.001 at
+    temperatures 2 to 4, with and without penalties) and whose top-p
+    nucleus holds tens of thousands of tokens: each token carries about
+    1e-5 of the row mass, and every row's cut and draw must still be
+    certified and match the reference."""
+    from metallix_amd.synth import Batch
+
+    rng = np.random.default_rng(4242)
+    rows, V = 24, 151936
+    x = (rng.standard_normal((rows, V)) * 2.0).astype(np.float32)
+    for r in range(rows):
+        ids = rng.choice(V, size=int(rng.integers(1, 30)), replace=False)
+        x[r, ids] += rng.uniform(2.0, 6.0, size=len(ids)).astype(np.float32)
+    hist = rng.integers(0, V, size=rows * 512).astype(np.uint32)
+    pen = np.arange(rows) % 2 == 0
+    b = Batch(name="wide-min-p", logits=x, temperature=rng.choice([2.0, 3.0, 4.0], size=rows),
+              uniform=rng.random(rows), top_k=np.zeros(rows, np.uint32), top_p=rng.choice([0.5, 0.7, 0.9], size=rows),
+              min_p=np.full(rows, 0.001), repetition=np.where(pen, 1.2, 1.0).astype(np.float32),
+              presence=np.where(pen, 0.4, 0.0).astype(np.float32), frequency=np.where(pen, 0.2, 0.0).astype(np.float32),
+              history_offsets=(np.arange(rows + 1, dtype=np.uint32) * 512), history_ids=hist)
+    say(f"case {b.name}: rows {b.rows} vocab {b.vocab}")
+    ref = orc.sample_batch(b, debug=True)
+    gpu = run_gpu(torch_mod, sampler, b)
+    kept = np.asarray(ref["kept"]).sum(axis=1)
+    say(f"kept sizes {int(kept.min())}..{int(kept.max())}")
+    assert (kept > 8192).all()
+    compare(b, gpu, ref)
 
 
 def test_min_p_near_one_over_log_softmax(torch_mod, sampler, orc):
