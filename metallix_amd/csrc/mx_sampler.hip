@@ -2708,6 +2708,82 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
 }
 
 // ---------------------------------------------------------------------------
+// The k-th largest (1 <= k <= active count) of the wave's active keys (WR per
+// lane, logits lv) and how many are larger, from one value histogram: 256
+// bins between lo (no active logit is below it) and the maximum Mf, the bin
+// index never decreasing as the logit decreases, the crossing bin found by a
+// scan, and its members ranked exactly.  False when the range is degenerate
+// or the crossing bin holds more than 64 members (ties, a narrow crowd): the
+// caller then takes the radix select.
+__device__ __forceinline__ bool wave_kth_bin(uint32_t* h, uint32_t* mk, const float (&lv)[WR],
+                                             const uint32_t (&key)[WR], uint32_t act, uint32_t k, float Mf, float lo,
+                                             uint32_t* kappa, uint32_t* above) {
+  const float span = Mf - lo;
+  if (!(span > 1e-30f) || !__builtin_isfinite(span)) return false;
+  const float sc = 255.0f / span;
+  const uint32_t ln = lane();
+  *reinterpret_cast<uint4*>(&h[4u * ln]) = make_uint4(0u, 0u, 0u, 0u);
+  wave_lds_sync();
+  uint32_t bin[WR];
+#pragma unroll
+  for (int r = 0; r < WR; ++r) {
+    const float d = (Mf - lv[r]) * sc;
+    bin[r] = d < 255.0f ? (uint32_t)d : 255u;
+    if ((act >> r) & 1u) atomicAdd(&h[bin[r]], 1u);
+  }
+  wave_lds_sync();
+  const uint4 v = *reinterpret_cast<const uint4*>(&h[4u * ln]);
+  const uint32_t c4[4] = {v.x, v.y, v.z, v.w};
+  const uint32_t s = c4[0] + c4[1] + c4[2] + c4[3];
+  const uint32_t inc = wave_scan_u32(s);
+  const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= k);
+  if (!reach) return false;
+  const uint32_t L = (uint32_t)__builtin_ctzll(reach);
+  uint32_t run = inc - s, b = 0u, bef = 0u;
+  bool found = false;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (!found && run + c4[i] >= k) { found = true; b = 4u * ln + (uint32_t)i; bef = run; }
+    run += c4[i];
+  }
+  b = (uint32_t)__builtin_amdgcn_readlane((int)b, (int)L);
+  bef = (uint32_t)__builtin_amdgcn_readlane((int)bef, (int)L);
+  // the crossing bin's members, packed to lanes
+  uint32_t mb = 0;
+#pragma unroll
+  for (int r = 0; r < WR; ++r) mb |= ((act >> r) & 1u) && bin[r] == b ? 1u << r : 0u;
+  const uint32_t cnt = (uint32_t)__builtin_popcount(mb);
+  const uint32_t pinc = wave_scan_u32(cnt);
+  const uint32_t cm = bcast63(pinc);
+  if (cm > 64u) return false;
+  wave_lds_sync();   // every lane has read h before mk (which may share it) is written
+  {
+    uint32_t at = pinc - cnt;
+#pragma unroll
+    for (int r = 0; r < WR; ++r)
+      if ((mb >> r) & 1u) mk[at++] = key[r];
+  }
+  wave_lds_sync();
+  const bool mine = ln < cm;
+  const uint32_t a = mine ? mk[ln] : 0u;
+  uint32_t ge = 0, gt = 0;
+  for (uint32_t j = 0; j < cm; ++j) {
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)a, (int)j);
+    ge += kj >= a ? 1u : 0u;
+    gt += kj > a ? 1u : 0u;
+  }
+  // kappa: the largest member key with at least `need` members at or above it
+  const uint32_t need = k - bef;
+  const bool cand = mine && ge >= need;
+  const uint32_t kap = wave_max_u32(cand ? a : 0u);
+  const uint64_t at_k = __builtin_amdgcn_ballot_w64(mine && a == kap);
+  const uint32_t g = (uint32_t)__builtin_amdgcn_readlane((int)gt, (int)__builtin_ctzll(at_k));
+  *kappa = kap;
+  *above = bef + g;
+  return true;
+}
+
+// ---------------------------------------------------------------------------
 // The short one-wave finisher: top-k rows with k <= 64 and min-p rows, at
 // most WR * 64 candidates (lane l holds candidates WR l .. WR l + WR - 1 from
 // LDS, so lane order is token-ID order) and a working set E of at most 64
@@ -2751,7 +2827,9 @@ __device__ __forceinline__ bool finish_w1(const FinCtx& X, FinSmem& F) {
   if (X.k_path) {
     if (c.k > 64u || c.k > n) return false;
     uint32_t kappa, above;
-    if (!wave_kth(F.eidx, key, act, c.k, &kappa, &above)) return false;
+    if (!wave_kth_bin(F.eidx, F.eidx + 256, lv, key, act, c.k, (float)X.M, F.hdr.lo, &kappa, &above) &&
+        !wave_kth(F.eidx, key, act, c.k, &kappa, &above))
+      return false;
     const uint32_t need_t = c.k - above;
     uint32_t tie = 0;
 #pragma unroll
@@ -2838,27 +2916,60 @@ __device__ __forceinline__ bool finish_w1(const FinCtx& X, FinSmem& F) {
   }
   bool kept = inp;
   if (theta_set && !(psum + sum_bound(psum, np, 8.0) < theta - theta_err)) {
-    // The nucleus can end inside P: each member takes the mass of the P
-    // members ranked before it; the reference keeps a member whose running
-    // sum before it is still below theta.
-    double pre = 0.0;
-    uint32_t rank = 0;
-    uint64_t m = pmask;
-    while (m) {
-      const uint32_t j = (uint32_t)__builtin_ctzll(m);
-      m &= m - 1ull;
-      const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)j);
-      const uint32_t pj = (uint32_t)__builtin_amdgcn_readlane((int)mp, (int)j);
-      const double wj = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, w), j));
-      const bool ahead = kj > mk || (kj == mk && pj < mp);
-      pre += ahead ? wj : 0.0;
-      rank += ahead ? 1u : 0u;
+    // The nucleus can end inside P.  P's masses on 64 value bins (bin 0
+    // holds the largest logits; lane b reads bin b), one scan finds the bin
+    // where the prefix reaches theta, and only that bin's members take the
+    // mass of the members ranked before them; the reference keeps a member
+    // whose running sum before it is still below theta.
+    const float Mf = (float)X.M;
+    const float plo = okey_value(~wave_max_u32(inp ? ~okey(ml) : 0u));   // P's smallest logit
+    const float span = Mf - plo;
+    const float sc = span > 1e-30f && __builtin_isfinite(span) ? 63.0f / span : 0.0f;
+    const float d = (Mf - ml) * sc;
+    const uint32_t pb = d < 63.0f ? (uint32_t)d : 63u;
+    double* bm = reinterpret_cast<double*>(F.eidx + 512);
+    bm[ln] = 0.0;
+    wave_lds_sync();
+    if (inp) atomicAdd(&bm[pb], w);
+    wave_lds_sync();
+    const double bv = bm[ln];
+    const double binc = wave_scan_f64(bv);
+    const uint64_t cross = __builtin_amdgcn_ballot_w64(binc >= theta);
+    if (!cross) {
+      // P's mass stays below theta: every member is kept when the bound clears it
+      const double tot = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, binc), 63));
+      if (!(tot + sum_bound(tot, np + 64u, 8.0) < theta - theta_err)) return false;
+    } else {
+      const uint32_t b = (uint32_t)__builtin_ctzll(cross);
+      const double bef = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, binc - bv), b));
+      const uint64_t inb = __builtin_amdgcn_ballot_w64(inp && pb == b);
+      const uint32_t nbef = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(inp && pb < b));
+      double pre = 0.0;
+      uint32_t rank = 0;
+      uint64_t m = inb;
+      while (m) {
+        const uint32_t j = (uint32_t)__builtin_ctzll(m);
+        m &= m - 1ull;
+        const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)j);
+        const uint32_t pj = (uint32_t)__builtin_amdgcn_readlane((int)mp, (int)j);
+        const double wj = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(unsigned long long, w), j));
+        const bool ahead = kj > mk || (kj == mk && pj < mp);
+        pre += ahead ? wj : 0.0;
+        rank += ahead ? 1u : 0u;
+      }
+      const bool mb = inp && pb == b;
+      const double prev = bef + pre, cum = prev + w;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(mb && prev < theta && theta <= cum);
+      if (__builtin_popcountll(hit) != 1) return false;
+      const uint32_t hx = (uint32_t)__builtin_ctzll(hit);
+      const uint32_t nb = nbef + rank;
+      const bool cert = prev + sum_bound(prev, nb + 64u, 8.0) < theta - theta_err &&
+                        cum - sum_bound(cum, nb + 65u, 8.0) >= theta + theta_err;
+      if (!__builtin_amdgcn_readlane((int)cert, (int)hx)) return false;
+      const uint32_t ck = (uint32_t)__builtin_amdgcn_readlane((int)mk, (int)hx);
+      const uint32_t cp = (uint32_t)__builtin_amdgcn_readlane((int)mp, (int)hx);
+      kept = inp && (pb < b || (pb == b && (mk > ck || (mk == ck && mp <= cp))));
     }
-    const double ep_ = sum_bound(pre, rank + 1u, 8.0);
-    const bool in_c = pre + ep_ < theta - theta_err;    // certainly before the cut
-    const bool out_c = pre - ep_ >= theta + theta_err;  // certainly after it
-    if (__builtin_amdgcn_ballot_w64(inp && !in_c && !out_c)) return false;
-    kept = inp && in_c;
   }
   sel_draw_wave(X, kept, w, s, mid, unc);
   return true;
