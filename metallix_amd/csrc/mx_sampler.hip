@@ -4108,13 +4108,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
       uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
       const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
-      if (last) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        st_dev(ctr, 0u);
-        // every chunk's exchange update precedes its arrival: clear the
-        // row's word so no value outlives this call
-        st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
-      }
+      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       S.xkey = last;
     }
     __syncthreads();
@@ -4746,13 +4740,7 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
       uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
       const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       last = prev + 1u == A.C ? 1u : 0u;
-      if (last) {
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        st_dev(ctr, 0u);
-        // every chunk's exchange update precedes its arrival: clear the
-        // row's word so no value outlives this call
-        st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
-      }
+      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       S.xkey = last;
     }
     __syncthreads();
@@ -4816,6 +4804,15 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   fin_issue(A, row, P);
   finish_row<In>(A, U.f, c, row, mode, (uint64_t)row * V, c.greedy ? 0.0 : 1.0 / c.T, P);
   stamp(A, row, MAXC, 7);
+  // The row's counter and exchange word are cleared for the next call here,
+  // after the finisher: every chunk has arrived (its exchange update came
+  // before), and stores issued at the arrival would hold the finisher's
+  // first loads behind their completion (a wave's memory counter is in
+  // order).
+  if (threadIdx.x == 0) {
+    st_dev(A.w.ctr + (uint64_t)row * CTR_STRIDE, 0u);
+    st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
+  }
 }
 
 }  // namespace mxs
