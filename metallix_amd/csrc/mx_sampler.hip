@@ -2412,9 +2412,12 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
       }
     }
   }
-  const double esum = block_sum<double>(wpart, F.red_d);
-  wmin = -block_max<double>(-wmin, F.red_d);
-  lmin = -block_max<float>(-lmin, F.red_f);
+  if (tid == 0) { F.s_u[13] = 0u; F.s_u[14] = 0u; }   // the kept pass's flags (ordered by the barriers below)
+  double esum = wpart, nwmin = -wmin;
+  float nlmin = -lmin;
+  block_sum_max_max(&esum, &nwmin, &nlmin, F.rd, F.red_f);
+  wmin = -nwmin;
+  lmin = -nlmin;
   double total = X.total, total_err = X.total_err;
   if (!X.have_total) { total = esum; total_err = sum_bound(esum, ne, 8.0); }
   fstamp(X, 4);
@@ -2466,9 +2469,9 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
 #pragma unroll
     for (uint32_t i = 0; i < BPT; ++i) { msum += F.u.h.hmass[b0 + i]; nsum += F.u.h.hcnt[b0 + i]; }
     double mtot, mexc;
-    uint32_t ntot;
-    const double minc = block_scan_pair<double>(msum, F.red_d, &mexc, &mtot);
-    const uint32_t nexc = block_scan_incl<uint32_t>(nsum, F.red_u, &ntot) - nsum;
+    uint32_t ntot, ninc;
+    const double minc = block_scan_pair_du(msum, nsum, F.red_d, F.red_u, &mexc, &mtot, &ninc, &ntot);
+    const uint32_t nexc = ninc - nsum;
     {
       double lo = mexc;
       uint32_t nlo = nexc;
@@ -2649,15 +2652,17 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
     ++kn;
     if (!isfinite(sv[r]) && !isfinite(((double)F.cl[j0 + r] - X.M) / c.T)) bad = 1;
   }
-  if (block_max<uint32_t>(bad, F.red_u)) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
-  if (block_max<uint32_t>(close, F.red_u)) uncert = true;
-  const uint32_t nkept = block_sum<uint32_t>(kn, F.red_u);
+  if (bad) F.s_u[13] = 1u;
+  if (close) F.s_u[14] = 1u;
   if (tid == 0) { F.s_u[0] = NONE; F.s_u[1] = 0u; F.s_u[2] = 0u; }
-  // the draw: one scan of the per-thread kept masses; the threads'
-  // intervals tile (0, S] exactly, and inside a thread the last positive
-  // weight's interval ends at the thread's inclusive prefix
+  // the draw: one scan of the per-thread kept masses (and counts); the
+  // threads' intervals tile (0, S] exactly, and inside a thread the last
+  // positive weight's interval ends at the thread's inclusive prefix
   double kexc, S;
-  const double kinc = block_scan_pair<double>(kpart, F.red_d, &kexc, &S);
+  uint32_t kninc, nkept;
+  const double kinc = block_scan_pair_du(kpart, kn, F.red_d, F.red_u, &kexc, &S, &kninc, &nkept);
+  if (F.s_u[13]) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return; }
+  if (F.s_u[14]) uncert = true;
   const double target = c.u * S;
   const double derr = sum_bound(S, nkept + 64u, 8.0);
   fstamp(X, 6);

@@ -442,6 +442,41 @@ __device__ __forceinline__ T block_scan_pair(T v, T* red, T* excl, T* total) {
   return before + v;
 }
 
+// Two or three reductions for the price of one barrier pair: the block's
+// sum of s, maximum of a and maximum of b (all threads receive them).
+__device__ __forceinline__ void block_sum_max_max(double* s, double* a, float* b, double (*rd)[2], float* rf) {
+  double vs = wave_sum(*s), va = wave_max(*a);
+  float vb = wave_max(*b);
+  if (lane() == 0) { rd[wave()][0] = vs; rd[wave()][1] = va; rf[wave()] = vb; }
+  __syncthreads();
+  const bool l = lane() < nwaves();
+  *s = wave_sum(l ? rd[lane()][0] : 0.0);
+  *a = wave_max(l ? rd[lane()][1] : -INFINITY);
+  *b = wave_max(l ? rf[lane()] : -INFINITY);
+  __syncthreads();
+}
+// block_scan_pair of an f64 together with an inclusive u32 scan (one
+// barrier pair for both).
+__device__ __forceinline__ double block_scan_pair_du(double v, uint32_t n, double* red_d, uint32_t* red_u, double* excl,
+                                                     double* total, uint32_t* nincl, uint32_t* ntotal) {
+  const uint32_t l = lane();
+  v = wave_scan(v);
+  n = wave_scan(n);
+  const double prev = __shfl_up(v, 1);
+  if (l == 63) { red_d[wave()] = v; red_u[wave()] = n; }
+  __syncthreads();
+  const double ws = wave_scan(l < nwaves() ? red_d[l] : 0.0);
+  const uint32_t wn = wave_scan(l < nwaves() ? red_u[l] : 0u);
+  const double before = wave() ? readlane_t(ws, wave() - 1u) : 0.0;
+  const uint32_t nbefore = wave() ? readlane_t(wn, wave() - 1u) : 0u;
+  *total = readlane_t(ws, nwaves() - 1u);
+  *ntotal = readlane_t(wn, nwaves() - 1u);
+  __syncthreads();
+  *excl = l == 0 ? before : before + prev;
+  *nincl = nbefore + n;
+  return before + v;
+}
+
 constexpr int NBR = 2048;                 // radix-select bins (11 bits)
 
 // LDS word of histogram bin b.  Lane j of a wave owns the 32 bins
