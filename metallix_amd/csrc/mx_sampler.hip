@@ -4865,7 +4865,14 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
   const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
   const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
-  const mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
+  // A batch whose chunks would not fill the CUs streams each row with twice
+  // as many workgroups (half the quads per thread), while the doubled count
+  // stays within the register-slot finishers' FW chunks.
+  mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
+  if ((uint64_t)b->rows * L.C < 256u) {
+    const mxs::ChunkLayout L2 = mxs::chunk_layout(b->vocab, (uint32_t)mxs::PER_MAX / 2u);
+    if (L2.C <= (uint32_t)mxs::FW) L = L2;
+  }
   const uint32_t C = L.C;
   A.C = L.C;
   A.CH = L.CH;

@@ -38,8 +38,10 @@ def sampler(torch_mod):
     s.close()
 
 
-def path_batch():
-    """One row per path: (expected path, logits, T, top_k, top_p, min_p)."""
+def path_batch(pad=0):
+    """One row per path: (expected path, logits, T, top_k, top_p, min_p),
+    then `pad` top-k rows named PAD (no expected path) that bring the batch
+    to the row count where each row streams in the default chunk layout."""
     from metallix_amd.synth import Batch
 
     rng = np.random.default_rng(2365)
@@ -86,6 +88,8 @@ def path_batch():
     # sequential sums settle
     rows.append(("EXACT_REPLAY", groups((7000, 5.0)), 1.0, 1200, 0.5, 0.0))
     rows.append(("LARGE", crowd(10000, step=1e-4), 1.0, 0, 0.7, 0.0))
+    for _ in range(pad):
+        rows.append(("PAD", noise(2.0), 0.8, 50, 0.9, 0.05))
     names = [r[0] for r in rows]
     words = (V + 31) // 32
     mask = np.full((len(rows), words), 0xFFFFFFFF, dtype=np.uint32)
@@ -107,7 +111,7 @@ def say(msg):
 
 def test_every_finisher_path(torch_mod, sampler, orc):
     torch = torch_mod
-    names, b = path_batch()
+    names, b = path_batch(pad=64 - 11)
     say(f"case finisher-paths: rows {b.rows} vocab {b.vocab}")
     buf = torch.zeros(b.rows, dtype=torch.int32, device="cuda")
     sampler.lib.mxs_debug_set_paths(sampler.ctx, buf.data_ptr())
@@ -117,7 +121,7 @@ def test_every_finisher_path(torch_mod, sampler, orc):
         sampler.lib.mxs_debug_set_paths(sampler.ctx, None)
     got = buf.cpu().numpy()
     inv = {v: k for k, v in PATHS.items()}
-    wrong = [(n, inv.get(int(p), int(p))) for n, p in zip(names, got) if PATHS[n] != int(p)]
+    wrong = [(n, inv.get(int(p), int(p))) for n, p in zip(names, got) if n != "PAD" and PATHS[n] != int(p)]
     assert not wrong, f"rows took other paths: {wrong}"
     ref = orc.sample_batch(b, debug=True)
     compare(b, gpu, ref, allow_uncertified=1)
@@ -147,3 +151,21 @@ def test_every_finisher_path(torch_mod, sampler, orc):
     for r in range(b.rows):
         if st[r] == 0 and names[r] != "LARGE":
             assert tok[r] == rref["token"][r], (names[r], tok[r], rref["token"][r])
+
+
+def test_path_rows_small_batch(torch_mod, sampler, orc):
+    """The same rows as one 11-row batch: fewer chunks than CUs, so each
+    row streams in twice as many chunks (and its candidates reach the
+    finishers from eight chunk lists instead of four).  Parity only: the
+    paths follow from the layout.  The replay row's 7000 equal logits
+    split into eight chunks of about 875, fewer than its k = 1200, so every
+    chunk also emits its 19000 floor logits (ties at its k-th value): the row
+    reaches the candidate-list finisher, which has no replay and reports the
+    exact token-boundary nucleus as uncertified."""
+    names, b = path_batch()
+    say(f"case finisher-paths-small: rows {b.rows} vocab {b.vocab}")
+    gpu = run_gpu(torch_mod, sampler, b)
+    ref = orc.sample_batch(b, debug=True)
+    compare(b, gpu, ref, allow_uncertified=2)
+    unc = [names[r] for r in np.nonzero(gpu["status"] == 1)[0]]
+    assert set(unc) <= {"LARGE", "EXACT_REPLAY"}, unc
