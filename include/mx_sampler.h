@@ -26,6 +26,11 @@
  *   mxs_spec_verify           <- engine::speculative::accept_or_resample
  *                                (crates/core/engine/src/speculative.rs:369-444) applied
  *                                position by position as in speculative_step (:202-227).
+ *   mxs_step                  <- the per-row pick loop of EngineLoop::decode_now
+ *                                (crates/app/cli/src/engine_loop.rs:1080-1134) through
+ *                                TurnLoop::pick (chat_turn.rs:290-303): ChatFormat::suppress,
+ *                                the pick, and token_logprob's receipt (chat_turn.rs:506-563)
+ *                                for every row of the batch in one call.
  *   mxs_sync                  <- Qwen3TokenPicks::wait (picks.rs:390-401).
  *   mxs_last_error            <- KernelError's message (mlx-kernels/src/lib.rs:444-450).
  *
@@ -175,6 +180,33 @@ int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int32_t dtype,
                                 uint32_t vocab, uint64_t row_stride, uint32_t n, int32_t* ids,
                                 double* logprobs, double* maximum, double* log_normalizer,
                                 int32_t* status);
+/* Log-probability receipts of one step (TokenLogprob, chat_turn.rs:506-563):
+ * over each row's logits after suppression (the batch's bias entries of
+ * -INFINITY read as f32::MIN, ChatFormat::suppress, chat-format/src/lib.rs:
+ * 771-780) and nothing else, the n most likely IDs by (total_cmp
+ * descending, ID ascending) with f64(l) - maximum - log_normalizer, and the
+ * picked token's log probability.  n is the largest top_logprobs + 8, the
+ * over-selection the reference ranks before it drops unspellable IDs.
+ * Device arrays; rows whose `top` entry is 0 are not written. */
+typedef struct {
+  const uint32_t* top;            /* rows entries: the row's top_logprobs, 0 => no receipt; NULL => every row */
+  uint32_t n;                     /* entries per row of ids and logprobs, 1..64 */
+  uint32_t reserved;
+  int32_t* ids;                   /* rows x n; -1 past the vocabulary */
+  double* logprobs;               /* rows x n; -inf past the vocabulary */
+  double* token_logprob;          /* rows: the picked token's; NaN when the row has no token */
+  int32_t* status;                /* rows: 0, or MXS_ROW_NON_FINITE_LOGIT */
+} mxs_receipts;
+
+/* One engine step: the pick of every row (mxs_sample, or mxs_sample_race
+ * when `race` is given), then, when `receipts` is given, the receipts of
+ * the rows that want one, queued behind the picks on the context's stream
+ * (their token_logprob reads out->token on the device).  Replaces the
+ * reference's per-row host loop; which receipts to keep (a stop token takes
+ * none, TurnLoop::receipt_wanted, chat_turn.rs:413-418) and the drop of
+ * unspellable IDs stay with the caller. */
+int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const mxs_out* out,
+             const mxs_receipts* receipts);
 int mxs_sync(mxs_ctx* ctx);
 /* Diagnostics (no reference counterpart): when `device_buffer` is non-null,
  * mxs_sample records 100 MHz wall-clock stamps at fixed phase boundaries:

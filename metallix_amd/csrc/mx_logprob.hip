@@ -25,6 +25,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <float.h>
 #include <math.h>
 #include <string.h>
 
@@ -61,11 +62,23 @@ struct TopnArgs {
   uint32_t rows, V, n, C;
   int32_t* ids;
   double* logprobs;
-  double* maximum;
-  double* lognorm;
+  double* maximum;              // nullptr: not written
+  double* lognorm;              // nullptr: not written
   int32_t* status;
   TopnStat* stat;               // [rows * C]
   unsigned long long* list;     // [rows * C * n], (okey << 32) | ~id, descending
+  // Step receipts (mxs_step): rows whose want entry is 0 are skipped; the
+  // bias CSR's -inf entries are the suppressed tokens, read as f32::MIN
+  // (ChatFormat::suppress, crates/core/chat-format/src/lib.rs:771-780);
+  // token_lp[row] is the picked token's log probability.  All nullptr for
+  // mxs_logsoftmax_topn.
+  const uint32_t* want;
+  const uint32_t* sup_off;
+  const uint32_t* sup_ids;
+  const float* sup_vals;
+  const int32_t* token;
+  double* token_lp;
+  uint32_t bf16;                // logits are bf16 (the merge's token read)
 };
 
 struct alignas(16) TopnSmem {
@@ -75,6 +88,7 @@ struct alignas(16) TopnSmem {
   } u;
   unsigned long long top[TOPN_MAX];                  // the exact select's list
   double etab[128];                                  // 2^(j/64) and its low parts (exp_neg_t)
+  uint32_t supw[TCH / 32];                           // the chunk's suppressed tokens (one bit each)
   uint32_t wcnt[TQ * TNW];
   uint32_t wkept[TNW];
   uint32_t red_u[3][TNW];
@@ -89,7 +103,7 @@ __device__ __forceinline__ unsigned long long entry_key(uint32_t k, uint32_t id)
 
 template <typename In>
 __device__ __noinline__ void exact_list(unsigned long long* list, TopnSmem& S, const In* src, uint32_t c0, uint32_t c1,
-                                        uint32_t take) {
+                                        uint32_t take, bool sup) {
   const uint32_t tid = threadIdx.x;
   if (tid == 0) S.s_cnt = 0u;
   uint32_t keys[TQ * 4];
@@ -98,8 +112,10 @@ __device__ __noinline__ void exact_list(unsigned long long* list, TopnSmem& S, c
     const uint32_t e0 = c0 + (uint32_t)q * TSL + tid * 4u;
     float v[4];
     Quad<In>::unpack(Quad<In>::load(src + (e0 < c1 ? e0 : c0)), v);
+    const uint32_t sb = sup ? (S.supw[(uint32_t)q * (TSL / 32u) + (tid >> 3)] >> ((tid & 7u) * 4u)) : 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
+      if ((sb >> e) & 1u) v[e] = -FLT_MAX;
       keys[q * 4 + e] = okey(v[e]);
       if (e0 + (uint32_t)e < c1) act |= 1ull << (q * 4 + e);
     }
@@ -168,6 +184,7 @@ __global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
   const uint32_t chunk = blockIdx.x >> 3;
   const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= A.rows) return;
+  if (A.want && A.want[row] == 0u) return;   // a step row without a receipt
   const uint32_t V = A.V;
   const uint32_t c0 = chunk * TCH;
   const uint32_t c1 = min(V, c0 + TCH);
@@ -188,11 +205,45 @@ __global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
 
   if (tid < 128u) S.etab[tid] = tab;
 
+  // The row's suppressed tokens in this chunk, as a bitmap (bit b of word w:
+  // token c0 + 32 w + b); a block-uniform branch.
+  bool sup = false;
+  if (A.sup_off) {
+    const uint32_t s0 = A.sup_off[row], s1 = A.sup_off[row + 1];
+    if (s1 > s0) {
+      sup = true;
+      static_assert(TCH / 32 == TNT, "one bitmap word per thread");
+      S.supw[tid] = 0u;
+      lds_barrier();
+      for (uint32_t j = s0 + tid; j < s1; j += TNT) {
+        const uint32_t d = A.sup_ids[j] - c0;
+        if (d < len && A.sup_vals[j] == -INFINITY) atomicOr(&S.supw[d >> 5], 1u << (d & 31u));
+      }
+      lds_barrier();
+    }
+  }
+
   // ---- pass 1: maximum, finite check, lane maxima ---------------------------
   float x[TQ][4];
   float t1 = -INFINITY;
   bool nf = false;
-  if (len == TCH) {
+  if (sup) {
+    // suppressed tokens read as f32::MIN; out-of-range ones as -inf
+    const int rem = (int)len - (int)(tid * 4u);
+#pragma unroll
+    for (int q = 0; q < TQ; ++q) {
+      float v[4];
+      Quad<In>::unpack(raw[q], v);
+      const uint32_t sb = S.supw[(uint32_t)q * (TSL / 32u) + (tid >> 3)] >> ((tid & 7u) * 4u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool inr = q * (int)TSL + e < rem;
+        x[q][e] = !inr ? -INFINITY : ((sb >> e) & 1u) ? -FLT_MAX : v[e];
+        nf |= inr && !__builtin_isfinite(x[q][e]);
+        t1 = fmaxf(t1, x[q][e]);
+      }
+    }
+  } else if (len == TCH) {
 #pragma unroll
     for (int q = 0; q < TQ; ++q) {
       Quad<In>::unpack(raw[q], x[q]);
@@ -340,7 +391,7 @@ __global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
       listed = take;
     } else if (take > 0u) {
       __syncthreads();   // the histograms overlay the candidate slots
-      exact_list<In>(A.list + ((uint64_t)row * A.C + chunk) * n, S, src, c0, c1, take);
+      exact_list<In>(A.list + ((uint64_t)row * A.C + chunk) * n, S, src, c0, c1, take, sup);
       listed = take;
     }
     lds_barrier();
@@ -429,6 +480,7 @@ __global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
   __shared__ MergeSmem S;
   const uint32_t tid = threadIdx.x;
   const uint32_t row = blockIdx.x;
+  if (A.want && A.want[row] == 0u) return;   // a step row without a receipt
   const uint32_t V = A.V, n = A.n;
   const uint32_t C = A.C;
   const unsigned long long* lists = A.list + (uint64_t)row * C * n;
@@ -477,8 +529,9 @@ __global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
     }
     if (tid == 0) {
       A.status[row] = MXS_ROW_NON_FINITE_LOGIT;
-      A.maximum[row] = __builtin_nan("");
-      A.lognorm[row] = __builtin_nan("");
+      if (A.maximum) A.maximum[row] = __builtin_nan("");
+      if (A.lognorm) A.lognorm[row] = __builtin_nan("");
+      if (A.token_lp) A.token_lp[row] = __builtin_nan("");
     }
     return;
   }
@@ -537,8 +590,32 @@ __global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
   }
   if (tid == 0) {
     A.status[row] = 0;
-    A.maximum[row] = M;
-    A.lognorm[row] = ln;
+    if (A.maximum) A.maximum[row] = M;
+    if (A.lognorm) A.lognorm[row] = ln;
+    if (A.token_lp) {
+      // the picked token's f64(l) - maximum - log_normalizer under the same
+      // suppressed logits (token_logprob's `logprob(selected)`); NaN for a
+      // row without a token
+      const int32_t t = A.token[row];
+      double lp = __builtin_nan("");
+      if (t >= 0 && (uint32_t)t < V) {
+        const uint64_t at = (uint64_t)row * A.stride + (uint32_t)t;
+        float l = A.bf16 ? bf16_to_f32(reinterpret_cast<const uint16_t*>(A.logits)[at])
+                         : reinterpret_cast<const float*>(A.logits)[at];
+        if (A.sup_off) {
+          // bias ids increase within a row: binary search for t
+          uint32_t lo = A.sup_off[row], hi = A.sup_off[row + 1];
+          while (lo < hi) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (A.sup_ids[mid] < (uint32_t)t) lo = mid + 1u;
+            else hi = mid;
+          }
+          if (lo < A.sup_off[row + 1] && A.sup_ids[lo] == (uint32_t)t && A.sup_vals[lo] == -INFINITY) l = -FLT_MAX;
+        }
+        lp = ((double)l - M) - ln;
+      }
+      A.token_lp[row] = lp;
+    }
   }
 }
 
@@ -565,9 +642,11 @@ static const char* topn_check(const void* logits, int32_t dtype, uint32_t vocab,
 // per-chunk statistics and lists at `stat` and `list`.
 static hipError_t topn_launch(hipStream_t stream, const void* logits, int32_t dtype, uint32_t rows, uint32_t vocab,
                               uint64_t row_stride, uint32_t n, int32_t* ids, double* logprobs, double* maximum,
-                              double* log_normalizer, int32_t* status, TopnStat* stat, unsigned long long* list) {
+                              double* log_normalizer, int32_t* status, TopnStat* stat, unsigned long long* list,
+                              const TopnArgs* step = nullptr) {
   const uint32_t C = (vocab + TCH - 1u) / TCH;
-  TopnArgs A;
+  TopnArgs A{};
+  if (step) A = *step;
   A.logits = logits;
   A.stride = row_stride;
   A.rows = rows;
@@ -581,6 +660,7 @@ static hipError_t topn_launch(hipStream_t stream, const void* logits, int32_t dt
   A.status = status;
   A.stat = stat;
   A.list = list;
+  A.bf16 = dtype == MXS_BF16 ? 1u : 0u;
   const dim3 grid(8u * C, (rows + 7u) / 8u);
   if (dtype == MXS_F32)
     hipLaunchKernelGGL(topn_kernel<float>, grid, dim3(TNT), 0, stream, A);
@@ -672,5 +752,44 @@ extern "C" int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int
   e = mxs::topn_launch((hipStream_t)stream, logits, dtype, rows, vocab, row_stride, n, ids, logprobs, maximum,
                        log_normalizer, status, stat, list);
   if (e != hipSuccess) return mxs::noalloc_fail(MXS_EHIP, std::string("topn launch: ") + hipGetErrorString(e));
+  return MXS_OK;
+}
+
+// One engine step (engine_loop.rs:1080-1134, ChatTurn::pick at
+// chat_turn.rs:290-303): every row's pick, then the log-probability receipt
+// of the rows that want one, over the logits after suppression.
+extern "C" int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const mxs_out* out,
+                        const mxs_receipts* receipts) {
+  if (!ctx || !batch || !out) return MXS_EINVAL;
+  if (receipts) {
+    const mxs_receipts& R = *receipts;
+    if (R.n == 0 || R.n > mxs::TOPN_MAX) return fail(ctx, MXS_EINVAL, "receipts->n must be in 1..64");
+    if (!R.ids || !R.logprobs || !R.token_logprob || !R.status)
+      return fail(ctx, MXS_EINVAL, "receipts: ids, logprobs, token_logprob and status are required");
+    if (const char* m = mxs::topn_check(batch->logits, batch->dtype, batch->vocab, batch->row_stride, R.n, R.ids,
+                                        R.logprobs, R.token_logprob, R.token_logprob, R.status))
+      return fail(ctx, MXS_EINVAL, m);
+  }
+  int rc = race ? mxs_sample_race(ctx, batch, race, out) : mxs_sample(ctx, batch, out);
+  if (rc != MXS_OK || !receipts || batch->rows == 0) return rc;
+  const mxs_receipts& R = *receipts;
+  mxs::TopnArgs X{};
+  X.want = R.top;
+  X.sup_off = batch->bias_offsets;
+  X.sup_ids = batch->bias_ids;
+  X.sup_vals = batch->bias_values;
+  X.token = out->token;
+  X.token_lp = R.token_logprob;
+  auto* stat = reinterpret_cast<mxs::TopnStat*>(ctx->topn_scratch);
+  auto* list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ctx->topn_scratch) +
+                                                     (size_t)ctx->max_rows * mxs::TMAXC * sizeof(mxs::TopnStat));
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  const hipError_t e = mxs::topn_launch(ctx->stream, batch->logits, batch->dtype, batch->rows, batch->vocab,
+                                        batch->row_stride, R.n, R.ids, R.logprobs, nullptr, nullptr, R.status, stat,
+                                        list, &X);
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "receipt launch");
   return MXS_OK;
 }

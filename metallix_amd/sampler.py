@@ -66,6 +66,13 @@ class MxsRace(ctypes.Structure):
     _fields_ = [("seed", _vp), ("choice", _vp), ("position", _vp)]
 
 
+class MxsReceipts(ctypes.Structure):
+    _fields_ = [
+        ("top", _vp), ("n", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+        ("ids", _vp), ("logprobs", _vp), ("token_logprob", _vp), ("status", _vp),
+    ]
+
+
 # Exported symbols and their prototypes, as declared in include/mx_sampler.h.
 PROTOTYPES = {
     "mxs_abi_version": (ctypes.c_int, []),
@@ -82,6 +89,8 @@ PROTOTYPES = {
                                                    ctypes.c_uint64, ctypes.c_uint32, _vp, _vp, _vp, _vp, _vp]),
     "mxs_spec_verify": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mxs_step": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), ctypes.POINTER(MxsRace), ctypes.POINTER(MxsOut),
+                                ctypes.POINTER(MxsReceipts)]),
     "mxs_sync": (ctypes.c_int, [_vp]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
     "mxs_debug_set_paths": (ctypes.c_int, [_vp, _vp]),
@@ -149,6 +158,15 @@ def _ptr(t) -> Optional[int]:
 
 
 @dataclass
+class ReceiptResult:
+    """Device tensors of one step's receipts (mxs_receipts)."""
+    ids: "object"
+    logprobs: "object"
+    token_logprob: "object"
+    status: "object"
+
+
+@dataclass
 class SampleResult:
     token: "object"
     sampling_logprob: "object"
@@ -206,6 +224,49 @@ class Sampler:
         selects race-v2 (Qwen3Selection::Race, picks.rs:40-66) instead of the
         inverse-CDF draw; `uniform` is then unused.
         """
+        b, o, r, out = self._structs(logits, temperature, top_k=top_k, top_p=top_p, min_p=min_p,
+                                     repetition=repetition, presence=presence, frequency=frequency, uniform=uniform,
+                                     history=history, bias=bias, mask=mask, tokenizer_vocab=tokenizer_vocab,
+                                     debug=debug, out=out, vocab=vocab, race=race)
+        if r is not None:
+            self._check(self.lib.mxs_sample_race(self.ctx, ctypes.byref(b), ctypes.byref(r), ctypes.byref(o)),
+                        "mxs_sample_race")
+            self._keep = (b, o, r)
+            return out
+        self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
+        self._keep = (b, o)
+        return out
+
+    def step(self, logits, temperature, *, receipt_top=None, n: int = 28, race=None, **kw):
+        """Queues one engine step (mxs_step): every row's pick as `sample`
+        does, then the receipts over the suppressed logits (the bias
+        entries of -inf) of the rows whose receipt_top entry (u32[rows] on
+        the device; None: every row) is non-zero, with n IDs per row.
+        Returns (SampleResult, ReceiptResult) of device tensors."""
+        torch = self.torch
+        b, o, r, out = self._structs(logits, temperature, race=race, **kw)
+        rows, dev = logits.shape[0], logits.device
+        with torch.cuda.stream(self.stream):   # the fills run before the step on its stream
+            rec = ReceiptResult(
+                ids=torch.full((rows, n), -1, dtype=torch.int32, device=dev),
+                logprobs=torch.full((rows, n), float("nan"), dtype=torch.float64, device=dev),
+                token_logprob=torch.full((rows,), float("nan"), dtype=torch.float64, device=dev),
+                status=torch.zeros(rows, dtype=torch.int32, device=dev),
+            )
+        R = MxsReceipts()
+        R.top = _ptr(receipt_top)
+        R.n = n
+        R.ids, R.logprobs = rec.ids.data_ptr(), rec.logprobs.data_ptr()
+        R.token_logprob, R.status = rec.token_logprob.data_ptr(), rec.status.data_ptr()
+        rp = ctypes.byref(r) if r is not None else None
+        self._check(self.lib.mxs_step(self.ctx, ctypes.byref(b), rp, ctypes.byref(o), ctypes.byref(R)), "mxs_step")
+        self._keep = (b, o, r, R)
+        return out, rec
+
+    def _structs(self, logits, temperature, *, top_k=None, top_p=None, min_p=None, repetition=None,
+                 presence=None, frequency=None, uniform=None, history=None, bias=None, mask=None,
+                 tokenizer_vocab=None, debug: bool = False, out: Optional[SampleResult] = None,
+                 vocab: Optional[int] = None, race=None):
         torch = self.torch
         rows = logits.shape[0]
         V = vocab if vocab is not None else logits.shape[1]
@@ -249,16 +310,11 @@ class Sampler:
         o.kept_count = _ptr(out.kept_count)
         o.adjusted = _ptr(out.adjusted)
         o.kept_bits = _ptr(out.kept_bits)
+        r = None
         if race is not None:
             r = MxsRace()
             r.seed, r.choice, r.position = _ptr(race[0]), _ptr(race[1]), _ptr(race[2])
-            self._check(self.lib.mxs_sample_race(self.ctx, ctypes.byref(b), ctypes.byref(r), ctypes.byref(o)),
-                        "mxs_sample_race")
-            self._keep = (b, o, r)
-            return out
-        self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
-        self._keep = (b, o)
-        return out
+        return b, o, r, out
 
     def launcher(self, logits, **kw):
         """Pre-built launch for repeated picks with the same parameters and
