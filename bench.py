@@ -266,6 +266,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--race", action="store_true", help="also time race-v2 picks (mxs_sample_race, config 2)")
+    ap.add_argument("--receipts", action="store_true",
+                    help="also time engine steps with top-20 receipts for every row (mxs_step, config 2)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device copies (scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -343,8 +345,74 @@ def main():
     }
     if args.race and cfg == 2:
         res["race"] = race_bench(torch, s, stream, data, args.steps, args.warmup)
+    if args.receipts and cfg == 2:
+        res["engine_step"] = step_bench(torch, s, stream, data, args.steps, args.warmup,
+                                        None if args.no_cpu else args.cpu_seconds)
     res["cpu_baseline"] = None if args.no_cpu else cpu_baseline(cfg, data, args.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+
+def step_bench(torch, s, stream, b, steps, warmup, cpu_seconds):
+    """Engine steps (mxs_step) on resident config-2 logits: every row's pick
+    plus a top-20 receipt (28 ranked IDs, the reference's top + 8) for every
+    row, over the logits with two suppressed IDs.  Time per step, back to
+    back, from events on the stream; beside it the reference's per-row host
+    loop (the oracle's pick and token_logprob per row) on a bounded sample."""
+    import numpy as np
+
+    from metallix_amd.sampler import with_suppression
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import to_device, u32
+
+    sup = [151643, 151645]
+    saved = (b.bias_offsets, b.bias_ids, b.bias_values)
+    b.bias_offsets, b.bias_ids, b.bias_values = with_suppression(b.rows, sup, *saved)
+    logits, kw = to_device(torch, b)
+    b.bias_offsets, b.bias_ids, b.bias_values = saved
+    nb = rotation(nbytes(logits))
+    bufs = [logits] + [logits.clone() for _ in range(nb - 1)]
+    tops = torch.from_numpy(u32(np.full(b.rows, 20, dtype=np.uint32))).to(logits.device)
+    with torch.cuda.stream(stream):
+        launch = s.step_launcher(bufs[0], receipt_top=tops, n=TOPN, **kw)
+        for i in range(warmup):
+            launch(bufs[i % nb])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for i in range(steps):
+            launch(bufs[i % nb])
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    st = launch.out.status.cpu().numpy()
+    rst = launch.receipts.status.cpu().numpy()
+    assert (st >= 0).all() and (rst == 0).all(), f"row errors in the step benchmark: {st} {rst}"
+    res = {"ms_per_step": round(ms, 6), "rows_per_s": round(b.rows / (ms / 1e3), 1),
+           "receipt_top": 20, "ranked_ids": TOPN, "suppressed_ids": sup,
+           "algorithmic_bytes": sample_bytes(logits, kw) + topn_bytes(logits, b.vocab, TOPN)}
+    if cpu_seconds:
+        from oracle import oracle
+
+        x = np.asarray(b.logits, dtype=np.float32)
+        rows_done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds / 2:
+            for r in range(0, 8):
+                oracle.sample_row(x[r], temperature=float(b.temperature[r]), top_p=float(b.top_p[r]),
+                                  min_p=float(b.min_p[r]), uniform=float(b.uniform[r]), top_k=int(b.top_k[r]),
+                                  repetition=float(b.repetition[r]), presence=float(b.presence[r]),
+                                  frequency=float(b.frequency[r]),
+                                  history=b.history_ids[b.history_offsets[r]:b.history_offsets[r + 1]],
+                                  bias_ids=sup, bias_values=[-np.inf] * len(sup))
+                xs = x[r].copy()
+                xs[sup] = np.finfo(np.float32).min
+                oracle.token_logprob_top(xs, TOPN)
+                rows_done += 1
+        res["cpu_per_row_loop"] = {"value": round(rows_done / (time.perf_counter() - t0), 2), "unit": "rows/s",
+                                   "cores": 1, "kind": "port",
+                                   "sample": f"{rows_done} rows (rows 0-7 of cfg2, pick + token_logprob each)"}
+    return res
 
 
 def race_bench(torch, s, stream, b, steps, warmup):

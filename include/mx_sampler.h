@@ -31,6 +31,9 @@
  *                                TurnLoop::pick (chat_turn.rs:290-303): ChatFormat::suppress,
  *                                the pick, and token_logprob's receipt (chat_turn.rs:506-563)
  *                                for every row of the batch in one call.
+ *   mxs_mask_host,            <- the per-step SimpleVob words (crates/core/engine/src/
+ *   mxs_mask_upload              constraint.rs:777-806) on their way to the device: pinned
+ *                                staging, an upload on a copy stream, double-buffered.
  *   mxs_sync                  <- Qwen3TokenPicks::wait (picks.rs:390-401).
  *   mxs_last_error            <- KernelError's message (mlx-kernels/src/lib.rs:444-450).
  *
@@ -207,6 +210,20 @@ typedef struct {
  * unspellable IDs stay with the caller. */
 int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const mxs_out* out,
              const mxs_receipts* receipts);
+/* Grammar-mask staging.  The constraint's allowed-token words for a step
+ * (SimpleVob: bit b of word w <-> token 32w+b, constraint.rs:793-806) are
+ * written by the host into a pinned staging slot (0 or 1) the context owns,
+ * then uploaded.  mxs_mask_host returns the slot's host words (max_rows rows
+ * of *stride_words words; allocated at the first call) after waiting until
+ * the slot's previous upload has read them.  mxs_mask_upload queues the copy
+ * of the slot's first `rows` rows on the context's copy stream, behind the
+ * last pick that read the slot's device words, and orders the context's
+ * stream after the copy; *device_words is the slot's device copy, to pass as
+ * batch->mask_words with mask_stride = *stride_words.  Two slots
+ * double-buffer consecutive steps: fill and upload slot 1 - s while the pick
+ * of slot s runs. */
+int mxs_mask_host(mxs_ctx* ctx, uint32_t slot, uint32_t** words, uint64_t* stride_words);
+int mxs_mask_upload(mxs_ctx* ctx, uint32_t slot, uint32_t rows, const uint32_t** device_words);
 int mxs_sync(mxs_ctx* ctx);
 /* Diagnostics (no reference counterpart): when `device_buffer` is non-null,
  * mxs_sample records 100 MHz wall-clock stamps at fixed phase boundaries:

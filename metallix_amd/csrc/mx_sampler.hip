@@ -3522,7 +3522,7 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 template <typename In, uint32_t MODE, bool HIST>
 __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                            const uint32_t row, const uint32_t chunk, const uint32_t c0,
-                                           const uint32_t c1, const uint32_t hn) {
+                                           const uint32_t c1, const uint32_t hn, const uint32_t bn) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
@@ -3539,10 +3539,24 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   uint32_t c0k = c0;
   __asm__ volatile("" : "+s"(c0k));
   uint32_t hreg[HCAP / NT];
+  // the row's logit-bias entry `tid` (at most NT entries, none above 0) and
+  // its predecessor's id
+  uint32_t bid = NONE, bprev = 0u;
+  float bval = 0.0f;
   if constexpr (HIST) {
     const uint32_t* hp = b.history_ids + c.hb;
+    if (hn) {
 #pragma unroll
-    for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
+      for (int r = 0; r < HCAP / NT; ++r) hreg[r] = hp[min((uint32_t)r * NT + tid, hn - 1u)];
+    } else {
+#pragma unroll
+      for (int r = 0; r < HCAP / NT; ++r) hreg[r] = 0u;
+    }
+    if (tid < bn) {
+      bid = b.bias_ids[c.bb + tid];
+      bval = b.bias_values[c.bb + tid];
+      if (tid > 0u) bprev = b.bias_ids[c.bb + tid - 1u];
+    }
   }
   // The slices stream through a window of LA loads in flight per wave: slice
   // i + LA is issued as slice i is processed.  A wave issues in order, and a
@@ -3582,9 +3596,14 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   // logit in where a slice can hold a candidate (a penalised logit at or
   // above a threshold was at or above it before the penalty).  The owner
   // leaves the adjusted logit in pvals and marks the token's table entry
-  // 0x8000 | slot.
-  uint32_t own = 0;              // bit r: this thread owns history entry r's token
+  // 0x8000 | slot.  Logit-bias entries join the same scheme when none of a
+  // row's values is above 0 (the kernel checks), so the bias never raises a
+  // logit either: each entry marks its token with 0x4000 before the history
+  // counts go in, and owns it (bias ids are distinct), adding the bias as
+  // bias_and_penalize does; its slot is hn + its index.
+  uint32_t own = 0;              // bit r < 4: this thread owns history entry r's token; bit 4: bias entry tid's
   float hraw[HCAP / NT];         // the owned tokens' logits
+  float braw = 0.0f;             // the biased token's logit
   float* pvals = reinterpret_cast<float*>(S.hids);   // HCAP adjusted logits by slot (the lean body stages no history)
   if constexpr (HIST) {
     const uint32_t n4 = A.per * (SLICE / 8);   // uint4 words covering per slices
@@ -3593,6 +3612,17 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   if constexpr (MODE == M_TOPK) S.hist[tid] = 0u;   // HB == NT
   if constexpr (HIST) {
     lds_barrier();
+    if (bn) {   // (uniform) the bias marks, then a barrier before the history counts
+      if (tid < bn) {
+        if (bid >= V || !bias_ok(bval) || (tid > 0u && bprev >= bid)) my_flags |= F_BIAS;
+        const uint32_t t = bid - c0;
+        if (t < clen) {
+          atomicAdd(&S.t.ct[t >> 1], 0x4000u << ((t & 1u) * 16u));
+          own |= 1u << 4;
+        }
+      }
+      lds_barrier();
+    }
 #pragma unroll
     for (int r = 0; r < HCAP / NT; ++r) {
       const uint32_t j = (uint32_t)r * NT + tid;
@@ -3611,6 +3641,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     // chunk's first token): a fixed count of loads in flight per wave
 #pragma unroll
     for (int r = 0; r < HCAP / NT; ++r) hraw[r] = Quad<In>::one(src + (((own >> r) & 1u) ? hreg[r] : c0k));
+    braw = Quad<In>::one(src + (((own >> 4) & 1u) ? bid : c0k));
     lds_barrier();
   }
   stamp(A, row, chunk, 3);
@@ -3734,15 +3765,9 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
       wait_mem();
       __syncthreads();
     }
-#pragma unroll
-    for (int r = 0; r < HCAP / NT; ++r) {
-      if (!((own >> r) & 1u)) continue;
-      const uint32_t id = hreg[r], t = id - c0, sh = (t & 1u) * 16u;
-      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0xffffu;
-      const float pv = bias_and_penalize(hraw[r], cnt, 0.0f, c.rep, inv_rep, c.freq, c.pres);
+    auto fold = [&](const float pv, const uint32_t id, const uint32_t t, const uint32_t slot) {
       if (!__builtin_isfinite(pv)) my_flags |= F_NONFINITE;
       if (A.o.adjusted) A.o.adjusted[(uint64_t)row * V + id] = pv;
-      const uint32_t slot = (uint32_t)r * NT + tid;
       pvals[slot] = pv;
       reinterpret_cast<uint16_t*>(S.t.ct)[t] = (uint16_t)(0x8000u | slot);
       if constexpr (MODE == M_GREEDY) {
@@ -3766,6 +3791,18 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
           mrun = mnew;
         }
       }
+    };
+#pragma unroll
+    for (int r = 0; r < HCAP / NT; ++r) {
+      if (!((own >> r) & 1u)) continue;
+      const uint32_t id = hreg[r], t = id - c0, sh = (t & 1u) * 16u;
+      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0xffffu;   // an unbiased token: its history count
+      fold(bias_and_penalize(hraw[r], cnt, 0.0f, c.rep, inv_rep, c.freq, c.pres), id, t, (uint32_t)r * NT + tid);
+    }
+    if ((own >> 4) & 1u) {
+      const uint32_t t = bid - c0, sh = (t & 1u) * 16u;
+      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0x3fffu;   // the history count under the bias mark
+      fold(bias_and_penalize(braw, 0x80000000u | cnt, bval, c.rep, inv_rep, c.freq, c.pres), bid, t, hn + tid);
     }
   }
   stamp(A, row, chunk, 6);
@@ -3946,7 +3983,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     // telescope to its distance from the chunk maximum), + n 2^-120 for
     // weights and factors below 2^-126, + 2^-40 S for the f64 sums.
     // (each owned history token is one more step)
-    const uint32_t steps = A.per + (HIST ? (uint32_t)(HCAP / NT) : 0u);
+    const uint32_t steps = A.per + (HIST ? (uint32_t)(HCAP / NT) + 1u : 0u);
     mass_err = 1.01 * (0x1p-22 * S0 * (double)(steps + 3u) + (double)(steps + 5u) * 0x1p-24 * S0 +
                        0.6931471805599453 * 3.0001 * 0x1p-24 * E0) +
                (double)nleg * 0x1p-120 + 0x1p-40 * S0;
@@ -3994,6 +4031,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
 #pragma unroll
           for (int r = 0; r < HCAP / NT; ++r)
             if ((own >> r) & 1u) part += exp_neg_p(((double)pvals[(uint32_t)r * NT + tid] - md) * invT);
+          if ((own >> 4) & 1u) part += exp_neg_p(((double)pvals[hn + tid] - md) * invT);
         }
         mass = block_sum<double>(part, reinterpret_cast<double*>(S.wq));
         // 2 ulp per weight plus the sums (sum_bound), and the rounding of
@@ -4781,19 +4819,27 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   bool last;
   {
     const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
+    // A logit bias of at most NT entries, none above 0 (-inf suppresses),
+    // never raises a logit: the lean body takes it (NaN and +inf values fail
+    // the test, and the general body reports them).
+    bool lean_bias = bn == 0u;
+    if (bn && bn <= (uint32_t)NT && hn + bn <= (uint32_t)HCAP && !c.err && A.masked == 0u) {
+      const float v = threadIdx.x < bn ? b.bias_values[c.bb + threadIdx.x] : 0.0f;
+      lean_bias = __syncthreads_and(v <= 0.0f) != 0;
+    }
     // (the lean body's penalties never raise a logit: others take the general body)
-    if (!c.err && A.masked == 0u && bn == 0u && hn <= (uint32_t)HCAP &&
+    if (!c.err && A.masked == 0u && lean_bias && hn <= (uint32_t)HCAP &&
         (hn == 0u || (c.rep >= 1.0f && c.freq >= 0.0f && c.pres >= 0.0f)) &&
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
-      if (hn) {
-        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn);
-        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn);
-        else last = chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn);
+      if (hn || bn) {
+        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn, bn);
+        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn, bn);
+        else last = chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn, bn);
       } else {
-        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u);
-        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u);
-        else last = chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u);
+        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
+        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
+        else last = chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
       }
     } else {
       last = chunk_general<In>(A, U, c, row, chunk);
@@ -4890,6 +4936,7 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
     hipLaunchKernelGGL((mxs::sample_kernel<uint16_t>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
 #undef MXS_ARGS
   hipError_t e = hipGetLastError();
+  if (e == hipSuccess) mask_note_read(ctx, b->mask_words);
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");
   return MXS_OK;
@@ -5013,6 +5060,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->race_ctr);
   hipFree(ctx->race_scratch);
   hipFree(ctx->race_kept);
+  mxs::mask_release(ctx);
   hipSetDevice(prev);
   delete ctx;
   return MXS_OK;

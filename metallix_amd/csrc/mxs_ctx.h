@@ -25,6 +25,12 @@ constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 // draw (token -1, status 0, the kept set still written).
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
 
+// A pick queued on ctx->stream read `words`: when they are a staging
+// slot's device words, the slot's next upload waits for that pick
+// (mx_mask.hip).
+void mask_note_read(mxs_ctx* ctx, const uint32_t* words);
+void mask_release(mxs_ctx* ctx);   // frees the staging slots (mxs_destroy)
+
 // Scratch sizes of the entry points other than mxs_sample (defined beside
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);
@@ -80,6 +86,18 @@ struct mxs_ctx {
   uint32_t* race_kept = nullptr;
   // the uniform of the inverse-CDF draw mxs_sample_race discards (below)
   double* d_race_u = nullptr;
+  // grammar-mask staging (mxs_mask_host / mxs_mask_upload, mx_mask.hip):
+  // two slots of max_rows rows of mask_stride words, pinned on the host and
+  // on the device, allocated at the first mxs_mask_host; copies run on
+  // their own stream (default priority)
+  uint32_t* mask_host[2] = {nullptr, nullptr};
+  uint32_t* mask_dev[2] = {nullptr, nullptr};
+  uint64_t mask_stride = 0;
+  hipStream_t copy_stream = nullptr;
+  hipEvent_t mask_copied[2] = {nullptr, nullptr};   // the slot's last upload has read the host words
+  hipEvent_t mask_read[2] = {nullptr, nullptr};     // the last pick that read the device slot is done
+  bool copy_queued[2] = {false, false};
+  bool read_queued[2] = {false, false};
   std::string last_error;
 };
 

@@ -91,6 +91,8 @@ PROTOTYPES = {
                                        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mxs_step": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), ctypes.POINTER(MxsRace), ctypes.POINTER(MxsOut),
                                 ctypes.POINTER(MxsReceipts)]),
+    "mxs_mask_host": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_uint64)]),
+    "mxs_mask_upload": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_vp)]),
     "mxs_sync": (ctypes.c_int, [_vp]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
     "mxs_debug_set_paths": (ctypes.c_int, [_vp, _vp]),
@@ -155,6 +157,21 @@ def with_suppression(rows: int, suppress_ids, bias_offsets=None, bias_ids=None, 
 
 def _ptr(t) -> Optional[int]:
     return None if t is None else t.data_ptr()
+
+
+class DeviceWords:
+    """A staging slot's device mask words, as `Sampler.sample(mask=...)`
+    takes them (a data pointer and a row stride in words)."""
+
+    def __init__(self, ptr: int, stride: int, rows: int):
+        self.ptr, self.stride_words, self.rows = ptr, stride, rows
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def stride(self, dim: int) -> int:
+        assert dim == 0
+        return self.stride_words
 
 
 @dataclass
@@ -262,6 +279,25 @@ class Sampler:
         self._check(self.lib.mxs_step(self.ctx, ctypes.byref(b), rp, ctypes.byref(o), ctypes.byref(R)), "mxs_step")
         self._keep = (b, o, r, R)
         return out, rec
+
+    def step_launcher(self, logits, *, receipt_top=None, n: int = 28, **kw):
+        """Pre-built mxs_step for repeated steps with the same rules and
+        outputs: returns f(logits) that only swaps the logits pointer (its
+        .out and .receipts hold the device outputs)."""
+        out, rec = self.step(logits, receipt_top=receipt_top, n=n, **kw)
+        b, o, r, R = self._keep
+        bp, op, Rp = ctypes.byref(b), ctypes.byref(o), ctypes.byref(R)
+        rp = ctypes.byref(r) if r is not None else None
+        ctx, fs = self.ctx, self.lib.mxs_step
+
+        def launch(t):
+            b.logits = t.data_ptr()
+            rc = fs(ctx, bp, rp, op, Rp)
+            if rc != 0:
+                self._check(rc, "mxs_step")
+
+        launch.out, launch.receipts = out, rec
+        return launch
 
     def _structs(self, logits, temperature, *, top_k=None, top_p=None, min_p=None, repetition=None,
                  presence=None, frequency=None, uniform=None, history=None, bias=None, mask=None,
@@ -426,6 +462,26 @@ class Sampler:
                                       st.data_ptr())
         self._check(rc, "mxs_spec_verify")
         return out, cnt, acc, st
+
+    def mask_host(self, slot: int):
+        """The pinned host words of staging slot `slot` as a numpy u32 array
+        [max_rows, stride] (mxs_mask_host: returns once the slot's previous
+        upload has read them, so the caller may overwrite them)."""
+        import numpy as np
+
+        ptr, stride = _vp(), ctypes.c_uint64()
+        self._check(self.lib.mxs_mask_host(self.ctx, slot, ctypes.byref(ptr), ctypes.byref(stride)), "mxs_mask_host")
+        self._mask_stride = stride.value
+        n = self.max_rows * stride.value
+        buf = (ctypes.c_uint32 * n).from_address(ptr.value)
+        return np.frombuffer(buf, dtype=np.uint32).reshape(self.max_rows, stride.value)
+
+    def mask_upload(self, slot: int, rows: int) -> DeviceWords:
+        """Queues the upload of the slot's first `rows` rows (mxs_mask_upload);
+        returns the device words for `sample(mask=...)`."""
+        ptr = _vp()
+        self._check(self.lib.mxs_mask_upload(self.ctx, slot, rows, ctypes.byref(ptr)), "mxs_mask_upload")
+        return DeviceWords(ptr.value, self._mask_stride, rows)
 
     def sync(self):
         self._check(self.lib.mxs_sync(self.ctx), "mxs_sync")

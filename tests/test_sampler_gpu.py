@@ -317,6 +317,46 @@ def test_keepall_rows_with_history_and_bias(torch_mod, sampler, orc):
     check(torch_mod, sampler, orc, b)
 
 
+def test_nonpositive_bias_rows(torch_mod, sampler, orc):
+    """Config 2's rows with logit-bias lists whose values are all at most 0
+    (-inf suppressions, negative and zero biases), of 1 to 1025 entries, on
+    tokens that are also in the row's history or are its argmax: the lean
+    chunk body takes lists of up to 1024 such entries, the general body the
+    rest; both are held to the oracle.  Then the lean body's validation:
+    repeated or out-of-range bias ids with non-positive values."""
+    from metallix_amd import synth
+    from metallix_amd.synth import Batch
+
+    b = synth.config2(rows=24)
+    b.name = "nonpositive-bias"
+    rng = np.random.default_rng(4242)
+    b.temperature[::7] = 0.0
+    sizes = [1, 8, 300, 1000, 1024, 1025] * 4
+    ids_l, vals_l, offs = [], [], [0]
+    for r in range(b.rows):
+        h = b.history_ids[b.history_offsets[r]:b.history_offsets[r + 1]]
+        pool = np.concatenate([rng.integers(0, b.vocab, sizes[r]), h[:sizes[r] // 3], [np.argmax(b.logits[r])]])
+        ids = np.unique(pool.astype(np.uint32))[: sizes[r]]
+        kind = rng.integers(0, 3, ids.size)
+        vals = np.where(kind == 0, -np.inf, np.where(kind == 1, -np.abs(rng.standard_normal(ids.size)) * 3.0, 0.0))
+        ids_l.append(ids)
+        vals_l.append(vals.astype(np.float32))
+        offs.append(offs[-1] + ids.size)
+    b.bias_offsets = np.array(offs, dtype=np.uint32)
+    b.bias_ids = np.concatenate(ids_l)
+    b.bias_values = np.concatenate(vals_l)
+    gpu, ref = check(torch_mod, sampler, orc, b)
+    assert (gpu["status"] == 0).all()
+
+    V = 100
+    x = np.tile(np.linspace(-2, 2, V, dtype=np.float32), (4, 1))
+    c = Batch(name="bias-ids", logits=x, temperature=np.ones(4), uniform=np.full(4, 0.5),
+              bias_offsets=np.array([0, 2, 4, 5, 7], np.uint32), bias_ids=np.array([3, 9, 5, 5, V, 1, 99], np.uint32),
+              bias_values=np.array([-1.0, -np.inf, -2.0, 0.0, -1.0, -np.inf, -0.5], np.float32))
+    gpu, ref = check(torch_mod, sampler, orc, c)
+    assert list(ref["status"]) == [0, -12, -12, 0]
+
+
 def test_suppressed_tokens(torch_mod, sampler, orc):
     """A7: the checkpoint's suppress list (ChatFormat::suppress,
     crates/core/chat-format/src/lib.rs:761-780), given to the device as -inf
