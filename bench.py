@@ -266,6 +266,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--race", action="store_true", help="also time race-v2 picks (mxs_sample_race, config 2)")
+    ap.add_argument("--masks", action="store_true",
+                    help="also time config-3 steps whose masks are uploaded from pinned staging each step")
     ap.add_argument("--receipts", action="store_true",
                     help="also time engine steps with top-20 receipts for every row (mxs_step, config 2)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -345,6 +347,8 @@ def main():
     }
     if args.race and cfg == 2:
         res["race"] = race_bench(torch, s, stream, data, args.steps, args.warmup)
+    if args.masks and cfg == 3:
+        res["mask_upload"] = mask_bench(torch, s, stream, data, args.steps, args.warmup)
     if args.receipts and cfg == 2:
         res["engine_step"] = step_bench(torch, s, stream, data, args.steps, args.warmup,
                                         None if args.no_cpu else args.cpu_seconds)
@@ -413,6 +417,66 @@ def step_bench(torch, s, stream, b, steps, warmup, cpu_seconds):
                                    "cores": 1, "kind": "port",
                                    "sample": f"{rows_done} rows (rows 0-7 of cfg2, pick + token_logprob each)"}
     return res
+
+
+def mask_bench(torch, s, stream, b, steps, warmup):
+    """Config-3 steps whose grammar masks come from the host each step: the
+    rows' words sit in the two pinned staging slots (where a constraint
+    engine would write them), and every step re-stages its slot
+    (mxs_mask_host, which waits for that slot's previous upload), uploads it
+    on the copy stream (mxs_mask_upload) and picks under it; slots
+    alternate, so step n + 1's upload overlaps step n's pick.  Time per
+    step, back to back, from events on the sampler's stream, beside the
+    same picks over device-resident masks."""
+    import ctypes
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import to_device
+
+    from metallix_amd.sampler import DeviceWords
+
+    logits, kw = to_device(torch, b)
+    nb = rotation(nbytes(logits))
+    bufs = [logits] + [logits.clone() for _ in range(nb - 1)]
+    words = b.mask_words.shape[1]
+    launches = []
+    with torch.cuda.stream(stream):
+        for slot in (0, 1):
+            host = s.mask_host(slot)
+            host[:] = 0
+            host[:b.rows, :words] = b.mask_words
+            dev = s.mask_upload(slot, b.rows)
+            kws = dict(kw)
+            kws["mask"] = DeviceWords(dev.data_ptr(), dev.stride(0), b.rows)
+            launches.append(s.launcher(bufs[0], **kws))
+    lib, ctx = s.lib, s.ctx
+    hp, hs, dp = ctypes.c_void_p(), ctypes.c_uint64(), ctypes.c_void_p()
+
+    def step(i):
+        slot = i & 1
+        if lib.mxs_mask_host(ctx, slot, ctypes.byref(hp), ctypes.byref(hs)) != 0:
+            raise RuntimeError("mxs_mask_host failed")
+        if lib.mxs_mask_upload(ctx, slot, b.rows, ctypes.byref(dp)) != 0:
+            raise RuntimeError("mxs_mask_upload failed")
+        launches[slot](bufs[i % nb])
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for i in range(steps):
+            step(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    st = launches[(steps - 1) & 1].out.status.cpu().numpy()
+    assert (st >= 0).all(), f"row errors in the mask benchmark: {st}"
+    mbytes = b.rows * hs.value * 4
+    return {"ms_per_step": round(ms, 6), "rows_per_s": round(b.rows / (ms / 1e3), 1),
+            "upload_bytes_per_step": mbytes, "upload_gbs": round(mbytes / (ms / 1e3) / 1e9, 2)}
 
 
 def race_bench(torch, s, stream, b, steps, warmup):

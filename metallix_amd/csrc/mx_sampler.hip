@@ -2230,7 +2230,7 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
                               : (key[u] > kap || (key[u] == kap && P.id[u] <= idk));
       if (!in) continue;
       ++ne;
-      const float y = (l - Mf) * c2;   // <= 0
+      const float y = vmax((l - Mf) * c2, -200.0f);   // <= 0 (clamped: f32::MIN would give -inf)
       const float wf = __builtin_amdgcn_exp2f(y);
       e32 += wf;
       eab32 = __builtin_fmaf(wf, -y, eab32);
@@ -4597,10 +4597,13 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
         }
         if (mass32) {
           float sw = 0.0f, ew = 0.0f;
+          // (y is clamped at -200: a suppressed token's f32::MIN logit
+          // would make it -inf, and its weight 0 times -y a NaN bound;
+          // exp2f is 0 below -149 either way)
           if (full) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float y = (lv[i][e] - m) * c2;
+              const float y = vmax((lv[i][e] - m) * c2, -200.0f);
               const float w = __builtin_amdgcn_exp2f(y);
               sw += w;
               ew = __builtin_fmaf(w, -y, ew);
@@ -4608,7 +4611,7 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float y = (lv[i][e] - m) * c2;
+              const float y = vmax((lv[i][e] - m) * c2, -200.0f);
               const float w = __builtin_amdgcn_exp2f(y);
               const bool lg = (qb >> e) & 1u;
               sw += lg ? w : 0.0f;
