@@ -2446,7 +2446,7 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
     // member's (key, ID) in one pass.  More than 64 members in the
     // crossing bin: the radix passes below.
     const float Mf = (float)X.M;
-    const float span = Mf - lmin;
+    const float span = Mf - fmaxf(lmin, Mf - (float)(746.0 * c.T));   // zero-weight members share the last bin
     const float sc = span > 1e-30f ? (float)(NB - 1) / span : 0.0f;
     for (uint32_t t = tid; t < (uint32_t)NB; t += FT) { F.u.h.hcnt[t] = 0u; F.u.h.hmass[t] = 0.0; }
     if (tid == 0) { F.s_u[4] = NONE; F.s_u[6] = 0u; F.s_u[10] = 0u; }
@@ -2927,7 +2927,9 @@ __device__ __forceinline__ bool finish_w1(const FinCtx& X, FinSmem& F) {
     // mass of the members ranked before them; the reference keeps a member
     // whose running sum before it is still below theta.
     const float Mf = (float)X.M;
-    const float plo = okey_value(~wave_max_u32(inp ? ~okey(ml) : 0u));   // P's smallest logit
+    // P's smallest logit, not below M - 746 T (members further down weigh 0
+    // and share the last bin)
+    const float plo = fmaxf(okey_value(~wave_max_u32(inp ? ~okey(ml) : 0u)), Mf - (float)(746.0 * c.T));
     const float span = Mf - plo;
     const float sc = span > 1e-30f && __builtin_isfinite(span) ? 63.0f / span : 0.0f;
     const float d = (Mf - ml) * sc;
@@ -3050,7 +3052,12 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       F.hdr.flags = fl; F.hdr.nlegal = nl; F.hdr.Mkey = mkey; F.hdr.bi = garg ? ~(uint32_t)garg : NONE;
       F.hdr.ncand = bcast63(cinc);
       F.hdr.qmax = qmax;
-      F.hdr.lo = okey_value(lokey);
+      // The value bins' lower end: no candidate below it matters to a bin's
+      // position, and members more than 746 T below the maximum weigh 0
+      // (exp underflows), so they share the last bin (a suppressed legal
+      // token's f32::MIN would otherwise stretch the bins over 3.4e38 and
+      // put every other candidate in bin 0).
+      F.hdr.lo = fmaxf(okey_value(lokey), okey_value(mkey) - (float)(746.0 * c.T));
     }
   } else if (wave() == 1 && !c.greedy) {
     // the chunk masses rescaled to the row maximum (f64: off wave 0's path)
