@@ -2215,31 +2215,39 @@ __device__ __forceinline__ bool finish_sel(const FinCtx& X, FinSmem& F, const Fi
     const bool lfin = __builtin_isfinite(lthr + band) && __builtin_isfinite(lthr - band);
     const float lhi = lfin ? lthr + band : INFINITY, llo = lfin ? lthr - band : -INFINITY;
     const float c2 = (float)(1.4426950408889634 / c.T);   // log2(e) / T
+    // Branch-free per slot (a slot outside E adds +0 to every sum, which
+    // leaves it unchanged); only the rare f64 min-p test near the threshold
+    // is a branch, taken by the waves that need it.
 #pragma unroll
     for (int u = 0; u < SR; ++u) {
-      if (!((act >> u) & 1u)) continue;
+      const bool a = (act >> u) & 1u;
       const float l = P.l[u];
       bool pm = l >= lhi;   // the min-p test (every token when min_p = 0)
-      if (minp_on && l >= llo && l < lhi) {
-        const double sd = ((double)l - X.M) / c.T;
-        pm = sd >= L;
-        if (fabs(sd - L) < X.Lclose) unc = true;
+      const bool near = a && minp_on && l >= llo && l < lhi;
+      if (__builtin_amdgcn_ballot_w64(near)) {
+        if (near) {
+          const double sd = ((double)l - X.M) / c.T;
+          pm = sd >= L;
+          if (fabs(sd - L) < X.Lclose) unc = true;
+        }
       }
-      const bool in = !X.k_path ? pm
-                      : whole ? bin[u] <= bstar
-                              : (key[u] > kap || (key[u] == kap && P.id[u] <= idk));
-      if (!in) continue;
-      ++ne;
-      const float y = vmax((l - Mf) * c2, -200.0f);   // <= 0 (clamped: f32::MIN would give -inf)
-      const float wf = __builtin_amdgcn_exp2f(y);
+      const bool in = a && (!X.k_path ? pm
+                            : whole ? bin[u] <= bstar
+                                    : (key[u] > kap || (key[u] == kap && P.id[u] <= idk)));
+      // (a stale slot's logit may be anything: it is replaced by Mf, so y
+      // stays finite and 0 times -y stays 0)
+      const float y = vmax(((a ? l : Mf) - Mf) * c2, -200.0f);   // <= 0 (clamped: f32::MIN would give -inf)
+      const float wx = __builtin_amdgcn_exp2f(y);
+      const float wf = in ? wx : 0.0f;
+      ne += in ? 1u : 0u;
       e32 += wf;
       eab32 = __builtin_fmaf(wf, -y, eab32);
-      if (need_wlo) wlo = fminf(wlo, wf * (1.0f - (0x1p-21f + 2.5e-7f * -y)));
-      if (pm) {
-        inP |= 1u << u;
-        p32 += wf;
-        pab32 = __builtin_fmaf(wf, -y, pab32);
-      }
+      if (need_wlo && in) wlo = fminf(wlo, wf * (1.0f - (0x1p-21f + 2.5e-7f * -y)));
+      const bool pin = in && pm;
+      inP |= pin ? 1u << u : 0u;
+      const float wp = pin ? wf : 0.0f;
+      p32 += wp;
+      pab32 = __builtin_fmaf(wp, -y, pab32);
     }
   }
   // per-thread partial sums to LDS (the E index space is free); wave 0
