@@ -11,8 +11,9 @@
 // Two launches.  The chunk pass: each row is split into C chunks of TCH tokens, one 256-thread
 // workgroup per chunk (small register and LDS footprints, so several
 // workgroups share a CU and their streams overlap).  A chunk streams its
-// logits once and reduces its maximum and its f64 sum of exp(l - chunk
-// maximum).  For its top n it takes a threshold that at least n of its
+// logits once and reduces its maximum and the f64 sum of exp(l - chunk
+// maximum) over weights each within 2^-22 of exact (a corrected f32 exp2;
+// the returned log probabilities stay within 2^-22 relative, see below).  For its top n it takes a threshold that at least n of its
 // tokens reach: each wave's n-th largest lane maximum (n lanes each hold a
 // token at least that large), the largest over the waves.  The tokens at or
 // above it (about n to 2n of 8192 on ordinary rows) are ranked exactly by
@@ -309,11 +310,26 @@ __global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
   }
   lds_barrier();   // the exp tables
   if (t1 > -INFINITY) {
+    // Each weight 2^y, y = (l - t1) log2(e) <= 0, from the f32 exp2 of y's
+    // f32 head corrected by its tail (y - head, below 2^-24 |y|): within
+    // 2^-22 of exp(l - t1), with no error on the thread maximum's weight 1;
+    // summed in f64.  Every weight but the row maximum's carries at most
+    // that relative error, so the sum S is within 2^-22 (S - 1) and
+    // ln S within 2^-22 (S - 1) / S <= 2^-22 of the exact values, and a
+    // log probability (l - M) - ln S, of magnitude at least (S - 1) / S,
+    // within 2^-22 relative.  y is clamped at -1000 (2^-1000 is 0 in f32):
+    // out-of-range tokens (-inf) and suppressed ones (f32::MIN) weigh 0.
     const double tm = (double)t1;
 #pragma unroll
     for (int q = 0; q < TQ; ++q)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part += exp_neg_t((double)x[q][e] - tm, S.etab, S.etab + 64);   // -inf -> 0
+      for (int e = 0; e < 4; ++e) {
+        const double y = fmax(((double)x[q][e] - tm) * 1.4426950408889634, -1000.0);
+        const float yh = (float)y;
+        const float yl = (float)(y - (double)yh);
+        const float eh = __builtin_amdgcn_exp2f(yh);
+        part += (double)__builtin_fmaf(eh, yl * 0.69314718f, eh);
+      }
   }
   {
     const uint32_t kmax = wave_max_u32(lk);
