@@ -357,6 +357,29 @@ def test_nonpositive_bias_rows(torch_mod, sampler, orc):
     assert list(ref["status"]) == [0, -12, -12, 0]
 
 
+def test_nonpositive_bias_default_layout(torch_mod, sampler, orc):
+    """All of config 2 (64 rows: four chunks per row, the layout of the
+    benchmark) with the checkpoint's suppressed IDs and a non-positive bias
+    list per row: every row takes the lean chunk body with bias owners."""
+    from metallix_amd import synth
+    from metallix_amd.sampler import with_suppression
+
+    b = synth.config2()
+    b.name = "nonpositive-bias-64"
+    rng = np.random.default_rng(991)
+    own_ids = [np.unique(rng.integers(0, b.vocab, 40)).astype(np.uint32) for _ in range(b.rows)]
+    for r in range(0, b.rows, 3):   # some rows bias their own argmax and history tokens down
+        h = b.history_ids[b.history_offsets[r]:b.history_offsets[r + 1]]
+        own_ids[r] = np.unique(np.concatenate([own_ids[r], h[:20], [np.argmax(b.logits[r])]]).astype(np.uint32))
+    own_off = np.concatenate([[0], np.cumsum([len(i) for i in own_ids])]).astype(np.uint32)
+    own_val = (-np.abs(rng.standard_normal(int(own_off[-1]))) * 2.0).astype(np.float32)
+    sup = [151643, 151645, int(np.argmax(b.logits[1]))]
+    b.bias_offsets, b.bias_ids, b.bias_values = with_suppression(b.rows, sup, own_off, np.concatenate(own_ids),
+                                                                 own_val)
+    gpu, ref = check(torch_mod, sampler, orc, b)
+    assert (gpu["status"] == 0).all()
+
+
 def test_suppressed_tokens(torch_mod, sampler, orc):
     """A7: the checkpoint's suppress list (ChatFormat::suppress,
     crates/core/chat-format/src/lib.rs:761-780), given to the device as -inf
