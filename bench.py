@@ -202,13 +202,17 @@ def cpu_baseline(cfg, data, seconds: float):
         "sample": f"{rows_done} rows of the same cfg{cfg} inputs (1 thread, rows serial, {seconds:.0f} s)",
     }
     if cfg in (2, 3):
-        threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
+        # Rows partitioned over host threads.  The GPU box gives one GPU's
+        # job a 16-core share of the host, whatever nproc reports, so the
+        # pool stops at 16; nproc is reported beside it.
+        nproc = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+        threads = max(1, min(16, nproc))
         rows_mt, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < seconds / 2:
             oracle.sample_batch_threads(data, threads)
             rows_mt += data.rows
         out["multi_thread"] = {"value": round(rows_mt / (time.perf_counter() - t0), 2), "cores": threads,
-                               "sample": f"{rows_mt} rows"}
+                               "nproc": nproc, "sample": f"{rows_mt} rows"}
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
@@ -371,7 +375,7 @@ def step_bench(torch, s, stream, b, steps, warmup, cpu_seconds):
 
     sup = [151643, 151645]
     saved = (b.bias_offsets, b.bias_ids, b.bias_values)
-    b.bias_offsets, b.bias_ids, b.bias_values = with_suppression(b.rows, sup, *saved)
+    b.bias_offsets, b.bias_ids, b.bias_values = with_suppression(b.rows, sup, *saved, vocab=b.vocab)
     logits, kw = to_device(torch, b)
     b.bias_offsets, b.bias_ids, b.bias_values = saved
     nb = rotation(nbytes(logits))

@@ -59,7 +59,7 @@
 extern "C" {
 #endif
 
-#define MXS_ABI_VERSION 1
+#define MXS_ABI_VERSION 2
 
 /* Call return codes. */
 enum {
@@ -190,9 +190,14 @@ int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int32_t dtype,
  * descending, ID ascending) with f64(l) - maximum - log_normalizer, and the
  * picked token's log probability.  n is the largest top_logprobs + 8, the
  * over-selection the reference ranks before it drops unspellable IDs.
- * Device arrays; rows whose `top` entry is 0 are not written. */
+ * Device arrays; rows whose `top` entry is MXS_RECEIPT_NONE are not
+ * written.  A `top` entry of 0 is a receipt with no top entries (the
+ * reference's `logprobs: true` without top_logprobs, Some(0):
+ * chat_completions.rs:241-243): the picked token's log probability is
+ * still written, with the ranked IDs (the caller keeps none of them). */
+#define MXS_RECEIPT_NONE 0xFFFFFFFFu
 typedef struct {
-  const uint32_t* top;            /* rows entries: the row's top_logprobs, 0 => no receipt; NULL => every row */
+  const uint32_t* top;            /* rows entries: the row's top_logprobs, MXS_RECEIPT_NONE => no receipt; NULL => every row */
   uint32_t n;                     /* entries per row of ids and logprobs, 1..64 */
   uint32_t reserved;
   int32_t* ids;                   /* rows x n; -1 past the vocabulary */

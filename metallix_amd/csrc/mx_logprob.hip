@@ -68,11 +68,11 @@ struct TopnArgs {
   int32_t* status;
   TopnStat* stat;               // [rows * C]
   unsigned long long* list;     // [rows * C * n], (okey << 32) | ~id, descending
-  // Step receipts (mxs_step): rows whose want entry is 0 are skipped; the
-  // bias CSR's -inf entries are the suppressed tokens, read as f32::MIN
-  // (ChatFormat::suppress, crates/core/chat-format/src/lib.rs:771-780);
-  // token_lp[row] is the picked token's log probability.  All nullptr for
-  // mxs_logsoftmax_topn.
+  // Step receipts (mxs_step): rows whose want entry is MXS_RECEIPT_NONE
+  // are skipped; the bias CSR's -inf entries are the suppressed tokens,
+  // read as f32::MIN (ChatFormat::suppress,
+  // crates/core/chat-format/src/lib.rs:771-780); token_lp[row] is the
+  // picked token's log probability.  All nullptr for mxs_logsoftmax_topn.
   const uint32_t* want;
   const uint32_t* sup_off;
   const uint32_t* sup_ids;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(TNT, 6) void topn_kernel(TopnArgs A) {
   const uint32_t chunk = blockIdx.x >> 3;
   const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= A.rows) return;
-  if (A.want && A.want[row] == 0u) return;   // a step row without a receipt
+  if (A.want && A.want[row] == MXS_RECEIPT_NONE) return;   // a step row without a receipt
   const uint32_t V = A.V;
   const uint32_t c0 = chunk * TCH;
   const uint32_t c1 = min(V, c0 + TCH);
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(TNT) void topn_merge_kernel(TopnArgs A) {
   __shared__ MergeSmem S;
   const uint32_t tid = threadIdx.x;
   const uint32_t row = blockIdx.x;
-  if (A.want && A.want[row] == 0u) return;   // a step row without a receipt
+  if (A.want && A.want[row] == MXS_RECEIPT_NONE) return;   // a step row without a receipt
   const uint32_t V = A.V, n = A.n;
   const uint32_t C = A.C;
   const unsigned long long* lists = A.list + (uint64_t)row * C * n;

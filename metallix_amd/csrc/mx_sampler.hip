@@ -385,6 +385,7 @@ struct FinCtx {
   uint32_t kappa, id_tie;
   double M, L, Lclose, total, total_err;
   bool have_total;
+  bool nodraw;         // race-v2: the draw is discarded, so only the kept set's certificate sets the status
   uint32_t* kbits;
   uint32_t nwords;
   uint64_t* timing;    // phase timestamps (diagnostics), null when off
@@ -645,13 +646,13 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
   __syncthreads();
   uint32_t tok = F.s_u[0];
   double shifted = F.s_d[0];
-  if (F.s_u[2]) uncert = true;
+  if (F.s_u[2] && !X.nodraw) uncert = true;
   if (tok == NONE && F.s_u[1]) {
     // rounding left the variate past the accumulated mass: last positive kept token
     const uint32_t j = F.s_u[1] - 1u;
     tok = cand_id(X, F, j);
     shifted = ((double)cand_l(X, F, j) - X.M) / c.T;
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   __syncthreads();
   if (tok == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
@@ -842,10 +843,10 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
   }
   __syncthreads();
   uint32_t pick = F.s_u[0];
-  if (F.s_u[2]) uncert = true;
+  if (F.s_u[2] && !X.nodraw) uncert = true;
   if (pick == NONE) {
     pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
   const double shifted = ((double)el(pick) - X.M) / c.T;
@@ -1239,12 +1240,12 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
   }
   Gr::sync();
   if (any_bad) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
-  bool uncert = unc != 0u || F.s_u[2] != 0u;
+  bool uncert = unc != 0u || (F.s_u[2] != 0u && !X.nodraw);
   uint32_t pick = F.s_u[0];
   if (pick == NONE) {
     // rounding left the variate past the accumulated mass: last positive kept token
     pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
   const uint32_t jp = F.eidx[pick];
@@ -1562,12 +1563,12 @@ __device__ __forceinline__ bool wave_finish(const FinCtx& X, FinSmem& F) {
   if (fb) {
     const uint32_t L = (uint32_t)__builtin_ctzll(fb);
     pick = (uint32_t)__builtin_amdgcn_readlane((int)found, (int)L);
-    uncert = uncert || __builtin_amdgcn_readlane((int)fnear, (int)L) != 0;
+    uncert = uncert || (__builtin_amdgcn_readlane((int)fnear, (int)L) != 0 && !X.nodraw);
   } else {
     // rounding left the variate past the accumulated mass: the last positive kept token
     const uint64_t lb = __builtin_amdgcn_ballot_w64(last != NONE);
     if (lb) pick = (uint32_t)__builtin_amdgcn_readlane((int)last, (int)(63 - __builtin_clzll(lb)));
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
   const double shifted = ((double)F.cl[pick] - X.M) / c.T;
@@ -1846,12 +1847,12 @@ __device__ __forceinline__ void sel_draw_wave(const FinCtx& X, bool kept, double
   const uint64_t fb = __builtin_amdgcn_ballot_w64(hit);
   if (fb) {
     pick = (uint32_t)__builtin_ctzll(fb);
-    uncert = uncert || __builtin_amdgcn_readlane((int)near, (int)pick) != 0;
+    uncert = uncert || (__builtin_amdgcn_readlane((int)near, (int)pick) != 0 && !X.nodraw);
   } else {
     // rounding left the variate past the accumulated mass: the last positive kept token
     const uint64_t lb = __builtin_amdgcn_ballot_w64(dw > 0.0);
     if (lb) pick = (uint32_t)(63 - __builtin_clzll(lb));
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return; }
   const int32_t tok = __builtin_amdgcn_readlane((int)id, (int)pick);
@@ -2070,11 +2071,11 @@ __device__ __forceinline__ bool sel_large(const FinCtx& X, FinSmem& F, const Sel
   uint32_t pick = F.s_u[0];
   bool uncert = Q.unc;
   if (pick != NONE) {
-    uncert = uncert || F.kflag[pick] != 0u;
+    uncert = uncert || (F.kflag[pick] != 0u && !X.nodraw);
   } else {
     // rounding left the variate past the accumulated mass: the last positive kept token
     pick = F.s_u[1] ? F.s_u[1] - 1u : NONE;
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   }
   if (pick == NONE) { write_result(X, MXS_ROW_EMPTY_SUPPORT, -1, 0.0, 0u); return true; }
   const double sp = ((double)F.u.s.pl[pick] - X.M) / c.T;
@@ -2694,13 +2695,13 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
   __syncthreads();
   uint32_t tok = F.s_u[0];
   double shifted = F.s_d[0];
-  if (F.s_u[2]) uncert = true;
+  if (F.s_u[2] && !X.nodraw) uncert = true;
   if (tok == NONE && F.s_u[1]) {
     // rounding left the variate past the accumulated mass: last positive kept token
     const uint32_t j = F.s_u[1] - 1u;
     tok = F.cid[j];
     shifted = ((double)F.cl[j] - X.M) / c.T;
-    uncert = true;
+    uncert = uncert || !X.nodraw;
   } else if (tok != NONE && !exact_s) {
     // the output takes the reference's quotient
     shifted = ((double)okey_value(F.s_u[8]) - X.M) / c.T;
@@ -3095,6 +3096,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   FinCtx X;
   X.cand_l = A.w.cand_l; X.cand_id = A.w.cand_id; X.CH = A.CH; X.o = A.o; X.c = c; X.row = row; X.mode = mode; X.C = C; X.V = V; X.nlegal = nlegal; X.rbase = rbase;
   X.kbits = kbits; X.nwords = nwords; X.M = M; X.timing = A.timing; X.paths = A.paths; X.etab = F.etab;
+  X.nodraw = A.nodraw != 0u;
   if (err) {
     fpath(X, MXS_PATH_ERROR);
     write_result(X, err, -1, 0.0, 0u);

@@ -14,15 +14,15 @@ namespace mxs {
 struct ChunkStat;
 
 // mxs_sample_race runs mxs_sample's pipeline for the kept set and discards
-// its inverse-CDF draw.  That draw still certifies itself: a uniform on a
-// CDF boundary (u = 0 always is) would flag the row uncertified.  This
-// value (the golden-ratio conjugate) keeps the draw's target off the
-// boundaries of equal-weight plateaus and, for other weights, on one only
-// with a probability of about the draw's error bound per kept token.
+// its inverse-CDF draw; with `nodraw` set, the draw's nearness to a CDF
+// boundary never flags a row (only the kept set's own certificate does).
+// Keep-all rows skip the draw; other rows still make one with this uniform
+// (the golden-ratio conjugate, any value in (0, 1) would do).
 constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 
 // mxs_sample's launch; `nodraw` makes keep-all rows skip the inverse-CDF
-// draw (token -1, status 0, the kept set still written).
+// draw (token -1, status 0, the kept set still written) and keeps every
+// row's draw out of its status.
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
 
 // A pick queued on ctx->stream read `words`: when they are a staging

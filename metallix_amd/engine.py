@@ -19,7 +19,7 @@ from typing import Mapping, Optional, Sequence
 
 import numpy as np
 
-from .sampler import with_suppression
+from .sampler import RECEIPT_NONE, with_suppression
 
 RECEIPT_OVERSELECT = 8   # token_logprob ranks top + 8 before dropping unspellable IDs (chat_turn.rs:527-530)
 
@@ -38,29 +38,40 @@ class RowRequest:
     history: Sequence[int] = ()
     bias: Mapping[int, float] = field(default_factory=dict)
     uniform: float = 0.0                # the draw's variate (unit_uniform of the turn's next u64)
-    top_logprobs: Optional[int] = None  # receipt size; None: no receipt
+    top_logprobs: Optional[int] = None  # receipt size; None: no receipt, 0: the token's logprob only
     mask: Optional[np.ndarray] = None   # u32 words over the logit row (SimpleVob layout), None: all legal
 
 
 @dataclass
 class Receipt:
-    logprob: float                      # the picked token's log probability
+    logprob: float                      # log probability of `token`
     top: list                           # [(id, logprob)], most likely first
+    token: int = -1                     # the token `logprob` scores: the device's pick
 
 
 @dataclass
 class RowResult:
+    """One row's pick.  A row with status 1 (uncertified) carries the
+    device's token, which the caller may settle again on the host
+    (chat_turn.rs:348-358); its receipt then still scores the device's token
+    (`receipt.token`): the top list and the normalizer do not depend on the
+    pick, so a caller that settles another token rescores only its logprob."""
     token: int
     status: int
     sampling_logprob: float
     receipt: Optional[Receipt]
 
 
-def pack_rows(requests: Sequence[RowRequest], vocab: int, suppress_ids=()) -> dict:
+def pack_rows(requests: Sequence[RowRequest], vocab: int, suppress_ids=(),
+              tokenizer_vocab: Optional[int] = None) -> dict:
     """Host arrays of one step's batch: per-row rule arrays, the history
     and bias CSRs (the suppressed IDs merged in as -inf bias entries, which
-    the sampler writes as f32::MIN), the receipt sizes, and the mask words
-    (all ones for rows without a mask) when any row has one."""
+    the sampler writes as f32::MIN; IDs past the row are skipped, as
+    ChatFormat::suppress skips them), the receipt sizes (RECEIPT_NONE for
+    rows without one), and the mask words when any row has one: all ones
+    for rows without a mask, and in masked rows every ID at or past
+    `tokenizer_vocab` cleared, as fill_legal_mask never marks them legal
+    (crates/core/engine/src/constraint.rs:793-806)."""
     R = len(requests)
     f = lambda name, dt: np.array([getattr(q, name) for q in requests], dtype=dt)
     out = dict(temperature=f("temperature", np.float64), top_k=f("top_k", np.uint32),
@@ -82,12 +93,13 @@ def pack_rows(requests: Sequence[RowRequest], vocab: int, suppress_ids=()) -> di
     ids = np.concatenate(bids) if boff[-1] else np.zeros(0, np.uint32)
     vals = np.concatenate(bvals) if boff[-1] else np.zeros(0, np.float32)
     if len(suppress_ids):
-        out["bias"] = with_suppression(R, suppress_ids, boff, ids, vals)
+        out["bias"] = with_suppression(R, suppress_ids, boff, ids, vals, vocab=vocab)
     elif boff[-1]:
         out["bias"] = (boff, ids, vals)
     else:
         out["bias"] = None
-    out["receipt_top"] = np.array([q.top_logprobs or 0 for q in requests], dtype=np.uint32)
+    out["receipt_top"] = np.array([RECEIPT_NONE if q.top_logprobs is None else int(q.top_logprobs)
+                                   for q in requests], dtype=np.uint32)
     if any(q.mask is not None for q in requests):
         words = (vocab + 31) // 32
         m = np.full((R, words), 0xFFFFFFFF, dtype=np.uint32)
@@ -96,6 +108,13 @@ def pack_rows(requests: Sequence[RowRequest], vocab: int, suppress_ids=()) -> di
                 w = np.asarray(q.mask, dtype=np.uint32)
                 assert w.size == words, "a mask covers the logit row: ceil(vocab / 32) words"
                 m[r] = w
+                if tokenizer_vocab is not None and tokenizer_vocab < 32 * words:
+                    tv = int(tokenizer_vocab)
+                    m[r, tv // 32 + 1:] = 0
+                    if tv % 32:
+                        m[r, tv // 32] &= np.uint32((1 << (tv % 32)) - 1)
+                    else:
+                        m[r, tv // 32] = 0
         out["mask"] = m
     else:
         out["mask"] = None
@@ -108,7 +127,8 @@ def settle_receipt(token: int, ids, logprobs, token_logprob: float, top: Optiona
     chat_turn.rs:420-433): none when the turn asked for none or the token
     is a stop token (receipt_wanted, :413-418); otherwise the over-selected
     head with IDs that have no spelling dropped (token_bytes fails past the
-    tokenizer's vocabulary, :543-554), its first `top` entries."""
+    tokenizer's vocabulary, :543-554), its first `top` entries (none for a
+    top of 0: the token's log probability alone)."""
     if top is None or token in set(int(t) for t in stop_ids):
         return None
     head = []
@@ -117,7 +137,7 @@ def settle_receipt(token: int, ids, logprobs, token_logprob: float, top: Optiona
         if i < 0 or (spellable is not None and not spellable(i)):
             continue
         head.append((i, float(lp)))
-    return Receipt(logprob=float(token_logprob), top=head[:top])
+    return Receipt(logprob=float(token_logprob), top=head[:top], token=int(token))
 
 
 class EngineStep:
@@ -136,7 +156,7 @@ class EngineStep:
         torch = s.torch
         R, V = logits.shape[0], logits.shape[1]
         assert len(requests) == R
-        h = pack_rows(requests, V, self.suppress_ids)
+        h = pack_rows(requests, V, self.suppress_ids, self.tokenizer_vocab)
         dev = logits.device
         T = lambda a, dt: torch.from_numpy(np.ascontiguousarray(np.asarray(a, dtype=dt))).to(dev)
         i32 = lambda a: T(np.asarray(a, dtype=np.uint32).view(np.int32), np.int32)
@@ -152,7 +172,8 @@ class EngineStep:
             kw["mask"] = i32(h["mask"])
             kw["tokenizer_vocab"] = V
         tops = h["receipt_top"]
-        n = int(min(64, max(1, int(tops.max()) + RECEIPT_OVERSELECT)))
+        wanted = tops[tops != RECEIPT_NONE]
+        n = int(min(64, max(1, (int(wanted.max()) if wanted.size else 0) + RECEIPT_OVERSELECT)))
         out, rec = s.step(logits, receipt_top=i32(tops), n=n, **kw)
         s.sync()
         tok, st = out.token.cpu().numpy(), out.status.cpu().numpy()
@@ -163,7 +184,7 @@ class EngineStep:
         res = []
         for r, q in enumerate(requests):
             receipt = None
-            if st[r] >= 0 and q.top_logprobs:
+            if st[r] >= 0 and q.top_logprobs is not None:
                 receipt = settle_receipt(int(tok[r]), ids[r], lps[r], float(tlp[r]), q.top_logprobs, self.stop_ids,
                                          spell)
             res.append(RowResult(token=int(tok[r]), status=int(st[r]), sampling_logprob=float(slp[r]),

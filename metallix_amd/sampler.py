@@ -106,6 +106,10 @@ class SamplerError(RuntimeError):
     pass
 
 
+ABI_VERSION = 2                 # MXS_ABI_VERSION of include/mx_sampler.h
+RECEIPT_NONE = 0xFFFFFFFF       # MXS_RECEIPT_NONE: a receipt_top entry for "no receipt"
+
+
 def load_library(path: Optional[Path] = None):
     """Loads the built library; raises when it is missing (no fallback)."""
     global _LIB
@@ -119,22 +123,32 @@ def load_library(path: Optional[Path] = None):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.mxs_abi_version() != ABI_VERSION:
+        raise SamplerError(f"{p} implements ABI {lib.mxs_abi_version()}, these bindings ABI {ABI_VERSION}: rebuild")
     if path is None:
         _LIB = lib
     return lib
 
 
-def with_suppression(rows: int, suppress_ids, bias_offsets=None, bias_ids=None, bias_values=None):
+def with_suppression(rows: int, suppress_ids, bias_offsets=None, bias_ids=None, bias_values=None, *,
+                     vocab: Optional[int] = None):
     """Host-side CSR for the sampler's bias stage with the checkpoint's
     suppressed tokens merged in (ChatFormat::suppress,
     crates/core/chat-format/src/lib.rs:761-780): every row gets a -inf entry
     for each id of `suppress_ids` (ids are per checkpoint, the same for every
     row), which the sampler turns into an adjusted logit of f32::MIN.  A
-    suppressed id keeps no bias of its own.  Returns numpy (offsets u32[rows
-    + 1], ids u32, values f32), ids strictly increasing within a row."""
+    suppressed id keeps no bias of its own.  An id at or past `vocab` (the
+    logit row's length) is skipped, as the reference's `logits.get_mut`
+    returns None for it (:771-778); without `vocab` every id is kept, and the
+    sampler reports one past the row as an invalid bias entry.  Returns
+    numpy (offsets u32[rows + 1], ids u32, values f32), ids strictly
+    increasing within a row."""
     import numpy as np
 
-    sup = np.unique(np.asarray(suppress_ids, dtype=np.uint32))
+    sup = np.unique(np.asarray(suppress_ids, dtype=np.int64))
+    if vocab is not None:
+        sup = sup[(sup >= 0) & (sup < int(vocab))]
+    sup = sup.astype(np.uint32)
     offs, ids, vals = [0], [], []
     for r in range(rows):
         if bias_offsets is not None:
@@ -258,7 +272,8 @@ class Sampler:
         """Queues one engine step (mxs_step): every row's pick as `sample`
         does, then the receipts over the suppressed logits (the bias
         entries of -inf) of the rows whose receipt_top entry (u32[rows] on
-        the device; None: every row) is non-zero, with n IDs per row.
+        the device; None: every row) is not RECEIPT_NONE, with n IDs per
+        row (an entry of 0 still gets the picked token's log probability).
         Returns (SampleResult, ReceiptResult) of device tensors."""
         torch = self.torch
         b, o, r, out = self._structs(logits, temperature, race=race, **kw)

@@ -26,7 +26,7 @@ def test_abi_version_and_status_strings():
     from metallix_amd import sampler
 
     lib = sampler.load_library()
-    assert lib.mxs_abi_version() == 1
+    assert lib.mxs_abi_version() == sampler.ABI_VERSION == 2
     assert lib.mxs_status_string(0) == b"ok"
     assert b"temperature" in lib.mxs_status_string(-4)
 

@@ -185,16 +185,18 @@ class SplitMix:
         return (self.next_u64() >> 11) / float(1 << 53)
 
 
+# The toy model both the exact-sequence-law check and the point-mass walk use.
+TOY_VOCAB, TOY_PROMPT = 3, [0, 2, 1]   # speculative/tests.rs:14-15
+
+
 def toy_logits(context):
-    """The deterministic toy model of speculative/tests.rs:448-510."""
-    last = context[-1]
+    """speculative/tests.rs:37-52: the toy model's next-token row."""
+    last = context[-1] if context else 0
     before = context[-2] if len(context) >= 2 else 0
-    length = len(context)
-    out = []
-    for tok in range(3):
-        mix = (last * 7 + before * 3 + tok * 5 + length) % 11
-        out.append(float(np.float32(np.float32(mix) * np.float32(0.37))) - (0.8 if tok == last else 0.0))
-    return f32(out)
+    n = len(context)
+    return np.array([np.float32(np.float32((last * 7 + before * 3 + t * 5 + n) % 11) * np.float32(0.37))
+                     - (np.float32(0.8) if t == last else np.float32(0.0)) for t in range(TOY_VOCAB)],
+                    dtype=np.float32)
 
 
 def weights(logits, T):
@@ -274,19 +276,6 @@ def test_law_check_sees_a_wrong_bonus_row(orc):
 
 
 # ---- A9: the point-mass verify walk (accept_and_roll_back) --------------------
-TOY_VOCAB, TOY_PROMPT = 3, [0, 2, 1]   # speculative/tests.rs:14-15
-
-
-def toy_logits(context):
-    """speculative/tests.rs:37-52: the toy model's next-token row."""
-    last = context[-1] if context else 0
-    before = context[-2] if len(context) >= 2 else 0
-    n = len(context)
-    return np.array([np.float32(np.float32((last * 7 + before * 3 + t * 5 + n) % 11) * np.float32(0.37))
-                     - (np.float32(0.8) if t == last else np.float32(0.0)) for t in range(TOY_VOCAB)],
-                    dtype=np.float32)
-
-
 def toy_sample(orc, row, uniform):
     st, tok, _ = orc.sample_categorical(row, None, 0.9, uniform)
     assert st == 0
