@@ -274,6 +274,9 @@ def main():
                     help="also time config-3 steps whose masks are uploaded from pinned staging each step")
     ap.add_argument("--receipts", action="store_true",
                     help="also time engine steps with top-20 receipts for every row (mxs_step, config 2)")
+    ap.add_argument("--stream-floor", action="store_true",
+                    help="also time mxs_sample's launch floor and stream floor (its grid, workgroup size and LDS; "
+                         "configs 1-4) and account for one call's time from the workgroups' entry and exit stamps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device copies (scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -356,8 +359,123 @@ def main():
     if args.receipts and cfg == 2:
         res["engine_step"] = step_bench(torch, s, stream, data, args.steps, args.warmup,
                                         None if args.no_cpu else args.cpu_seconds)
+    if args.stream_floor and cfg in (1, 2, 3, 4):
+        res["floors"] = floor_bench(torch, s, stream, data, args.steps, args.warmup)
     res["cpu_baseline"] = None if args.no_cpu else cpu_baseline(cfg, data, args.cpu_seconds)
     print(json.dumps(res), flush=True)
+
+
+def floor_bench(torch, s, stream, b, steps, warmup):
+    """What bounds one mxs_sample call, on resident logits rotated as in the
+    main timing:
+    - launch_floor: a kernel of mxs_sample's grid, workgroup size and LDS per
+      workgroup whose workgroups exit at once;
+    - stream_floor: the same launch, each workgroup reading its chunk of the
+      logits once (all loads issued up front) and writing the maximum;
+    - sample: mxs_sample itself;
+    each back to back, from events on the stream.  Then `accounting`: single
+    calls (the queue kept busy before each, so the events bracket the kernel
+    alone), medians over 12 calls of the event-timed duration and of the
+    workgroups' wall-clock stamps (100 MHz, relative to the first
+    workgroup's first instruction): the last workgroup's entry, the last
+    chunk body's start, the last exit of a chunk workgroup that does not
+    finish its row, the last finisher's end and the last exit.
+    The difference between the event time and the last exit is the launch's
+    dispatch and completion overhead."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from helpers import to_device
+
+    logits, kw = to_device(torch, b)
+    nb = rotation(nbytes(logits))
+    bufs = [logits] + [logits.clone() for _ in range(nb - 1)]
+    dev = logits.device
+    rows, V = logits.shape
+    dt = 0 if logits.dtype == torch.float32 else 1     # MXS_F32, MXS_BF16
+    out = torch.empty(rows * 64, dtype=torch.float32, device=dev)
+    fst = torch.zeros(rows * 64 * 2, dtype=torch.int64, device=dev)
+
+    def floor(mode):
+        def f(i):
+            rc = s.lib.mxs_debug_floor(s.ctx, bufs[i % nb].data_ptr(), dt, rows, V, V, mode, out.data_ptr(),
+                                       fst.data_ptr() if mode == 2 else None)
+            assert rc == 0, s.lib.mxs_last_error(s.ctx)
+        return f
+
+    with torch.cuda.stream(stream):
+        launch = s.launcher(bufs[0], **kw)
+    res = {}
+    for name, fn in (("launch_floor", floor(0)), ("stream_floor", floor(1)), ("sample", lambda i: launch(bufs[i % nb]))):
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for i in range(steps):
+                fn(i)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        res[name] = {"us_per_launch": round(ms * 1e3, 3), "logits_gbs": round(nbytes(logits) / (ms / 1e3) / 1e9, 1)}
+    # the stream floor read every logit: its chunk maxima make the row maxima
+    floor(1)(0)
+    torch.cuda.synchronize()
+    C = int(out.view(rows, 64).isfinite().sum(dim=1).max().item())
+    got = out.view(rows, 64)[:, :C].max(dim=1).values
+    assert torch.equal(got, bufs[0].float().max(dim=1).values), "stream floor maxima differ from torch.max"
+
+    # the stream floor's own span: first entry to last exit, one call at a time
+    spans = []
+    for it in range(12):
+        fst.zero_()
+        floor(1)(it + 1)
+        floor(2)(it)
+        torch.cuda.synchronize()
+        f = fst.view(rows, 64, 2).cpu().numpy().astype(np.float64)
+        ok = f[..., 0] > 0
+        spans.append([(f[..., 1][ok].max() - f[..., 0][ok].min()) / 100.0,
+                      (f[..., 0][ok].max() - f[..., 0][ok].min()) / 100.0])
+    sp = np.median(np.array(spans), axis=0)
+    res["stream_floor"]["span_us"] = round(sp[0], 2)
+    res["stream_floor"]["last_entry_us"] = round(sp[1], 2)
+
+    SL, TS = 65, 16
+    tb = torch.zeros(rows * SL * TS, dtype=torch.int64, device=dev)
+    s.lib.mxs_debug_set_timing(s.ctx, tb.data_ptr())
+    acc = []
+    try:
+        for it in range(12):
+            tb.zero_()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                for j in range(8):      # keeps the queue busy while the host queues the timed call
+                    floor(1)(j + 1)
+                e0.record(stream)
+                launch(bufs[0])
+                e1.record(stream)
+            torch.cuda.synchronize()
+            t = tb.view(rows, SL, TS).cpu().numpy().astype(np.float64)
+            ent = t[:, :SL - 1, 8]
+            t0 = ent[ent > 0].min()
+            rel = lambda a: (a[a > 0] - t0) / 100.0     # µs
+            ce, fe = rel(t[:, :SL - 1, 9]), rel(t[:, SL - 1, 9])
+            acc.append([e0.elapsed_time(e1) * 1e3, rel(ent).max(), rel(t[:, :SL - 1, 0]).max(),
+                        ce.max() if ce.size else 0.0, rel(t[:, SL - 1, 7]).max(), max(ce.max() if ce.size else 0.0,
+                                                                                      fe.max())])
+    finally:
+        s.lib.mxs_debug_set_timing(s.ctx, None)
+    m = np.median(np.array(acc), axis=0)
+    res["accounting_us"] = {
+        "event_duration": round(m[0], 2), "last_workgroup_entry": round(m[1], 2),
+        "last_chunk_body_start": round(m[2], 2), "last_chunk_exit": round(m[3], 2),
+        "last_finisher_end": round(m[4], 2), "last_exit": round(m[5], 2),
+        "dispatch_and_completion": round(m[0] - m[5], 2),
+    }
+    return res
 
 
 def step_bench(torch, s, stream, b, steps, warmup, cpu_seconds):

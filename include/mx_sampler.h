@@ -232,10 +232,23 @@ int mxs_mask_upload(mxs_ctx* ctx, uint32_t slot, uint32_t rows, const uint32_t**
 int mxs_sync(mxs_ctx* ctx);
 /* Diagnostics (no reference counterpart): when `device_buffer` is non-null,
  * mxs_sample records 100 MHz wall-clock stamps at fixed phase boundaries:
- * u64 [rows][MXS_DEBUG_TIMING_SLOTS][8], chunk workgroups at slot = chunk,
- * the row finisher at slot MXS_DEBUG_TIMING_SLOTS - 1.  NULL disables. */
+ * u64 [rows][MXS_DEBUG_TIMING_SLOTS][MXS_DEBUG_TIMING_STAMPS], chunk
+ * workgroups at slot = chunk, the row finisher at slot
+ * MXS_DEBUG_TIMING_SLOTS - 1; stamp 8 is a workgroup's first instruction,
+ * stamp 9 its exit.  NULL disables. */
 #define MXS_DEBUG_TIMING_SLOTS 65
+#define MXS_DEBUG_TIMING_STAMPS 16
 int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer);
+/* Diagnostics (no reference counterpart): measurement floors in
+ * mxs_sample's launch shape (grid, workgroup size, LDS per workgroup) on the
+ * context's stream.  mode 0: every workgroup exits at once (the launch
+ * floor); mode 1: every workgroup reads its chunk of the logits once and
+ * writes its maximum (the stream floor); mode 2: mode 1 that also writes
+ * each workgroup's 100 MHz wall-clock stamps at entry and exit to `stamps`
+ * (device u64 [rows][MXS_DEBUG_TIMING_SLOTS - 1][2]; NULL otherwise).
+ * `out`: device f32 [rows][MXS_DEBUG_TIMING_SLOTS - 1]. */
+int mxs_debug_floor(mxs_ctx* ctx, const void* logits, int32_t dtype, uint32_t rows, uint32_t vocab,
+                    uint32_t row_stride, uint32_t mode, float* out, uint64_t* stamps);
 /* Diagnostics (no reference counterpart): when `device_buffer` (int32
  * [rows]) is non-null, mxs_sample writes the finisher path each row took. */
 enum {

@@ -95,12 +95,14 @@ struct SampleArgs {
 };
 
 // Phase timestamps for diagnostics: wall clock (100 MHz) at fixed points of
-// each chunk workgroup and each row finisher.
+// each chunk workgroup and each row finisher, TSTAMPS per record.  Slots
+// 0-7 are phases; slot 8 is the workgroup's first instruction and slot 9 its
+// exit (for the workgroup that finishes the row, in the finisher's record).
 // Every lane stores the same value (a uniform branch only): a lane-0
 // condition would make the compiler move uniform values into vector
 // registers.
 __device__ __forceinline__ void stamp(const SampleArgs& A, uint32_t row, uint32_t chunk, uint32_t k) {
-  if (A.timing) A.timing[((uint64_t)row * (MAXC + 1) + chunk) * 8 + k] = wall_clock64();
+  if (A.timing) A.timing[((uint64_t)row * (MAXC + 1) + chunk) * TSTAMPS + k] = wall_clock64();
 }
 
 // IEEE argmax with the lowest index on ties (-0.0 ties 0.0): greedy_token's
@@ -401,7 +403,7 @@ __device__ __forceinline__ void fpath(const FinCtx& X, int32_t p) {
 
 // Finisher phase timestamp k (slot MAXC of the row's timing record).
 __device__ __forceinline__ void fstamp(const FinCtx& X, uint32_t k) {
-  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + k] = wall_clock64();
+  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * TSTAMPS + k] = wall_clock64();
 }
 
 __device__ __forceinline__ uint64_t cand_pos_of(const FinSmem& F, uint32_t C, uint64_t rbase, uint32_t CH, uint32_t j) {
@@ -1590,7 +1592,7 @@ __device__ __forceinline__ bool finish_fast(const FinCtx& X, FinSmem& F) {
   const RowCfg& c = X.c;
   const uint32_t tid = threadIdx.x;
   const uint32_t n = X.ncand;
-  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * 8 + 3] = n;   // candidate count (diagnostics)
+  if (X.timing) X.timing[((uint64_t)X.row * (MAXC + 1) + MAXC) * TSTAMPS + 3] = n;   // candidate count (diagnostics)
   if (n == 0 || n > (uint32_t)CCAP || !X.lds_c) return false;
   const uint32_t R = (n + FT - 1u) / FT;
   const uint32_t j0 = tid * R;
@@ -4815,9 +4817,9 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
 
 // ---------------------------------------------------------------------------
 // The chunk kernel.  Workgroup -> (row, chunk) as in the general body.  The
-// first slice goes out before the row's parameters arrive; rows the lean
-// body covers then issue the history ids and the rest of the stream and run
-// it, the others run the general body (which issues its own loads).
+// row's parameters decide the body: rows the lean body covers issue the
+// history ids and the stream there and run it, the others run the general
+// body (which issues its own loads).
 template <typename In>
 __global__ __launch_bounds__(NT) void sample_kernel(
     SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
@@ -4830,6 +4832,7 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const uint32_t chunk = blockIdx.x >> 3;
   const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= b.rows) return;
+  stamp(A, row, chunk, 8);
   const uint32_t V = b.vocab;
   const uint32_t c0 = chunk * A.CH;
   const uint32_t c1 = min(V, c0 + A.CH);
@@ -4869,7 +4872,10 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   // per row, mostly down code no other wave of the workgroup has run, so its
   // instruction fetches miss the instruction cache; one shared copy keeps the
   // kernel's code (and the lines every row's finisher fetches) small.
-  if (!last) return;
+  if (!last) {
+    stamp(A, row, chunk, 9);
+    return;
+  }
   stamp(A, row, MAXC, 0);
   FinLoads P;
   fin_issue(A, row, P);
@@ -4884,6 +4890,21 @@ __global__ __launch_bounds__(NT) void sample_kernel(
     st_dev(A.w.ctr + (uint64_t)row * CTR_STRIDE, 0u);
     st_dev(A.w.rowx + (uint64_t)row * ROWX_STRIDE, 0ull);
   }
+  stamp(A, row, MAXC, 9);
+}
+
+size_t sample_lds_bytes() { return sizeof(FusedSmem); }
+
+// A batch whose chunks would not fill the CUs streams each row with twice
+// as many workgroups (half the quads per thread), while the doubled count
+// stays within the register-slot finishers' FW chunks.
+ChunkLayout sample_layout(uint32_t rows, uint32_t V) {
+  ChunkLayout L = chunk_layout(V);
+  if ((uint64_t)rows * L.C < 256u) {
+    const ChunkLayout L2 = chunk_layout(V, (uint32_t)PER_MAX / 2u);
+    if (L2.C <= (uint32_t)FW) L = L2;
+  }
+  return L;
 }
 
 }  // namespace mxs
@@ -4931,14 +4952,7 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   const float* p_rep = b->repetition ? b->repetition : ctx->d_one_f32;
   const float* p_pres = b->presence ? b->presence : ctx->d_zero_f32;
   const float* p_freq = b->frequency ? b->frequency : ctx->d_zero_f32;
-  // A batch whose chunks would not fill the CUs streams each row with twice
-  // as many workgroups (half the quads per thread), while the doubled count
-  // stays within the register-slot finishers' FW chunks.
-  mxs::ChunkLayout L = mxs::chunk_layout(b->vocab);
-  if ((uint64_t)b->rows * L.C < 256u) {
-    const mxs::ChunkLayout L2 = mxs::chunk_layout(b->vocab, (uint32_t)mxs::PER_MAX / 2u);
-    if (L2.C <= (uint32_t)mxs::FW) L = L2;
-  }
+  const mxs::ChunkLayout L = sample_layout(b->rows, b->vocab);
   const uint32_t C = L.C;
   A.C = L.C;
   A.CH = L.CH;

@@ -25,6 +25,12 @@ constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 // row's draw out of its status.
 int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
 
+// The sample kernel's LDS bytes per workgroup and its chunk layout for a
+// batch of `rows` rows of V tokens (mx_floor.hip launches with both).
+size_t sample_lds_bytes();
+struct ChunkLayout;
+ChunkLayout sample_layout(uint32_t rows, uint32_t V);
+
 // A pick queued on ctx->stream read `words`: when they are a staging
 // slot's device words, the slot's next upload waits for that pick
 // (mx_mask.hip).

@@ -15,6 +15,7 @@ constexpr int PER_MAX = 10;               // 4-token quads per thread per chunk
 constexpr int SLICE = NT * 4;             // tokens per slice (one quad per thread)
 constexpr int CHUNK_MAX = SLICE * PER_MAX;
 constexpr int MAXC = 64;                  // chunks per row (vocab <= MAXC * CHUNK_MAX)
+constexpr int TSTAMPS = 16;               // diagnostic timestamps per timing record
 constexpr uint32_t NONE = 0xffffffffu;
 constexpr double U = 1.1102230246251565e-16;  // 2^-53
 

@@ -95,6 +95,8 @@ PROTOTYPES = {
     "mxs_mask_upload": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_vp)]),
     "mxs_sync": (ctypes.c_int, [_vp]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
+    "mxs_debug_floor": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                       ctypes.c_uint32, _vp, _vp]),
     "mxs_debug_set_paths": (ctypes.c_int, [_vp, _vp]),
     "mxs_last_error": (ctypes.c_char_p, [_vp]),
 }
