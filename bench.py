@@ -517,7 +517,9 @@ def step_bench(torch, s, stream, b, steps, warmup, cpu_seconds):
     assert (st >= 0).all() and (rst == 0).all(), f"row errors in the step benchmark: {st} {rst}"
     res = {"ms_per_step": round(ms, 6), "rows_per_s": round(b.rows / (ms / 1e3), 1),
            "receipt_top": 20, "ranked_ids": TOPN, "suppressed_ids": sup,
-           "algorithmic_bytes": sample_bytes(logits, kw) + topn_bytes(logits, b.vocab, TOPN)}
+           # one read of the logits (the receipts come from the pick's pass) and
+           # the receipts' outputs
+           "algorithmic_bytes": sample_bytes(logits, kw) + b.rows * (TOPN * (4 + 8) + 8 + 4)}
     if cpu_seconds:
         from oracle import oracle
 

@@ -235,7 +235,8 @@ int mxs_sync(mxs_ctx* ctx);
  * u64 [rows][MXS_DEBUG_TIMING_SLOTS][MXS_DEBUG_TIMING_STAMPS], chunk
  * workgroups at slot = chunk, the row finisher at slot
  * MXS_DEBUG_TIMING_SLOTS - 1; stamp 8 is a workgroup's first instruction,
- * stamp 9 its exit.  NULL disables. */
+ * stamp 9 its exit, stamps 10 and 11 bracket a step receipt's work.  NULL
+ * disables. */
 #define MXS_DEBUG_TIMING_SLOTS 65
 #define MXS_DEBUG_TIMING_STAMPS 16
 int mxs_debug_set_timing(mxs_ctx* ctx, void* device_buffer);

@@ -772,8 +772,9 @@ extern "C" int mxs_logsoftmax_topn_noalloc(void* stream, const void* logits, int
 }
 
 // One engine step (engine_loop.rs:1080-1134, ChatTurn::pick at
-// chat_turn.rs:290-303): every row's pick, then the log-probability receipt
-// of the rows that want one, over the logits after suppression.
+// chat_turn.rs:290-303): every row's pick and the log-probability receipt of
+// the rows that want one, over the logits after suppression: one pass of
+// the sample kernel, or, under race-v2, the top-n kernels after the race.
 extern "C" int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const mxs_out* out,
                         const mxs_receipts* receipts) {
   if (!ctx || !batch || !out) return MXS_EINVAL;
@@ -786,7 +787,13 @@ extern "C" int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* ra
                                         R.logprobs, R.token_logprob, R.token_logprob, R.status))
       return fail(ctx, MXS_EINVAL, m);
   }
-  int rc = race ? mxs_sample_race(ctx, batch, race, out) : mxs_sample(ctx, batch, out);
+  if (!race) {
+    // the receipts come from the pick's own pass over the logits
+    if (batch->rows == 0) return MXS_OK;
+    return mxs::sample_launch(ctx, batch, out, false, receipts);
+  }
+  // race-v2: the token comes from the race kernel, so the receipts follow it
+  int rc = mxs_sample_race(ctx, batch, race, out);
   if (rc != MXS_OK || !receipts || batch->rows == 0) return rc;
   const mxs_receipts& R = *receipts;
   mxs::TopnArgs X{};

@@ -80,6 +80,15 @@ struct ChunkStat {
 };
 
 
+// Per-chunk receipt statistics (step receipts fused into the pick).
+struct RxStat {
+  float maxv;          // the chunk's largest logit after suppression
+  uint32_t flags;      // 1: a non-finite logit
+  uint32_t count;      // entries listed
+  uint32_t pad;
+  double sum;          // sum of exp(l - maxv) over the chunk
+};
+
 struct SampleArgs {
   mxs_batch b;
   mxs_out o;
@@ -92,12 +101,25 @@ struct SampleArgs {
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
   uint32_t epoch;      // this call's tag for Work::rowx (never 0; the row's last chunk also clears its word)
   uint32_t nodraw;     // keep-all rows skip the inverse-CDF draw (race-v2 calls)
+  // Step receipts fused into the pick (mxs_step without race-v2): rows whose
+  // rx_want entry is not MXS_RECEIPT_NONE also get the log-softmax top rx_n
+  // of their logits after suppression, read in the same pass; rx_want null:
+  // no receipts
+  const uint32_t* rx_want;
+  uint32_t rx_n;
+  int32_t* rx_ids;             // [rows * rx_n]
+  double* rx_lps;              // [rows * rx_n]
+  double* rx_token_lp;         // [rows]
+  int32_t* rx_status;          // [rows]
+  RxStat* rx_stat;             // [rows * MAXC]
+  unsigned long long* rx_list; // [rows * MAXC * rx_n], (okey << 32) | ~id, descending
 };
 
 // Phase timestamps for diagnostics: wall clock (100 MHz) at fixed points of
 // each chunk workgroup and each row finisher, TSTAMPS per record.  Slots
 // 0-7 are phases; slot 8 is the workgroup's first instruction and slot 9 its
-// exit (for the workgroup that finishes the row, in the finisher's record).
+// exit (for the workgroup that finishes the row, in the finisher's record);
+// slots 10 and 11 bracket the step receipt's work (chunk share, merge).
 // Every lane stores the same value (a uniform branch only): a lane-0
 // condition would make the compiler move uniform values into vector
 // registers.
@@ -3520,6 +3542,499 @@ union alignas(16) FusedSmem {
 __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 
 // ---------------------------------------------------------------------------
+// Step receipts fused into the pick.  A receipt is the log-softmax top n of
+// the row's logits after suppression (ChatFormat::suppress writes f32::MIN,
+// crates/core/chat-format/src/lib.rs:771-780) and the picked token's log
+// probability (token_logprob, crates/app/cli/src/chat_turn.rs:506-563): what
+// mx_logprob.hip's top-n kernels compute for a receipt, here from the chunk
+// pass's own read of the logits.  Each chunk publishes its maximum, its sum
+// of exp(l - maximum) and its exact top min(n, length) entries (key desc,
+// token ID asc); the row's finisher merges them after the pick.
+constexpr uint32_t RX_CAP = 2048;   // entries at or above the lower bound, collected in LDS
+static_assert(offsetof(ChunkSmem, bvals) == offsetof(ChunkSmem, bids) + BCAP * 4 && BCAP * 2 >= (int)RX_CAP,
+              "the receipt candidates take bids and bvals");
+static_assert(MCAP >= 1024 + 128, "the receipt histogram, wave values and counters take mask");
+static_assert(offsetof(FinSmem, cid) == offsetof(FinSmem, cl) + CCAP * 4 && CCAP * 8 >= (MAXC * 64 + 16) * 8,
+              "the receipt merge takes the finisher's candidate cache (cl, then cid)");
+
+// f(i) for the slices i < A.per: unrolled (UNR > 1: a getter over register
+// arrays needs compile-time indices) or rolled.
+template <int UNR, typename F>
+__device__ __forceinline__ void rx_slices(const SampleArgs& A, F f) {
+  if constexpr (UNR > 1) {
+#pragma unroll
+    for (int i = 0; i < PER_MAX; ++i)
+      if (i < (int)A.per) f(i);
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < (int)A.per; ++i) f(i);
+  }
+}
+
+__device__ __forceinline__ unsigned long long rx_entry(uint32_t k, uint32_t id) {
+  return ((unsigned long long)k << 32) | (unsigned long long)(~id);
+}
+
+// The rank (descending) of `mine` among m distinct nonzero entries v[0, m),
+// by counting.  v must hold zeros up to the next multiple of 8 (they count
+// for no entry); the comparisons read 8 entries per round as 4 independent
+// 16-byte loads, not one dependent load each.
+__device__ __forceinline__ uint32_t rx_rank_of(const unsigned long long* v, uint32_t m, unsigned long long mine) {
+  const uint32_t m8 = (m + 7u) & ~7u;
+  uint32_t rank = 0;
+  for (uint32_t k = 0; k < m8; k += 8u) {
+    ulonglong2 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u] = *reinterpret_cast<const ulonglong2*>(&v[k + 2u * (uint32_t)u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) rank += (q[u].x > mine ? 1u : 0u) + (q[u].y > mine ? 1u : 0u);
+  }
+  return rank;
+}
+
+// The entries of v[0, m) ranked below `want`, stored in rank order to out
+// (device scope); v padded as rx_rank_of needs.
+__device__ __forceinline__ void rx_rank(const unsigned long long* v, uint32_t m, uint32_t want,
+                                        unsigned long long* out) {
+  for (uint32_t j = threadIdx.x; j < m; j += NT) {
+    const unsigned long long mine = v[j];
+    const uint32_t rank = rx_rank_of(v, m, mine);
+    if (rank < want) st_dev(reinterpret_cast<double*>(&out[rank]), __builtin_bit_cast(double, mine));
+  }
+}
+
+// The receipt's exact top-take of a chunk, where the fast path of
+// receipt_chunk failed: the take-th largest key K by a bit search over block
+// counts (one counter per round), then the keys above K and the ties at K in
+// token-ID order, ranked and written out.
+template <typename GetQ>
+__device__ __forceinline__ void receipt_exact(const SampleArgs& A, ChunkSmem& S, uint32_t row, uint32_t chunk,
+                                              uint32_t c0, uint32_t take, GetQ getq) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t* rcnt = S.mask + 1088;
+  unsigned long long* rc = reinterpret_cast<unsigned long long*>(S.bids);
+  unsigned long long* list = A.rx_list + ((uint64_t)row * MAXC + chunk) * A.rx_n;
+  lds_barrier();   // every thread has read the fast path's counters
+  if (tid < 40u) rcnt[tid] = 0u;
+  lds_barrier();
+    uint32_t K = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = K | (1u << bit);
+      uint32_t cnt = 0;
+#pragma unroll 1
+      for (int i = 0; i < (int)A.per; ++i) {
+        float r[4];
+        uint32_t rb;
+        getq(i, r, rb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cnt += (((rb >> e) & 1u) && okey(r[e]) >= cand) ? 1u : 0u;
+      }
+      cnt = wave_sum_u32(cnt);
+      if (lane() == 0) atomicAdd(&rcnt[2 + bit], cnt);
+      lds_barrier();
+      if (rcnt[2 + bit] >= take) K = cand;
+    }
+    // keys above K (fewer than take) first, then the ties: counts per
+    // (slice, wave) in token-ID order
+#pragma unroll 1
+    for (int i = 0; i < (int)A.per; ++i) {
+      uint32_t tq = 0;
+      float r[4];
+      uint32_t rb;
+      getq(i, r, rb);
+      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool inr = (rb >> e) & 1u;
+        const uint32_t k = okey(r[e]);
+        if (inr && k > K) rc[atomicAdd(&rcnt[1], 1u)] = rx_entry(k, e0 + (uint32_t)e);
+        tq += (inr && k == K) ? 1u : 0u;
+      }
+      const uint32_t wt = wave_sum_u32(tq);
+      if (lane() == 0) S.wcnt[i * NW + wave()] = wt;
+    }
+    lds_barrier();
+    const uint32_t above = rcnt[1], need = take - above;
+    const uint32_t nent = A.per * NW;
+    const uint32_t v0 = lane() < nent ? S.wcnt[lane()] : 0u;
+    const uint32_t v1 = lane() + 64u < nent ? S.wcnt[lane() + 64u] : 0u;
+    const uint32_t v2 = lane() + 128u < nent ? S.wcnt[lane() + 128u] : 0u;
+    const uint32_t i0 = wave_scan_u32(v0), i1 = wave_scan_u32(v1), i2 = wave_scan_u32(v2);
+    const uint32_t s0 = (uint32_t)__builtin_amdgcn_readlane((int)i0, 63);
+    const uint32_t s1 = (uint32_t)__builtin_amdgcn_readlane((int)i1, 63);
+    const uint32_t x0 = i0 - v0, x1 = i1 - v1 + s0, x2 = i2 - v2 + s0 + s1;
+#pragma unroll 1
+    for (int i = 0; i < (int)A.per; ++i) {
+      {
+        float r[4];
+        uint32_t rb;
+        getq(i, r, rb);
+        bool tie[4];
+        uint32_t tq = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          tie[e] = ((rb >> e) & 1u) && okey(r[e]) == K;
+          tq += tie[e] ? 1u : 0u;
+        }
+        const uint32_t idx = (uint32_t)i * NW + wave();
+        const uint32_t xv = (idx >> 6) == 0 ? x0 : ((idx >> 6) == 1 ? x1 : x2);
+        uint32_t rk = (uint32_t)__builtin_amdgcn_readlane((int)xv, (int)(idx & 63u)) + (wave_scan_u32(tq) - tq);
+        const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (tie[e]) {
+            if (rk < need) rc[above + rk] = rx_entry(K, e0 + (uint32_t)e);
+            ++rk;
+          }
+        }
+      }
+    }
+    lds_barrier();
+  if (tid < 16u) rc[take + tid] = 0ull;
+  lds_barrier();
+  rx_rank(rc, take, take, list);
+}
+
+// getq(i, r, rb): this thread's quad of slice i after suppression (f32::MIN)
+// into r, its in-range bits into rb.  UNR: PER_MAX for a getter over
+// register arrays (compile-time slice indices), 1 for one that loads (the
+// slice loop stays rolled, so no pass holds the whole chunk in registers).
+// Uses mask, bids, bvals and wcnt of the chunk's LDS; every thread of the
+// workgroup calls it.
+template <int UNR, typename GetQ>
+__device__ __forceinline__ bool receipt_chunk(const SampleArgs& A, ChunkSmem& S, uint32_t row, uint32_t chunk,
+                                              uint32_t c0, uint32_t c1, GetQ getq) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t len = c1 - c0;
+  const uint32_t n = A.rx_n, take = min(n, len);
+  uint32_t* rh = S.mask;                                   // [1024] histogram of the thread maxima
+  uint32_t* rwk = S.mask + 1024;                           // [NW] wave maxima (keys)
+  uint32_t* rwf = S.mask + 1040;                           // [NW] wave non-finite flags
+  double* rws = reinterpret_cast<double*>(S.mask + 1056);  // [NW] wave sums
+  uint32_t* rcnt = S.mask + 1088;                          // [40] counters, each used once
+  unsigned long long* rc = reinterpret_cast<unsigned long long*>(S.bids);   // [RX_CAP]
+  unsigned long long* list = A.rx_list + ((uint64_t)row * MAXC + chunk) * n;
+  rh[tid] = 0u;
+  if (tid < 40u) rcnt[tid] = 0u;
+  float tmax = -INFINITY;
+  bool nf = false;
+  rx_slices<UNR>(A, [&](int i) {
+    float r[4];
+    uint32_t rb;
+    getq(i, r, rb);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const bool inr = (rb >> e) & 1u;
+      nf |= inr && !__builtin_isfinite(r[e]);
+      tmax = fmaxf(tmax, inr ? r[e] : -INFINITY);
+    }
+  });
+  stamp(A, row, chunk, 12);
+  // Each weight 2^y, y = (l - tmax) log2(e) <= 0, in f32: the subtraction
+  // and the product each round y by at most 2^-24 |y|, and the exp2 adds an
+  // ulp, so a weight is within 2^-23 (1 + ln2 |y|) of exp(l - tmax); a
+  // quad's four weights are summed in f32 (3 more roundings), the quads in
+  // f64.  Relative to this thread's sum S_t, which holds the maximum's exact
+  // weight 1 besides at most 39 others, the error is at most
+  // 2^-23 (1 + ln2 max_t(39 t 2^-t / (1 + 39 2^-t)) + 1.5) < 2^-20.9 (the
+  // ratio peaks near 2.7); rescaled in f64 and summed, the row's S is within
+  // 2^-20.9 (S - 1) of the exact sum, so ln S and every log probability
+  // (l - M) - ln S, of magnitude at least (S - 1) / S, within 2^-20.9
+  // relative.  y is clamped at -200 (2^-200 is 0 in f32): suppressed and
+  // out-of-range tokens weigh 0.
+  double part = 0.0;
+  if (tmax > -INFINITY) {
+    rx_slices<UNR>(A, [&](int i) {
+      float r[4];
+      uint32_t rb;
+      getq(i, r, rb);
+      float qs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = fmaxf((((rb >> e) & 1u) ? r[e] - tmax : -INFINITY) * 1.44269504f, -200.0f);
+        qs += __builtin_amdgcn_exp2f(y);
+      }
+      part += (double)qs;
+    });
+  }
+  stamp(A, row, chunk, 13);
+  {
+    const uint32_t wk = wave_max_u32(okey(tmax));
+    const bool wf = __builtin_amdgcn_ballot_w64(nf) != 0ull;
+    if (lane() == 0) {
+      rwk[wave()] = wk;
+      rwf[wave()] = wf ? 1u : 0u;
+    }
+  }
+  lds_barrier();
+  uint32_t ck = 0u, flags = 0u;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    ck = max(ck, rwk[w]);
+    flags |= rwf[w];
+  }
+  const float cmax = okey_value(ck);
+  const bool listing = !flags && take > 0u;
+  bool exact = false;
+  // the thread's sum rescaled to the chunk maximum; the thread maxima
+  // histogrammed on a 1/32-logit grid below it
+  if (tmax > -INFINITY) part *= exp_neg_p((double)tmax - (double)cmax);
+  part = wave_sum_f64(part);
+  if (lane() == 0) rws[wave()] = part;
+  if (listing && tmax > -INFINITY) {
+    const float d = (cmax - tmax) * 32.0f;
+    if (d < 1023.0f) atomicAdd(&rh[(uint32_t)d], 1u);
+  }
+  lds_barrier();
+  if (listing) {
+    // take threads hold a maximum at or above the crossing bin's lower edge,
+    // so the chunk's take-th largest logit is too (one bin of margin for
+    // the rounding of d): every wave finds the bin (lane j: bins 16 j ..)
+    float L = -INFINITY;
+    {
+      uint32_t sm = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint4 h4 = *reinterpret_cast<const uint4*>(&rh[lane() * 16u + (uint32_t)q * 4u]);
+        sm += h4.x + h4.y + h4.z + h4.w;
+      }
+      const uint32_t inc = wave_scan_u32(sm);
+      const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= take);
+      if (reach) {
+        const uint32_t g = (uint32_t)__builtin_ctzll(reach);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - sm), (int)g);
+        const uint32_t v = lane() < 16u ? rh[16u * g + lane()] : 0u;
+        const uint32_t vi = base + wave_scan_u32(v);
+        const uint64_t r2 = __builtin_amdgcn_ballot_w64(lane() < 16u && vi >= take);
+        const uint32_t tb = 16u * g + (uint32_t)__builtin_ctzll(r2);
+        L = cmax - (float)(tb + 2u) / 32.0f;
+      }
+    }
+    const uint32_t Lk = okey(L);
+    stamp(A, row, chunk, 14);
+    // the tokens at or above L, into LDS
+    // the tokens at or above L, into LDS
+    rx_slices<UNR>(A, [&](int i) {
+      float r[4];
+      uint32_t rb;
+      getq(i, r, rb);
+      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = okey(r[e]);
+        if (((rb >> e) & 1u) && k >= Lk) {
+          const uint32_t at = atomicAdd(&rcnt[0], 1u);
+          if (at < RX_CAP) rc[at] = rx_entry(k, e0 + (uint32_t)e);
+        }
+      }
+    });
+    lds_barrier();
+    stamp(A, row, chunk, 15);
+    const uint32_t m = rcnt[0];
+    // too many at or above L (ties, or a flat chunk), or (logits past 2^19
+    // in magnitude, where the bin edges round) too few: the exact path
+    if (m > RX_CAP - 16u || m < take) exact = true;
+    // rank by counting (entries are distinct), the first take out in order
+    if (!exact) {
+      if (tid < 16u && m + tid < RX_CAP) rc[m + tid] = 0ull;   // (m <= RX_CAP - 16: see above)
+      lds_barrier();
+      rx_rank(rc, m, take, list);
+    }
+  }
+  if (tid == 0) {
+    double sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += rws[w];
+    RxStat* st = &A.rx_stat[(uint64_t)row * MAXC + chunk];
+    st_dev(&st->maxv, cmax);
+    st_dev(&st->flags, flags);
+    st_dev(&st->count, listing ? take : 0u);
+    st_dev(&st->sum, sum);
+  }
+  return !exact;
+}
+
+// The row's suppressed tokens (bias entries of -inf) in the chunk, as a
+// bitmap (bit t - c0) over the count table, dead after the chunk body.
+__device__ __forceinline__ void rx_supmap(const SampleArgs& A, ChunkSmem& S, uint32_t c0, uint32_t c1, uint32_t bb,
+                                          uint32_t bn) {
+  const uint32_t tid = threadIdx.x;
+  const mxs_batch& b = A.b;
+  uint32_t* supw = S.t.ct;
+  lds_barrier();   // the candidates' copy-out has read the staging area
+  const uint32_t nwd = A.per * ((uint32_t)SLICE / 32u);
+  for (uint32_t t = tid; t < nwd; t += NT) supw[t] = 0u;
+  lds_barrier();
+  for (uint32_t j = tid; j < bn; j += NT) {
+    const uint32_t d = b.bias_ids[bb + j] - c0;
+    if (d < c1 - c0 && b.bias_values[bb + j] == -INFINITY) atomicOr(&supw[d >> 5], 1u << (d & 31u));
+  }
+  lds_barrier();
+}
+
+// The row's receipt from its chunks' statistics and lists, on the finisher's
+// workgroup after the pick (thread 0 wrote the token).  The merge of the
+// top-n kernel: a list of n entries has n at or above its last, so only
+// entries at or above the largest such last entry can rank below n.  The
+// loads go out together: every thread its list entries and their chunks'
+// counts, wave 0 the statistics, wave 1 the row's suppressed IDs, thread 0
+// the token's logit; one barrier later the filter, the rank and the writes.
+template <typename In>
+__device__ __forceinline__ void receipt_finish(const SampleArgs& A, FinSmem& F, uint32_t row) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t n = A.rx_n, C = A.C, V = A.b.vocab;
+  const mxs_batch& b = A.b;
+  const RxStat* st = A.rx_stat + (uint64_t)row * MAXC;
+  const unsigned long long* lists = A.rx_list + (uint64_t)row * MAXC * n;
+  unsigned long long* dense = reinterpret_cast<unsigned long long*>(F.cl);   // [MAXC * 64 + 16] over cl, cid
+  uint32_t* supl = F.eidx;                                                   // [64] suppressed IDs
+  constexpr int RL = (MAXC * 64 + NT - 1) / NT;   // list entries per thread
+  unsigned long long ent[RL];
+  uint32_t ecnt[RL];
+#pragma unroll
+  for (int u = 0; u < RL; ++u) {
+    const uint32_t jj = tid + (uint32_t)u * NT;
+    ent[u] = 0ull;
+    ecnt[u] = 0u;
+    if (jj < C * n) {
+      const uint32_t q = jj / n;
+      ent[u] = __builtin_bit_cast(unsigned long long, ld_dev(reinterpret_cast<const double*>(&lists[jj])));
+      ecnt[u] = ld_dev(&st[q].count) > jj - q * n ? 1u : 0u;
+    }
+  }
+  int32_t t = -1;
+  float tl = 0.0f;
+  if (tid == 0) {
+    t = A.o.token[row];
+    if (t >= 0 && (uint32_t)t < V) tl = Quad<In>::one(reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride + (uint32_t)t);
+  }
+  const uint32_t b0 = b.bias_offsets[row], b1 = b.bias_offsets[row + 1];
+  const uint32_t bn = b1 > b0 ? b1 - b0 : 0u;
+  if (wave() == 1 && bn <= 64u) {
+    const uint32_t l = lane();
+    const bool sp = l < bn && b.bias_values[b0 + l] == -INFINITY;
+    const uint32_t id = l < bn ? b.bias_ids[b0 + l] : NONE;
+    supl[l] = sp ? id : NONE;
+  }
+  if (wave() == 0) {
+    const uint32_t q = lane();   // chunk q (C <= MAXC = 64)
+    float cm = -INFINITY;
+    double cs = 0.0;
+    uint32_t fl = 0u;
+    unsigned long long last = 0ull;
+    if (q < C) {
+      cm = ld_dev(&st[q].maxv);
+      cs = ld_dev(&st[q].sum);
+      fl = ld_dev(&st[q].flags);
+      if (ld_dev(&st[q].count) == n)
+        last = __builtin_bit_cast(unsigned long long, ld_dev(reinterpret_cast<const double*>(&lists[(uint64_t)q * n + n - 1u])));
+    }
+    const uint32_t flags = wave_or_u32(fl);
+    const uint32_t mkey = wave_max_u32(okey(cm));
+    const double M = (double)okey_value(mkey);
+    const double S = wave_sum_f64(cs > 0.0 ? cs * exp_neg_p((double)cm - M) : 0.0);
+    const unsigned long long thr = wave_max_u64(last);
+    if (lane() == 0) {
+      F.s_u[0] = flags;
+      F.s_u[1] = 0u;
+      F.s_d[0] = M;
+      F.s_d[1] = S;
+      F.s_l[0] = thr;
+    }
+  }
+  lds_barrier();
+  const uint32_t flags = F.s_u[0];
+  const double M = F.s_d[0];
+  int32_t* ids = A.rx_ids + (uint64_t)row * n;
+  double* lps = A.rx_lps + (uint64_t)row * n;
+  if (flags) {   // a non-finite logit: the chunks listed nothing
+    for (uint32_t j = tid; j < n; j += NT) {
+      ids[j] = -1;
+      lps[j] = __builtin_nan("");
+    }
+    if (tid == 0) {
+      A.rx_status[row] = MXS_ROW_NON_FINITE_LOGIT;
+      A.rx_token_lp[row] = __builtin_nan("");
+    }
+    return;
+  }
+  const unsigned long long thr = F.s_l[0];
+#pragma unroll
+  for (int u = 0; u < RL; ++u)
+    if (ecnt[u] && ent[u] >= thr) dense[atomicAdd(&F.s_u[1], 1u)] = ent[u];
+  lds_barrier();
+  const uint32_t m = F.s_u[1];
+  if (tid < 16u) dense[m + tid] = 0ull;
+  lds_barrier();
+  const double ln = log(F.s_d[1]);
+  const uint32_t nout = min(n, V);
+  for (uint32_t j = tid; j < m; j += NT) {
+    const unsigned long long mine = dense[j];
+    const uint32_t rank = rx_rank_of(dense, m, mine);
+    if (rank < nout) {
+      ids[rank] = (int32_t)(~(uint32_t)mine);
+      lps[rank] = ((double)okey_value((uint32_t)(mine >> 32)) - M) - ln;
+    }
+  }
+  for (uint32_t j = min(m, nout) + tid; j < n; j += NT) {
+    ids[j] = -1;
+    lps[j] = -INFINITY;
+  }
+  if (tid == 0) {
+    A.rx_status[row] = 0;
+    // the picked token's f64(l) - maximum - log_normalizer under the same
+    // suppressed logits; NaN for a row without a token
+    double lp = __builtin_nan("");
+    if (t >= 0 && (uint32_t)t < V) {
+      bool sup = false;
+      if (bn <= 64u) {
+        for (uint32_t l = 0; l < bn; ++l) sup |= supl[l] == (uint32_t)t;
+      } else {
+        uint32_t lo = b0, hi = b1;
+        while (lo < hi) {   // bias ids increase within a row
+          const uint32_t mid = (lo + hi) >> 1;
+          if (b.bias_ids[mid] < (uint32_t)t) lo = mid + 1u;
+          else hi = mid;
+        }
+        sup = lo < b1 && b.bias_ids[lo] == (uint32_t)t && b.bias_values[lo] == -INFINITY;
+      }
+      lp = ((double)(sup ? -FLT_MAX : tl) - M) - ln;
+    }
+    A.rx_token_lp[row] = lp;
+  }
+}
+
+// What a chunk body leaves of the step receipt for the kernel to do after
+// it: nothing, or the chunk's share (RX_FULL: the general body, whose raw
+// logits are not in registers, or a lean chunk whose fast path failed).
+// The kernel's share re-reads the chunk into registers after the body: in
+// a body, next to its live registers, the reread share made it spill.
+constexpr uint32_t RX_FULL = 2u;
+
+// The row's last chunk to finish becomes its finisher.  Every wave waits for
+// its own device-scope stores to complete before the workgroup barrier,
+// which comes before thread 0's increment of the row counter; the last
+// arriver's acquire fence, then the barrier, order its workgroup's loads
+// after all of the row's stores (the ordering argument of arrive_last: a
+// relaxed increment, no L2 write-back per arrival).
+__device__ __forceinline__ bool arrive_row(const SampleArgs& A, ChunkSmem& S, uint32_t row) {
+  wait_mem();
+  __syncthreads();
+  uint32_t last = 0;
+  if (threadIdx.x == 0) {
+    uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
+    const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = prev + 1u == A.C ? 1u : 0u;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    S.xkey = last;
+  }
+  __syncthreads();
+  last = S.xkey;
+  lds_barrier();   // the finisher's LDS overlays the chunk's
+  return last != 0u;
+}
+
+// ---------------------------------------------------------------------------
 // The lean chunk body: rows with no grammar mask, no logit bias and a history
 // that fits the register staging (at most HCAP ids), in the greedy, top-k or
 // min-p mode.  It writes the same chunk statistics and token-ID-ordered
@@ -3538,10 +4053,10 @@ __device__ __forceinline__ ChunkSmem& chunk_smem(FusedSmem& u) { return u.s; }
 //   - each wave publishes its maximum to the row's exchange word as soon as
 //     its pass 1 ends, so the min-p threshold sees the other chunks' maxima
 //     as early as possible.
-template <typename In, uint32_t MODE, bool HIST>
-__device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
+template <typename In, uint32_t MODE, bool HIST, bool RX>
+__device__ __forceinline__ uint32_t chunk_fast(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
                                            const uint32_t row, const uint32_t chunk, const uint32_t c0,
-                                           const uint32_t c1, const uint32_t hn, const uint32_t bn) {
+                                           const uint32_t c1, const uint32_t hn, const uint32_t bn, const bool rx) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
@@ -3636,7 +4151,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
         if (bid >= V || !bias_ok(bval) || (tid > 0u && bprev >= bid)) my_flags |= F_BIAS;
         const uint32_t t = bid - c0;
         if (t < clen) {
-          atomicAdd(&S.t.ct[t >> 1], 0x4000u << ((t & 1u) * 16u));
+          atomicAdd(&S.t.ct[t >> 1], (RX && bval == -INFINITY ? 0x6000u : 0x4000u) << ((t & 1u) * 16u));
           own |= 1u << 4;
         }
       }
@@ -3788,7 +4303,10 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
       if (!__builtin_isfinite(pv)) my_flags |= F_NONFINITE;
       if (A.o.adjusted) A.o.adjusted[(uint64_t)row * V + id] = pv;
       pvals[slot] = pv;
-      reinterpret_cast<uint16_t*>(S.t.ct)[t] = (uint16_t)(0x8000u | slot);
+      // (with step receipts, a suppressed token's 0x2000, set with its bias
+      // mark, stays: the receipt reads it)
+      const uint32_t sflag = RX ? (S.t.ct[t >> 1] >> ((t & 1u) * 16u)) & 0x2000u : 0u;
+      reinterpret_cast<uint16_t*>(S.t.ct)[t] = (uint16_t)(0x8000u | sflag | slot);
       if constexpr (MODE == M_GREEDY) {
         if (better(pv, id, gv, gi)) { gv = pv; gi = id; }
       } else {
@@ -3820,7 +4338,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     }
     if ((own >> 4) & 1u) {
       const uint32_t t = bid - c0, sh = (t & 1u) * 16u;
-      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0x3fffu;   // the history count under the bias mark
+      const uint32_t cnt = (S.t.ct[t >> 1] >> sh) & 0x1fffu;   // the history count under the bias marks
       fold(bias_and_penalize(braw, 0x80000000u | cnt, bval, c.rep, inv_rep, c.freq, c.pres), bid, t, hn + tid);
     }
   }
@@ -3876,6 +4394,30 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
   const float m = okey_value(maxkey);   // chunk's largest logit
   const double md = (double)m;
   const bool row_ok = !(cflags & (F_HIST | F_NONFINITE));
+
+  // ---- the step receipt's share of this chunk, from the raw logits in
+  // registers (before the candidate pass swaps adjusted logits in); a
+  // suppressed token (a bias entry of -inf) carries 0x2000 in the table.
+  // Where its fast path fails, the kernel redoes the share after the body.
+  bool rx_left = rx;
+  if (RX && rx) {
+    stamp(A, row, chunk, 10);
+    rx_left = !receipt_chunk<PER_MAX>(A, S, row, chunk, c0, c1, [&](int i, float* r, uint32_t& rb) {
+      const uint32_t sbase = c0 + (uint32_t)i * SLICE, e0 = sbase + tid * 4u;
+      rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+      uint32_t sup = 0u;
+      if constexpr (HIST) {
+        if ((pq >> i) & 1u) {
+          const uint2 cw = *reinterpret_cast<const uint2*>(&S.t.ct[((uint32_t)i * SLICE + tid * 4u) >> 1]);
+          sup = ((cw.x & 0x2000u) ? 1u : 0u) | ((cw.x & 0x20000000u) ? 2u : 0u) | ((cw.y & 0x2000u) ? 4u : 0u) |
+                ((cw.y & 0x20000000u) ? 8u : 0u);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] = ((sup >> e) & 1u) ? -FLT_MAX : lv[i][e];
+    });
+    stamp(A, row, chunk, 11);
+  }
 
   // ---- candidate threshold and counts --------------------------------------
   float thr = -INFINITY;
@@ -4156,28 +4698,7 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
     st_dev(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
-  {
-    // The row's last chunk to finish becomes its finisher.  Every wave
-    // waits for its own device-scope stores to complete before the
-    // workgroup barrier, which comes before thread 0's increment of the row
-    // counter; the last arriver's acquire fence, then the barrier, order its
-    // workgroup's loads after all of the row's stores (the ordering argument
-    // of arrive_last: a relaxed increment, no L2 write-back per arrival).
-    wait_mem();
-    __syncthreads();
-    uint32_t last = 0;
-    if (tid == 0) {
-      uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
-      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = prev + 1u == A.C ? 1u : 0u;
-      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      S.xkey = last;
-    }
-    __syncthreads();
-    last = S.xkey;
-    lds_barrier();   // the finisher's LDS overlays the chunk's
-    return last != 0u;
-  }
+  return rx_left ? RX_FULL : 0u;
 }
 
 // The general chunk body: every row the lean body does not cover (grammar
@@ -4187,8 +4708,8 @@ __device__ __forceinline__ bool chunk_fast(const SampleArgs& A, FusedSmem& U, co
 // first slice is not passed in (it would stay live across both bodies): the
 // general body issues its slices itself.
 template <typename In>
-__device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
-                                              const uint32_t row, const uint32_t chunk) {
+__device__ __forceinline__ uint32_t chunk_general(const SampleArgs& A, FusedSmem& U, const RowCfg& c,
+                                              const uint32_t row, const uint32_t chunk, const bool rx) {
   ChunkSmem& S = chunk_smem(U);
   const mxs_batch& b = A.b;
   const uint32_t tid = threadIdx.x;
@@ -4794,25 +5315,7 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
     st_dev(&st.thr, thr);
   }
   stamp(A, row, chunk, 2);
-  {
-    // The row's last chunk to finish becomes its finisher (stores complete,
-    // barrier, relaxed increment of the row counter, acquire by the last
-    // arriver, as above).
-    wait_mem();
-    __syncthreads();
-    uint32_t last = 0;
-    if (tid == 0) {
-      uint32_t* ctr = A.w.ctr + (uint64_t)row * CTR_STRIDE;
-      const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      last = prev + 1u == A.C ? 1u : 0u;
-      if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      S.xkey = last;
-    }
-    __syncthreads();
-    last = S.xkey;
-    lds_barrier();   // the finisher's LDS overlays the chunk's
-    return last != 0u;
-  }
+  return rx ? RX_FULL : 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -4820,7 +5323,7 @@ __device__ __forceinline__ bool chunk_general(const SampleArgs& A, FusedSmem& U,
 // row's parameters decide the body: rows the lean body covers issue the
 // history ids and the stream there and run it, the others run the general
 // body (which issues its own loads).
-template <typename In>
+template <typename In, bool RX>
 __global__ __launch_bounds__(NT) void sample_kernel(
     SampleArgs A, const double* __restrict__ p_temperature, const uint32_t* __restrict__ p_top_k,
     const double* __restrict__ p_top_p, const double* __restrict__ p_min_p, const float* __restrict__ p_rep,
@@ -4839,7 +5342,9 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_rep, p_pres, p_freq, p_uniform, p_hoff,
                             p_boff, row);
   const uint32_t mode = chunk_mode(c, V);
-  bool last;
+  // a step receipt for this row (mxs_step)
+  const bool rx = RX && A.rx_want[row] != MXS_RECEIPT_NONE;
+  uint32_t rxw;   // the receipt work left after the body
   {
     const uint32_t hn = c.he > c.hb ? c.he - c.hb : 0u, bn = c.be > c.bb ? c.be - c.bb : 0u;
     // A logit bias of at most NT entries, none above 0 (-inf suppresses),
@@ -4856,18 +5361,46 @@ __global__ __launch_bounds__(NT) void sample_kernel(
         (mode == M_GREEDY || mode == M_TOPK || mode == M_MINP)) {
       stamp(A, row, chunk, 0);
       if (hn || bn) {
-        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, true>(A, U, c, row, chunk, c0, c1, hn, bn);
-        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, true>(A, U, c, row, chunk, c0, c1, hn, bn);
-        else last = chunk_fast<In, M_MINP, true>(A, U, c, row, chunk, c0, c1, hn, bn);
+        if (mode == M_GREEDY) rxw = chunk_fast<In, M_GREEDY, true, RX>(A, U, c, row, chunk, c0, c1, hn, bn, rx);
+        else if (mode == M_TOPK) rxw = chunk_fast<In, M_TOPK, true, RX>(A, U, c, row, chunk, c0, c1, hn, bn, rx);
+        else rxw = chunk_fast<In, M_MINP, true, RX>(A, U, c, row, chunk, c0, c1, hn, bn, rx);
       } else {
-        if (mode == M_GREEDY) last = chunk_fast<In, M_GREEDY, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
-        else if (mode == M_TOPK) last = chunk_fast<In, M_TOPK, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
-        else last = chunk_fast<In, M_MINP, false>(A, U, c, row, chunk, c0, c1, 0u, 0u);
+        if (mode == M_GREEDY) rxw = chunk_fast<In, M_GREEDY, false, RX>(A, U, c, row, chunk, c0, c1, 0u, 0u, rx);
+        else if (mode == M_TOPK) rxw = chunk_fast<In, M_TOPK, false, RX>(A, U, c, row, chunk, c0, c1, 0u, 0u, rx);
+        else rxw = chunk_fast<In, M_MINP, false, RX>(A, U, c, row, chunk, c0, c1, 0u, 0u, rx);
       }
     } else {
-      last = chunk_general<In>(A, U, c, row, chunk);
+      rxw = chunk_general<In>(A, U, c, row, chunk, rx);
     }
   }
+  // The step receipt's reload paths run here, after the body, where its
+  // registers are dead (inside a body they made the kernel spill), then the
+  // row arrival.
+  if (RX && rxw) {
+    stamp(A, row, chunk, 10);
+    ChunkSmem& S = chunk_smem(U);
+    rx_supmap(A, S, c0, c1, c.bb, c.be > c.bb ? c.be - c.bb : 0u);
+    const uint32_t* supw = S.t.ct;
+    const In* src = reinterpret_cast<const In*>(b.logits) + (uint64_t)row * b.row_stride;
+    // each pass reads the chunk again (just streamed: from the caches), its
+    // slice loop rolled: held in registers across the passes, the chunk made
+    // the kernel spill (the opaque pointer keeps the passes' loads apart)
+    const auto getq = [&](int i, float* r, uint32_t& rb) {
+      const uint32_t sbase = c0 + (uint32_t)i * SLICE, e0 = sbase + threadIdx.x * 4u;
+      rb = sbase + (uint32_t)SLICE <= c1 ? 0xfu : (e0 < c1 ? (c1 - e0 >= 4u ? 0xfu : (1u << (c1 - e0)) - 1u) : 0u);
+      const In* p = src;
+      __asm__ volatile("" : "+s"(p));
+      Quad<In>::unpack(Quad<In>::load(p + (e0 < c1 ? e0 : c0)), r);
+      const uint32_t sb = supw[(uint32_t)i * ((uint32_t)SLICE / 32u) + (threadIdx.x >> 3)] >> ((threadIdx.x & 7u) * 4u);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if ((sb >> e) & 1u) r[e] = -FLT_MAX;
+    };
+    if (!receipt_chunk<1>(A, S, row, chunk, c0, c1, getq))
+      receipt_exact(A, S, row, chunk, c0, min(A.rx_n, c1 - c0), getq);
+    stamp(A, row, chunk, 11);
+  }
+  const bool last = arrive_row(A, chunk_smem(U), row);
   // The row finisher: one copy for every chunk body.  The finisher runs once
   // per row, mostly down code no other wave of the workgroup has run, so its
   // instruction fetches miss the instruction cache; one shared copy keeps the
@@ -4881,6 +5414,12 @@ __global__ __launch_bounds__(NT) void sample_kernel(
   fin_issue(A, row, P);
   finish_row<In>(A, U.f, c, row, mode, (uint64_t)row * V, c.greedy ? 0.0 : 1.0 / c.T, P);
   stamp(A, row, MAXC, 7);
+  if (RX && rx) {
+    __syncthreads();   // the finisher's LDS is free
+    stamp(A, row, MAXC, 10);
+    receipt_finish<In>(A, U.f, row);
+    stamp(A, row, MAXC, 11);
+  }
   // The row's counter and exchange word are cleared for the next call here,
   // after the finisher: every chunk has arrived (its exchange update came
   // before), and stores issued at the arrival would hold the finisher's
@@ -4915,7 +5454,7 @@ ChunkLayout sample_layout(uint32_t rows, uint32_t V) {
 
 namespace mxs {
 
-int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw) {
+int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw, const mxs_receipts* rx) {
   if (!ctx || !b || !o) return MXS_EINVAL;
   if (b->rows == 0) return MXS_OK;
   if (!b->logits || !b->temperature || !o->token || !o->status) return fail(ctx, MXS_EINVAL, "logits, temperature, token and status are required");
@@ -4938,6 +5477,24 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   A.epoch = ctx->epoch;
   A.nodraw = nodraw ? 1u : 0u;
   A.masked = b->mask_words != nullptr;
+  A.rx_want = nullptr;
+  if (rx) {
+    // step receipts in the same pass: a NULL top asks one of every row (the
+    // zeros stand in); the per-chunk statistics and lists take the top-n
+    // scratch, which is larger
+    static_assert(sizeof(mxs::RxStat) == 24, "RxStat layout");
+    A.rx_want = rx->top ? rx->top : ctx->d_zero_u32;
+    A.rx_n = rx->n;
+    A.rx_ids = rx->ids;
+    A.rx_lps = rx->logprobs;
+    A.rx_token_lp = rx->token_logprob;
+    A.rx_status = rx->status;
+    A.rx_stat = reinterpret_cast<mxs::RxStat*>(ctx->topn_scratch);
+    A.rx_list = reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ctx->topn_scratch) +
+                                                      (size_t)ctx->max_rows * mxs::MAXC * sizeof(mxs::RxStat));
+    if ((size_t)ctx->max_rows * mxs::MAXC * (sizeof(mxs::RxStat) + (size_t)rx->n * 8u) > topn_scratch_bytes(ctx->max_rows))
+      return fail(ctx, MXS_EINVAL, "receipt scratch too small");
+  }
   if (!A.masked) {
     A.b.mask_words = ctx->d_mask_ones;
     A.b.mask_stride = 0;
@@ -4964,10 +5521,15 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   if (prev != ctx->device) hipSetDevice(ctx->device);
   // One kernel: each row's last chunk to finish decides the row.
 #define MXS_ARGS A, b->temperature, p_k, p_tp, p_mp, p_rep, p_pres, p_freq, p_u, A.b.history_offsets, A.b.bias_offsets
-  if (b->dtype == MXS_F32)
-    hipLaunchKernelGGL((mxs::sample_kernel<float>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
-  else
-    hipLaunchKernelGGL((mxs::sample_kernel<uint16_t>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+  // (step receipts: their own instantiation, so picks without receipts run
+  // the kernel's code unchanged)
+  if (b->dtype == MXS_F32) {
+    if (A.rx_want) hipLaunchKernelGGL((mxs::sample_kernel<float, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    else hipLaunchKernelGGL((mxs::sample_kernel<float, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+  } else {
+    if (A.rx_want) hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, true>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+    else hipLaunchKernelGGL((mxs::sample_kernel<uint16_t, false>), grid, dim3(mxs::NT), 0, ctx->stream, MXS_ARGS);
+  }
 #undef MXS_ARGS
   hipError_t e = hipGetLastError();
   if (e == hipSuccess) mask_note_read(ctx, b->mask_words);

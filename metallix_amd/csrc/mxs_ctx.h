@@ -22,8 +22,10 @@ constexpr double RACE_DRAW_UNIFORM = 0.6180339887498949;
 
 // mxs_sample's launch; `nodraw` makes keep-all rows skip the inverse-CDF
 // draw (token -1, status 0, the kept set still written) and keeps every
-// row's draw out of its status.
-int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw);
+// row's draw out of its status; `rx` (checked by the caller) adds the step
+// receipts of the rows that want one, computed in the same pass.
+int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodraw,
+                  const mxs_receipts* rx = nullptr);
 
 // The sample kernel's LDS bytes per workgroup and its chunk layout for a
 // batch of `rows` rows of V tokens (mx_floor.hip launches with both).

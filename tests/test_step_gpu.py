@@ -51,7 +51,7 @@ def suppressed(b, sup):
     return b
 
 
-def check_step(torch, sampler, orc, b, sup, tops, n):
+def check_step(torch, sampler, orc, b, sup, tops, n, allow_uncertified=0):
     say(f"case step {b.name}: rows {b.rows} vocab {b.vocab} n {n} suppressed {len(sup)}")
     logits, kw = to_device(torch, b)
     top_t = torch.from_numpy(u32(tops)).to(logits.device)
@@ -61,7 +61,7 @@ def check_step(torch, sampler, orc, b, sup, tops, n):
                sampling_logprob=out.sampling_logprob.cpu().numpy(), adjusted=out.adjusted.cpu().numpy(),
                kept=unpack_bits(out.kept_bits.cpu().numpy(), b.vocab))
     ref = orc.sample_batch(b, debug=True)
-    compare(b, gpu, ref)
+    compare(b, gpu, ref, allow_uncertified=allow_uncertified)
     ids, lps = rec.ids.cpu().numpy(), rec.logprobs.cpu().numpy()
     tlp, rst = rec.token_logprob.cpu().numpy(), rec.status.cpu().numpy()
     problems = []
@@ -72,6 +72,14 @@ def check_step(torch, sampler, orc, b, sup, tops, n):
             continue
         x = np.asarray(b.logits[r], dtype=np.float32).copy()
         x[np.asarray([i for i in sup if i < b.vocab], dtype=np.int64)] = F32_MIN   # (IDs past the row: skipped)
+        if not np.all(np.isfinite(x)):
+            # A non-finite logit fails the row's pick (the reference's turn
+            # stops there and scores no receipt): the receipt reports the
+            # same status, with no entries and NaN log probabilities.
+            if not (rst[r] == ref["status"][r] == -6 and np.all(ids[r] == -1) and np.all(np.isnan(lps[r]))
+                    and np.isnan(tlp[r])):
+                problems.append(f"row {r}: non-finite receipt {rst[r]} {ids[r, :3]} {lps[r, :3]} {tlp[r]}")
+            continue
         st, rids, rlps, rmx, rln = orc.token_logprob_top(x, n)
         if rst[r] != 0 or st != 0:
             problems.append(f"row {r}: receipt status {rst[r]} ref {st}")
@@ -80,6 +88,8 @@ def check_step(torch, sampler, orc, b, sup, tops, n):
         if not np.array_equal(ids[r, :k], rids):
             problems.append(f"row {r}: ids {ids[r, :6]} ref {rids[:6]}")
             continue
+        if k < n and not (np.all(ids[r, k:] == -1) and np.all(np.isneginf(lps[r, k:]))):
+            problems.append(f"row {r}: entries past the vocabulary {ids[r, k:k + 3]} {lps[r, k:k + 3]}")
         if not np.allclose(lps[r, :k], rlps, rtol=1e-5, atol=0.0):
             problems.append(f"row {r}: logprobs {lps[r, :4]} ref {rlps[:4]}")
         t = int(gpu["token"][r])
@@ -120,6 +130,53 @@ def test_step_bf16_masked_rows(torch_mod, sampler, orc):
     b = suppressed(b, sup)
     tops = np.array([3, NONE, 1, 20, 0, 5, 56, NONE], dtype=np.uint32)
     check_step(torch_mod, sampler, orc, b, sup, tops, 64)
+
+
+def test_step_receipt_ties_flat_and_nonfinite(torch_mod, sampler, orc):
+    """Receipt edge cases of the one-pass step: a constant row and a top
+    plateau of 3000 equal logits (ties past the chunks' candidate capacity:
+    the exact path, ties in token-ID order), a NaN (non-finite status, no
+    entries), a suppressed row maximum, a masked row (the general chunk
+    body: the receipt reads the chunk again) and ordinary rows; n = 64."""
+    from metallix_amd.synth import Batch
+
+    V, R = 50000, 8
+    rng = np.random.default_rng(91)
+    x = (rng.standard_normal((R, V)) * 2.0).astype(np.float32)
+    x[0, :] = 0.5                                   # constant row
+    x[1, rng.choice(V // 4, 3000, replace=False)] = 9.0   # a plateau inside chunk 0
+    x[2, 777] = np.nan                              # non-finite
+    x[3, 4242] = 12.0                               # the row maximum, suppressed below
+    x[4, :] = np.round(x[4, :])                     # many ties at every integer
+    words = (V + 31) // 32
+    mask = np.zeros((R, words), dtype=np.uint32)
+    mask[:] = 0xFFFFFFFF
+    mask[5, : words // 2] = 0x55555555              # a masked row: every other token in the first half
+    b = Batch(name="step-edges", logits=x, temperature=np.array([0.7, 1.0, 1.0, 0.0, 1.2, 0.9, 1.0, 0.5]),
+              uniform=rng.random(R), top_k=np.array([20, 0, 5, 0, 50, 0, 1000, 0], dtype=np.uint32),
+              top_p=np.array([0.9, 1.0, 0.9, 1.0, 0.8, 0.95, 0.7, 1.0]),
+              min_p=np.array([0.0, 0.05, 0.0, 0.0, 0.0, 0.1, 0.05, 0.0]), mask_words=mask, tokenizer_vocab=V)
+    sup = [4242, 11, 49999]
+    b = suppressed(b, sup)
+    tops = np.array([56, 56, 56, 56, 56, 56, NONE, 0], dtype=np.uint32)
+    # (the constant row's pick: a nucleus cut among equal weights may come
+    # back uncertified, with the oracle's token or a boundary draw)
+    gpu, _ = check_step(torch_mod, sampler, orc, b, sup, tops, 64, allow_uncertified=1)
+    assert set(np.nonzero(gpu["status"] == 1)[0]) <= {0}
+
+
+def test_step_receipt_small_vocab(torch_mod, sampler, orc):
+    """A vocabulary of 40 under n = 64: 40 entries, the rest -1 / -inf."""
+    from metallix_amd.synth import Batch
+
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((3, 40)) * 3.0).astype(np.float32)
+    x[1, :] = 1.0
+    b = Batch(name="step-small", logits=x, temperature=np.array([1.0, 0.5, 0.0]), uniform=rng.random(3),
+              top_k=np.array([0, 5, 0], dtype=np.uint32), top_p=np.array([0.9, 1.0, 1.0]),
+              min_p=np.array([0.0, 0.0, 0.0]))
+    b = suppressed(b, [7])
+    check_step(torch_mod, sampler, orc, b, [7], np.array([56, 3, 0], dtype=np.uint32), 64)
 
 
 def test_step_race_rows(torch_mod, sampler, orc):
