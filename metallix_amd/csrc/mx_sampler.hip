@@ -5596,7 +5596,7 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
   e = e ? e : hipMalloc(&ctx->spec_ctr, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->spec_ctr, 0, (size_t)max_rows * mxs::SPEC_COUNTERS_PER_ROW * mxs::CTR_STRIDE * sizeof(uint32_t));
-  e = e ? e : hipMalloc(&ctx->spec_scratch, mxs::spec_scratch_bytes(max_rows));
+  e = e ? e : hipMalloc(&ctx->spec_scratch, mxs::spec_scratch_bytes(max_rows, max_vocab));
   e = e ? e : hipMalloc(&ctx->race_ctr, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMemset(ctx->race_ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->race_scratch, mxs::race_scratch_bytes(max_rows, max_vocab));

@@ -12,16 +12,26 @@
 // emits a draw from max(0, t / sum t - q / sum q) and stops; when every draft
 // is accepted, the bonus token is sample_categorical over target row K.
 //
-// Two launches on the context's stream.  Pass 1 (one workgroup per (row,
-// position, chunk)) reduces each chunk's maxima and f64 weight sums; the
-// last chunk of a (row, position) decides acceptance.  Pass 2 (one
-// workgroup per (row, chunk)) finds the first rejected position (or the
-// bonus position), writes 256-token segment masses of the distribution to
-// draw from, and the row's last chunk locates the draw: the segment by a
-// prefix over segment masses, then the token by re-deriving the segment's
-// 256 weights in f64.  Every comparison against a reference f64 sum is
-// taken only when a rigorous error bound certifies it; otherwise the row is
-// reported uncertified (status 1) with the device's decision.
+// Two launches on the context's stream.
+//   Pass 1, one workgroup per (row, position, chunk): the chunk's maxima and
+//   weight sums, the weights from the f32 exp2 (weight2, within 2^-22) summed
+//   in f64.  The last chunk of a (row, position) decides acceptance: the
+//   ratio p/q needs only that relative accuracy to be certified.
+//   Pass 2, one workgroup per (row, chunk): the first rejected position (or
+//   the bonus position) from pass 1's verdicts, then the drawn
+//   distribution's weights at that position in f64 (exp_neg_t).  The residual
+//   max(0, t_i / sum t - q_i / sum q) needs the totals to f64 accuracy, which
+//   pass 1 does not have; its approximate totals only classify each token's
+//   sign with a margin, so that each 256-token segment stores the exact sums
+//   of t_i and q_i over its positive tokens and the residual mass follows
+//   once the row's exact totals (summed here too) are known.  Tokens inside
+//   the margin (|p_i - q_i| within a few 2^-22 of p_i + q_i) count as 0 and
+//   their possible mass joins the error bound.  The row's last chunk locates
+//   the draw: the segment by a prefix over segment masses, then the token by
+//   re-deriving the segment's 256 residual weights in f64.
+// Every comparison against a reference f64 sum is taken only when a
+// rigorous error bound certifies it; otherwise the row is reported
+// uncertified (status 1) with the device's decision.
 
 #include <hip/hip_runtime.h>
 
@@ -35,10 +45,11 @@
 
 namespace mxs {
 
-constexpr int SP = 5;                 // quads per thread per chunk
+constexpr int SQ = 2;                 // quads per thread per chunk (default layout)
+constexpr int SP = 5;                 // quads per thread per chunk (vocabularies past SMAXC default chunks)
 constexpr int SMAXC = 128;            // chunks per row
 constexpr uint32_t SPEC_KMAX = 8;     // draft positions per row
-constexpr int SSEG = SP * NW;         // 256-token segments per chunk
+constexpr uint32_t SPART = 5;         // pass 2's per-chunk partials
 
 struct SpecStat {                     // per (row, position, chunk)
   float tmax, dmax, tmin;
@@ -52,7 +63,7 @@ struct SpecPos {                      // per (row, position): pass 1's verdict
   int32_t unc;                        // the decision is not certified
   int32_t pad;
   float mt, md;                       // row maxima of target and draft
-  double tt, td;                      // totals of exp((l - row max) / T)
+  double tt, td;                      // totals of exp((l - row max) / T), weight2 terms
   double tterr, tderr;                // bounds on |total - reference total|
 };
 
@@ -73,24 +84,50 @@ struct SpecArgs {
   uint32_t* ctr2;                     // [rows], CTR_STRIDE words apart
   SpecStat* stat;                     // [rows * (SPEC_KMAX + 1) * SMAXC]
   SpecPos* pos;                       // [rows * (SPEC_KMAX + 1)]
-  double* seg;                        // [rows * SMAXC * SSEG]
+  uint32_t C2, CH2, per2;             // pass 2's chunk layout
+  // pass 2, per row (seg_stride doubles): the segments' positive sums
+  // (sum t, sum q) at [2 s, 2 s + 1], s = chunk * per2 * NW + slice * NW +
+  // wave in token order, then at 2 nseg_cap + SPART chunk the chunk's
+  // partials: sum t, sum q, margin mass, positive sum t, positive sum q
+  double* seg;
+  uint64_t seg_stride;
+  uint32_t nseg_cap;
 };
 
 struct SpecSmem {
   double etab[128];                   // exp_neg's tables
-  SpecStat st[SMAXC];
   SpecPos ps[SPEC_KMAX + 1];
   uint32_t red_u[4][NW];
-  double red_d[4][NW];
+  double red_d[8][NW];
   double s_d[4];
   uint32_t s_u[8];
 };
 
+// Weight exp(x) of x = (l - M) / T <= 0 as 2^y, y = (l - M) c2 with c2 =
+// log2(e) / T, formed in f64 and clamped at -1000 (2^-1000 is 0 in f32):
+// the f32 exp2 of y's f32 head corrected by its tail (|tail| <= 2^-24 |head|,
+// one fma).  Within 2^-22 relative of 2^y where the result is in f32's
+// normal range, within 2^-125 absolute below it; the maximum weighs exactly
+// 1 and l = -inf weighs 0.
+__device__ __forceinline__ double weight2(float l, double M, double c2) {
+  const double y = fmax(((double)l - M) * c2, -1000.0);
+  const float yh = (float)y;
+  const float yl = (float)(y - (double)yh);
+  const float eh = __builtin_amdgcn_exp2f(yh);
+  return (double)__builtin_fmaf(eh, yl * 0.69314718f, eh);
+}
+
 // Bound on |device sum - reference sum| for n weights exp(x), x = (l - M) / T
-// <= 0, summed in different orders: each side's f64 rounding of the sums and
-// of the terms (8 ulp), and the rounding of x (x e^x <= 1/e per term).
+// <= 0, both in f64 (4 ulp per term against the reference's exp), summed in
+// different orders; the rounding of x (x e^x <= 1/e per term).
 __device__ __forceinline__ double weight_sum_err(double s, uint32_t n) {
   return (2.0 * (double)n + 16.0) * U * s * 1.0001 + 1.5 * (double)n * U + 1e-300;
+}
+// As weight_sum_err for weight2 terms (2^-22 relative, 2^-125 absolute) and
+// the device's x through c2 (4 ulp of x against the reference's 2; 2.5 ulp
+// absolute per term for both roundings).
+__device__ __forceinline__ double weight2_sum_err(double s, uint32_t n) {
+  return (0x1p-22 + (2.0 * (double)n + 16.0) * U) * s * 1.0001 + (double)n * (2.5 * U + 0x1p-125) + 1e-300;
 }
 
 template <bool ALIGNED>
@@ -106,12 +143,19 @@ __device__ __forceinline__ void load_quad(const float* p, uint32_t e0, uint32_t 
 
 __device__ __forceinline__ bool temperature_ok(double T) { return T > 0.0 && isfinite(T); }
 __device__ __forceinline__ bool uniform_ok(double u) { return isfinite(u) && u >= 0.0 && u < 1.0; }
+// 1 / T capped at 2^1000: below T = 2^-1000 every weight but the maximum's
+// is 0 either way (|l - M| >= 2^-149 otherwise), and the maximum's x stays 0
+// instead of 0 * inf.
+__device__ __forceinline__ double inv_temperature(double T) {
+  return temperature_ok(T) ? fmin(1.0 / T, 0x1p1000) : 0.0;
+}
 
 // ---------------------------------------------------------------------------
 // Pass 1: per (row, position, chunk) maxima and weight sums; the last chunk
 // of a (row, position) decides acceptance.
-template <bool ALIGNED>
-__global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
+// (two workgroups per CU in the default layout: at most 64 VGPRs)
+template <bool ALIGNED, int Q>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q == SQ ? 8 : 4))) void spec_pass1(SpecArgs A) {
   __shared__ SpecSmem S;
   const uint32_t tid = threadIdx.x;
   const uint32_t xcd = blockIdx.x & 7u;
@@ -126,21 +170,36 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
   const float* dp = A.draft + ((uint64_t)row * K + (has_draft ? j : 0u)) * V;
   const double T = A.T[row];
   const bool tok_T = temperature_ok(T);
-  const double invT = tok_T ? 1.0 / T : 0.0;
+  const double invT = inv_temperature(T);
+  const double c2 = invT * 1.4426950408889634;
 
-  if (tid < 128u) S.etab[tid] = tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u];
-  float tv[SP][4], dv[SP][4];
+  // the drafted token and its uniforms and logits, for the verdict that the
+  // position's last chunk takes (loaded up front, off its critical path;
+  // uniform across the workgroup, so scalar loads into scalar registers)
+  int32_t d = -1;
+  double ua = 0.0, ur = 0.0;
+  float tpd = 0.0f, dpd = 0.0f;
+  if (has_draft) {
+    d = A.tok[(uint64_t)row * K + j];
+    ua = A.ua[(uint64_t)row * K + j];
+    ur = A.ur[(uint64_t)row * K + j];
+  }
+  float tv[Q][4], dv[Q][4];
 #pragma unroll
-  for (int i = 0; i < SP; ++i) {
+  for (int i = 0; i < Q; ++i) {
     const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
     const uint32_t es = e0 < c1 ? e0 : c0;
     load_quad<ALIGNED>(tp, es, c1, tv[i]);
     if (has_draft) load_quad<ALIGNED>(dp, es, c1, dv[i]);
   }
+  if (has_draft && d >= 0 && (uint32_t)d < V) {
+    tpd = tp[d];
+    dpd = dp[d];
+  }
   float tmax = -INFINITY, dmax = -INFINITY, tmin = INFINITY;
   uint64_t nft = 0, nfd = 0;
 #pragma unroll
-  for (int i = 0; i < SP; ++i) {
+  for (int i = 0; i < Q; ++i) {
     const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -181,11 +240,11 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     const double mtd = (double)mt, mdd = (double)md;
     double pt = 0.0, pd = 0.0;
 #pragma unroll
-    for (int i = 0; i < SP; ++i)
+    for (int i = 0; i < Q; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        pt += exp_neg_t(((double)tv[i][e] - mtd) * invT, S.etab, S.etab + 64);
-        if (has_draft) pd += exp_neg_t(((double)dv[i][e] - mdd) * invT, S.etab, S.etab + 64);
+        pt += weight2(tv[i][e], mtd, c2);
+        if (has_draft) pd += weight2(dv[i][e], mdd, c2);
       }
     pt = wave_sum_f64(pt);
     pd = wave_sum_f64(pd);
@@ -205,30 +264,44 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
   }
   if (!arrive_last(&A.ctr1[(row * (SPEC_KMAX + 1) + j) * CTR_STRIDE], A.C, &S.s_u[0])) return;
 
-  // ---- the position's verdict (one thread does the arithmetic) -------------
+  // ---- the position's verdict: wave 0 reduces the chunks' statistics (two
+  // chunks per lane, C <= SMAXC = 128), lane 0 decides
+  if (wave() != 0) return;
   const uint32_t slot = row * (SPEC_KMAX + 1) + j;
   const uint32_t C = A.C;
-  for (uint32_t q = tid; q < C; q += NT) {
-    const SpecStat* st = &A.stat[(uint64_t)slot * SMAXC + q];
-    SpecStat v;
-    v.tmax = ld_dev(&st->tmax);
-    v.dmax = ld_dev(&st->dmax);
-    v.tmin = ld_dev(&st->tmin);
-    v.flags = ld_dev(&st->flags);
-    v.tsum = ld_dev(&st->tsum);
-    v.dsum = ld_dev(&st->dsum);
-    S.st[q] = v;
+  float cmt[2], cmd[2];
+  double cts[2], cds[2];
+  uint32_t fl = 0u, kt = 0u, kd = 0u, kn = 0u;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t q = lane() + 64u * (uint32_t)h;
+    cmt[h] = cmd[h] = -INFINITY;
+    cts[h] = cds[h] = 0.0;
+    if (q < C) {
+      const SpecStat* st = &A.stat[(uint64_t)slot * SMAXC + q];
+      cmt[h] = ld_dev(&st->tmax);
+      cmd[h] = ld_dev(&st->dmax);
+      kn = max(kn, ~okey(ld_dev(&st->tmin)));
+      fl |= ld_dev(&st->flags);
+      cts[h] = ld_dev(&st->tsum);
+      cds[h] = ld_dev(&st->dsum);
+      kt = max(kt, okey(cmt[h]));
+      kd = max(kd, okey(cmd[h]));
+    }
   }
-  __syncthreads();
-  if (tid != 0) return;
-  uint32_t fl = 0;
-  float Mt = -INFINITY, Md = -INFINITY, Mn = INFINITY;
-  for (uint32_t q = 0; q < C; ++q) {
-    fl |= S.st[q].flags;
-    Mt = fmaxf(Mt, S.st[q].tmax);
-    Md = fmaxf(Md, S.st[q].dmax);
-    Mn = fminf(Mn, S.st[q].tmin);
+  fl = wave_or_u32(fl);
+  const float Mt = okey_value(wave_max_u32(kt)), Md = okey_value(wave_max_u32(kd));
+  const float Mn = okey_value(~wave_max_u32(kn));
+  // totals: the chunk sums rescaled from the chunk maxima to the row maxima
+  double tt = 0.0, td = 0.0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    tt += cts[h] * exp_neg_p(((double)cmt[h] - (double)Mt) * invT);
+    td += cds[h] * exp_neg_p(((double)cmd[h] - (double)Md) * invT);
   }
+  tt = wave_sum_f64(tt);
+  td = wave_sum_f64(td);
+  if (lane() != 0) return;
   SpecPos P;
   P.err = 0;
   P.accept = 0;
@@ -240,26 +313,19 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
   if (!tok_T) {
     P.err = MXS_ROW_INVALID_TEMPERATURE;
   } else if (has_draft) {
-    const int32_t d = A.tok[(uint64_t)row * K + j];
-    const double ua = A.ua[(uint64_t)row * K + j], ur = A.ur[(uint64_t)row * K + j];
     if (fl) P.err = MXS_ROW_NON_FINITE_LOGIT;
     else if (d < 0) P.err = MXS_ROW_TOKEN_OUT_OF_RANGE;
     else if (!uniform_ok(ua) || !uniform_ok(ur)) P.err = MXS_ROW_INVALID_UNIFORM;
     else if ((uint32_t)d >= V) P.err = MXS_ROW_TOKEN_OUT_OF_RANGE;
     if (!P.err) {
-      double tt = 0.0, td = 0.0;
-      for (uint32_t q = 0; q < C; ++q) {
-        tt += S.st[q].tsum * exp_neg(((double)S.st[q].tmax - (double)Mt) * invT);
-        td += S.st[q].dsum * exp_neg(((double)S.st[q].dmax - (double)Md) * invT);
-      }
       P.tt = tt;
       P.td = td;
-      P.tterr = weight_sum_err(tt, V + C);
-      P.tderr = weight_sum_err(td, V + C);
-      const double wt = exp_neg(((double)tp[d] - (double)Mt) * invT);
-      const double wd = exp_neg(((double)dp[d] - (double)Md) * invT);
-      const double xq = ((double)dp[d] - (double)Md) * invT;
-      const double xt = ((double)tp[d] - (double)Mt) * invT;
+      P.tterr = weight2_sum_err(tt, V + C);
+      P.tderr = weight2_sum_err(td, V + C);
+      const double xt = ((double)tpd - (double)Mt) * invT;
+      const double xq = ((double)dpd - (double)Md) * invT;
+      const double wt = exp_neg_p(xt);
+      const double wd = exp_neg_p(xq);
       if (wd <= 0.0) {
         // the reference's q <= 0 rejection; near the f64 underflow edge the
         // two exp implementations may disagree
@@ -268,7 +334,7 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
       } else {
         const double p = wt / tt, qq = wd / td;
         const double ratio = p / qq;
-        // relative error of the ratio: both weights (exp 1 ulp and the
+        // relative error of the ratio: both weights (exp 2 ulp and the
         // rounding of x, 4 ulp each with margin), both totals, the divisions
         const double rel = 16.0 * U + P.tterr / tt + P.tderr / td + 2e-15 * (fabs(xq) + fabs(xt) + 1.0);
         P.accept = ua < ratio ? 1 : 0;
@@ -282,10 +348,8 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     else if (fl & 1u) P.err = MXS_ROW_NON_FINITE_LOGIT;
     else if (!isfinite(((double)Mn - (double)Mt) / T)) P.err = MXS_ROW_INVALID_TEMPERATURE;
     else {
-      double tt = 0.0;
-      for (uint32_t q = 0; q < C; ++q) tt += S.st[q].tsum * exp_neg(((double)S.st[q].tmax - (double)Mt) * invT);
       P.tt = tt;
-      P.tterr = weight_sum_err(tt, V + C);
+      P.tterr = weight2_sum_err(tt, V + C);
     }
   }
   SpecPos* out = &A.pos[slot];
@@ -318,21 +382,18 @@ __device__ Plan row_plan(const SpecPos* ps, uint32_t K) {
   return pl;
 }
 
-// Weight of token i in the distribution drawn at the plan's position:
-// the residual max(0, t_i / sum t - q_i / sum q), or the target weight t_i
-// for the bonus draw.
-__device__ __forceinline__ double draw_weight(bool bonus, float t, float q, const SpecPos& P, double invT,
-                                              const double* etab) {
-  const double wt = exp_neg_t(((double)t - (double)P.mt) * invT, etab, etab + 64);
-  if (bonus) return wt;
-  const double wq = exp_neg_t(((double)q - (double)P.md) * invT, etab, etab + 64);
-  return fmax(wt / P.tt - wq / P.td, 0.0);
+// Margin of pass 2's sign classification: |(t_i a' - q_i b') - (p_i - q_i)|
+// <= rho (t_i a' + q_i b') with a' = 1 / tt', b' = 1 / td' from pass 1's
+// totals; their relative errors, the f64 weights' (4 ulp and 2 ulp |x| for
+// the rounding of x, |x| <= 746) and the products' roundings.
+__device__ __forceinline__ double sign_margin(const SpecPos& P) {
+  return 1.01 * (P.tterr / P.tt + P.tderr / P.td) + 2000.0 * U;
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: segment masses of the drawn distribution; the row's last chunk
-// draws.
-template <bool ALIGNED>
+// Pass 2: the drawn distribution's segment and chunk sums; the row's last
+// chunk draws.
+template <bool ALIGNED, int Q>
 __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   __shared__ SpecSmem S;
   const uint32_t tid = threadIdx.x;
@@ -360,37 +421,108 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   __syncthreads();
   const Plan pl = row_plan(S.ps, K);
   const bool bonus = pl.r == K;
-  const double T = A.T[row];
-  const double invT = temperature_ok(T) ? 1.0 / T : 0.0;
-  const uint32_t c0 = chunk * A.CH, c1 = min(V, c0 + A.CH);
+  const double invT = inv_temperature(A.T[row]);
+  const uint32_t C = A.C2, CH = A.CH2, per = A.per2;
+  const uint32_t c0 = chunk * CH, c1 = min(V, c0 + CH);
+  const uint32_t spc = per * NW;                          // segments per chunk
+  double* rs = A.seg + (uint64_t)row * A.seg_stride;     // [2 * nseg_cap] segments
+  double* parts = rs + 2u * (uint64_t)A.nseg_cap;        // [SPART * C] chunk partials
+  const float* tp = A.target + ((uint64_t)row * (K + 1u) + pl.r) * V;
+  const float* dp = A.draft + ((uint64_t)row * K + (bonus ? 0u : pl.r)) * V;
   if (!pl.err) {
     const SpecPos& P = S.ps[pl.r];
-    const float* tp = A.target + ((uint64_t)row * (K + 1u) + pl.r) * V;
-    const float* dp = A.draft + ((uint64_t)row * K + (bonus ? 0u : pl.r)) * V;
+    const double ra = bonus ? 1.0 : 1.0 / P.tt, rb = bonus ? 0.0 : 1.0 / P.td;
+    const double rho = bonus ? 0.0 : sign_margin(P);
+    float t[Q][4], q[Q][4];
 #pragma unroll
-    for (int i = 0; i < SP; ++i) {
-      double s = 0.0;
-      if (i < (int)A.per) {
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+      const uint32_t es = e0 < c1 ? e0 : c0;
+      q[i][0] = q[i][1] = q[i][2] = q[i][3] = 0.0f;
+      load_quad<ALIGNED>(tp, es, c1, t[i]);
+      if (!bonus) load_quad<ALIGNED>(dp, es, c1, q[i]);
+    }
+    // per thread: sum t, sum q, margin mass, positive sum t, positive sum q
+    double pt = 0.0, pd = 0.0, pe = 0.0, pa = 0.0, pb = 0.0;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      if (i < (int)per) {
         const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-        const uint32_t es = e0 < c1 ? e0 : c0;
-        float t[4], q[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        load_quad<ALIGNED>(tp, es, c1, t);
-        if (!bonus) load_quad<ALIGNED>(dp, es, c1, q);
+        double sa = 0.0, sb = 0.0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (e0 + (uint32_t)e < c1) s += draw_weight(bonus, t[e], q[e], P, invT, S.etab);
+        for (int e = 0; e < 4; ++e) {
+          if (e0 + (uint32_t)e < c1) {
+            const double wt = exp_neg_t(((double)t[i][e] - (double)P.mt) * invT, S.etab, S.etab + 64);
+            pt += wt;
+            if (bonus) {
+              sa += wt;
+            } else {
+              const double wq = exp_neg_t(((double)q[i][e] - (double)P.md) * invT, S.etab, S.etab + 64);
+              pd += wq;
+              const double x = wt * ra, y = wq * rb;
+              const double dd = x - y, ss = x + y;
+              if (dd > rho * ss) { sa += wt; sb += wq; }
+              else if (dd >= -(rho * ss)) pe += ss;
+            }
+          }
+        }
+        pa += sa;
+        pb += sb;
+        sa = wave_sum_f64(sa);
+        if (!bonus) sb = wave_sum_f64(sb);
+        if (lane() == 0) {
+          double* o = rs + 2u * (chunk * spc + (uint32_t)i * NW + wave());
+          st_dev(o, sa);
+          st_dev(o + 1, sb);
+        }
       }
-      const double ws = wave_sum_f64(s);
-      if (lane() == 0) st_dev(&A.seg[((uint64_t)row * SMAXC + chunk) * SSEG + i * NW + wave()], ws);
+    }
+    // the chunk's partials: wave sums, then lanes f < SPART of wave 0 add
+    // the waves' values of partial f
+    pt = wave_sum_f64(pt);
+    pa = wave_sum_f64(pa);
+    if (!bonus) { pd = wave_sum_f64(pd); pe = wave_sum_f64(pe); pb = wave_sum_f64(pb); }
+    if (lane() == 0) {
+      S.red_d[0][wave()] = pt;
+      S.red_d[1][wave()] = pd;
+      S.red_d[2][wave()] = pe;
+      S.red_d[3][wave()] = pa;
+      S.red_d[4][wave()] = pb;
+    }
+    lds_barrier();
+    if (tid < SPART) {
+      double v = 0.0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += S.red_d[tid][w];
+      st_dev(&parts[SPART * chunk + tid], v);
     }
   }
-  if (!arrive_last(&A.ctr2[row * CTR_STRIDE], A.C, &S.s_u[0])) return;
+  // The residual draw's error bound, before the arrive (every workgroup has
+  // the inputs; the row's last one then adds the margin mass): the bound on
+  // |device cumulative - reference cumulative| at any index, for cumulatives
+  // of chunk masses, then segment masses, then the segment's own residual
+  // terms.  Every term p_i - q_i carries the two totals' relative errors
+  // (weight_sum_err of a total over the total, at most weight_sum_err(1, n):
+  // the row maximum weighs 1) and 8 ulp, over sum p = sum q = 1, plus each
+  // side's f64 summation; tokens inside the classification margin, counted
+  // as 0 in the sums, weigh at most 2 rho (p_i + q_i) each.  (The bonus
+  // draw's bound is weight_sum_err of its mass.)
+  const uint32_t nseg = C * spc;
+  const uint32_t nsum = V + nseg + C;
+  double errm = 0.0, erra = 0.0;
+  if (!pl.err && !bonus) {
+    const double rel = 16.0 * U + 2.0 * weight_sum_err(1.0, V + C);
+    errm = 2.02 * sign_margin(S.ps[pl.r]);
+    erra = 2.0 * rel + (2.0 * (double)nsum + 32.0) * U * 1.0001 + 1e-300;
+  }
+  if (!arrive_last(&A.ctr2[row * CTR_STRIDE], C, &S.s_u[0])) return;
 
-  // ---- the row's last chunk: outputs and the draw ---------------------------
+  // ---- the row's last chunk: outputs and the draw, in wave 0 ---------------
+  if (wave() != 0) return;
   int32_t* ot = A.out_tokens + (uint64_t)row * (K + 1u);
-  for (uint32_t j = tid; j <= K; j += NT) ot[j] = (j < pl.r) ? A.tok[(uint64_t)row * K + j] : -1;
+  for (uint32_t j = lane(); j <= K; j += 64u) ot[j] = (j < pl.r) ? A.tok[(uint64_t)row * K + j] : -1;
   if (pl.err) {
-    if (tid == 0) {
+    if (lane() == 0) {
       A.status[row] = pl.err;
       A.out_count[row] = (int32_t)pl.r;
       A.out_accepted[row] = (int32_t)pl.r;
@@ -399,87 +531,140 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   }
   const SpecPos& P = S.ps[pl.r];
   const double u = bonus ? A.ub[row] : A.ur[(uint64_t)row * K + pl.r];
-  const uint32_t C = A.C;
-  const uint32_t segs_per_chunk = A.per * NW;
-  const uint32_t nseg = C * segs_per_chunk;
-  auto seg_mass = [&](uint32_t s) {
-    const uint32_t q = s / segs_per_chunk, r = s % segs_per_chunk;
-    return ld_dev(&A.seg[((uint64_t)row * SMAXC + q) * SSEG + r]);
-  };
-  double part = 0.0;
-  for (uint32_t s = tid; s < nseg; s += NT) part += seg_mass(s);
-  part = wave_sum_f64(part);
-  if (lane() == 0) S.red_d[0][wave()] = part;
-  __syncthreads();
-  double mass = 0.0;
+  // chunk partials: lane l holds chunks 2l and 2l + 1 (C <= SMAXC = 128)
+  double cp[2][SPART];
 #pragma unroll
-  for (int w = 0; w < NW; ++w) mass += S.red_d[0][w];
-  // Bound on |device cumulative - reference cumulative| at any index.  Bonus:
-  // target weights as in the sampler's full-row draw.  Residual: every term
-  // p_i - q_i carries the two totals' relative errors and 8 ulp, over
-  // sum p = sum q = 1, plus each side's f64 summation.
-  double err;
-  if (bonus) {
-    err = weight_sum_err(mass, V + nseg);
-  } else {
-    const double rel = 16.0 * U + P.tterr / P.tt + P.tderr / P.td;
-    err = 2.0 * rel + (2.0 * (double)(V + nseg) + 16.0) * U * 1.0001 + 1e-300;
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t qc = 2u * lane() + (uint32_t)h;
+#pragma unroll
+    for (uint32_t f = 0; f < SPART; ++f) cp[h][f] = qc < C ? ld_dev(&parts[SPART * qc + f]) : 0.0;
   }
+  const double tt = wave_sum_f64(cp[0][0] + cp[1][0]);
+  const double td = bonus ? 1.0 : wave_sum_f64(cp[0][1] + cp[1][1]);
+  const double emass = bonus ? 0.0 : wave_sum_f64(cp[0][2] + cp[1][2]);
+  const double a = bonus ? 1.0 : 1.0 / tt, b = bonus ? 0.0 : 1.0 / td;
+  double cm[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) cm[h] = fmax(cp[h][3] * a - cp[h][4] * b, 0.0);
+  const double lsum2 = cm[0] + cm[1];
+  const double cinc = wave_scan(lsum2);                           // inclusive over lanes
+  const double mass = readlane_t(cinc, 63u);
+  const double err = bonus ? weight_sum_err(mass, nsum) : errm * emass + erra;
   const double thr = u * mass;
   bool unc = pl.unc;
   if (!bonus && !(mass > 2.0 * err)) unc = true;   // the reference's mass <= 0 fallback may apply
-  // the segment: first s with thr < cumulative through s
-  if (tid == 0) { S.s_u[1] = NONE; S.s_u[2] = 0u; S.s_u[3] = 0u; }
-  __syncthreads();
-  double run = 0.0;
-  for (uint32_t base = 0; base < nseg; base += NT) {
-    const uint32_t s = base + tid;
-    const double w = s < nseg ? seg_mass(s) : 0.0;
-    double tot;
-    const double inc = run + block_scan_incl<double>(w, S.red_d[1], &tot);
-    const double exc = inc - w;
-    if (w > 0.0) {
-      atomicMax(&S.s_u[2], s + 1u);
-      if (thr < inc && !(thr < exc)) {
-        S.s_u[1] = s;
-        S.s_d[0] = exc;
-        if (fabs(thr - exc) <= err || fabs(inc - thr) <= err) S.s_u[3] = 1u;
+  // the chunk: first qc with thr < cumulative through qc
+  uint32_t fq = NONE, lastq = NONE;
+  bool near = false;
+  double fbefore = 0.0;
+  {
+    double cum = cinc - lsum2;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const double prev = cum;
+      cum += cm[h];
+      if (cm[h] > 0.0) {
+        lastq = 2u * lane() + (uint32_t)h;
+        if (fq == NONE && thr < cum && !(thr < prev)) {
+          fq = 2u * lane() + (uint32_t)h;
+          fbefore = prev;
+          near = fabs(thr - prev) <= err || fabs(cum - thr) <= err;
+        }
       }
     }
-    run += tot;
   }
-  __syncthreads();
-  uint32_t seg = S.s_u[1];
-  double before = S.s_d[0];
-  if (S.s_u[3]) unc = true;
-  if (seg == NONE) {
-    // rounding left the target past the accumulated mass: last positive token
-    seg = S.s_u[2] ? S.s_u[2] - 1u : NONE;
-    unc = true;
-    before = -INFINITY;
+  uint32_t qc = NONE;
+  double before = 0.0;
+  {
+    const uint64_t fb = __ballot(fq != NONE), lb = __ballot(lastq != NONE);
+    if (fb) {
+      const int sl = __ffsll((unsigned long long)fb) - 1;
+      qc = __shfl(fq, sl);
+      before = __shfl(fbefore, sl);
+      if (__shfl(near ? 1 : 0, sl)) unc = true;
+    } else if (lb) {
+      // rounding left the target past the accumulated mass: the last
+      // positive chunk, from its start
+      const int sl = 63 - __clzll((long long)lb);
+      qc = __shfl(lastq, sl);
+      before = -INFINITY;
+      unc = true;
+    }
   }
-  if (wave() == 0) {
-    uint32_t tok = NONE;
-    bool tunc = true;
+  uint32_t tok = NONE;
+  bool tunc = true;
+  if (qc != NONE) {
+    // the segment within chunk qc: lane l holds segments l, l + 64 (spc <= SP * NW = 80)
+    double sm[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t s = lane() + 64u * (uint32_t)h;
+      double sa = 0.0, sb = 0.0;
+      if (s < spc) {
+        sa = ld_dev(&rs[2u * (qc * spc + s)]);
+        sb = ld_dev(&rs[2u * (qc * spc + s) + 1u]);
+      }
+      sm[h] = fmax(sa * a - sb * b, 0.0);
+    }
+    // token order within the chunk is segment order (slice-major, then wave)
+    const double s0inc = wave_scan(sm[0]);
+    const double s0tot = readlane_t(s0inc, 63u);
+    const double s1inc = wave_scan(sm[1]) + s0tot;
+    uint32_t fs = NONE, lasts = NONE;
+    double sbefore = 0.0;
+    bool snear = false;
+    const double base = before == -INFINITY ? 0.0 : before;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const double inc = base + (h == 0 ? s0inc : s1inc);
+      const double exc = inc - sm[h];
+      const uint32_t s = lane() + 64u * (uint32_t)h;
+      if (sm[h] > 0.0) {
+        lasts = s;
+        if (fs == NONE && before != -INFINITY && thr < inc && !(thr < exc)) {
+          fs = s;
+          sbefore = exc;
+          snear = fabs(thr - exc) <= err || fabs(inc - thr) <= err;
+        }
+      }
+    }
+    // first found segment (lowest s), or the last positive one
+    uint32_t seg = NONE;
+    {
+      const uint32_t fmin = ~wave_max_u32(~fs);
+      const uint32_t lmax = lasts == NONE ? 0u : lasts + 1u;
+      const uint32_t lm = wave_max_u32(lmax);
+      if (fmin != NONE) {
+        seg = fmin;
+        const int sl = (int)(fmin & 63u);
+        before = __shfl(sbefore, sl);
+        if (__shfl(snear ? 1 : 0, sl)) unc = true;
+      } else if (lm) {
+        seg = lm - 1u;
+        before = -INFINITY;
+        unc = true;
+      }
+    }
     if (seg != NONE) {
-      const uint32_t q = seg / segs_per_chunk, r = seg % segs_per_chunk;
-      const uint32_t i = r / NW, w = r % NW;
-      const uint32_t qc1 = min(V, q * A.CH + A.CH);
-      const uint32_t id0 = q * A.CH + i * SLICE + w * 256u + lane() * 4u;
-      const float* tp = A.target + ((uint64_t)row * (K + 1u) + pl.r) * V;
-      const float* dp = A.draft + ((uint64_t)row * K + (bonus ? 0u : pl.r)) * V;
+      const uint32_t i = seg / NW, w = seg % NW;
+      const uint32_t qc1 = min(V, qc * CH + CH);
+      const uint32_t id0 = qc * CH + i * SLICE + w * 256u + lane() * 4u;
+      float lt[4], lq[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t id = min(id0 + (uint32_t)e, V - 1u);
+        lt[e] = tp[id];
+        lq[e] = bonus ? 0.0f : dp[id];
+      }
       double wl[4], lsum = 0.0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const uint32_t id = id0 + (uint32_t)e;
-        wl[e] = id < qc1 ? draw_weight(bonus, tp[id], bonus ? 0.0f : dp[id], P, invT, S.etab) : 0.0;
+        const double wt = exp_neg_t(((double)lt[e] - (double)P.mt) * invT, S.etab, S.etab + 64);
+        double wv = bonus ? wt : fmax(wt * a - exp_neg_t(((double)lq[e] - (double)P.md) * invT, S.etab, S.etab + 64) * b, 0.0);
+        wl[e] = id0 + (uint32_t)e < qc1 ? wv : 0.0;
         lsum += wl[e];
       }
-      double inc = lsum;
-      for (int o = 1; o < 64; o <<= 1) {
-        const double t = __shfl_up(inc, o);
-        if (lane() >= (uint32_t)o) inc += t;
-      }
+      const double inc = wave_scan(lsum);
       double cum = (before == -INFINITY ? 0.0 : before) + inc - lsum;
       uint32_t found = NONE, lastpos = NONE;
       bool fnear = false;
@@ -506,25 +691,52 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
         tok = __shfl(lastpos, sl);
       }
     }
-    if (lane() == 0) {
-      unc = unc || tunc;
-      if (tok == NONE) {
-        A.status[row] = unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_PROBABILITIES;
-        A.out_count[row] = (int32_t)pl.r;
-        A.out_accepted[row] = (int32_t)pl.r;
-      } else {
-        ot[pl.r] = (int32_t)tok;
-        A.status[row] = unc ? MXS_ROW_UNCERTIFIED : 0;
-        A.out_count[row] = (int32_t)pl.r + 1;
-        A.out_accepted[row] = (int32_t)pl.r;
-      }
+  }
+  if (lane() == 0) {
+    unc = unc || tunc;
+    if (tok == NONE) {
+      A.status[row] = unc ? MXS_ROW_UNCERTIFIED : MXS_ROW_PROBABILITIES;
+      A.out_count[row] = (int32_t)pl.r;
+      A.out_accepted[row] = (int32_t)pl.r;
+    } else {
+      ot[pl.r] = (int32_t)tok;
+      A.status[row] = unc ? MXS_ROW_UNCERTIFIED : 0;
+      A.out_count[row] = (int32_t)pl.r + 1;
+      A.out_accepted[row] = (int32_t)pl.r;
     }
   }
 }
 
-size_t spec_scratch_bytes(uint32_t max_rows) {
+// Chunk layouts of a vocabulary.  Pass 1: SQ quads per thread unless that
+// needs more than SMAXC chunks.  Pass 2 (one position per row): one quad per
+// thread, for more workgroups over the CUs, under the same limit.
+static ChunkLayout spec_layout1(uint32_t V) {
+  const ChunkLayout L = chunk_layout(V, SQ);
+  return L.C <= (uint32_t)SMAXC ? L : chunk_layout(V, SP);
+}
+static ChunkLayout spec_layout2(uint32_t V) {
+  const ChunkLayout L = chunk_layout(V, 1);
+  return L.C <= (uint32_t)SMAXC ? L : chunk_layout(V, SP);
+}
+
+// Pass 2's segment capacity per row for vocabularies up to max_vocab: chunk
+// counts grow with V within a layout, so each layout's count at the largest
+// vocabulary it serves bounds the smaller ones.
+static uint32_t spec_nseg_cap(uint32_t max_vocab) {
+  const ChunkLayout a = chunk_layout(max_vocab, 1);
+  uint32_t ns = min(a.C, (uint32_t)SMAXC) * NW;
+  if (a.C > (uint32_t)SMAXC) ns = max(ns, chunk_layout(max_vocab, SP).C * (uint32_t)SP * NW);
+  return ns;
+}
+
+static uint64_t spec_seg_stride(uint32_t max_vocab) {
+  return 2ull * spec_nseg_cap(max_vocab) + (uint64_t)SPART * SMAXC;
+}
+
+size_t spec_scratch_bytes(uint32_t max_rows, uint32_t max_vocab) {
   const size_t pairs = (size_t)max_rows * (SPEC_KMAX + 1);
-  return pairs * SMAXC * sizeof(SpecStat) + pairs * sizeof(SpecPos) + (size_t)max_rows * SMAXC * SSEG * sizeof(double);
+  return pairs * SMAXC * sizeof(SpecStat) + pairs * sizeof(SpecPos) +
+         (size_t)max_rows * spec_seg_stride(max_vocab) * sizeof(double);
 }
 
 }  // namespace mxs
@@ -544,8 +756,11 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   if (rows > ctx->max_rows || vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
   if (vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
   if (draft_len > SPEC_KMAX) return fail(ctx, MXS_EINVAL, "draft_len must be at most 8");
-  const ChunkLayout L = chunk_layout(vocab, SP);
-  if (L.per > (uint32_t)SP || L.C > (uint32_t)SMAXC) return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
+  const ChunkLayout L = spec_layout1(vocab), L2 = spec_layout2(vocab);
+  if (L.per > (uint32_t)SP || L.C > (uint32_t)SMAXC || L2.per > (uint32_t)SP || L2.C > (uint32_t)SMAXC ||
+      L2.C * L2.per * NW > spec_nseg_cap(ctx->max_vocab))
+    return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
+  const bool q1 = L.per <= (uint32_t)SQ, q2 = L2.per <= 1u;
   SpecArgs A;
   A.target = target_logits;
   A.draft = draft_len ? draft_logits : target_logits;
@@ -555,6 +770,9 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   A.C = L.C;
   A.CH = L.CH;
   A.per = L.per;
+  A.C2 = L2.C;
+  A.CH2 = L2.CH;
+  A.per2 = L2.per;
   A.tok = draft_tokens;
   A.T = temperature;
   A.ua = accept_uniform;
@@ -571,20 +789,24 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   A.stat = reinterpret_cast<SpecStat*>(base);
   A.pos = reinterpret_cast<SpecPos*>(base + pairs * SMAXC * sizeof(SpecStat));
   A.seg = reinterpret_cast<double*>(base + pairs * SMAXC * sizeof(SpecStat) + pairs * sizeof(SpecPos));
+  A.seg_stride = spec_seg_stride(ctx->max_vocab);
+  A.nseg_cap = spec_nseg_cap(ctx->max_vocab);
   const bool aligned = (vocab % 4u) == 0 && ((uintptr_t)target_logits % 16u) == 0 &&
                        ((uintptr_t)A.draft % 16u) == 0;
   const dim3 grid1(8u * L.C, (rows * (draft_len + 1u) + 7u) / 8u);
-  const dim3 grid2(8u * L.C, (rows + 7u) / 8u);
+  const dim3 grid2(8u * L2.C, (rows + 7u) / 8u);
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
-  if (aligned) {
-    hipLaunchKernelGGL(spec_pass1<true>, grid1, dim3(NT), 0, ctx->stream, A);
-    hipLaunchKernelGGL(spec_pass2<true>, grid2, dim3(NT), 0, ctx->stream, A);
-  } else {
-    hipLaunchKernelGGL(spec_pass1<false>, grid1, dim3(NT), 0, ctx->stream, A);
-    hipLaunchKernelGGL(spec_pass2<false>, grid2, dim3(NT), 0, ctx->stream, A);
-  }
+#define MXS_SPEC(AL)                                                                                     \
+  do {                                                                                                   \
+    if (q1) hipLaunchKernelGGL((spec_pass1<AL, SQ>), grid1, dim3(NT), 0, ctx->stream, A);               \
+    else hipLaunchKernelGGL((spec_pass1<AL, SP>), grid1, dim3(NT), 0, ctx->stream, A);                  \
+    if (q2) hipLaunchKernelGGL((spec_pass2<AL, 1>), grid2, dim3(NT), 0, ctx->stream, A);                \
+    else hipLaunchKernelGGL((spec_pass2<AL, SP>), grid2, dim3(NT), 0, ctx->stream, A);                  \
+  } while (0)
+  if (aligned) MXS_SPEC(true); else MXS_SPEC(false);
+#undef MXS_SPEC
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "spec kernels launch");

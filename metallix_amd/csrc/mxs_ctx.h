@@ -43,7 +43,7 @@ void mask_release(mxs_ctx* ctx);   // frees the staging slots (mxs_destroy)
 // their kernels).
 size_t topn_scratch_bytes(uint32_t max_rows);
 const char* noalloc_last_error();   // this thread's last mxs_logsoftmax_topn_noalloc error, or nullptr
-size_t spec_scratch_bytes(uint32_t max_rows);
+size_t spec_scratch_bytes(uint32_t max_rows, uint32_t max_vocab);
 size_t race_scratch_bytes(uint32_t max_rows, uint32_t max_vocab);
 constexpr uint32_t SPEC_COUNTERS_PER_ROW = 10;   // one per (row, position <= 8), one per row
 

@@ -480,6 +480,28 @@ class Sampler:
         self._check(rc, "mxs_spec_verify")
         return out, cnt, acc, st
 
+    def spec_launcher(self, target, draft, draft_tokens, temperature, accept_uniform, resample_uniform,
+                      bonus_uniform):
+        """Pre-built spec_verify for repeated calls with the same per-row
+        inputs and outputs: returns f(target, draft) that only swaps the two
+        logits pointers (f.out holds spec_verify's output tensors)."""
+        out = self.spec_verify(target, draft, draft_tokens, temperature, accept_uniform, resample_uniform,
+                               bonus_uniform)
+        rows, k1, V = target.shape
+        K = k1 - 1
+        fn, ctx = self.lib.mxs_spec_verify, self.ctx
+        rest = (_ptr(draft_tokens) if K else None, temperature.data_ptr(),
+                _ptr(accept_uniform) if K else None, _ptr(resample_uniform) if K else None,
+                bonus_uniform.data_ptr(), *(t.data_ptr() for t in out))
+
+        def launch(tgt, drf):
+            rc = fn(ctx, tgt.data_ptr(), drf.data_ptr() if K else None, rows, K, V, *rest)
+            if rc != 0:
+                self._check(rc, "mxs_spec_verify")
+
+        launch.out = out
+        return launch
+
     def mask_host(self, slot: int):
         """The pinned host words of staging slot `slot` as a numpy u32 array
         [max_rows, stride] (mxs_mask_host: returns once the slot's previous
