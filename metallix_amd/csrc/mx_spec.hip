@@ -38,6 +38,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "../../include/mx_sampler.h"
 #include "mxs_ctx.h"
 #include "mxs_device.h"
@@ -45,7 +47,6 @@
 
 namespace mxs {
 
-constexpr int SQ = 2;                 // quads per thread per chunk (default layout)
 constexpr int SP = 5;                 // quads per thread per chunk (vocabularies past SMAXC default chunks)
 constexpr int SMAXC = 128;            // chunks per row
 constexpr uint32_t SPEC_KMAX = 8;     // draft positions per row
@@ -53,7 +54,9 @@ constexpr uint32_t SPART = 5;         // pass 2's per-chunk partials
 
 struct SpecStat {                     // per (row, position, chunk)
   float tmax, dmax, tmin;
-  uint32_t flags;                     // 1: non-finite target logit, 2: non-finite draft logit
+  uint32_t tflags, dflags;            // a non-finite target / draft logit
+  float te, de;                       // sums of w |y|, y = (l - chunk max) log2(e) / T
+  uint32_t pad;
   double tsum, dsum;                  // sums of exp((l - chunk max) / T)
 };
 
@@ -103,6 +106,18 @@ struct SpecSmem {
   uint32_t s_u[8];
 };
 
+// Pass 1's per (item, wave) statistics.
+struct WaveStat {
+  float m, mn;                        // the wave's maximum and minimum
+  float e;                            // sum of w |y|, y relative to the wave maximum
+  uint32_t bad;                       // a non-finite logit
+  double s;                           // sum of weights relative to the wave maximum
+};
+struct SpecSmem1 {
+  WaveStat w[2 * SPEC_KMAX + 1][NW];
+  uint32_t s_u[4];
+};
+
 // Weight exp(x) of x = (l - M) / T <= 0 as 2^y, y = (l - M) c2 with c2 =
 // log2(e) / T, formed in f64 and clamped at -1000 (2^-1000 is 0 in f32):
 // the f32 exp2 of y's f32 head corrected by its tail (|tail| <= 2^-24 |head|,
@@ -123,11 +138,18 @@ __device__ __forceinline__ double weight2(float l, double M, double c2) {
 __device__ __forceinline__ double weight_sum_err(double s, uint32_t n) {
   return (2.0 * (double)n + 16.0) * U * s * 1.0001 + 1.5 * (double)n * U + 1e-300;
 }
-// As weight_sum_err for weight2 terms (2^-22 relative, 2^-125 absolute) and
-// the device's x through c2 (4 ulp of x against the reference's 2; 2.5 ulp
-// absolute per term for both roundings).
-__device__ __forceinline__ double weight2_sum_err(double s, uint32_t n) {
-  return (0x1p-22 + (2.0 * (double)n + 16.0) * U) * s * 1.0001 + (double)n * (2.5 * U + 0x1p-125) + 1e-300;
+// Bound on |device total - reference total| for a row total s of n
+// weights exp(x), x = (l - M) / T, from pass 1's weights: each 2^y with y =
+// (l - wave max) c2 rounded three times in f32 (3.0001 2^-24 |y| relative, so
+// ln2 3.0001 2^-24 |y| w in the weight), exp2f (2^-23), the 4-term f32 sums
+// (3 2^-24), and the wave-to-chunk factor (the same, its |y| joining the
+// token's in e = sum of w |y| with y relative to the chunk maximum; weight2
+// terms instead: 2^-22 each, e = 0), 2^-21 s in all; weights below f32's
+// normal range 2^-125 each; f64 sums in different orders and the rounding of
+// x as weight_sum_err.
+__device__ __forceinline__ double spec_sum_err(double s, double e, uint32_t n) {
+  return (0x1p-21 + (2.0 * (double)n + 16.0) * U) * s * 1.0001 +
+         0.6931471805599453 * 3.0001 * 0x1p-24 * e * 1.01 + (double)n * (2.5 * U + 0x1p-125) + 1e-300;
 }
 
 template <bool ALIGNED>
@@ -151,140 +173,226 @@ __device__ __forceinline__ double inv_temperature(double T) {
 }
 
 // ---------------------------------------------------------------------------
-// Pass 1: per (row, position, chunk) maxima and weight sums; the last chunk
-// of a (row, position) decides acceptance.
-// (two workgroups per CU in the default layout: at most 64 VGPRs)
+// Pass 1: one workgroup per (row, chunk) streams the chunk of the row's
+// 2K + 1 logit rows (items: target position j at j <= K, draft position j at
+// K + 1 + j), two items in flight per thread.  Each wave reduces its part of
+// an item to statistics on its own (no barrier per item); the workgroup
+// combines them per item at its end.  The row's last workgroup takes the
+// K + 1 verdicts, wave j position j.
 template <bool ALIGNED, int Q>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q == SQ ? 8 : 4))) void spec_pass1(SpecArgs A) {
-  __shared__ SpecSmem S;
+__global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
+  __shared__ SpecSmem1 S;
   const uint32_t tid = threadIdx.x;
   const uint32_t xcd = blockIdx.x & 7u;
   const uint32_t chunk = blockIdx.x >> 3;
-  const uint32_t pair = blockIdx.y * 8u + xcd;
-  const uint32_t K = A.K, V = A.V;
-  if (pair >= A.rows * (K + 1u)) return;
-  const uint32_t row = pair / (K + 1u), j = pair % (K + 1u);
-  const bool has_draft = j < K;
+  const uint32_t row = blockIdx.y * 8u + xcd;
+  if (row >= A.rows) return;
+  const uint32_t K = A.K, V = A.V, nit = 2u * K + 1u;
   const uint32_t c0 = chunk * A.CH, c1 = min(V, c0 + A.CH);
-  const float* tp = A.target + (uint64_t)pair * V;
-  const float* dp = A.draft + ((uint64_t)row * K + (has_draft ? j : 0u)) * V;
   const double T = A.T[row];
   const bool tok_T = temperature_ok(T);
   const double invT = inv_temperature(T);
   const double c2 = invT * 1.4426950408889634;
+  const bool f32w = c2 <= 0x1p126;   // y in f32 (c2 a normal f32); weight2's f64 y above
+  const float c2f = (float)c2;
+  const float* tb = A.target + (uint64_t)row * (K + 1u) * V;
+  const float* db = A.draft + (uint64_t)row * K * V;
 
-  // the drafted token and its uniforms and logits, for the verdict that the
-  // position's last chunk takes (loaded up front, off its critical path;
-  // uniform across the workgroup, so scalar loads into scalar registers)
+  // wave j's position for the verdict, should this workgroup take them:
+  // the drafted token, its uniforms and logits (wave-uniform, so scalar
+  // loads into scalar registers, off the verdict's critical path)
+  const uint32_t wj = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave());
   int32_t d = -1;
   double ua = 0.0, ur = 0.0;
   float tpd = 0.0f, dpd = 0.0f;
-  if (has_draft) {
-    d = A.tok[(uint64_t)row * K + j];
-    ua = A.ua[(uint64_t)row * K + j];
-    ur = A.ur[(uint64_t)row * K + j];
-  }
-  float tv[Q][4], dv[Q][4];
-#pragma unroll
-  for (int i = 0; i < Q; ++i) {
-    const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-    const uint32_t es = e0 < c1 ? e0 : c0;
-    load_quad<ALIGNED>(tp, es, c1, tv[i]);
-    if (has_draft) load_quad<ALIGNED>(dp, es, c1, dv[i]);
-  }
-  if (has_draft && d >= 0 && (uint32_t)d < V) {
-    tpd = tp[d];
-    dpd = dp[d];
-  }
-  float tmax = -INFINITY, dmax = -INFINITY, tmin = INFINITY;
-  uint64_t nft = 0, nfd = 0;
-#pragma unroll
-  for (int i = 0; i < Q; ++i) {
-    const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool inr = i < (int)A.per && e0 + (uint32_t)e < c1;
-      nft |= __builtin_amdgcn_ballot_w64(inr && !__builtin_isfinite(tv[i][e]));
-      tv[i][e] = inr ? tv[i][e] : -INFINITY;
-      tmax = fmaxf(tmax, tv[i][e]);
-      tmin = inr ? fminf(tmin, tv[i][e]) : tmin;
-      if (has_draft) {
-        nfd |= __builtin_amdgcn_ballot_w64(inr && !__builtin_isfinite(dv[i][e]));
-        dv[i][e] = inr ? dv[i][e] : -INFINITY;
-        dmax = fmaxf(dmax, dv[i][e]);
-      }
+  if (wj < K) {
+    d = A.tok[(uint64_t)row * K + wj];
+    ua = A.ua[(uint64_t)row * K + wj];
+    ur = A.ur[(uint64_t)row * K + wj];
+    if (d >= 0 && (uint32_t)d < V) {
+      tpd = tb[(uint64_t)wj * V + (uint32_t)d];
+      dpd = db[(uint64_t)wj * V + (uint32_t)d];
     }
   }
-  {
-    const uint32_t a = wave_max_u32(okey(tmax)), b = wave_max_u32(okey(dmax));
-    const uint32_t c = ~wave_max_u32(~okey(tmin));
+
+  auto item_row = [&](uint32_t it) -> const float* {   // past the last item: the last item again
+    it = min(it, nit - 1u);
+    return it <= K ? tb + (uint64_t)it * V : db + (uint64_t)(it - K - 1u) * V;
+  };
+  auto load = [&](float (&x)[Q][4], const float* p) {
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+      load_quad<ALIGNED>(p, e0 < c1 ? e0 : c0, c1, x[i]);
+    }
+  };
+  // one item: non-finite flag, wave maximum (and minimum, for the bonus
+  // position), the wave's sum of weights relative to its maximum and the
+  // sum of w |y| for the bound.  FULL: a whole chunk (every chunk but a
+  // row's last), whose quads 0..Q-2 are in range ((per - 1) SLICE < CH); only
+  // the last quad is masked.
+  auto process = [&](auto full_tag, float (&x)[Q][4], uint32_t it) {
+    constexpr bool FULL = decltype(full_tag)::value;
+    float mx = -INFINITY, mn = INFINITY;
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < Q; ++i) {
+      const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool inr = (FULL && i < Q - 1) || e0 + (uint32_t)e < c1;
+        bad = bad || (inr && !__builtin_isfinite(x[i][e]));
+        if (!(FULL && i < Q - 1)) x[i][e] = inr ? x[i][e] : -INFINITY;
+        mx = fmaxf(mx, x[i][e]);
+      }
+    }
+    if (it == K) {
+#pragma unroll
+      for (int i = 0; i < Q; ++i) {
+        const uint32_t e0 = c0 + (uint32_t)i * SLICE + tid * 4u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mn = ((FULL && i < Q - 1) || e0 + (uint32_t)e < c1) ? fminf(mn, x[i][e]) : mn;
+      }
+    }
+    const float Mw = okey_value(wave_max_u32(okey(mx)));
+    const float Mn = it == K ? okey_value(~wave_max_u32(~okey(mn))) : INFINITY;
+    const bool wbad = __builtin_amdgcn_ballot_w64(bad) != 0;
+    double s = 0.0;
+    float E = 0.0f;
+    if (tok_T && !wbad && Mw > -INFINITY) {
+      if (f32w) {
+        // every in-range logit is finite here; out-of-range ones are -inf
+        // (weight 0, and w y taken as 0)
+#pragma unroll
+        for (int i = 0; i < Q; ++i) {
+          float q = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float y = (x[i][e] - Mw) * c2f;
+            const float w = __builtin_amdgcn_exp2f(y);
+            q += w;
+            E = fmaf(w, (FULL && i < Q - 1) ? y : fmaxf(y, -1e30f), E);
+          }
+          s += (double)q;
+        }
+        E = -E;
+      } else {
+#pragma unroll
+        for (int i = 0; i < Q; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s += weight2(x[i][e], (double)Mw, c2);
+      }
+    }
+    s = wave_sum_f64(s);
+    E = wave_sum_f32(E);
     if (lane() == 0) {
-      S.red_u[0][wave()] = a;
-      S.red_u[1][wave()] = b;
-      S.red_u[2][wave()] = c;
-      S.red_u[3][wave()] = (nft ? 1u : 0u) | (nfd ? 2u : 0u);
+      WaveStat& ws = S.w[it][wave()];
+      ws.m = Mw;
+      ws.mn = Mn;
+      ws.e = E;
+      ws.bad = wbad ? 1u : 0u;
+      ws.s = s;
+    }
+  };
+  const bool full = c1 - c0 == A.CH;
+  using FullT = std::integral_constant<bool, true>;
+  using PartT = std::integral_constant<bool, false>;
+
+  float xa[Q][4], xb[Q][4];
+  load(xa, item_row(0u));
+  load(xb, item_row(1u));
+  if (full) {
+    for (uint32_t it = 0; it < nit; it += 2u) {
+      process(FullT(), xa, it);
+      load(xa, item_row(it + 2u));
+      if (it + 1u < nit) process(FullT(), xb, it + 1u);
+      load(xb, item_row(it + 3u));
+    }
+  } else {
+    for (uint32_t it = 0; it < nit; it += 2u) {
+      process(PartT(), xa, it);
+      load(xa, item_row(it + 2u));
+      if (it + 1u < nit) process(PartT(), xb, it + 1u);
+      load(xb, item_row(it + 3u));
     }
   }
   lds_barrier();
-  uint32_t ka = 0u, kb = 0u, kc = NONE, flags = 0u;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    ka = max(ka, S.red_u[0][w]);
-    kb = max(kb, S.red_u[1][w]);
-    kc = min(kc, S.red_u[2][w]);
-    flags |= S.red_u[3][w];
-  }
-  const float mt = okey_value(ka), md = okey_value(kb), mn = okey_value(kc);
-  double tsum = 0.0, dsum = 0.0;
-  if (tok_T && !flags && c1 > c0) {
-    const double mtd = (double)mt, mdd = (double)md;
-    double pt = 0.0, pd = 0.0;
-#pragma unroll
-    for (int i = 0; i < Q; ++i)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pt += weight2(tv[i][e], mtd, c2);
-        if (has_draft) pd += weight2(dv[i][e], mdd, c2);
-      }
-    pt = wave_sum_f64(pt);
-    pd = wave_sum_f64(pd);
-    if (lane() == 0) { S.red_d[0][wave()] = pt; S.red_d[1][wave()] = pd; }
-    lds_barrier();
-#pragma unroll
-    for (int w = 0; w < NW; ++w) { tsum += S.red_d[0][w]; dsum += S.red_d[1][w]; }
-  }
-  if (tid == 0) {
-    SpecStat* st = &A.stat[((uint64_t)row * (SPEC_KMAX + 1) + j) * SMAXC + chunk];
-    st_dev(&st->tmax, mt);
-    st_dev(&st->dmax, md);
-    st_dev(&st->tmin, mn);
-    st_dev(&st->flags, flags);
-    st_dev(&st->tsum, tsum);
-    st_dev(&st->dsum, dsum);
-  }
-  if (!arrive_last(&A.ctr1[(row * (SPEC_KMAX + 1) + j) * CTR_STRIDE], A.C, &S.s_u[0])) return;
 
-  // ---- the position's verdict: wave 0 reduces the chunks' statistics (two
+  // per item, the chunk's statistics from the waves': maximum, minimum,
+  // flag, and the waves' sums rescaled to the chunk maximum (their E with
+  // the rescale's own |y|)
+  if (tid < nit) {
+    const uint32_t it = tid;
+    float M = -INFINITY, Mn = INFINITY;
+    uint32_t bad = 0u;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      M = fmaxf(M, S.w[it][w].m);
+      Mn = fminf(Mn, S.w[it][w].mn);
+      bad |= S.w[it][w].bad;
+    }
+    double s = 0.0;
+    float E = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const WaveStat& ws = S.w[it][w];
+      if (ws.s > 0.0) {
+        if (f32w) {
+          const float dy = (ws.m - M) * c2f;
+          const float f = __builtin_amdgcn_exp2f(dy);
+          s += ws.s * (double)f;
+          E += f * (ws.e + (float)ws.s * fminf(-dy, 1e30f));
+        } else {
+          s += ws.s * weight2(ws.m, (double)M, c2);
+        }
+      }
+    }
+    const uint32_t j = it <= K ? it : it - K - 1u;
+    SpecStat* st = &A.stat[((uint64_t)row * (SPEC_KMAX + 1) + j) * SMAXC + chunk];
+    if (it <= K) {
+      st_dev(&st->tmax, M);
+      st_dev(&st->tmin, Mn);
+      st_dev(&st->tflags, bad);
+      st_dev(&st->tsum, s);
+      st_dev(&st->te, E);
+    } else {
+      st_dev(&st->dmax, M);
+      st_dev(&st->dflags, bad);
+      st_dev(&st->dsum, s);
+      st_dev(&st->de, E);
+    }
+  }
+  if (!arrive_last(&A.ctr1[row * (SPEC_KMAX + 1) * CTR_STRIDE], A.C, &S.s_u[0])) return;
+
+  // ---- the verdicts: wave j reduces position j's chunk statistics (two
   // chunks per lane, C <= SMAXC = 128), lane 0 decides
-  if (wave() != 0) return;
+  if (wj > K) return;
+  const uint32_t j = wj;
+  const bool has_draft = j < K;
   const uint32_t slot = row * (SPEC_KMAX + 1) + j;
   const uint32_t C = A.C;
-  float cmt[2], cmd[2];
+  float cmt[2], cmd[2], cte[2], cde[2];
   double cts[2], cds[2];
   uint32_t fl = 0u, kt = 0u, kd = 0u, kn = 0u;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const uint32_t q = lane() + 64u * (uint32_t)h;
     cmt[h] = cmd[h] = -INFINITY;
+    cte[h] = cde[h] = 0.0f;
     cts[h] = cds[h] = 0.0;
     if (q < C) {
       const SpecStat* st = &A.stat[(uint64_t)slot * SMAXC + q];
       cmt[h] = ld_dev(&st->tmax);
-      cmd[h] = ld_dev(&st->dmax);
       kn = max(kn, ~okey(ld_dev(&st->tmin)));
-      fl |= ld_dev(&st->flags);
+      fl |= ld_dev(&st->tflags);
       cts[h] = ld_dev(&st->tsum);
-      cds[h] = ld_dev(&st->dsum);
+      cte[h] = ld_dev(&st->te);
+      if (has_draft) {
+        cmd[h] = ld_dev(&st->dmax);
+        fl |= ld_dev(&st->dflags) << 1;
+        cds[h] = ld_dev(&st->dsum);
+        cde[h] = ld_dev(&st->de);
+      }
       kt = max(kt, okey(cmt[h]));
       kd = max(kd, okey(cmd[h]));
     }
@@ -293,15 +401,24 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q == SQ ? 8 
   const float Mt = okey_value(wave_max_u32(kt)), Md = okey_value(wave_max_u32(kd));
   const float Mn = okey_value(~wave_max_u32(kn));
   // totals: the chunk sums rescaled from the chunk maxima to the row maxima
-  double tt = 0.0, td = 0.0;
+  double tt = 0.0, td = 0.0, et = 0.0, ed = 0.0;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    tt += cts[h] * exp_neg_p(((double)cmt[h] - (double)Mt) * invT);
-    td += cds[h] * exp_neg_p(((double)cmd[h] - (double)Md) * invT);
+    const double ft = exp_neg_p(((double)cmt[h] - (double)Mt) * invT);
+    const double fd = exp_neg_p(((double)cmd[h] - (double)Md) * invT);
+    tt += cts[h] * ft;
+    et += (double)cte[h] * ft;
+    td += cds[h] * fd;
+    ed += (double)cde[h] * fd;
   }
   tt = wave_sum_f64(tt);
-  td = wave_sum_f64(td);
+  et = wave_sum_f64(et);
+  if (has_draft) {
+    td = wave_sum_f64(td);
+    ed = wave_sum_f64(ed);
+  }
   if (lane() != 0) return;
+  const uint32_t nsum = V + C * NW;
   SpecPos P;
   P.err = 0;
   P.accept = 0;
@@ -320,8 +437,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q == SQ ? 8 
     if (!P.err) {
       P.tt = tt;
       P.td = td;
-      P.tterr = weight2_sum_err(tt, V + C);
-      P.tderr = weight2_sum_err(td, V + C);
+      P.tterr = spec_sum_err(tt, et, nsum);
+      P.tderr = spec_sum_err(td, ed, nsum);
       const double xt = ((double)tpd - (double)Mt) * invT;
       const double xq = ((double)dpd - (double)Md) * invT;
       const double wt = exp_neg_p(xt);
@@ -349,7 +466,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(Q == SQ ? 8 
     else if (!isfinite(((double)Mn - (double)Mt) / T)) P.err = MXS_ROW_INVALID_TEMPERATURE;
     else {
       P.tt = tt;
-      P.tterr = weight2_sum_err(tt, V + C);
+      P.tterr = spec_sum_err(tt, et, nsum);
     }
   }
   SpecPos* out = &A.pos[slot];
@@ -707,12 +824,19 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   }
 }
 
-// Chunk layouts of a vocabulary.  Pass 1: SQ quads per thread unless that
-// needs more than SMAXC chunks.  Pass 2 (one position per row): one quad per
-// thread, for more workgroups over the CUs, under the same limit.
-static ChunkLayout spec_layout1(uint32_t V) {
-  const ChunkLayout L = chunk_layout(V, SQ);
-  return L.C <= (uint32_t)SMAXC ? L : chunk_layout(V, SP);
+// Chunk layouts of a vocabulary.  Pass 1 (a workgroup per (row, chunk)
+// streams all of the row's logit rows): chunks enough for about 256
+// workgroups over the batch, at least what SP quads per thread need, at most
+// SMAXC.  Pass 2 (one position per row): one quad per thread, for more
+// workgroups over the CUs, under the same limit.
+static ChunkLayout spec_layout1(uint32_t V, uint32_t rows) {
+  const uint32_t quads = (V + 3u) / 4u;
+  const uint32_t cmin = (quads + (uint32_t)NT * SP - 1u) / ((uint32_t)NT * SP);
+  const uint32_t cw = (256u + rows - 1u) / rows;
+  uint32_t C = min((uint32_t)SMAXC, max(max(cmin, cw), 1u));
+  const uint32_t ch = ((V + C - 1u) / C + 3u) & ~3u;
+  C = (V + ch - 1u) / ch;
+  return {C, ch, (ch / 4u + (uint32_t)NT - 1u) / (uint32_t)NT};
 }
 static ChunkLayout spec_layout2(uint32_t V) {
   const ChunkLayout L = chunk_layout(V, 1);
@@ -756,11 +880,11 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   if (rows > ctx->max_rows || vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
   if (vocab == 0) return fail(ctx, MXS_EINVAL, "vocab must be positive");
   if (draft_len > SPEC_KMAX) return fail(ctx, MXS_EINVAL, "draft_len must be at most 8");
-  const ChunkLayout L = spec_layout1(vocab), L2 = spec_layout2(vocab);
+  const ChunkLayout L = spec_layout1(vocab, rows), L2 = spec_layout2(vocab);
   if (L.per > (uint32_t)SP || L.C > (uint32_t)SMAXC || L2.per > (uint32_t)SP || L2.C > (uint32_t)SMAXC ||
       L2.C * L2.per * NW > spec_nseg_cap(ctx->max_vocab))
     return fail(ctx, MXS_EINVAL, "vocab too large for the chunk layout");
-  const bool q1 = L.per <= (uint32_t)SQ, q2 = L2.per <= 1u;
+  const bool q2 = L2.per <= 1u;
   SpecArgs A;
   A.target = target_logits;
   A.draft = draft_len ? draft_logits : target_logits;
@@ -793,15 +917,20 @@ extern "C" int mxs_spec_verify(mxs_ctx* ctx, const float* target_logits, const f
   A.nseg_cap = spec_nseg_cap(ctx->max_vocab);
   const bool aligned = (vocab % 4u) == 0 && ((uintptr_t)target_logits % 16u) == 0 &&
                        ((uintptr_t)A.draft % 16u) == 0;
-  const dim3 grid1(8u * L.C, (rows * (draft_len + 1u) + 7u) / 8u);
+  const dim3 grid1(8u * L.C, (rows + 7u) / 8u);
   const dim3 grid2(8u * L2.C, (rows + 7u) / 8u);
   int prev = 0;
   hipGetDevice(&prev);
   if (prev != ctx->device) hipSetDevice(ctx->device);
 #define MXS_SPEC(AL)                                                                                     \
   do {                                                                                                   \
-    if (q1) hipLaunchKernelGGL((spec_pass1<AL, SQ>), grid1, dim3(NT), 0, ctx->stream, A);               \
-    else hipLaunchKernelGGL((spec_pass1<AL, SP>), grid1, dim3(NT), 0, ctx->stream, A);                  \
+    switch (L.per) {                                                                                     \
+      case 1: hipLaunchKernelGGL((spec_pass1<AL, 1>), grid1, dim3(NT), 0, ctx->stream, A); break;        \
+      case 2: hipLaunchKernelGGL((spec_pass1<AL, 2>), grid1, dim3(NT), 0, ctx->stream, A); break;        \
+      case 3: hipLaunchKernelGGL((spec_pass1<AL, 3>), grid1, dim3(NT), 0, ctx->stream, A); break;        \
+      case 4: hipLaunchKernelGGL((spec_pass1<AL, 4>), grid1, dim3(NT), 0, ctx->stream, A); break;        \
+      default: hipLaunchKernelGGL((spec_pass1<AL, 5>), grid1, dim3(NT), 0, ctx->stream, A); break;       \
+    }                                                                                                    \
     if (q2) hipLaunchKernelGGL((spec_pass2<AL, 1>), grid2, dim3(NT), 0, ctx->stream, A);                \
     else hipLaunchKernelGGL((spec_pass2<AL, SP>), grid2, dim3(NT), 0, ctx->stream, A);                  \
   } while (0)
