@@ -13,13 +13,16 @@
 // is accepted, the bonus token is sample_categorical over target row K.
 //
 // Two launches on the context's stream.
-//   Pass 1, one workgroup per (row, position, chunk): the chunk's maxima and
-//   weight sums, the weights from the f32 exp2 (weight2, within 2^-22) summed
-//   in f64.  The last chunk of a (row, position) decides acceptance: the
-//   ratio p/q needs only that relative accuracy to be certified.
+//   Pass 1, one workgroup per (row, chunk), streaming that chunk of all the
+//   row's 2K + 1 logit rows: per row of logits the chunk's maximum and
+//   weight sum, the weights from the f32 exp2 summed in f64 (a few 2^-23
+//   relative, plus a term in sum w |y| for the rounding of y; spec_sum_err).
+//   The row's last workgroup decides acceptance at every position: the ratio
+//   p/q needs only that relative accuracy to be certified.
 //   Pass 2, one workgroup per (row, chunk): the first rejected position (or
 //   the bonus position) from pass 1's verdicts, then the drawn
-//   distribution's weights at that position in f64 (exp_neg_t).  The residual
+//   distribution's weights at that position in f64 (exp_neg16_t, its
+//   16-entry table read from LDS without bank conflicts).  The residual
 //   max(0, t_i / sum t - q_i / sum q) needs the totals to f64 accuracy, which
 //   pass 1 does not have; its approximate totals only classify each token's
 //   sign with a margin, so that each 256-token segment stores the exact sums
@@ -98,7 +101,7 @@ struct SpecArgs {
 };
 
 struct SpecSmem {
-  double etab[128];                   // exp_neg's tables
+  double etab[32];                    // exp_neg16_t's tables: 2^(j/16), hi then lo
   SpecPos ps[SPEC_KMAX + 1];
   uint32_t red_u[4][NW];
   double red_d[8][NW];
@@ -114,7 +117,7 @@ struct WaveStat {
   double s;                           // sum of weights relative to the wave maximum
 };
 struct SpecSmem1 {
-  WaveStat w[2 * SPEC_KMAX + 1][NW];
+  WaveStat w[NW][2 * SPEC_KMAX + 1];  // [wave][item]: the per-item combine reads consecutive entries
   uint32_t s_u[4];
 };
 
@@ -286,7 +289,7 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     s = wave_sum_f64(s);
     E = wave_sum_f32(E);
     if (lane() == 0) {
-      WaveStat& ws = S.w[it][wave()];
+      WaveStat& ws = S.w[wave()][it];
       ws.m = Mw;
       ws.mn = Mn;
       ws.e = E;
@@ -327,15 +330,15 @@ __global__ __launch_bounds__(NT) void spec_pass1(SpecArgs A) {
     uint32_t bad = 0u;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      M = fmaxf(M, S.w[it][w].m);
-      Mn = fminf(Mn, S.w[it][w].mn);
-      bad |= S.w[it][w].bad;
+      M = fmaxf(M, S.w[w][it].m);
+      Mn = fminf(Mn, S.w[w][it].mn);
+      bad |= S.w[w][it].bad;
     }
     double s = 0.0;
     float E = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const WaveStat& ws = S.w[it][w];
+      const WaveStat& ws = S.w[w][it];
       if (ws.s > 0.0) {
         if (f32w) {
           const float dy = (ws.m - M) * c2f;
@@ -519,7 +522,7 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
   const uint32_t row = blockIdx.y * 8u + xcd;
   if (row >= A.rows) return;
   const uint32_t K = A.K, V = A.V;
-  if (tid < 128u) S.etab[tid] = tid < 64u ? kExp2Tab[tid] : kExp2TabLo[tid - 64u];
+  if (tid < 32u) S.etab[tid] = tid < 16u ? kExp2Tab[4u * tid] : kExp2TabLo[4u * (tid - 16u)];
   for (uint32_t j = tid; j <= K; j += NT) {
     const SpecPos* src = &A.pos[row * (SPEC_KMAX + 1) + j];
     SpecPos P;
@@ -569,12 +572,12 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           if (e0 + (uint32_t)e < c1) {
-            const double wt = exp_neg_t(((double)t[i][e] - (double)P.mt) * invT, S.etab, S.etab + 64);
+            const double wt = exp_neg16_t(((double)t[i][e] - (double)P.mt) * invT, S.etab, S.etab + 16);
             pt += wt;
             if (bonus) {
               sa += wt;
             } else {
-              const double wq = exp_neg_t(((double)q[i][e] - (double)P.md) * invT, S.etab, S.etab + 64);
+              const double wq = exp_neg16_t(((double)q[i][e] - (double)P.md) * invT, S.etab, S.etab + 16);
               pd += wq;
               const double x = wt * ra, y = wq * rb;
               const double dd = x - y, ss = x + y;
@@ -776,8 +779,8 @@ __global__ __launch_bounds__(NT) void spec_pass2(SpecArgs A) {
       double wl[4], lsum = 0.0;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const double wt = exp_neg_t(((double)lt[e] - (double)P.mt) * invT, S.etab, S.etab + 64);
-        double wv = bonus ? wt : fmax(wt * a - exp_neg_t(((double)lq[e] - (double)P.md) * invT, S.etab, S.etab + 64) * b, 0.0);
+        const double wt = exp_neg16_t(((double)lt[e] - (double)P.mt) * invT, S.etab, S.etab + 16);
+        double wv = bonus ? wt : fmax(wt * a - exp_neg16_t(((double)lq[e] - (double)P.md) * invT, S.etab, S.etab + 16) * b, 0.0);
         wl[e] = id0 + (uint32_t)e < qc1 ? wv : 0.0;
         lsum += wl[e];
       }

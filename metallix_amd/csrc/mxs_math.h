@@ -97,6 +97,34 @@ MXS_HD double exp_neg_t(double x, const double* tab_hi, const double* tab_lo) {
 }
 MXS_HD double exp_neg(double x) { return exp_neg_t(x, kExp2Tab, kExp2TabLo); }
 
+// exp(x) for x <= 0 in f64 from a 16-entry two-part table, 2^(j/16) for j <
+// 16 (entries 4j of the 64-entry one): a kernel's LDS copy, 16 doubles per
+// part, is read without bank conflicts (distinct entries fall in distinct
+// banks, equal ones broadcast).  x = n ln2/16 + r, |r| <= ln2/32, degree-7
+// Taylor polynomial for e^r - 1 (truncation below 2e-18 relative), scaled
+// by 2^(n div 16).  Within 1 ulp of glibc's exp (checked in tests).
+// Returns 0 below -746 and for -inf.
+MXS_HD double exp_neg16_t(double x, const double* tab_hi, const double* tab_lo) {
+  if (!(x > -746.0)) return 0.0;
+  const double kInvL = 23.083120654223414;         // 16 / ln 2
+  const double kLHi = 0.04332169878499658;         // ln 2 / 16, high part (trailing zero bits: t kLHi exact)
+  const double kLLo = 1.4494042586539372e-18;      // ln 2 / 16 - kLHi
+  double t = rint(x * kInvL);
+  int n = (int)t;
+  double r = fma(-t, kLHi, x);
+  r = fma(-t, kLLo, r);
+  double p = fma(r, 1.0 / 5040.0, 1.0 / 720.0);
+  p = fma(r, p, 1.0 / 120.0);
+  p = fma(r, p, 1.0 / 24.0);
+  p = fma(r, p, 1.0 / 6.0);
+  p = fma(r, p, 0.5);
+  double q = fma(r * r, p, r);  // e^r - 1
+  int j = n & 15;
+  int k = n >> 4;  // arithmetic shift: floor division
+  const double th = tab_hi[j], tl = tab_lo[j];
+  return ldexp(th + fma(th, q, tl), k);
+}
+
 // exp(x) for x <= 0 in f64 without tables (for loops over registers, where
 // table gathers would be hoisted and held): x = n ln2 + r, |r| <= ln2 / 2
 // (Cody-Waite reduction with a 32-bit high part of ln2, so n * hi is exact

@@ -104,6 +104,32 @@ static void check_exp(long n) {
   printf("exp_neg %ld %ld differing=%ld\n", fail, n, diff);
 }
 
+// exp_neg16_t (1 ulp) and exp_neg_p (2 ulp) against the C library's exp.
+static void check_exp_variants(long n) {
+  double hi16[16], lo16[16];
+  for (int j = 0; j < 16; ++j) { hi16[j] = mxs::kExp2Tab[4 * j]; lo16[j] = mxs::kExp2TabLo[4 * j]; }
+  long f16 = 0, fp = 0, d16 = 0, dp = 0;
+  auto one = [&](double x) {
+    const double a = exp(x), b = mxs::exp_neg16_t(x, hi16, lo16), c = mxs::exp_neg_p(x);
+    if (!(x > -746.0)) {
+      if (b != 0.0) ++f16;
+      if (c != 0.0) ++fp;
+      return;
+    }
+    const int64_t u = (int64_t)d_bits(a) - (int64_t)d_bits(b), v = (int64_t)d_bits(a) - (int64_t)d_bits(c);
+    if (u) ++d16;
+    if (v) ++dp;
+    if (u > 1 || u < -1) ++f16;
+    if (v > 2 || v < -2) ++fp;
+  };
+  for (long i = 0; i < n; ++i) one(-746.0 * (double)(splitmix() >> 11) * 0x1.0p-53);
+  for (long i = 0; i < n / 4; ++i) one(-(double)(splitmix() >> 11) * 0x1.0p-53);   // |x| < 1
+  const double edge[] = {0.0, -0.0, -1e-300, -745.1, -746.0, -800.0, -INFINITY, -708.39, -1.0, -0.02166, -0.0433};
+  for (double x : edge) one(x);
+  printf("exp_neg16 %ld %ld differing=%ld\n", f16, n, d16);
+  printf("exp_neg_p %ld %ld differing=%ld\n", fp, n, dp);
+}
+
 static void check_okey(long n) {
   long fail = 0;
   for (long i = 0; i < n; ++i) {
@@ -122,6 +148,7 @@ int main(void) {
   check_division(20000000);
   check_penalize(2000000);
   check_exp(2000000);
+  check_exp_variants(2000000);
   check_okey(2000000);
   return 0;
 }

@@ -1,6 +1,7 @@
 """Host checks of the kernels' numeric building blocks (mxs_math.h): the
 reciprocal-based f32 division of the repetition penalty, the composed bias
-and penalty stage, the f64 exp used for weights, and the total-order key."""
+and penalty stage, the f64 exps used for weights (64- and 16-entry tables,
+table-free), and the total-order key."""
 import os
 import subprocess
 import tempfile
@@ -28,7 +29,7 @@ def results():
     return res
 
 
-@pytest.mark.parametrize("name", ["division", "penalize", "exp_neg", "okey"])
+@pytest.mark.parametrize("name", ["division", "penalize", "exp_neg", "exp_neg16", "exp_neg_p", "okey"])
 def test_math(results, name):
     fail, cases, rest = results[name]
     assert cases > 1000
