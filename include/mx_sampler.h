@@ -34,6 +34,9 @@
  *   mxs_mask_host,            <- the per-step SimpleVob words (crates/core/engine/src/
  *   mxs_mask_upload              constraint.rs:777-806) on their way to the device: pinned
  *                                staging, an upload on a copy stream, double-buffered.
+ *   mxs_export_candidates     <- Qwen3TokenPicks::wait_with_candidates (picks.rs:429-466), the
+ *                                candidates TurnLoop::settle_row hands pick_from_candidates
+ *                                (chat_turn.rs:332-358; chat_generation.rs:2088-2131).
  *   mxs_sync                  <- Qwen3TokenPicks::wait (picks.rs:390-401).
  *   mxs_last_error            <- KernelError's message (mlx-kernels/src/lib.rs:444-450).
  *
@@ -227,6 +230,21 @@ int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const m
  * batch->mask_words with mask_stride = *stride_words.  Two slots
  * double-buffer consecutive steps: fill and upload slot 1 - s while the pick
  * of slot s runs. */
+/* Candidates of the context's last mxs_sample or mxs_step call, per row of
+ * its first `rows` rows, queued on the context's stream behind that call:
+ * the list the row's finisher chose from (every candidate at or above its
+ * chunk's threshold; it holds the row's top-k head for a top-k row and its
+ * min-p set for a min-p row), as adjusted logits (penalties, bias, mask
+ * applied) with their token IDs, in token-ID order.  count[r] = the list's
+ * length when at most `width`; else its top `width` by (logit desc, ID asc)
+ * and count[r] = width; -1 for a row with no list (greedy, keep-all, error
+ * rows).  ids and logits are rows x width.  The settle of an uncertified
+ * (status 1) top-k row with k <= width: sort by (logit desc, ID asc), keep
+ * the first k, and apply the row's rule to them, as pick_from_candidates'
+ * sample_top_k_candidates does; the row need not be read back.  A later
+ * pick on the context overwrites the lists. */
+int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* count, int32_t* ids,
+                          float* logits);
 int mxs_mask_host(mxs_ctx* ctx, uint32_t slot, uint32_t** words, uint64_t* stride_words);
 int mxs_mask_upload(mxs_ctx* ctx, uint32_t slot, uint32_t rows, const uint32_t** device_words);
 int mxs_sync(mxs_ctx* ctx);

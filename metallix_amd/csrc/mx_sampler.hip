@@ -3058,6 +3058,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     F.s_u[11] = 0u;
     F.hdr.L = c.min_p > 0.0 ? log(c.min_p) : -INFINITY;
   }
+  if (tid == 0) A.w.cand_rows[row] = -1;   // no candidate list unless a candidate path runs
   uint32_t sq, sj;                // this thread's chunk and slot group (slot_map)
   slot_map(C, &sq, &sj);
   const uint32_t cov = slot_cov(C);   // candidates per chunk held in registers
@@ -3275,6 +3276,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
 
   // =================== candidate paths ====================================
   const uint32_t ncand = F.hdr.ncand;
+  if (tid == 0) A.w.cand_rows[row] = (int32_t)ncand;   // mxs_export_candidates
   X.ncand = ncand;
   X.lds_c = ncand <= (uint32_t)CCAP;
   const double L = F.hdr.L;
@@ -5532,10 +5534,119 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   }
 #undef MXS_ARGS
   hipError_t e = hipGetLastError();
-  if (e == hipSuccess) mask_note_read(ctx, b->mask_words);
+  if (e == hipSuccess) {
+    mask_note_read(ctx, b->mask_words);
+    ctx->last_rows = b->rows;
+    ctx->last_C = L.C;
+    ctx->last_CH = L.CH;
+    ctx->last_V = b->vocab;
+  }
   if (prev != ctx->device) hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "sample_kernel launch");
   return MXS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Candidate export (mxs_export_candidates): row r's candidate list from the
+// last mxs_sample / mxs_step call, chunk q's candidates at r V + q CH
+// (ncand of them, token-ID order), copied out whole when at most `width`,
+// else its top `width` by (logit desc, ID asc): a radix select of the
+// width-th largest order key over four 8-bit digits, then every key above it
+// and the lowest-ID ties at it.  Output in token-ID order.
+__global__ __launch_bounds__(NT) void cand_export_kernel(Work w, uint32_t C, uint32_t CH, uint32_t V,
+                                                         uint32_t width, int32_t* count, int32_t* ids,
+                                                         float* logits) {
+  __shared__ uint32_t coff[MAXC + 1];
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t red[NW];
+  __shared__ uint32_t s_u[2];
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const int32_t n0 = w.cand_rows[row];
+  if (n0 < 0) {
+    if (tid == 0) count[row] = -1;
+    return;
+  }
+  if (tid < 64u) {   // chunk offsets (C <= MAXC = 64)
+    const uint32_t nq = tid < C ? w.stat[(uint64_t)row * MAXC + tid].ncand : 0u;
+    const uint32_t inc = wave_scan_u32(nq);
+    if (tid < C) coff[tid] = inc - nq;
+    const uint32_t tot = bcast63(inc);
+    if (tid == 0) coff[C] = tot;
+  }
+  __syncthreads();
+  const uint32_t n = min((uint32_t)n0, coff[C]);
+  const uint64_t rbase = (uint64_t)row * V;
+  // candidate j's position: the last chunk q < C with coff[q] <= j
+  auto pos_of = [&](uint32_t j) -> uint64_t {
+    uint32_t lo = 0, hi = C - 1u;
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi + 1u) >> 1;
+      if (coff[mid] <= j) lo = mid; else hi = mid - 1u;
+    }
+    return rbase + (uint64_t)lo * CH + (j - coff[lo]);
+  };
+  int32_t* oi = ids + (uint64_t)row * width;
+  float* ol = logits + (uint64_t)row * width;
+  if (n <= width) {
+    for (uint32_t j = tid; j < n; j += NT) {
+      const uint64_t p = pos_of(j);
+      oi[j] = (int32_t)ld_dev(&w.cand_id[p]);
+      ol[j] = ld_dev(&w.cand_l[p]);
+    }
+    if (tid == 0) count[row] = (int32_t)n;
+    return;
+  }
+  uint32_t prefix = 0u, need = width;   // the key's fixed high digits; members still to take at or below them
+  for (int d = 3; d >= 0; --d) {
+    if (tid < 256u) hist[tid] = 0u;
+    __syncthreads();
+    const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
+    for (uint32_t j = tid; j < n; j += NT) {
+      const uint32_t key = okey(ld_dev(&w.cand_l[pos_of(j)]));
+      if ((key & pm) == prefix) atomicAdd(&hist[(key >> (8 * d)) & 255u], 1u);
+    }
+    __syncthreads();
+    if (tid == 0) {   // the digit, from the top, where the count above reaches `need`
+      uint32_t cum = 0u;
+      int b = 255;
+      for (; b > 0; --b) {
+        if (cum + hist[b] >= need) break;
+        cum += hist[b];
+      }
+      s_u[0] = (uint32_t)b;
+      s_u[1] = cum;
+    }
+    __syncthreads();
+    prefix |= s_u[0] << (8 * d);
+    need -= s_u[1];
+    __syncthreads();
+  }
+  // keys above `prefix` (width - need of them), then the first `need` ties in ID order
+  uint32_t base = 0u, tbase = 0u;
+  for (uint32_t j0 = 0; j0 < n; j0 += NT) {
+    const uint32_t j = j0 + tid;
+    uint32_t key = 0u, id = 0u;
+    float l = 0.0f;
+    if (j < n) {
+      const uint64_t p = pos_of(j);
+      l = ld_dev(&w.cand_l[p]);
+      id = ld_dev(&w.cand_id[p]);
+      key = okey(l);
+    }
+    const bool tie = j < n && key == prefix;
+    uint32_t ttot;
+    const uint32_t trank = tbase + block_scan_incl<uint32_t>(tie ? 1u : 0u, red, &ttot) - (tie ? 1u : 0u);
+    const bool take = (j < n && key > prefix) || (tie && trank < need);
+    uint32_t tot;
+    const uint32_t at = base + block_scan_incl<uint32_t>(take ? 1u : 0u, red, &tot) - (take ? 1u : 0u);
+    if (take && at < width) {
+      oi[at] = (int32_t)id;
+      ol[at] = l;
+    }
+    base += tot;
+    tbase += ttot;
+  }
+  if (tid == 0) count[row] = (int32_t)min(base, width);
 }
 
 }  // namespace mxs
@@ -5543,6 +5654,26 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
 extern "C" {
 
 int mxs_abi_version(void) { return MXS_ABI_VERSION; }
+
+int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* count, int32_t* ids,
+                          float* logits) {
+  using namespace mxs;
+  if (!ctx) return MXS_EINVAL;
+  if (rows == 0) return MXS_OK;
+  if (!count || !ids || !logits || width == 0)
+    return fail(ctx, MXS_EINVAL, "count, ids and logits are required and width must be positive");
+  if (ctx->last_rows == 0) return fail(ctx, MXS_EINVAL, "no mxs_sample or mxs_step call on this context yet");
+  if (rows > ctx->last_rows) return fail(ctx, MXS_EINVAL, "rows exceeds the last call's batch");
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  hipLaunchKernelGGL(cand_export_kernel, dim3(rows), dim3(NT), 0, ctx->stream, ctx->work, ctx->last_C,
+                     ctx->last_CH, ctx->last_V, width, count, ids, logits);
+  hipError_t e = hipGetLastError();
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "cand_export_kernel launch");
+  return MXS_OK;
+}
 
 const char* mxs_status_string(int32_t s) {
   switch (s) {
@@ -5591,6 +5722,8 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMalloc(&ctx->work.cand_l, rv * sizeof(float));
   e = e ? e : hipMalloc(&ctx->work.cand_id, rv * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->work.seg, (size_t)max_rows * mxs::MAXC * mxs::PER_MAX * mxs::NW * sizeof(double));
+  e = e ? e : hipMalloc(&ctx->work.cand_rows, (size_t)max_rows * sizeof(int32_t));
+  e = e ? e : hipMemset(ctx->work.cand_rows, 0xff, (size_t)max_rows * sizeof(int32_t));
   e = e ? e : hipMemset(ctx->work.rowx, 0, (size_t)max_rows * mxs::ROWX_STRIDE * sizeof(unsigned long long));
   e = e ? e : hipMemset(ctx->work.ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->topn_scratch, mxs::topn_scratch_bytes(max_rows));
@@ -5643,6 +5776,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->work.cand_l);
   hipFree(ctx->work.cand_id);
   hipFree(ctx->work.seg);
+  hipFree(ctx->work.cand_rows);
   hipFree(ctx->d_zero_u32);
   hipFree(ctx->d_one_f64);
   hipFree(ctx->d_race_u);

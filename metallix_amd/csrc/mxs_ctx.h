@@ -61,6 +61,7 @@ struct Work {
   float* cand_l;              // [max_rows * max_vocab]
   uint32_t* cand_id;          // [max_rows * max_vocab]
   double* seg;                // [max_rows * MAXC * PER_MAX * NW]
+  int32_t* cand_rows;         // [max_rows] candidates the row's finisher chose from (-1: no list)
 };
 
 }  // namespace mxs
@@ -82,6 +83,8 @@ struct mxs_ctx {
   uint64_t* timing = nullptr;
   int32_t* paths = nullptr;             // finisher path per row (diagnostics)
   uint32_t epoch = 0;                 // mxs_sample calls so far (tags Work::rowx entries)
+  // the last mxs_sample / mxs_step call's layout (mxs_export_candidates)
+  uint32_t last_rows = 0, last_C = 0, last_CH = 0, last_V = 0;
   // mxs_logsoftmax_topn: per-chunk results
   void* topn_scratch = nullptr;
   // mxs_spec_verify: per-position arrival counters and per-chunk results

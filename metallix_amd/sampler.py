@@ -94,6 +94,7 @@ PROTOTYPES = {
     "mxs_mask_host": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_uint64)]),
     "mxs_mask_upload": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_vp)]),
     "mxs_sync": (ctypes.c_int, [_vp]),
+    "mxs_export_candidates": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _vp]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
     "mxs_debug_floor": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                        ctypes.c_uint32, _vp, _vp]),
@@ -479,6 +480,21 @@ class Sampler:
                                       st.data_ptr())
         self._check(rc, "mxs_spec_verify")
         return out, cnt, acc, st
+
+    def export_candidates(self, rows: int, width: int):
+        """Queues mxs_export_candidates for the first `rows` rows of the last
+        pick on this context: returns device tensors (count i32[rows], ids
+        i32[rows, width], logits f32[rows, width]); count -1 marks a row with
+        no candidate list, otherwise the first count entries are the row's
+        candidates (its top `width` when it had more) in token-ID order."""
+        torch = self.torch
+        dev = torch.device("cuda", self.device)
+        count = torch.empty(rows, dtype=torch.int32, device=dev)
+        ids = torch.empty((rows, width), dtype=torch.int32, device=dev)
+        logits = torch.empty((rows, width), dtype=torch.float32, device=dev)
+        self._check(self.lib.mxs_export_candidates(self.ctx, rows, width, count.data_ptr(), ids.data_ptr(),
+                                                   logits.data_ptr()), "mxs_export_candidates")
+        return count, ids, logits
 
     def spec_launcher(self, target, draft, draft_tokens, temperature, accept_uniform, resample_uniform,
                       bonus_uniform):

@@ -126,3 +126,22 @@ def compare(b, gpu, ref, *, allow_uncertified=0, check_kept=True, rel=1e-5):
         if abs(g - e) > rel * max(abs(e), 1e-300) and abs(g - e) > 1e-12:
             problems.append(f"row {r}: logprob gpu {g!r} ref {e!r}")
     assert not problems, "\n".join(problems[:20])
+
+
+def settle_from_candidates(orc, b, r, ids, logits):
+    """The host settle of row r from its exported candidates
+    (mxs_export_candidates), as pick_from_candidates does for a top-k rule
+    (crates/app/cli/src/chat_generation.rs:2088-2131): the row's rule (T,
+    top_k, top_p, min_p and its uniform) applied by the oracle to the list
+    alone, every other token at f32::MIN (weight 0, below any head); the
+    list's logits already carry the penalties, bias and mask."""
+    from metallix_amd.synth import Batch
+
+    x = np.full(b.vocab, np.finfo(np.float32).min, dtype=np.float32)
+    x[np.asarray(ids, dtype=np.int64)] = np.asarray(logits, dtype=np.float32)
+    pick = lambda a, dflt: (np.asarray(a)[r:r + 1] if a is not None else dflt)
+    one = Batch(name="settle", logits=x[None, :], temperature=b.temperature[r:r + 1],
+                uniform=b.uniform[r:r + 1], top_k=pick(b.top_k, np.zeros(1, np.uint32)),
+                top_p=pick(b.top_p, np.ones(1)), min_p=pick(b.min_p, np.zeros(1)),
+                tokenizer_vocab=b.tokenizer_vocab)
+    return int(orc.sample_batch(one)["token"][0])

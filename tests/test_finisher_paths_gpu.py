@@ -176,3 +176,44 @@ def test_path_rows_small_batch(torch_mod, sampler, orc):
     compare(b, gpu, ref, allow_uncertified=2)
     unc = [names[r] for r in np.nonzero(gpu["status"] == 1)[0]]
     assert set(unc) <= {"LARGE", "EXACT_REPLAY"}, unc
+
+
+def test_settle_uncertified_rows_from_exported_candidates(torch_mod, sampler, orc):
+    """Candidate export (mxs_export_candidates; the reference's
+    wait_with_candidates and pick_from_candidates, picks.rs:429-466,
+    chat_generation.rs:2088-2131).  After the small-batch pick of the path
+    rows, every status-1 row is a top-k row whose exported list settles on
+    the host to the oracle's token without reading the row back; every
+    certified top-k row's list settles to the device's token; the greedy,
+    keep-all and error rows have no list (-1)."""
+    from helpers import settle_from_candidates
+
+    torch = torch_mod
+    names, b = path_batch()
+    say(f"case export-candidates: rows {b.rows} vocab {b.vocab}")
+    gpu = run_gpu(torch, sampler, b, debug=False)
+    ref = orc.sample_batch(b)
+    W = 2048
+    cnt, ids, lg = sampler.export_candidates(b.rows, W)
+    torch.cuda.synchronize()
+    cnt, ids, lg = cnt.cpu().numpy(), ids.cpu().numpy(), lg.cpu().numpy()
+    unc = [r for r in range(b.rows) if gpu["status"][r] == 1]
+    assert unc, "the path rows in the small-batch layout leave the replay row uncertified"
+    settled = []
+    for r in range(b.rows):
+        if names[r] in ("ERROR", "GREEDY", "KEEPALL"):
+            assert cnt[r] == -1, (names[r], cnt[r])
+            continue
+        k = int(b.top_k[r])
+        if not 0 < k <= W:
+            assert gpu["status"][r] != 1, f"uncertified row {names[r]} is not a top-k row the export settles"
+            continue
+        assert k <= cnt[r] <= W, (names[r], cnt[r])
+        n = int(cnt[r])
+        assert np.all(np.diff(ids[r, :n]) > 0), "token-ID order"
+        tok = settle_from_candidates(orc, b, r, ids[r, :n], lg[r, :n])
+        assert tok == ref["token"][r], (names[r], tok, ref["token"][r])
+        if gpu["status"][r] == 0:
+            assert tok == gpu["token"][r], (names[r], tok, gpu["token"][r])
+        settled.append(names[r])
+    assert all(names[r] in settled for r in unc), (unc, settled)
