@@ -279,6 +279,9 @@ def main():
     ap.add_argument("--stream-floor", action="store_true",
                     help="also time mxs_sample's launch floor and stream floor (its grid, workgroup size and LDS; "
                          "configs 1-4) and account for one call's time from the workgroups' entry and exit stamps")
+    ap.add_argument("--lmhead", action="store_true",
+                    help="also time the lm_head GEMM + mxs_sample against the GEMM with tile statistics + "
+                         "mxs_finish_tiles (config 2)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 256 MiB device copies (scales the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
@@ -361,6 +364,8 @@ def main():
     if args.receipts and cfg == 2:
         res["engine_step"] = step_bench(torch, s, stream, data, args.steps, args.warmup,
                                         None if args.no_cpu else args.cpu_seconds)
+    if args.lmhead and cfg == 2:
+        res["lmhead"] = lmhead_bench(torch, s, stream, args.steps, args.warmup)
     if args.stream_floor and cfg in (1, 2, 3, 4):
         res["floors"] = floor_bench(torch, s, stream, data, args.steps, args.warmup)
     res["cpu_baseline"] = None if args.no_cpu else cpu_baseline(cfg, data, args.cpu_seconds)
@@ -603,6 +608,87 @@ def mask_bench(torch, s, stream, b, steps, warmup):
     mbytes = b.rows * hs.value * 4
     return {"ms_per_step": round(ms, 6), "rows_per_s": round(b.rows / (ms / 1e3), 1),
             "upload_bytes_per_step": mbytes, "upload_gbs": round(mbytes / (ms / 1e3) / 1e9, 2)}
+
+
+def lmhead_bench(torch, s, stream, steps, warmup):
+    """The lm_head epilogue fusion on a Qwen3-0.6B-shaped head (hidden 1024,
+    V 151936, 64 rows; bf16 hidden states and weights, seeded, the 311 MB of
+    weights larger than the 256 MB Infinity Cache so every GEMM streams them
+    from HBM): the GEMM writing f32 logits, then mxs_sample over them, beside
+    the GEMM whose epilogue also writes tile statistics, then
+    mxs_finish_tiles.  Rules: config 2's mix with its k = 0 (whole-row
+    nucleus) rows made greedy, since the finish-only pick serves greedy and
+    top-k rows: T U[0.3, 1.5], top_k in {20, 50, 1000}, top_p U[0.5, 1),
+    min_p 0.05 on a quarter of the rows, one seeded uniform per row.  Time
+    per step and per call, back to back, from events on the stream."""
+    import numpy as np
+
+    R, K, V = 64, 1024, 151936
+    g = torch.Generator(device="cuda").manual_seed(20261202)
+    with torch.cuda.stream(stream):
+        w = (torch.randn((V, K), generator=g, device="cuda") * (2.0 / K ** 0.5)).to(torch.bfloat16)
+        h = torch.randn((R, K), generator=g, device="cuda").to(torch.bfloat16)
+        logits = torch.empty((R, V), dtype=torch.float32, device="cuda")
+        stats = torch.empty((R, ((V + 255) // 256) * 16), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(20261202)
+    T = rng.uniform(0.3, 1.5, R)
+    kk = np.array([(0, 20, 50, 1000)[i % 4] for i in range(R)], dtype=np.uint32)
+    T[kk == 0] = 0.0
+    D = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    rule = dict(top_k=D(kk.view(np.int32)), top_p=D(rng.uniform(0.5, 1.0, R)),
+                min_p=D(np.where(np.arange(R) % 4 == 1, 0.05, 0.0)), uniform=D(rng.random(R)))
+    gemm = s.lmhead_launcher(h, w, logits)
+    gemm_st = s.lmhead_launcher(h, w, logits, stats)
+    with torch.cuda.stream(stream):
+        gemm_st()
+        fin = s.finish_launcher(logits, stats, D(T), **rule)
+        samp = s.launcher(logits, temperature=D(T), **rule)
+    torch.cuda.synchronize()
+
+    def timed(fns):
+        with torch.cuda.stream(stream):
+            for _ in range(warmup):
+                for f in fns:
+                    f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(steps):
+                for f in fns:
+                    f()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    sample_path = timed([gemm, lambda: samp(logits)])
+    t_sample = samp.out.token.cpu().numpy().copy()
+    s_sample = samp.out.status.cpu().numpy().copy()
+    fused_path = timed([gemm_st, fin])
+    t_fin, s_fin = fin.out.token.cpu().numpy(), fin.out.status.cpu().numpy()
+    assert (s_fin >= 0).all() and (s_sample >= 0).all(), (s_fin, s_sample)
+    both = (s_fin == 0) & (s_sample == 0)
+    assert (t_fin[both] == t_sample[both]).all(), "the two paths picked different tokens"
+    ms = {"gemm": timed([gemm]), "gemm_stats": timed([gemm_st]), "mxs_sample": timed([lambda: samp(logits)]),
+          "mxs_finish_tiles": timed([fin])}
+    gemm_bytes = V * K * 2 + R * K * 2 + R * V * 4
+    stat_bytes = stats.numel()
+    gbs = gemm_bytes / (ms["gemm"] / 1e3) / 1e9
+    return {
+        "workload": f"lm_head bf16 [{R} x {K}] x [{V} x {K}]^T -> f32 logits, then the pick",
+        "gemm_plus_sample_ms": round(sample_path, 6),
+        "gemm_plus_finish_ms": round(fused_path, 6),
+        "rows_per_s_sample_path": round(R / (sample_path / 1e3), 1),
+        "rows_per_s_fused_path": round(R / (fused_path / 1e3), 1),
+        "call_ms": {k: round(v, 6) for k, v in ms.items()},
+        "gemm_algorithmic_bytes": gemm_bytes,
+        "gemm_achieved_gbs": round(gbs, 1),
+        "gemm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "tile_stat_bytes": stat_bytes,
+        "uncertified_rows": {"sample": int((s_sample == 1).sum()), "finish": int((s_fin == 1).sum())},
+        "same_tokens_rows": int(both.sum()),
+    }
 
 
 def race_bench(torch, s, stream, b, steps, warmup):

@@ -37,6 +37,11 @@
  *   mxs_export_candidates     <- Qwen3TokenPicks::wait_with_candidates (picks.rs:429-466), the
  *                                candidates TurnLoop::settle_row hands pick_from_candidates
  *                                (chat_turn.rs:332-358; chat_generation.rs:2088-2131).
+ *   mxs_lmhead_bf16,          <- the lm_head that feeds Qwen3TokenPicks::start_with in
+ *   mxs_finish_tiles             Qwen3ForwardExecutor::append_picks (crates/models/qwen/src/
+ *                                forward.rs:1745-1761), with the pick fused into its epilogue:
+ *                                the GEMM's tiles publish mxs_epilogue.h statistics and the
+ *                                finish-only pick reads those and the tiles a head can reach.
  *   mxs_sync                  <- Qwen3TokenPicks::wait (picks.rs:390-401).
  *   mxs_last_error            <- KernelError's message (mlx-kernels/src/lib.rs:444-450).
  *
@@ -90,7 +95,8 @@ enum {
   MXS_ROW_INVALID_HISTORY = -11,
   MXS_ROW_INVALID_BIAS = -12,
   MXS_ROW_TOKEN_OUT_OF_RANGE = -13,
-  MXS_ROW_PROBABILITIES = -14
+  MXS_ROW_PROBABILITIES = -14,
+  MXS_ROW_UNSUPPORTED_RULE = -15  /* mxs_finish_tiles: a rule other than greedy or top-k <= 4096 */
 };
 
 typedef enum { MXS_F32 = 0, MXS_BF16 = 1 } mxs_dtype;
@@ -245,6 +251,27 @@ int mxs_step(mxs_ctx* ctx, const mxs_batch* batch, const mxs_race* race, const m
  * pick on the context overwrites the lists. */
 int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* count, int32_t* ids,
                           float* logits);
+/* A bf16 lm_head for gfx950: logits[n][v] = sum_k hidden[n][k] weight[v][k]
+ * (f32 accumulate), hidden rows x hidden_dim, weight vocab x hidden_dim, both
+ * row-major bf16 and 16-byte aligned; rows <= 64, hidden_dim a multiple of
+ * 32, vocab a multiple of 4; logits f32 rows x logits_stride.  When
+ * tile_stats is non-null, the epilogue also writes, per (row, 256-token
+ * tile), the statistics mxs_finish_tiles reads (16 bytes each, rows x
+ * ceil(vocab / 256); the layout is mxs::EpiTileStat of
+ * metallix_amd/csrc/mxs_epilogue.h, whose device functions any producer's
+ * epilogue can call). */
+int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* weight, uint32_t rows, uint32_t hidden_dim,
+                    uint32_t vocab, float* logits, uint64_t logits_stride, void* tile_stats);
+/* The pick of mxs_sample from a producer's tile statistics: batch->logits
+ * (f32) are the producer's logits, of which only the tiles a row's top-k
+ * head can reach are read; the rows' rules are greedy (temperature 0) or
+ * top-k with 1 <= top_k <= 4096 (with top_p, min_p and the uniform as in
+ * mxs_sample); no penalties, bias or mask (the reference's device picks
+ * take none, picks.rs:273-381); a row with another rule reports
+ * MXS_ROW_UNSUPPORTED_RULE.  vocab <= 262144.  Outputs as mxs_sample's
+ * (adjusted must be NULL); results are identical to mxs_sample's on the
+ * same logits. */
+int mxs_finish_tiles(mxs_ctx* ctx, const mxs_batch* batch, const void* tile_stats, const mxs_out* out);
 int mxs_mask_host(mxs_ctx* ctx, uint32_t slot, uint32_t** words, uint64_t* stride_words);
 int mxs_mask_upload(mxs_ctx* ctx, uint32_t slot, uint32_t rows, const uint32_t** device_words);
 int mxs_sync(mxs_ctx* ctx);

@@ -1,0 +1,136 @@
+// mx_lmhead.hip -- a bf16 lm_head GEMM for gfx950 (mxs_lmhead_bf16): the
+// logits producer whose epilogue writes the tile statistics of
+// mxs_epilogue.h for mxs_finish_tiles.
+//
+// logits[n][v] = sum_k hidden[n][k] weight[v][k] (bf16 in, f32 accumulate),
+// the lm_head of a Qwen3-shaped forward (the reference computes it in MLX
+// before its picks, crates/models/qwen/src/forward.rs:1745-1761).  One
+// 256-thread workgroup per 256-row vocabulary tile; wave w owns the tile's
+// vocabulary rows 64 w .. 64 w + 63 against every batch row (at most 64), as
+// 4 x 4 blocks of v_mfma_f32_16x16x32_bf16 (A: 16 vocabulary rows x 32 k, B:
+// 32 k x 16 batch rows; lane l holds row l % 16 and k (l / 16) 8 .. + 7 of
+// each, 16 contiguous bytes; D: lane l holds vocabulary rows (l / 16) 4 + j
+// of batch row l % 16).  The weights stream from HBM once (the roofline:
+// V K 2 bytes); the hidden states are re-read from L2 by every wave.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mx_sampler.h"
+#include "mxs_ctx.h"
+#include "mxs_device.h"
+#include "mxs_epilogue.h"
+
+namespace mxs {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t LM_ROWS = 64;   // batch rows per launch (four 16-row MFMA blocks)
+
+template <bool STATS>
+__global__ __launch_bounds__(256) void lmhead_kernel(const __bf16* __restrict__ H, const __bf16* __restrict__ W,
+                                                     uint32_t rows, uint32_t K, uint32_t V,
+                                                     float* __restrict__ logits, uint64_t ld,
+                                                     EpiTileStat* __restrict__ stats, uint32_t ntiles) {
+  __shared__ EpiPartial part[4][LM_ROWS];
+  const uint32_t tile = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63u;
+  const uint32_t lr = l & 15u, lg = l >> 4;
+  const uint32_t vw = tile * EPI_TILE + w * 64u;   // this wave's first vocabulary row
+  // operand rows, clamped in range (the clamped rows' results are dropped)
+  const __bf16* ap[4];
+  const __bf16* bp[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const uint32_t v = min(vw + (uint32_t)mb * 16u + lr, V - 1u);
+    ap[mb] = W + (uint64_t)v * K + lg * 8u;
+  }
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const uint32_t n = min((uint32_t)nb * 16u + lr, rows - 1u);
+    bp[nb] = H + (uint64_t)n * K + lg * 8u;
+  }
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 2
+  for (uint32_t k0 = 0; k0 < K; k0 += 32u) {
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) a[mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k0);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) b[nb] = *reinterpret_cast<const bf16x8*>(bp[nb] + k0);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+  }
+  // acc[mb][nb][j]: token vw + 16 mb + 4 lg + j of batch row 16 nb + lr
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const uint32_t n = (uint32_t)nb * 16u + lr;
+    EpiPartial p = epi_empty();
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const uint32_t v0 = vw + (uint32_t)mb * 16u + lg * 4u;
+      if (v0 < V) {   // V % 4 == 0: the quad is in range
+        if (n < rows) *reinterpret_cast<f32x4*>(logits + (uint64_t)n * ld + v0) = acc[mb][nb];
+        if (STATS) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) epi_add(p, acc[mb][nb][j], v0 + (uint32_t)j);
+        }
+      }
+    }
+    if (STATS) {
+      epi_xor(p, 16);
+      epi_xor(p, 32);
+      if (lg == 0u) part[w][n] = p;
+    }
+  }
+  if (STATS) {
+    __syncthreads();
+    if (threadIdx.x < rows) {
+      const uint32_t n = threadIdx.x;
+      EpiPartial p = part[0][n];
+#pragma unroll
+      for (int q = 1; q < 4; ++q) epi_merge(p, part[q][n]);
+      epi_store(&stats[(uint64_t)n * ntiles + tile], p);
+    }
+  }
+}
+
+}  // namespace mxs
+
+extern "C" int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* weight, uint32_t rows,
+                               uint32_t hidden_dim, uint32_t vocab, float* logits, uint64_t logits_stride,
+                               void* tile_stats) {
+  using namespace mxs;
+  if (!ctx) return MXS_EINVAL;
+  if (rows == 0) return MXS_OK;
+  if (!hidden || !weight || !logits) return fail(ctx, MXS_EINVAL, "hidden, weight and logits are required");
+  if (rows > LM_ROWS) return fail(ctx, MXS_EINVAL, "rows must be at most 64");
+  if (hidden_dim == 0 || hidden_dim % 32u) return fail(ctx, MXS_EINVAL, "hidden_dim must be a positive multiple of 32");
+  if (vocab == 0 || vocab % 4u) return fail(ctx, MXS_EINVAL, "vocab must be a positive multiple of 4");
+  if (logits_stride < vocab || logits_stride % 4u) return fail(ctx, MXS_EINVAL, "logits_stride must be >= vocab and a multiple of 4");
+  if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)logits) % 16u)
+    return fail(ctx, MXS_EINVAL, "hidden, weight and logits must be 16-byte aligned");
+  const uint32_t ntiles = (vocab + EPI_TILE - 1u) / EPI_TILE;
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  const __bf16* H = reinterpret_cast<const __bf16*>(hidden);
+  const __bf16* W = reinterpret_cast<const __bf16*>(weight);
+  EpiTileStat* S = reinterpret_cast<EpiTileStat*>(tile_stats);
+  if (S)
+    hipLaunchKernelGGL(lmhead_kernel<true>, dim3(ntiles), dim3(256), 0, ctx->stream, H, W, rows, hidden_dim, vocab,
+                       logits, logits_stride, S, ntiles);
+  else
+    hipLaunchKernelGGL(lmhead_kernel<false>, dim3(ntiles), dim3(256), 0, ctx->stream, H, W, rows, hidden_dim, vocab,
+                       logits, logits_stride, S, ntiles);
+  hipError_t e = hipGetLastError();
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "lmhead_kernel launch");
+  return MXS_OK;
+}

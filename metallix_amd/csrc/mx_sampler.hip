@@ -37,6 +37,7 @@
 #include "../../include/mx_sampler.h"
 #include "mxs_ctx.h"
 #include "mxs_device.h"
+#include "mxs_epilogue.h"
 #include "mxs_math.h"
 
 namespace mxs {
@@ -5649,11 +5650,225 @@ __global__ __launch_bounds__(NT) void cand_export_kernel(Work w, uint32_t C, uin
   if (tid == 0) count[row] = (int32_t)min(base, width);
 }
 
+// ---------------------------------------------------------------------------
+// Finish-only pick over a logits producer's tile statistics
+// (mxs_finish_tiles; the producer's epilogue wrote them with mxs_epilogue.h):
+// one workgroup per row builds the one-chunk statistics and candidate list
+// the row finisher takes, reading the logits of only the tiles a top-k head
+// can reach, then runs finish_row as the sample kernel's last chunk does.
+//   - greedy: the argmax is the largest tile gkey (ties: lowest token);
+//   - top-k: kappa = the k-th largest tile maximum (order keys).  A tile
+//     holding a member of the head has its maximum at or above the head's
+//     k-th value, which is at least kappa (the k largest tile maxima are k
+//     distinct tokens' values), so the tokens at or above kappa of the tiles
+//     whose maximum reaches kappa hold the head and every tie at its edge.
+//     kappa is the candidate threshold, as a chunk's is in the sample kernel.
+__global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const EpiTileStat* __restrict__ ts,
+                                                         uint32_t ntiles, const double* __restrict__ p_temperature,
+                                                         const uint32_t* __restrict__ p_top_k,
+                                                         const double* __restrict__ p_top_p,
+                                                         const double* __restrict__ p_min_p,
+                                                         const double* __restrict__ p_uniform,
+                                                         const float* __restrict__ p_one, const float* __restrict__ p_zero,
+                                                         const uint32_t* __restrict__ p_zero_u) {
+  __shared__ __align__(16) FusedSmem U;
+  const mxs_batch& b = A.b;
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
+  const uint32_t V = b.vocab;
+  const RowCfg c = load_cfg(p_temperature, p_top_k, p_top_p, p_min_p, p_one, p_zero, p_zero, p_uniform, p_zero_u,
+                            p_zero_u, row);
+  const uint32_t mode = chunk_mode(c, V);
+  if (!c.err && mode != M_GREEDY && mode != M_TOPK) {
+    if (tid == 0) {
+      A.o.token[row] = -1;
+      A.o.status[row] = MXS_ROW_UNSUPPORTED_RULE;
+      if (A.o.sampling_logprob) A.o.sampling_logprob[row] = 0.0;
+      if (A.o.kept_count) A.o.kept_count[row] = 0u;
+      A.w.cand_rows[row] = -1;
+    }
+    return;
+  }
+  // scratch in the finisher's LDS, before the finisher writes it
+  uint32_t* tk = reinterpret_cast<uint32_t*>(&U);   // [1024] the tiles' maxima
+  uint32_t* tl = tk + 1024;                         // [1024] candidate tiles, ascending
+  uint32_t* hist = tl + 1024;                       // [256]
+  uint32_t* red = hist + 256;                       // [NW]
+  uint32_t* su = red + NW;                          // [4]
+  unsigned long long* red64 = reinterpret_cast<unsigned long long*>(su + 4);   // [NW]
+  const EpiTileStat* rs = ts + (uint64_t)row * ntiles;
+  unsigned long long g = 0ull;
+  uint32_t tm = 0u, bad = 0u;
+  for (uint32_t t = tid; t < ntiles; t += NT) {
+    const EpiTileStat s = rs[t];
+    g = s.gkey > g ? s.gkey : g;
+    tm = max(tm, s.tmax);
+    bad |= s.bad;
+    tk[t] = s.tmax;
+  }
+  g = wave_max_u64(g);
+  if (lane() == 0) red64[wave()] = g;
+  tm = block_max<uint32_t>(tm, red);   // (its barriers order red64 too)
+  bad = block_max<uint32_t>(bad, red);
+  g = 0ull;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) g = red64[w] > g ? red64[w] : g;
+  uint32_t kappa = 0u, n = 0u;
+  const uint64_t rbase = (uint64_t)row * V;
+  if (!c.err && !bad && mode == M_TOPK) {
+    // kappa: the k-th largest tile maximum, by four 8-bit digit passes
+    const uint32_t k = min(c.k, ntiles);
+    uint32_t prefix = 0u, need = k;
+    for (int d = 3; d >= 0; --d) {
+      if (tid < 256u) hist[tid] = 0u;
+      __syncthreads();
+      const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
+      if (tid < ntiles && (tk[tid] & pm) == prefix) atomicAdd(&hist[(tk[tid] >> (8 * d)) & 255u], 1u);
+      __syncthreads();
+      if (wave() == 0) {   // lane l: bins 255 - 4l .. 252 - 4l, from the top
+        uint32_t hb[4], hs = 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { hb[i] = hist[255u - 4u * lane() - (uint32_t)i]; hs += hb[i]; }
+        const uint32_t inc = wave_scan_u32(hs);
+        const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+        const uint32_t L = (uint32_t)__builtin_ctzll(reach);   // need <= the matching count: some lane reaches it
+        if (lane() == L) {
+          uint32_t cum = inc - hs;
+          uint32_t bin = 252u - 4u * L;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if (cum + hb[i] >= need) { bin = 255u - 4u * L - (uint32_t)i; break; }
+            cum += hb[i];
+          }
+          su[0] = bin;
+          su[1] = cum;
+        }
+      }
+      __syncthreads();
+      prefix |= su[0] << (8 * d);
+      need -= su[1];
+      __syncthreads();
+    }
+    kappa = prefix;
+    const float* lg = reinterpret_cast<const float*>(b.logits) + (uint64_t)row * b.row_stride;
+    for (;;) {
+      // the candidate tiles (maximum at or above kappa), in tile order
+      uint32_t m;
+      const bool ct = tid < ntiles && tk[tid] >= kappa;
+      const uint32_t at = block_scan_incl<uint32_t>(ct ? 1u : 0u, red, &m) - (ct ? 1u : 0u);
+      if (ct) tl[at] = tid;
+      __syncthreads();
+      // their tokens at or above kappa, in token-ID order
+      for (uint32_t base = 0; base < m * EPI_TILE; base += NT) {
+        const uint32_t idx = base + tid;
+        float x = 0.0f;
+        uint32_t v = 0u;
+        bool keep = false;
+        if (idx < m * EPI_TILE) {
+          v = tl[idx / EPI_TILE] * EPI_TILE + idx % EPI_TILE;
+          if (v < V) {
+            x = lg[v];
+            keep = okey(x) >= kappa;
+          }
+        }
+        uint32_t tot;
+        const uint32_t pos = n + block_scan_incl<uint32_t>(keep ? 1u : 0u, red, &tot) - (keep ? 1u : 0u);
+        if (keep) {
+          st_dev(&A.w.cand_l[rbase + pos], x);
+          st_dev(&A.w.cand_id[rbase + pos], v);
+        }
+        n += tot;
+      }
+      // With k above the tile count the bound holds only when at least k
+      // tokens reach kappa; otherwise every token is a candidate (kappa 0,
+      // the smallest order key), which reads the whole row.
+      if (n >= c.k || kappa == 0u) break;
+      kappa = 0u;
+      n = 0u;
+      __syncthreads();   // tl is rewritten
+    }
+  }
+  if (tid == 0) {
+    ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC];
+    st_dev(&st->maxkey, tm);
+    st_dev(&st->gbest_id, g ? ~(uint32_t)g : NONE);
+    st_dev(&st->gbest_val, okey_value((uint32_t)(g >> 32)));
+    st_dev(&st->nlegal, V);
+    st_dev(&st->ncand, n);
+    st_dev(&st->flags, bad ? (uint32_t)F_NONFINITE : 0u);
+    st_dev(&st->minkey, 0u);
+    st_dev(&st->thr, okey_value(kappa));
+    st_dev(&st->mass, 0.0);
+    st_dev(&st->mass_err, 0.0);
+  }
+  wait_mem();
+  __syncthreads();
+  FinLoads P;
+  fin_issue(A, row, P);
+  finish_row<float>(A, U.f, c, row, mode, rbase, c.greedy ? 0.0 : 1.0 / c.T, P);
+}
+
 }  // namespace mxs
 
 extern "C" {
 
 int mxs_abi_version(void) { return MXS_ABI_VERSION; }
+
+int mxs_finish_tiles(mxs_ctx* ctx, const mxs_batch* b, const void* tile_stats, const mxs_out* o) {
+  using namespace mxs;
+  if (!ctx || !b || !o) return MXS_EINVAL;
+  if (b->rows == 0) return MXS_OK;
+  if (!b->logits || !b->temperature || !tile_stats || !o->token || !o->status)
+    return fail(ctx, MXS_EINVAL, "logits, temperature, tile_stats, token and status are required");
+  if (b->rows > ctx->max_rows || b->vocab > ctx->max_vocab) return fail(ctx, MXS_EINVAL, "batch exceeds the context's max_rows/max_vocab");
+  if (b->vocab == 0 || b->vocab > 1024u * EPI_TILE) return fail(ctx, MXS_EINVAL, "vocab must be in 1..262144");
+  if (b->dtype != MXS_F32) return fail(ctx, MXS_EINVAL, "the finish-only pick reads f32 logits");
+  if (b->row_stride < b->vocab || (b->row_stride & 3u)) return fail(ctx, MXS_EINVAL, "row_stride must be >= vocab and a multiple of 4");
+  if (((uintptr_t)b->logits) % 16u) return fail(ctx, MXS_EINVAL, "logits must be 16-byte aligned");
+  if (b->history_offsets || b->bias_offsets || b->mask_words || b->repetition || b->presence || b->frequency)
+    return fail(ctx, MXS_EINVAL, "the finish-only pick takes no penalties, bias or mask");
+  if (o->adjusted) return fail(ctx, MXS_EINVAL, "the finish-only pick writes no adjusted logits");
+  SampleArgs A;
+  A.b = *b;
+  A.o = *o;
+  A.w = ctx->work;
+  A.timing = nullptr;
+  A.paths = ctx->paths;
+  if (++ctx->epoch == 0u) ctx->epoch = 1u;
+  A.epoch = ctx->epoch;
+  A.nodraw = 0u;
+  A.masked = 0u;
+  A.rx_want = nullptr;
+  A.b.mask_words = ctx->d_mask_ones;
+  A.b.mask_stride = 0;
+  A.b.tokenizer_vocab = b->vocab;
+  A.b.history_offsets = ctx->d_zero_u32;
+  A.b.history_ids = ctx->d_zero_u32;
+  A.b.bias_offsets = ctx->d_zero_u32;
+  A.b.bias_ids = ctx->d_zero_u32;
+  A.b.bias_values = ctx->d_zero_f32;
+  A.C = 1u;
+  A.CH = b->vocab;
+  A.per = 1u;
+  const uint32_t ntiles = (b->vocab + EPI_TILE - 1u) / EPI_TILE;
+  int prev = 0;
+  hipGetDevice(&prev);
+  if (prev != ctx->device) hipSetDevice(ctx->device);
+  hipLaunchKernelGGL(tile_finish_kernel, dim3(b->rows), dim3(NT), 0, ctx->stream, A,
+                     reinterpret_cast<const EpiTileStat*>(tile_stats), ntiles, b->temperature,
+                     b->top_k ? b->top_k : ctx->d_zero_u32, b->top_p ? b->top_p : ctx->d_one_f64,
+                     b->min_p ? b->min_p : ctx->d_zero_f64, b->uniform ? b->uniform : ctx->d_zero_f64,
+                     ctx->d_one_f32, ctx->d_zero_f32, ctx->d_zero_u32);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) {
+    ctx->last_rows = b->rows;
+    ctx->last_C = 1u;
+    ctx->last_CH = b->vocab;
+    ctx->last_V = b->vocab;
+  }
+  if (prev != ctx->device) hipSetDevice(prev);
+  if (e != hipSuccess) return hip_fail(ctx, e, "tile_finish_kernel launch");
+  return MXS_OK;
+}
 
 int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* count, int32_t* ids,
                           float* logits) {
@@ -5693,6 +5908,7 @@ const char* mxs_status_string(int32_t s) {
     case MXS_ROW_INVALID_BIAS: return "logit bias IDs must be strictly increasing, below the vocabulary, with finite values (or -inf: suppressed)";
     case MXS_ROW_TOKEN_OUT_OF_RANGE: return "drafted token outside the vocabulary";
     case MXS_ROW_PROBABILITIES: return "invalid probability vectors";
+    case MXS_ROW_UNSUPPORTED_RULE: return "the finish-only pick serves greedy and top-k (k <= 4096) rows";
     default: return "unknown status";
   }
 }

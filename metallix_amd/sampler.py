@@ -95,6 +95,9 @@ PROTOTYPES = {
     "mxs_mask_upload": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_vp)]),
     "mxs_sync": (ctypes.c_int, [_vp]),
     "mxs_export_candidates": (ctypes.c_int, [_vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _vp, _vp]),
+    "mxs_lmhead_bf16": (ctypes.c_int, [_vp, _vp, _vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _vp,
+                                       ctypes.c_uint64, _vp]),
+    "mxs_finish_tiles": (ctypes.c_int, [_vp, ctypes.POINTER(MxsBatch), _vp, ctypes.POINTER(MxsOut)]),
     "mxs_debug_set_timing": (ctypes.c_int, [_vp, _vp]),
     "mxs_debug_floor": (ctypes.c_int, [_vp, _vp, ctypes.c_int32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                        ctypes.c_uint32, _vp, _vp]),
@@ -270,6 +273,76 @@ class Sampler:
         self._check(self.lib.mxs_sample(self.ctx, ctypes.byref(b), ctypes.byref(o)), "mxs_sample")
         self._keep = (b, o)
         return out
+
+    def lmhead(self, hidden, weight, *, stats: bool = False, logits=None):
+        """Queues the bf16 lm_head GEMM (mxs_lmhead_bf16): hidden bf16[rows,
+        hidden_dim], weight bf16[vocab, hidden_dim] on the device; returns
+        (logits f32[rows, vocab], tile statistics u8[rows, ceil(vocab/256)
+        * 16] or None).  With stats the epilogue also writes the statistics
+        finish_tiles reads."""
+        torch = self.torch
+        rows, K = hidden.shape
+        V = weight.shape[0]
+        dev = hidden.device
+        with torch.cuda.stream(self.stream):
+            if logits is None:
+                logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
+            st = torch.empty((rows, ((V + 255) // 256) * 16), dtype=torch.uint8, device=dev) if stats else None
+        self._check(self.lib.mxs_lmhead_bf16(self.ctx, hidden.data_ptr(), weight.data_ptr(), rows, K, V,
+                                             logits.data_ptr(), logits.stride(0), _ptr(st)), "mxs_lmhead_bf16")
+        return logits, st
+
+    def finish_tiles(self, logits, tile_stats, temperature, *, top_k=None, top_p=None, min_p=None, uniform=None,
+                     debug: bool = False, out: Optional[SampleResult] = None) -> SampleResult:
+        """Queues the finish-only pick (mxs_finish_tiles) over the lm_head's
+        logits and tile statistics: greedy and top-k rows, as `sample`
+        picks them (no penalties, bias or mask)."""
+        rows, V = logits.shape
+        need = rows * ((V + 255) // 256) * 16
+        if tile_stats.device != logits.device or tile_stats.numel() * tile_stats.element_size() < need:
+            raise ValueError(f"tile_stats must hold {need} bytes on the logits' device")
+        b, o, _, out = self._structs(logits, temperature, top_k=top_k, top_p=top_p, min_p=min_p, uniform=uniform,
+                                     debug=debug, out=out)
+        o.adjusted = None
+        out.adjusted = None
+        self._check(self.lib.mxs_finish_tiles(self.ctx, ctypes.byref(b), tile_stats.data_ptr(), ctypes.byref(o)),
+                    "mxs_finish_tiles")
+        self._keep = (b, o)
+        return out
+
+    def lmhead_launcher(self, hidden, weight, logits, tile_stats=None):
+        """Pre-built lmhead for repeated calls into the same logits (and tile
+        statistics): returns f() that re-issues mxs_lmhead_bf16."""
+        rows, K = hidden.shape
+        V = weight.shape[0]
+        fn = self.lib.mxs_lmhead_bf16
+        args = (self.ctx, hidden.data_ptr(), weight.data_ptr(), rows, K, V, logits.data_ptr(), logits.stride(0),
+                _ptr(tile_stats))
+
+        def launch():
+            rc = fn(*args)
+            if rc != 0:
+                self._check(rc, "mxs_lmhead_bf16")
+
+        return launch
+
+    def finish_launcher(self, logits, tile_stats, temperature, **rule):
+        """Pre-built finish_tiles for repeated calls over the same logits and
+        tile statistics with the same rules and outputs: returns f() that
+        re-issues mxs_finish_tiles (f.out holds the outputs)."""
+        out = self.finish_tiles(logits, tile_stats, temperature, **rule)
+        b, o = self._keep
+        bp, op, sp = ctypes.byref(b), ctypes.byref(o), tile_stats.data_ptr()
+        fn, ctx = self.lib.mxs_finish_tiles, self.ctx
+
+        def launch():
+            rc = fn(ctx, bp, sp, op)
+            if rc != 0:
+                self._check(rc, "mxs_finish_tiles")
+
+        launch.out = out
+        launch.keep = (b, o)
+        return launch
 
     def step(self, logits, temperature, *, receipt_top=None, n: int = 28, race=None, **kw):
         """Queues one engine step (mxs_step): every row's pick as `sample`
