@@ -616,11 +616,12 @@ def lmhead_bench(torch, s, stream, steps, warmup):
     weights larger than the 256 MB Infinity Cache so every GEMM streams them
     from HBM): the GEMM writing f32 logits, then mxs_sample over them, beside
     the GEMM whose epilogue also writes tile statistics, then
-    mxs_finish_tiles.  Rules: config 2's mix with its k = 0 (whole-row
-    nucleus) rows made greedy, since the finish-only pick serves greedy and
-    top-k rows: T U[0.3, 1.5], top_k in {20, 50, 1000}, top_p U[0.5, 1),
-    min_p 0.05 on a quarter of the rows, one seeded uniform per row.  Time
-    per step and per call, back to back, from events on the stream."""
+    mxs_finish_tiles.  Rules: the greedy and top-k rows the finish-only
+    pick serves, with a head small enough that the tile maxima prune the
+    read (a quarter greedy, the rest top_k in {20, 50, 100} at T U[0.3,
+    1.5], top_p U[0.5, 1), min_p 0.05 on a quarter of the rows), one seeded
+    uniform per row.  Time per step and per call, back to back, from events
+    on the stream."""
     import numpy as np
 
     R, K, V = 64, 1024, 151936
@@ -633,7 +634,7 @@ def lmhead_bench(torch, s, stream, steps, warmup):
     torch.cuda.synchronize()
     rng = np.random.default_rng(20261202)
     T = rng.uniform(0.3, 1.5, R)
-    kk = np.array([(0, 20, 50, 1000)[i % 4] for i in range(R)], dtype=np.uint32)
+    kk = np.array([(0, 20, 50, 100)[i % 4] for i in range(R)], dtype=np.uint32)
     T[kk == 0] = 0.0
     D = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
     rule = dict(top_k=D(kk.view(np.int32)), top_p=D(rng.uniform(0.5, 1.0, R)),

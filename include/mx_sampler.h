@@ -254,7 +254,7 @@ int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* 
 /* A bf16 lm_head for gfx950: logits[n][v] = sum_k hidden[n][k] weight[v][k]
  * (f32 accumulate), hidden rows x hidden_dim, weight vocab x hidden_dim, both
  * row-major bf16 and 16-byte aligned; rows <= 64, hidden_dim a multiple of
- * 32, vocab a multiple of 4; logits f32 rows x logits_stride.  When
+ * 128, vocab a multiple of 4; logits f32 rows x logits_stride.  When
  * tile_stats is non-null, the epilogue also writes, per (row, 256-token
  * tile), the statistics mxs_finish_tiles reads (16 bytes each, rows x
  * ceil(vocab / 256); the layout is mxs::EpiTileStat of
@@ -270,7 +270,11 @@ int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* weight, uint32
  * take none, picks.rs:273-381); a row with another rule reports
  * MXS_ROW_UNSUPPORTED_RULE.  vocab <= 262144.  Outputs as mxs_sample's
  * (adjusted must be NULL); results are identical to mxs_sample's on the
- * same logits. */
+ * same logits.  One workgroup per row reads the tiles whose maximum reaches
+ * the k-th largest tile maximum, so the read shrinks with k / tile count:
+ * greedy and small-k rows (k up to about 128 at vocab 151936) finish faster
+ * than mxs_sample; a row with k above the tile count reads its row twice in
+ * one workgroup, slower than mxs_sample's chunked read. */
 int mxs_finish_tiles(mxs_ctx* ctx, const mxs_batch* batch, const void* tile_stats, const mxs_out* out);
 int mxs_mask_host(mxs_ctx* ctx, uint32_t slot, uint32_t** words, uint64_t* stride_words);
 int mxs_mask_upload(mxs_ctx* ctx, uint32_t slot, uint32_t rows, const uint32_t** device_words);

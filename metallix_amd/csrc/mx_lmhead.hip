@@ -26,6 +26,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t LM_ROWS = 64;   // batch rows per launch (four 16-row MFMA blocks)
+constexpr uint32_t LM_KC = 128;    // hidden-state k staged in LDS per chunk
+constexpr uint32_t LM_BST = LM_KC + 8u;   // LDS row stride (bf16): rows 16 B apart in the banks
 
 template <bool STATS>
 __global__ __launch_bounds__(256) void lmhead_kernel(const __bf16* __restrict__ H, const __bf16* __restrict__ W,
@@ -33,39 +35,72 @@ __global__ __launch_bounds__(256) void lmhead_kernel(const __bf16* __restrict__ 
                                                      float* __restrict__ logits, uint64_t ld,
                                                      EpiTileStat* __restrict__ stats, uint32_t ntiles) {
   __shared__ EpiPartial part[4][LM_ROWS];
+  __shared__ __align__(16) __bf16 Bs[2][LM_ROWS * LM_BST];   // staged hidden-state chunks
   const uint32_t tile = blockIdx.x, w = threadIdx.x >> 6, l = threadIdx.x & 63u;
   const uint32_t lr = l & 15u, lg = l >> 4;
   const uint32_t vw = tile * EPI_TILE + w * 64u;   // this wave's first vocabulary row
-  // operand rows, clamped in range (the clamped rows' results are dropped)
+  // weight rows, clamped in range (the clamped rows' results are dropped)
   const __bf16* ap[4];
-  const __bf16* bp[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     const uint32_t v = min(vw + (uint32_t)mb * 16u + lr, V - 1u);
     ap[mb] = W + (uint64_t)v * K + lg * 8u;
-  }
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
-    const uint32_t n = min((uint32_t)nb * 16u + lr, rows - 1u);
-    bp[nb] = H + (uint64_t)n * K + lg * 8u;
   }
   f32x4 acc[4][4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 2
-  for (uint32_t k0 = 0; k0 < K; k0 += 32u) {
-    bf16x8 a[4], b[4];
+  // The hidden states pass through LDS in chunks of LM_KC k, double
+  // buffered: thread t stages 32 k of row t / 4 (rows clamped; the clamped
+  // rows' results are dropped), once per workgroup instead of once per wave.
+  const uint32_t sn = min(threadIdx.x >> 2, rows - 1u), sk = (threadIdx.x & 3u) * 32u;
+  const __bf16* hsrc = H + (uint64_t)sn * K + sk;
+  bf16x8 st[4];
+  auto stage_load = [&](uint32_t c) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) a[mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k0);
+    for (int j = 0; j < 4; ++j) st[j] = *reinterpret_cast<const bf16x8*>(hsrc + c * LM_KC + 8u * (uint32_t)j);
+  };
+  auto stage_store = [&](uint32_t buf) {
+    __bf16* dst = &Bs[buf][(threadIdx.x >> 2) * LM_BST + sk];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) b[nb] = *reinterpret_cast<const bf16x8*>(bp[nb] + k0);
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<bf16x8*>(dst + 8u * (uint32_t)j) = st[j];
+  };
+  // The weights stream from HBM into registers two K steps ahead: step
+  // s + 2's rows load while step s's products issue.  The loads are
+  // unconditional (past the last step they repeat it, in bounds, unused) so
+  // the memory counter waits stay exact.
+  const uint32_t steps = K / 32u, nch = K / LM_KC;
+  bf16x8 a[2][4];
+  auto load_a = [&](bf16x8* d, uint32_t s) {
+    const uint32_t k0 = min(s, steps - 1u) * 32u;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < 4; ++mb) d[mb] = *reinterpret_cast<const bf16x8*>(ap[mb] + k0);
+  };
+  stage_load(0u);
+  load_a(a[0], 0u);
+  load_a(a[1], 1u);
+  stage_store(0u);
+  __syncthreads();
+  for (uint32_t c = 0; c < nch; ++c) {
+    if (c + 1u < nch) stage_load(c + 1u);
+    const __bf16* bs = &Bs[c & 1u][0];
+#pragma unroll
+    for (uint32_t ks = 0; ks < LM_KC / 32u; ++ks) {
+      bf16x8 b[4];
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
-        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mb], b[nb], acc[mb][nb], 0, 0, 0);
+        b[nb] = *reinterpret_cast<const bf16x8*>(bs + ((uint32_t)nb * 16u + lr) * LM_BST + ks * 32u + lg * 8u);
+      bf16x8* ac = a[ks & 1u];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mb], b[nb], acc[mb][nb], 0, 0, 0);
+      load_a(ac, c * (LM_KC / 32u) + ks + 2u);
+    }
+    if (c + 1u < nch) stage_store((c + 1u) & 1u);
+    __syncthreads();
   }
   // acc[mb][nb][j]: token vw + 16 mb + 4 lg + j of batch row 16 nb + lr
 #pragma unroll
@@ -111,15 +146,15 @@ extern "C" int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* wei
   if (rows == 0) return MXS_OK;
   if (!hidden || !weight || !logits) return fail(ctx, MXS_EINVAL, "hidden, weight and logits are required");
   if (rows > LM_ROWS) return fail(ctx, MXS_EINVAL, "rows must be at most 64");
-  if (hidden_dim == 0 || hidden_dim % 32u) return fail(ctx, MXS_EINVAL, "hidden_dim must be a positive multiple of 32");
+  if (hidden_dim == 0 || hidden_dim % LM_KC) return fail(ctx, MXS_EINVAL, "hidden_dim must be a positive multiple of 128");
   if (vocab == 0 || vocab % 4u) return fail(ctx, MXS_EINVAL, "vocab must be a positive multiple of 4");
   if (logits_stride < vocab || logits_stride % 4u) return fail(ctx, MXS_EINVAL, "logits_stride must be >= vocab and a multiple of 4");
   if (((uintptr_t)hidden | (uintptr_t)weight | (uintptr_t)logits) % 16u)
     return fail(ctx, MXS_EINVAL, "hidden, weight and logits must be 16-byte aligned");
   const uint32_t ntiles = (vocab + EPI_TILE - 1u) / EPI_TILE;
   int prev = 0;
-  hipGetDevice(&prev);
-  if (prev != ctx->device) hipSetDevice(ctx->device);
+  (void)hipGetDevice(&prev);
+  if (prev != ctx->device) (void)hipSetDevice(ctx->device);
   const __bf16* H = reinterpret_cast<const __bf16*>(hidden);
   const __bf16* W = reinterpret_cast<const __bf16*>(weight);
   EpiTileStat* S = reinterpret_cast<EpiTileStat*>(tile_stats);
@@ -130,7 +165,7 @@ extern "C" int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* wei
     hipLaunchKernelGGL(lmhead_kernel<false>, dim3(ntiles), dim3(256), 0, ctx->stream, H, W, rows, hidden_dim, vocab,
                        logits, logits_stride, S, ntiles);
   hipError_t e = hipGetLastError();
-  if (prev != ctx->device) hipSetDevice(prev);
+  if (prev != ctx->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "lmhead_kernel launch");
   return MXS_OK;
 }

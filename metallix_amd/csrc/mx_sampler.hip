@@ -5663,6 +5663,12 @@ __global__ __launch_bounds__(NT) void cand_export_kernel(Work w, uint32_t C, uin
 //     distinct tokens' values), so the tokens at or above kappa of the tiles
 //     whose maximum reaches kappa hold the head and every tie at its edge.
 //     kappa is the candidate threshold, as a chunk's is in the sample kernel.
+//     With k above the tile count the tile maxima bound nothing: the row is
+//     histogrammed on the sample kernel's value grid (HB bins of HRANGE / HB
+//     logits below the row maximum) and the candidates are the tokens in
+//     the bins down to the one where the count reaches k (two reads of the
+//     row instead of one; every bin above holds fewer than k tokens, so the
+//     head and its edge ties are inside).
 __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const EpiTileStat* __restrict__ ts,
                                                          uint32_t ntiles, const double* __restrict__ p_temperature,
                                                          const uint32_t* __restrict__ p_top_k,
@@ -5695,6 +5701,7 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
   uint32_t* red = hist + 256;                       // [NW]
   uint32_t* su = red + NW;                          // [4]
   unsigned long long* red64 = reinterpret_cast<unsigned long long*>(su + 4);   // [NW]
+  stamp(A, row, 0, 8);
   const EpiTileStat* rs = ts + (uint64_t)row * ntiles;
   unsigned long long g = 0ull;
   uint32_t tm = 0u, bad = 0u;
@@ -5712,81 +5719,144 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
   g = 0ull;
 #pragma unroll
   for (int w = 0; w < NW; ++w) g = red64[w] > g ? red64[w] : g;
-  uint32_t kappa = 0u, n = 0u;
+  uint32_t kappa = 0u, n = 0u, bstar = 0u;
+  bool hmode = false;   // k above the tile count: the value-grid histogram decides
   const uint64_t rbase = (uint64_t)row * V;
+  const float Mrow = okey_value(tm);
+  const float hscale = (float)HB / HRANGE;
+  // the value grid: bin 0 holds the row maximum, HB - 1 everything more than
+  // HRANGE below it (monotone non-increasing in the value)
+  auto vbin = [&](float x) -> uint32_t {
+    const float d = (Mrow - x) * hscale;
+    return d < (float)(HB - 1) ? (uint32_t)d : (uint32_t)(HB - 1);
+  };
   if (!c.err && !bad && mode == M_TOPK) {
-    // kappa: the k-th largest tile maximum, by four 8-bit digit passes
-    const uint32_t k = min(c.k, ntiles);
-    uint32_t prefix = 0u, need = k;
-    for (int d = 3; d >= 0; --d) {
-      if (tid < 256u) hist[tid] = 0u;
-      __syncthreads();
-      const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
-      if (tid < ntiles && (tk[tid] & pm) == prefix) atomicAdd(&hist[(tk[tid] >> (8 * d)) & 255u], 1u);
-      __syncthreads();
-      if (wave() == 0) {   // lane l: bins 255 - 4l .. 252 - 4l, from the top
-        uint32_t hb[4], hs = 0u;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) { hb[i] = hist[255u - 4u * lane() - (uint32_t)i]; hs += hb[i]; }
-        const uint32_t inc = wave_scan_u32(hs);
-        const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
-        const uint32_t L = (uint32_t)__builtin_ctzll(reach);   // need <= the matching count: some lane reaches it
-        if (lane() == L) {
-          uint32_t cum = inc - hs;
-          uint32_t bin = 252u - 4u * L;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            if (cum + hb[i] >= need) { bin = 255u - 4u * L - (uint32_t)i; break; }
-            cum += hb[i];
-          }
-          su[0] = bin;
-          su[1] = cum;
-        }
-      }
-      __syncthreads();
-      prefix |= su[0] << (8 * d);
-      need -= su[1];
-      __syncthreads();
-    }
-    kappa = prefix;
     const float* lg = reinterpret_cast<const float*>(b.logits) + (uint64_t)row * b.row_stride;
-    for (;;) {
-      // the candidate tiles (maximum at or above kappa), in tile order
-      uint32_t m;
+    uint32_t m;   // candidate tiles in tl[0 .. m), ascending
+    if (c.k <= ntiles) {
+      // kappa: the k-th largest tile maximum, by four 8-bit digit passes
+      uint32_t prefix = 0u, need = c.k;
+      for (int d = 3; d >= 0; --d) {
+        if (tid < 256u) hist[tid] = 0u;
+        __syncthreads();
+        const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
+        if (tid < ntiles && (tk[tid] & pm) == prefix) atomicAdd(&hist[(tk[tid] >> (8 * d)) & 255u], 1u);
+        __syncthreads();
+        if (wave() == 0) {   // lane l: bins 255 - 4l .. 252 - 4l, from the top
+          uint32_t hb[4], hs = 0u;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) { hb[i] = hist[255u - 4u * lane() - (uint32_t)i]; hs += hb[i]; }
+          const uint32_t inc = wave_scan_u32(hs);
+          const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+          const uint32_t L = (uint32_t)__builtin_ctzll(reach);   // need <= the matching count: some lane reaches it
+          if (lane() == L) {
+            uint32_t cum = inc - hs;
+            uint32_t bin = 252u - 4u * L;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if (cum + hb[i] >= need) { bin = 255u - 4u * L - (uint32_t)i; break; }
+              cum += hb[i];
+            }
+            su[0] = bin;
+            su[1] = cum;
+          }
+        }
+        __syncthreads();
+        prefix |= su[0] << (8 * d);
+        need -= su[1];
+        __syncthreads();
+      }
+      kappa = prefix;
       const bool ct = tid < ntiles && tk[tid] >= kappa;
       const uint32_t at = block_scan_incl<uint32_t>(ct ? 1u : 0u, red, &m) - (ct ? 1u : 0u);
       if (ct) tl[at] = tid;
       __syncthreads();
-      // their tokens at or above kappa, in token-ID order
-      for (uint32_t base = 0; base < m * EPI_TILE; base += NT) {
-        const uint32_t idx = base + tid;
-        float x = 0.0f;
-        uint32_t v = 0u;
-        bool keep = false;
-        if (idx < m * EPI_TILE) {
-          v = tl[idx / EPI_TILE] * EPI_TILE + idx % EPI_TILE;
-          if (v < V) {
-            x = lg[v];
-            keep = okey(x) >= kappa;
-          }
+    } else {
+      // More heads than tiles: the tile maxima bound nothing, so the whole
+      // row is histogrammed on the value grid (tk becomes the HB bins) and
+      // the head is the bins down to the one where the count reaches k.
+      hmode = true;
+      m = ntiles;
+      if (tid < ntiles) tl[tid] = tid;
+      for (uint32_t i = tid; i < (uint32_t)HB; i += NT) tk[i] = 0u;
+      __syncthreads();
+      for (uint32_t v0 = tid * 16u; v0 < V; v0 += NT * 16u) {
+        float4 xv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t v = v0 + 4u * (uint32_t)u;
+          xv[u] = v < V ? *reinterpret_cast<const float4*>(lg + v) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        uint32_t tot;
-        const uint32_t pos = n + block_scan_incl<uint32_t>(keep ? 1u : 0u, red, &tot) - (keep ? 1u : 0u);
-        if (keep) {
-          st_dev(&A.w.cand_l[rbase + pos], x);
-          st_dev(&A.w.cand_id[rbase + pos], v);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const float e4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (v0 + 4u * (uint32_t)u + (uint32_t)e < V) atomicAdd(&tk[vbin(e4[e])], 1u);
         }
-        n += tot;
       }
-      // With k above the tile count the bound holds only when at least k
-      // tokens reach kappa; otherwise every token is a candidate (kappa 0,
-      // the smallest order key), which reads the whole row.
-      if (n >= c.k || kappa == 0u) break;
-      kappa = 0u;
-      n = 0u;
-      __syncthreads();   // tl is rewritten
+      __syncthreads();
+      if (wave() == 0) {   // lane j: bins 16 j .. 16 j + 15, from the top value down
+        uint32_t hs = 0u;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) hs += tk[lane() * 16u + (uint32_t)i];
+        const uint32_t inc = wave_scan_u32(hs);
+        const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= c.k);
+        uint32_t bs = (uint32_t)(HB - 1);
+        if (reach) {
+          const uint32_t gi = (uint32_t)__builtin_ctzll(reach);
+          const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - hs), (int)gi);
+          const uint32_t hv = lane() < 16u ? tk[16u * gi + lane()] : 0u;
+          const uint32_t vi = base + wave_scan_u32(hv);
+          const uint64_t r2 = __builtin_amdgcn_ballot_w64(lane() < 16u && vi >= c.k);
+          bs = 16u * gi + (uint32_t)__builtin_ctzll(r2);
+        }
+        if (lane() == 0) su[0] = bs;
+      }
+      __syncthreads();
+      bstar = su[0];
+    }
+    stamp(A, row, 0, 1);
+    // the candidate tiles' tokens in the head's range, in token-ID order:
+    // 16 threads per tile, 16 consecutive tokens each, 64 tiles a pass
+    for (uint32_t t0 = 0; t0 < m; t0 += NT / 16u) {
+      const uint32_t ti = t0 + tid / 16u;
+      const uint32_t v0 = ti < m ? tl[ti] * EPI_TILE + (tid % 16u) * 16u : V;
+      float4 xv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t v = v0 + 4u * (uint32_t)u;
+        xv[u] = v < V ? *reinterpret_cast<const float4*>(lg + v) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      uint32_t keep = 0u;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float e4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t v = v0 + 4u * (uint32_t)u + (uint32_t)e;
+          const bool in = v < V && (hmode ? vbin(e4[e]) <= bstar : okey(e4[e]) >= kappa);
+          keep |= in ? 1u << (4 * u + e) : 0u;
+        }
+      }
+      const uint32_t cnt = (uint32_t)__builtin_popcount(keep);
+      uint32_t tot;
+      uint32_t pos = n + block_scan_incl<uint32_t>(cnt, red, &tot) - cnt;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float e4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if ((keep >> (4 * u + e)) & 1u) {
+            st_dev(&A.w.cand_l[rbase + pos], e4[e]);
+            st_dev(&A.w.cand_id[rbase + pos], v0 + 4u * (uint32_t)u + (uint32_t)e);
+            ++pos;
+          }
+      }
+      n += tot;
     }
   }
+  stamp(A, row, 0, 2);
   if (tid == 0) {
     ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC];
     st_dev(&st->maxkey, tm);
@@ -5796,7 +5866,7 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
     st_dev(&st->ncand, n);
     st_dev(&st->flags, bad ? (uint32_t)F_NONFINITE : 0u);
     st_dev(&st->minkey, 0u);
-    st_dev(&st->thr, okey_value(kappa));
+    st_dev(&st->thr, hmode ? -INFINITY : okey_value(kappa));
     st_dev(&st->mass, 0.0);
     st_dev(&st->mass_err, 0.0);
   }
@@ -5831,7 +5901,7 @@ int mxs_finish_tiles(mxs_ctx* ctx, const mxs_batch* b, const void* tile_stats, c
   A.b = *b;
   A.o = *o;
   A.w = ctx->work;
-  A.timing = nullptr;
+  A.timing = ctx->timing;
   A.paths = ctx->paths;
   if (++ctx->epoch == 0u) ctx->epoch = 1u;
   A.epoch = ctx->epoch;

@@ -135,7 +135,7 @@ def test_finish_tiles_nonfinite_and_greedy_ties(torch_mod, sampler, orc):
     path refuse them); and a head of equal logits across tiles keeps the
     lowest ID (greedy) and the lowest-ID ties of a top-k head."""
     torch = torch_mod
-    K2, V2, R2 = 64, 4096, 4
+    K2, V2, R2 = 128, 4096, 4
     hid = torch.ones((R2, K2), dtype=torch.bfloat16, device="cuda")
     wt = torch.zeros((V2, K2), dtype=torch.bfloat16, device="cuda")
     wt[1000, 0] = 3e38
