@@ -284,7 +284,9 @@ int mxs_sync(mxs_ctx* ctx);
  * u64 [rows][MXS_DEBUG_TIMING_SLOTS][MXS_DEBUG_TIMING_STAMPS], chunk
  * workgroups at slot = chunk, the row finisher at slot
  * MXS_DEBUG_TIMING_SLOTS - 1; stamp 8 is a workgroup's first instruction,
- * stamp 9 its exit, stamps 10 and 11 bracket a step receipt's work.  NULL
+ * stamp 9 its exit, stamps 10 and 11 bracket a step receipt's work, and
+ * the finisher's stamps 12 to 14 its reduction of candidate lists beyond its
+ * LDS cache (histogram start, histogram end, compaction end).  NULL
  * disables. */
 #define MXS_DEBUG_TIMING_SLOTS 65
 #define MXS_DEBUG_TIMING_STAMPS 16

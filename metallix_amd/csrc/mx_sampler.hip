@@ -3037,6 +3037,163 @@ __device__ __forceinline__ void keepall_bits(const SampleArgs& A, uint32_t row, 
   }
 }
 
+#ifndef MXS_REDUCE_RW
+#define MXS_REDUCE_RW 4u
+#endif
+// A top-k row whose chunk lists exceed the finisher's LDS cache (heads above
+// 1024, or flat rows): one pass histograms the lists on a value grid below
+// the row maximum (NBS bins of HRANGE / NBS logits), and the candidates in
+// the bins down to the one where the count reaches k (the head and every tie
+// at its edge: every bin above holds fewer than k) are compacted into the
+// LDS cache in token-ID order when they fit.  Returns their count, or NONE
+// (the lists do not reduce to the cache).  The lists themselves stay as they
+// are (mxs_export_candidates reads them).
+__device__ __forceinline__ uint32_t reduce_head(const float* cand_l, const uint32_t* cand_id, uint64_t rbase,
+                                             uint32_t CH, uint32_t C, uint32_t k, uint32_t Mkey, FinSmem& F,
+                                             uint64_t* timing, uint32_t row) {
+  const uint32_t tid = threadIdx.x;
+  uint32_t res = NONE;
+  constexpr uint32_t RW = MXS_REDUCE_RW;   // list entries per thread per round (loads in flight)
+  static_assert(RW >= 1u && RW <= 16u, "the offset tables hold 16 entries per wave");
+  const float Mf = okey_value(Mkey);
+  const float sc = (float)NBS / HRANGE;
+  auto vb = [&](float x) -> uint32_t {
+    const float d = (Mf - x) * sc;
+    return d < (float)(NBS - 1) ? (uint32_t)d : (uint32_t)(NBS - 1);
+  };
+  // 8 copies of the histogram, lane l adding to copy l % 8: lanes whose
+  // entries share a bin mostly hit different words (the bulk of a row's
+  // values falls in a few hundred bins)
+  constexpr uint32_t HCP = 8;
+  uint32_t* hc = reinterpret_cast<uint32_t*>(&F.u);   // HCP x NBS words; F.u.s is cleared again below
+  static_assert(sizeof(F.u) >= HCP * NBS * sizeof(uint32_t), "histogram copies fit the finisher's union");
+  for (uint32_t i = tid; i < HCP * (uint32_t)NBS; i += FT) hc[i] = 0u;
+  __syncthreads();
+  if (timing) timing[((uint64_t)row * (MAXC + 1) + MAXC) * TSTAMPS + 12] = wall_clock64();
+  // A chunk with at least k candidates holds k tokens at or above its
+  // threshold, so the head's k-th value is at least the largest such
+  // threshold: entries below it are never in the head's bins.
+  float hthr = -INFINITY;
+  for (uint32_t q = 0; q < C; ++q)
+    if (F.st[q].ncand >= k) hthr = fmaxf(hthr, F.st[q].thr);
+  uint32_t* hl = hc + (lane() % HCP) * (uint32_t)NBS;
+  for (uint32_t q = 0; q < C; ++q) {   // coalesced, RW loads in flight per thread
+    const uint32_t nq = F.st[q].ncand;
+    const float* cl = cand_l + rbase + (uint64_t)q * CH;
+    for (uint32_t j0 = tid; j0 < nq; j0 += (uint32_t)FT * RW) {
+      float xv[RW];
+#pragma unroll
+      for (uint32_t u = 0; u < RW; ++u) {
+        const uint32_t j = j0 + u * (uint32_t)FT;
+        xv[u] = j < nq ? ld_dev(&cl[j]) : -INFINITY;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < RW; ++u)
+        if (j0 + u * (uint32_t)FT < nq && xv[u] >= hthr) atomicAdd(&hl[vb(xv[u])], 1u);
+    }
+  }
+  __syncthreads();
+  if (wave() == 0) {   // lane l: bins 32 l .. 32 l + 31, from the row maximum down
+    auto bin = [&](uint32_t i) {
+      uint32_t t = 0u;
+#pragma unroll
+      for (uint32_t p = 0; p < HCP; ++p) t += hc[p * (uint32_t)NBS + i];
+      return t;
+    };
+    uint32_t hs = 0u;
+    for (uint32_t i = 0; i < 32u; ++i) hs += bin(lane() * 32u + i);
+    const uint32_t inc = wave_scan_u32(hs);
+    const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= k);
+    uint32_t bs = (uint32_t)(NBS - 1), kept = bcast63(inc);
+    if (reach) {
+      const uint32_t gi = (uint32_t)__builtin_ctzll(reach);
+      const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - hs), (int)gi);
+      const uint32_t hv = lane() < 32u ? bin(32u * gi + lane()) : 0u;
+      const uint32_t vi = base + wave_scan_u32(hv);
+      const uint32_t lb = (uint32_t)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lane() < 32u && vi >= k));
+      bs = 32u * gi + lb;
+      kept = (uint32_t)__builtin_amdgcn_readlane((int)vi, (int)lb);
+    }
+    if (lane() == 0) { F.s_u[12] = bs; F.s_u[14] = kept; }
+  }
+  __syncthreads();
+  if (timing) timing[((uint64_t)row * (MAXC + 1) + MAXC) * TSTAMPS + 13] = wall_clock64();
+  const uint32_t bs = F.s_u[12], kept = F.s_u[14];
+  if (kept <= (uint32_t)CCAP) {
+    // Compaction in token-ID order from coalesced rounds: entry
+    // r0 + u FT + tid of a round goes after every kept entry of the
+    // round's earlier u, then of the earlier waves at this u, then of the
+    // wave's lower lanes (ballots); wave 0 turns the waves' per-u counts
+    // into offsets, one exchange per round.
+    uint32_t* wc = hc;              // [NW][16] kept counts per wave and u
+    uint32_t* off = hc + NW * 16u;  // [NW][16] offsets; [NW * 16]: the round's total
+    uint32_t n = 0;
+    const uint32_t w = wave();
+    for (uint32_t q = 0; q < C; ++q) {
+      const uint32_t nq = F.st[q].ncand;
+      const uint64_t cb = rbase + (uint64_t)q * CH;
+      for (uint32_t r0 = 0; r0 < nq; r0 += (uint32_t)FT * RW) {   // uniform trip count
+        float xv[RW];
+        uint32_t iv[RW];
+        uint32_t keep = 0u;
+#pragma unroll
+        for (uint32_t u = 0; u < RW; ++u) {
+          const uint32_t j = r0 + u * (uint32_t)FT + tid;
+          xv[u] = j < nq ? ld_dev(&cand_l[cb + j]) : -INFINITY;
+          iv[u] = j < nq ? ld_dev(&cand_id[cb + j]) : 0u;
+        }
+        uint32_t pl[RW];
+#pragma unroll
+        for (uint32_t u = 0; u < RW; ++u) {
+          const bool in = r0 + u * (uint32_t)FT + tid < nq && xv[u] >= hthr && vb(xv[u]) <= bs;
+          keep |= in ? 1u << u : 0u;
+          const uint64_t bm = __builtin_amdgcn_ballot_w64(in);
+          pl[u] = lanes_below(bm);
+          if (lane() == u) wc[w * 16u + u] = (uint32_t)__builtin_popcountll(bm);
+        }
+        __syncthreads();
+        if (w == 0) {
+          // lane u < 16: the per-wave offsets at u, then the scan over u
+          uint32_t tu = 0u;
+          uint32_t cv[NW];
+#pragma unroll
+          for (int v = 0; v < NW; ++v) {
+            cv[v] = lane() < RW ? wc[(uint32_t)v * 16u + lane()] : 0u;
+            tu += cv[v];
+          }
+          const uint32_t bu = wave_scan_u32(tu) - tu;
+          if (lane() < RW) {
+            uint32_t run = n + bu;
+#pragma unroll
+            for (int v = 0; v < NW; ++v) {
+              off[(uint32_t)v * 16u + lane()] = run;
+              run += cv[v];
+            }
+          }
+          if (lane() == RW - 1u) off[NW * 16u] = bu + tu;
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t u = 0; u < RW; ++u)
+          if ((keep >> u) & 1u) {
+            const uint32_t at = off[w * 16u + u] + pl[u];
+            F.cl[at] = xv[u];
+            F.cid[at] = iv[u];
+          }
+        n += off[NW * 16u];
+        __syncthreads();   // wc and off are rewritten next round
+      }
+    }
+    res = n;
+  }
+  if (timing) timing[((uint64_t)row * (MAXC + 1) + MAXC) * TSTAMPS + 14] = wall_clock64();
+  __syncthreads();
+  reinterpret_cast<uint2*>(F.u.s.cnt)[tid] = make_uint2(0u, 0u);
+  reinterpret_cast<ulonglong2*>(F.u.s.mass)[tid] = make_ulonglong2(0ull, 0ull);
+  __syncthreads();
+  return res;
+}
+
 template <typename In>
 __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, const RowCfg& c, uint32_t row, uint32_t mode,
                            uint64_t rbase, double invT, const FinLoads& P) {
@@ -3276,8 +3433,23 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   }
 
   // =================== candidate paths ====================================
-  const uint32_t ncand = F.hdr.ncand;
+  uint32_t ncand = F.hdr.ncand;
   if (tid == 0) A.w.cand_rows[row] = (int32_t)ncand;   // mxs_export_candidates
+  // A top-k row whose chunk lists exceed the LDS cache (heads above 1024,
+  // or flat rows): one pass histograms the lists on a value grid below the
+  // row maximum (NBS bins of HRANGE / NBS logits), and the candidates in
+  // the bins down to the one where the count reaches k (the head and every
+  // tie at its edge: every bin above holds fewer than k) are compacted into
+  // the LDS cache in token-ID order when they fit; the lists themselves stay
+  // as they are (mxs_export_candidates reads them).
+  bool pre = false;   // the LDS cache holds the reduced list
+  if (ncand > (uint32_t)CCAP && k_act && (mode == M_TOPK || mode == M_ALL)) {
+    const uint32_t n = reduce_head(A.w.cand_l, A.w.cand_id, rbase, A.CH, C, c.k, F.hdr.Mkey, F, A.timing, row);
+    if (n != NONE) {
+      ncand = n;
+      pre = true;
+    }
+  }
   X.ncand = ncand;
   X.lds_c = ncand <= (uint32_t)CCAP;
   const double L = F.hdr.L;
@@ -3345,10 +3517,10 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
     lds_barrier();
   };
   // short rows first: the one-wave finisher
-  bool loaded = false;
+  bool loaded = pre;
   if (((mode == M_TOPK && c.k <= 64u) || mode == M_MINP) && ncand > 0u && ncand <= (uint32_t)(WR * 64) &&
       X.lds_c) {
-    bulk_load();
+    if (!loaded) bulk_load();
     loaded = true;
     if (wave() == 0) {
       const bool ok = finish_w1(X, F);
