@@ -624,13 +624,15 @@ def lmhead_bench(torch, s, stream, steps, warmup):
     on the stream."""
     import numpy as np
 
+    from metallix_amd.sampler import TILE_STAT_BYTES, TILE_TOKENS
+
     R, K, V = 64, 1024, 151936
     g = torch.Generator(device="cuda").manual_seed(20261202)
     with torch.cuda.stream(stream):
         w = (torch.randn((V, K), generator=g, device="cuda") * (2.0 / K ** 0.5)).to(torch.bfloat16)
         h = torch.randn((R, K), generator=g, device="cuda").to(torch.bfloat16)
         logits = torch.empty((R, V), dtype=torch.float32, device="cuda")
-        stats = torch.empty((R, ((V + 255) // 256) * 16), dtype=torch.uint8, device="cuda")
+        stats = torch.empty((R, -(-V // TILE_TOKENS) * TILE_STAT_BYTES), dtype=torch.uint8, device="cuda")
     torch.cuda.synchronize()
     rng = np.random.default_rng(20261202)
     T = rng.uniform(0.3, 1.5, R)

@@ -256,10 +256,12 @@ int mxs_export_candidates(mxs_ctx* ctx, uint32_t rows, uint32_t width, int32_t* 
  * row-major bf16 and 16-byte aligned; rows <= 64, hidden_dim a multiple of
  * 128, vocab a multiple of 4; logits f32 rows x logits_stride.  When
  * tile_stats is non-null, the epilogue also writes, per (row, 256-token
- * tile), the statistics mxs_finish_tiles reads (16 bytes each, rows x
- * ceil(vocab / 256); the layout is mxs::EpiTileStat of
+ * tile), the statistics mxs_finish_tiles reads (MXS_TILE_STAT_BYTES each,
+ * rows x ceil(vocab / MXS_TILE_TOKENS); the layout is mxs::EpiTileStat of
  * metallix_amd/csrc/mxs_epilogue.h, whose device functions any producer's
  * epilogue can call). */
+#define MXS_TILE_TOKENS 256      /* vocabulary entries per tile of the epilogue statistics */
+#define MXS_TILE_STAT_BYTES 8    /* bytes per (row, tile): the tile maximum's order key, a non-finite flag */
 int mxs_lmhead_bf16(mxs_ctx* ctx, const void* hidden, const void* weight, uint32_t rows, uint32_t hidden_dim,
                     uint32_t vocab, float* logits, uint64_t logits_stride, void* tile_stats);
 /* The pick of mxs_sample from a producer's tile statistics: batch->logits

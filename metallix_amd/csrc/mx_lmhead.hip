@@ -25,6 +25,8 @@ namespace mxs {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+static_assert(sizeof(EpiTileStat) == MXS_TILE_STAT_BYTES && EPI_TILE == MXS_TILE_TOKENS, "the header's tile layout");
+
 constexpr uint32_t LM_ROWS = 64;   // batch rows per launch (four 16-row MFMA blocks)
 constexpr uint32_t LM_KC = 128;    // hidden-state k staged in LDS per chunk
 constexpr uint32_t LM_BST = LM_KC + 8u;   // LDS row stride (bf16): rows 16 B apart in the banks
@@ -114,7 +116,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(const __bf16* __restrict__ 
         if (n < rows) *reinterpret_cast<f32x4*>(logits + (uint64_t)n * ld + v0) = acc[mb][nb];
         if (STATS) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) epi_add(p, acc[mb][nb][j], v0 + (uint32_t)j);
+          for (int j = 0; j < 4; ++j) epi_add(p, acc[mb][nb][j]);
         }
       }
     }

@@ -5872,26 +5872,18 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
   uint32_t* hist = tl + 1024;                       // [256]
   uint32_t* red = hist + 256;                       // [NW]
   uint32_t* su = red + NW;                          // [4]
-  unsigned long long* red64 = reinterpret_cast<unsigned long long*>(su + 4);   // [NW]
   stamp(A, row, 0, 8);
   const EpiTileStat* rs = ts + (uint64_t)row * ntiles;
-  unsigned long long g = 0ull;
   uint32_t tm = 0u, bad = 0u;
   for (uint32_t t = tid; t < ntiles; t += NT) {
     const EpiTileStat s = rs[t];
-    g = s.gkey > g ? s.gkey : g;
     tm = max(tm, s.tmax);
     bad |= s.bad;
     tk[t] = s.tmax;
   }
-  g = wave_max_u64(g);
-  if (lane() == 0) red64[wave()] = g;
-  tm = block_max<uint32_t>(tm, red);   // (its barriers order red64 too)
+  tm = block_max<uint32_t>(tm, red);
   bad = block_max<uint32_t>(bad, red);
-  g = 0ull;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) g = red64[w] > g ? red64[w] : g;
-  uint32_t kappa = 0u, n = 0u, bstar = 0u;
+  uint32_t kappa = 0u, n = 0u, bstar = 0u, gid = NONE;
   bool hmode = false;   // k above the tile count: the value-grid histogram decides
   const uint64_t rbase = (uint64_t)row * V;
   const float Mrow = okey_value(tm);
@@ -5902,43 +5894,79 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
     const float d = (Mrow - x) * hscale;
     return d < (float)(HB - 1) ? (uint32_t)d : (uint32_t)(HB - 1);
   };
-  if (!c.err && !bad && mode == M_TOPK) {
+  if (!c.err && !bad && (mode == M_TOPK || mode == M_GREEDY)) {
     const float* lg = reinterpret_cast<const float*>(b.logits) + (uint64_t)row * b.row_stride;
     uint32_t m;   // candidate tiles in tl[0 .. m), ascending
-    if (c.k <= ntiles) {
-      // kappa: the k-th largest tile maximum, by four 8-bit digit passes
-      uint32_t prefix = 0u, need = c.k;
-      for (int d = 3; d >= 0; --d) {
-        if (tid < 256u) hist[tid] = 0u;
-        __syncthreads();
-        const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
-        if (tid < ntiles && (tk[tid] & pm) == prefix) atomicAdd(&hist[(tk[tid] >> (8 * d)) & 255u], 1u);
-        __syncthreads();
-        if (wave() == 0) {   // lane l: bins 255 - 4l .. 252 - 4l, from the top
-          uint32_t hb[4], hs = 0u;
+    if (mode == M_GREEDY) {
+      // the tiles holding the row maximum, and their tokens equal to it
+      // (-0.0 and +0.0 are adjacent order keys: a zero maximum takes both)
+      kappa = Mrow == 0.0f ? okey(-0.0f) : tm;
+      const bool ct = tid < ntiles && tk[tid] >= kappa;
+      const uint32_t at = block_scan_incl<uint32_t>(ct ? 1u : 0u, red, &m) - (ct ? 1u : 0u);
+      if (ct) tl[at] = tid;
+      __syncthreads();
+    } else if (c.k <= ntiles) {
+      // kappa: a lower bound of the k-th largest tile maximum.  One pass
+      // puts the tile maxima on the value grid below the row maximum (tl
+      // holds the HB bins until the compaction below): the bin where their
+      // count reaches k, less one bin for rounding, bounds the k-th from
+      // below.  A k-th maximum beyond the grid takes the exact k-th by four
+      // 8-bit digit passes instead.
+      for (uint32_t i = tid; i < (uint32_t)HB; i += NT) tl[i] = 0u;
+      __syncthreads();
+      if (tid < ntiles) atomicAdd(&tl[vbin(okey_value(tk[tid]))], 1u);
+      __syncthreads();
+      if (wave() == 0) {   // lane j: bins 16 j .. 16 j + 15
+        uint32_t hs = 0u;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) { hb[i] = hist[255u - 4u * lane() - (uint32_t)i]; hs += hb[i]; }
-          const uint32_t inc = wave_scan_u32(hs);
-          const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
-          const uint32_t L = (uint32_t)__builtin_ctzll(reach);   // need <= the matching count: some lane reaches it
-          if (lane() == L) {
-            uint32_t cum = inc - hs;
-            uint32_t bin = 252u - 4u * L;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              if (cum + hb[i] >= need) { bin = 255u - 4u * L - (uint32_t)i; break; }
-              cum += hb[i];
-            }
-            su[0] = bin;
-            su[1] = cum;
-          }
-        }
-        __syncthreads();
-        prefix |= su[0] << (8 * d);
-        need -= su[1];
-        __syncthreads();
+        for (int i = 0; i < 16; ++i) hs += tl[lane() * 16u + (uint32_t)i];
+        const uint32_t inc = wave_scan_u32(hs);
+        const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= c.k);   // k <= ntiles: some lane reaches it
+        const uint32_t gi = (uint32_t)__builtin_ctzll(reach);
+        const uint32_t base = (uint32_t)__builtin_amdgcn_readlane((int)(inc - hs), (int)gi);
+        const uint32_t hv = lane() < 16u ? tl[16u * gi + lane()] : 0u;
+        const uint32_t vi = base + wave_scan_u32(hv);
+        const uint32_t lb = (uint32_t)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lane() < 16u && vi >= c.k));
+        if (lane() == 0) su[3] = 16u * gi + lb;
       }
-      kappa = prefix;
+      __syncthreads();
+      const uint32_t bk = su[3];
+      if (bk + 2u < (uint32_t)HB) {
+        kappa = okey(Mrow - (float)(bk + 2u) / hscale);
+      } else {
+        uint32_t prefix = 0u, need = c.k;
+        for (int d = 3; d >= 0; --d) {
+          if (tid < 256u) hist[tid] = 0u;
+          __syncthreads();
+          const uint32_t pm = d == 3 ? 0u : (0xffffffffu << (8 * (d + 1)));
+          if (tid < ntiles && (tk[tid] & pm) == prefix) atomicAdd(&hist[(tk[tid] >> (8 * d)) & 255u], 1u);
+          __syncthreads();
+          if (wave() == 0) {   // lane l: bins 255 - 4l .. 252 - 4l, from the top
+            uint32_t hb[4], hs = 0u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { hb[i] = hist[255u - 4u * lane() - (uint32_t)i]; hs += hb[i]; }
+            const uint32_t inc = wave_scan_u32(hs);
+            const uint64_t reach = __builtin_amdgcn_ballot_w64(inc >= need);
+            const uint32_t L = (uint32_t)__builtin_ctzll(reach);   // need <= the matching count: some lane reaches it
+            if (lane() == L) {
+              uint32_t cum = inc - hs;
+              uint32_t bin = 252u - 4u * L;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                if (cum + hb[i] >= need) { bin = 255u - 4u * L - (uint32_t)i; break; }
+                cum += hb[i];
+              }
+              su[0] = bin;
+              su[1] = cum;
+            }
+          }
+          __syncthreads();
+          prefix |= su[0] << (8 * d);
+          need -= su[1];
+          __syncthreads();
+        }
+        kappa = prefix;
+      }
       const bool ct = tid < ntiles && tk[tid] >= kappa;
       const uint32_t at = block_scan_incl<uint32_t>(ct ? 1u : 0u, red, &m) - (ct ? 1u : 0u);
       if (ct) tl[at] = tid;
@@ -6011,6 +6039,10 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
           keep |= in ? 1u << (4 * u + e) : 0u;
         }
       }
+      if (mode == M_GREEDY) {   // the argmax: the lowest ID holding the maximum, no list
+        if (keep) gid = min(gid, v0 + (uint32_t)__builtin_ctz(keep));
+        continue;
+      }
       const uint32_t cnt = (uint32_t)__builtin_popcount(keep);
       uint32_t tot;
       uint32_t pos = n + block_scan_incl<uint32_t>(cnt, red, &tot) - cnt;
@@ -6027,13 +6059,14 @@ __global__ __launch_bounds__(NT) void tile_finish_kernel(SampleArgs A, const Epi
       }
       n += tot;
     }
+    if (mode == M_GREEDY) gid = ~block_max<uint32_t>(~gid, red);
   }
   stamp(A, row, 0, 2);
   if (tid == 0) {
     ChunkStat* st = &A.w.stat[(uint64_t)row * MAXC];
     st_dev(&st->maxkey, tm);
-    st_dev(&st->gbest_id, g ? ~(uint32_t)g : NONE);
-    st_dev(&st->gbest_val, okey_value((uint32_t)(g >> 32)));
+    st_dev(&st->gbest_id, gid);
+    st_dev(&st->gbest_val, Mrow == 0.0f ? 0.0f : Mrow);
     st_dev(&st->nlegal, V);
     st_dev(&st->ncand, n);
     st_dev(&st->flags, bad ? (uint32_t)F_NONFINITE : 0u);

@@ -37,6 +37,7 @@ ROW_STATUS = {
     -12: "InvalidBias",
     -13: "TokenOutOfRange",
     -14: "Probabilities",
+    -15: "UnsupportedRule",   # mxs_finish_tiles: a rule other than greedy or top-k
 }
 
 _vp = ctypes.c_void_p
@@ -114,6 +115,8 @@ class SamplerError(RuntimeError):
 
 ABI_VERSION = 2                 # MXS_ABI_VERSION of include/mx_sampler.h
 RECEIPT_NONE = 0xFFFFFFFF       # MXS_RECEIPT_NONE: a receipt_top entry for "no receipt"
+TILE_TOKENS = 256               # MXS_TILE_TOKENS: vocabulary entries per epilogue-statistics tile
+TILE_STAT_BYTES = 8             # MXS_TILE_STAT_BYTES: bytes per (row, tile)
 
 
 def load_library(path: Optional[Path] = None):
@@ -278,7 +281,7 @@ class Sampler:
         """Queues the bf16 lm_head GEMM (mxs_lmhead_bf16): hidden bf16[rows,
         hidden_dim], weight bf16[vocab, hidden_dim] on the device; returns
         (logits f32[rows, vocab], tile statistics u8[rows, ceil(vocab/256)
-        * 16] or None).  With stats the epilogue also writes the statistics
+        * TILE_STAT_BYTES] or None).  With stats the epilogue also writes the statistics
         finish_tiles reads."""
         torch = self.torch
         rows, K = hidden.shape
@@ -287,7 +290,8 @@ class Sampler:
         with torch.cuda.stream(self.stream):
             if logits is None:
                 logits = torch.empty((rows, V), dtype=torch.float32, device=dev)
-            st = torch.empty((rows, ((V + 255) // 256) * 16), dtype=torch.uint8, device=dev) if stats else None
+            st = (torch.empty((rows, -(-V // TILE_TOKENS) * TILE_STAT_BYTES), dtype=torch.uint8, device=dev)
+                  if stats else None)
         self._check(self.lib.mxs_lmhead_bf16(self.ctx, hidden.data_ptr(), weight.data_ptr(), rows, K, V,
                                              logits.data_ptr(), logits.stride(0), _ptr(st)), "mxs_lmhead_bf16")
         return logits, st
@@ -298,7 +302,7 @@ class Sampler:
         logits and tile statistics: greedy and top-k rows, as `sample`
         picks them (no penalties, bias or mask)."""
         rows, V = logits.shape
-        need = rows * ((V + 255) // 256) * 16
+        need = rows * -(-V // TILE_TOKENS) * TILE_STAT_BYTES
         if tile_stats.device != logits.device or tile_stats.numel() * tile_stats.element_size() < need:
             raise ValueError(f"tile_stats must hold {need} bytes on the logits' device")
         b, o, _, out = self._structs(logits, temperature, top_k=top_k, top_p=top_p, min_p=min_p, uniform=uniform,
