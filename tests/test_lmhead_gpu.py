@@ -162,3 +162,44 @@ def test_finish_tiles_nonfinite_and_greedy_ties(torch_mod, sampler, orc):
                sampling_logprob=out2.sampling_logprob.cpu().numpy(), kept_count=out2.kept_count.cpu().numpy())
     compare(b, gpu, ref, check_kept=False)
     assert gpu["token"][0] == 0 and gpu["token"][2] == 0
+
+
+def test_entry_points_reject_what_they_do_not_serve(torch_mod, sampler):
+    """mxs_lmhead_bf16 refuses more than 64 rows, a hidden size that is not
+    a multiple of 128, a vocabulary that is not a multiple of 4 and
+    misaligned pointers; mxs_finish_tiles refuses bf16 logits, penalties and
+    too small a statistics buffer (the Python side) before any launch."""
+    import ctypes
+
+    from metallix_amd.sampler import SamplerError
+
+    torch = torch_mod
+    lib, ctx = sampler.lib, sampler.ctx
+    h = torch.zeros((65, 128), dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros((256, 128), dtype=torch.bfloat16, device="cuda")
+    lg = torch.zeros((65, 256), dtype=torch.float32, device="cuda")
+    EINVAL = -1
+    call = lambda rows, K, V, hp=h.data_ptr(), wp=w.data_ptr(), lp=lg.data_ptr(), ld=256: lib.mxs_lmhead_bf16(
+        ctx, hp, wp, rows, K, V, lp, ld, None)
+    assert call(65, 128, 256) == EINVAL                  # more than 64 rows
+    assert call(4, 96, 256) == EINVAL                    # hidden_dim not a multiple of 128
+    assert call(4, 128, 254) == EINVAL                   # vocab not a multiple of 4
+    assert call(4, 128, 256, hp=h.data_ptr() + 2) == EINVAL   # misaligned hidden
+    assert call(4, 128, 256, ld=255) == EINVAL           # stride below vocab / not a multiple of 4
+    assert call(0, 128, 256) == 0                        # nothing to do
+    assert b"128" in lib.mxs_last_error(ctx) or b"stride" in lib.mxs_last_error(ctx)
+    torch.cuda.synchronize()
+
+    logits, st = sampler.lmhead(h[:4], w, stats=True)
+    T = torch.full((4,), 0.7, dtype=torch.float64, device="cuda")
+    kk = torch.full((4,), 20, dtype=torch.int32, device="cuda")
+    with pytest.raises(SamplerError):                    # bf16 logits
+        sampler.finish_tiles(logits.to(torch.bfloat16), st, T, top_k=kk)
+    with pytest.raises(ValueError):                      # statistics buffer too small
+        sampler.finish_tiles(logits, st[:, :4], T, top_k=kk)
+    with pytest.raises(SamplerError):                    # penalties are not served
+        b, o, _, _ = sampler._structs(logits, T, top_k=kk,
+                                      repetition=torch.full((4,), 1.1, dtype=torch.float32, device="cuda"))
+        o.adjusted = None
+        sampler._check(lib.mxs_finish_tiles(ctx, ctypes.byref(b), st.data_ptr(), ctypes.byref(o)), "mxs_finish_tiles")
+    torch.cuda.synchronize()
