@@ -267,3 +267,31 @@ def test_large_heads_reduce_into_the_lds_cache(torch_mod, sampler, orc):
     t = tb.view(R, 65, 16).cpu().numpy()
     big = k >= 2000
     assert (t[big, 64, 14] > 0).all(), t[:, 64, 12:15]
+
+
+@pytest.mark.parametrize("seed", [21, 22])
+def test_large_heads_random_plateaus(torch_mod, sampler, orc, seed):
+    """Large heads over rows whose logits sit on a coarse grid (many equal
+    values, so the head's value bin can hold more than the finisher's LDS
+    cache and the list finisher keeps the row), with random k, T, top_p and
+    min_p: parity with the oracle (status-1 rows only at exact boundaries,
+    each still the oracle's token or a boundary draw)."""
+    from metallix_amd.synth import Batch
+
+    torch = torch_mod
+    rng = np.random.default_rng(seed)
+    R = 12
+    x = (rng.standard_normal((R, V)) * 2.0).astype(np.float32)
+    grid = rng.choice([0.25, 0.5, 1.0], R)
+    coarse = rng.random(R) < 0.6
+    x[coarse] = (np.round(x[coarse] / grid[coarse, None]) * grid[coarse, None]).astype(np.float32)
+    k = rng.integers(1000, 4097, R).astype(np.uint32)
+    T = rng.uniform(0.4, 1.5, R)
+    top_p = np.where(rng.random(R) < 0.5, 1.0, rng.uniform(0.5, 0.99, R))
+    min_p = np.where(rng.random(R) < 0.3, 0.01, 0.0)
+    b = Batch(name="large-heads-plateaus", logits=x, temperature=T, uniform=rng.random(R), top_k=k,
+              top_p=top_p, min_p=min_p)
+    say(f"case large-heads-plateaus seed {seed}: rows {R} vocab {V}")
+    gpu = run_gpu(torch, sampler, b)
+    ref = orc.sample_batch(b, debug=True)
+    compare(b, gpu, ref, allow_uncertified=R)

@@ -203,3 +203,47 @@ def test_entry_points_reject_what_they_do_not_serve(torch_mod, sampler):
         o.adjusted = None
         sampler._check(lib.mxs_finish_tiles(ctx, ctypes.byref(b), st.data_ptr(), ctypes.byref(o)), "mxs_finish_tiles")
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("seed", [11, 12, 13])
+def test_finish_tiles_random_shapes(torch_mod, sampler, orc, seed):
+    """Random shapes and rules through the GEMM + finish-only pick: vocab
+    from 1000 to 40000 (some below the 256-token tile count of a head, so
+    the value-grid histogram path runs), 1 to 64 rows, k from 1 to 4096,
+    logits with plateaus (rounded to 1/8) on some rows; picks as the oracle
+    over the read-back logits and as mxs_sample over the same logits."""
+    from metallix_amd.synth import Batch
+
+    torch = torch_mod
+    rng = np.random.default_rng(seed)
+    K2 = 128 * int(rng.integers(1, 4))
+    V2 = 4 * int(rng.integers(250, 10000))
+    R2 = int(rng.integers(1, 65))
+    say(f"case finish-tiles-random seed {seed}: rows {R2} hidden {K2} vocab {V2}")
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn((V2, K2), generator=g, device="cuda") * (2.5 / K2 ** 0.5)).to(torch.bfloat16)
+    h = torch.randn((R2, K2), generator=g, device="cuda").to(torch.bfloat16)
+    if seed % 2:   # plateaus: many equal weights rows, so equal logits
+        w[: V2 // 3] = torch.round(w[: V2 // 3].float() * 8).to(torch.bfloat16) / 8
+    logits, st = sampler.lmhead(h.contiguous(), w.contiguous(), stats=True)
+    T = rng.uniform(0.3, 1.5, R2)
+    T[rng.random(R2) < 0.25] = 0.0
+    k = rng.choice([1, 2, 7, 20, 64, 300, 1000, 4096], R2).astype(np.uint32)
+    k = np.minimum(k, V2 - 1).astype(np.uint32)
+    top_p = np.where(rng.random(R2) < 0.5, 1.0, rng.uniform(0.3, 0.99, R2))
+    min_p = np.where(rng.random(R2) < 0.3, 0.02, 0.0)
+    u = rng.random(R2)
+    D = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+    kw = dict(top_k=D(u32(k)), top_p=D(top_p), min_p=D(min_p), uniform=D(u))
+    out = sampler.finish_tiles(logits, st, D(T), **kw)
+    full = sampler.sample(logits, D(T), **kw)
+    torch.cuda.synchronize()
+    gpu = dict(token=out.token.cpu().numpy(), status=out.status.cpu().numpy(),
+               sampling_logprob=out.sampling_logprob.cpu().numpy(), kept_count=out.kept_count.cpu().numpy())
+    b = Batch(name="finish-random", logits=logits.cpu().numpy(), temperature=T, uniform=u, top_k=k,
+              top_p=top_p, min_p=min_p, tokenizer_vocab=V2)
+    ref = orc.sample_batch(b, debug=True)
+    compare(b, gpu, ref, allow_uncertified=max(2, R2 // 8), check_kept=False)
+    ft, fs = full.token.cpu().numpy(), full.status.cpu().numpy()
+    both = (gpu["status"] == 0) & (fs == 0)
+    assert (gpu["token"][both] == ft[both]).all()
