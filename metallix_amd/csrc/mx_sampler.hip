@@ -1182,7 +1182,14 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
     for (int r = 0; r < FE; ++r) {
       if (((inP >> r) & 1u) && ((ek[r] >> sh) & (NBG - 1)) == bstar) {
         const uint32_t at = atomicAdd(&F.s_u[10], 1u);
-        if (at < (uint32_t)G) { F.u.f.mkey[at] = ek[r]; F.u.f.mpos[at] = p0 + r; F.u.f.mw[at] = W[r]; }
+        if (at < (uint32_t)G) {
+          F.u.f.mkey[at] = ek[r];
+          F.u.f.mpos[at] = p0 + r;
+          F.u.f.mw[at] = W[r];
+          // (key, ~position) in one word: ordered before <=> larger (the
+          // mass histogram is read by now)
+          if (G == FT) F.u.f.mass[at] = ((unsigned long long)ek[r] << 32) | (unsigned long long)(~(p0 + (uint32_t)r));
+        }
       }
     }
     Gr::sync();
@@ -1200,10 +1207,17 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
         if (k2 > mk || (k2 == mk && p2 < mp)) ahead += w2;
       }
     } else if (gi < cm) {
-      for (uint32_t i = 0; i < cm; ++i) {
-        const uint32_t k2 = F.u.f.mkey[i], p2 = F.u.f.mpos[i];
-        if (k2 > mk || (k2 == mk && p2 < mp)) ahead += F.u.f.mw[i];
+      // two members per 16-byte read of the packed (key, ~position) words
+      // and of the weights (the crossing bin of a tied row holds hundreds)
+      const unsigned long long my = ((unsigned long long)mk << 32) | (unsigned long long)(~mp);
+      const unsigned long long* cp = F.u.f.mass;
+      uint32_t i = 0;
+      for (; i + 2u <= cm; i += 2u) {
+        const ulonglong2 c2 = *reinterpret_cast<const ulonglong2*>(&cp[i]);
+        const ulonglong2 w2 = *reinterpret_cast<const ulonglong2*>(&F.u.f.mw[i]);
+        ahead += (c2.x > my ? w2.x : 0ull) + (c2.y > my ? w2.y : 0ull);
       }
+      if (i < cm) ahead += cp[i] > my ? F.u.f.mw[i] : 0ull;
     }
     if (gi < cm) {
       const unsigned long long prev = bbefore + ahead, incl = prev + mwv;
