@@ -658,8 +658,11 @@ __device__ __forceinline__ void finish_large(const FinCtx& X, FinSmem& F, uint32
     double tot;
     const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
     const double exc = inc - w;
+    {   // the last positive weight's position: one LDS atomic per wave
+      const uint32_t lj = wave_max_u32(w > 0.0 ? j + 1u : 0u);
+      if (lane() == 0 && lj) atomicMax(&F.s_u[1], lj);
+    }
     if (w > 0.0) {
-      atomicMax(&F.s_u[1], j + 1u);
       if (target < inc && !(target < exc)) {
         F.s_u[0] = id;
         F.s_d[0] = s;
@@ -857,8 +860,11 @@ __device__ __forceinline__ void finish_exact(const FinCtx& X, FinSmem& F, uint32
     double tot;
     const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
     const double exc = inc - w;
+    {   // the last positive weight's position: one LDS atomic per wave
+      const uint32_t lt = wave_max_u32(w > 0.0 ? t + 1u : 0u);
+      if (lane() == 0 && lt) atomicMax(&F.s_u[1], lt);
+    }
     if (w > 0.0) {
-      atomicMax(&F.s_u[1], t + 1u);
       if (target < inc && !(target < exc)) {
         F.s_u[0] = t;
         if (fabs(target - exc) <= derr || fabs(inc - target) <= derr) F.s_u[2] = 1u;
@@ -1264,18 +1270,23 @@ __device__ __forceinline__ bool e_finish(const FinCtx& X, FinSmem& F, uint32_t n
   const double target = c.u * S;
   const double derr = sum_bound(S, nkept + 64u, 8.0);
   double cum = kinc - kpart;
+  uint32_t lastp = 0u;   // this lane's last positive kept weight, position + 1
 #pragma unroll
   for (int r = 0; r < FE; ++r) {
     if (!((kept >> r) & 1u)) continue;
     const double prev = cum;
     cum += w[r];
     if (w[r] > 0.0) {
-      atomicMax(&F.s_u[1], p0 + (uint32_t)r + 1u);
+      lastp = p0 + (uint32_t)r + 1u;
       if (target < cum && !(target < prev)) {
         F.s_u[0] = p0 + (uint32_t)r;
         if (fabs(target - prev) <= derr || fabs(cum - target) <= derr) F.s_u[2] = 1u;
       }
     }
+  }
+  {   // one LDS atomic per wave, not per kept slot (they all hit one word)
+    const uint32_t lp = wave_max_u32(lastp);
+    if (lane() == 0 && lp) atomicMax(&F.s_u[1], lp);
   }
   Gr::sync();
   if (any_bad) { write_result(X, MXS_ROW_INVALID_TEMPERATURE, -1, 0.0, 0u); return true; }
@@ -2723,13 +2734,16 @@ __device__ __forceinline__ void finish_large_r(const FinCtx& X, FinSmem& F, uint
     if (!((kept >> r) & 1u) || !(wv[r] > 0.0)) continue;
     const double prev = run;
     run = ((lastw >> r) & 1u) ? kinc : run + wv[r];
-    atomicMax(&F.s_u[1], j0 + (uint32_t)r + 1u);
     if (target < run && !(target < prev)) {
       F.s_u[0] = F.cid[j0 + r];
       F.s_u[8] = kv[r];
       F.s_d[0] = sv[r];
       if (fabs(target - prev) <= derr || fabs(run - target) <= derr) F.s_u[2] = 1u;
     }
+  }
+  {   // the last positive kept weight's position: one LDS atomic per wave
+    const uint32_t lp = wave_max_u32(lastw ? j0 + (uint32_t)__builtin_ctz(lastw) + 1u : 0u);
+    if (lane() == 0 && lp) atomicMax(&F.s_u[1], lp);
   }
   __syncthreads();
   uint32_t tok = F.s_u[0];
@@ -3348,8 +3362,11 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
       double tot;
       const double inc = run + block_scan_incl<double>(w, F.red_d, &tot);
       const double exc = inc - w;
+      {   // the last positive segment: one LDS atomic per wave
+        const uint32_t ls = wave_max_u32(w > 0.0 ? s + 1u : 0u);
+        if (lane() == 0 && ls) atomicMax(&F.s_u[1], ls);
+      }
       if (w > 0.0) {
-        atomicMax(&F.s_u[1], s + 1u);
         if (target < inc && !(target < exc)) {
           F.s_u[0] = s;
           F.s_d[0] = exc;
