@@ -5309,8 +5309,10 @@ __device__ __forceinline__ uint32_t chunk_general(const SampleArgs& A, FusedSmem
   const bool mass32 = row_ok && nleg > 0 &&
                       ((mode == M_MINP && c.top_p < 1.0) || (mode == M_TOPK && masked_row));
   // (all-candidates rows emit every legal token: the finisher's own f64
-  // sum over its working set is their row total, no chunk mass needed)
-  const bool mass64 = row_ok && nleg > 0 && mode == M_KEEPALL;
+  // sum over its working set is their row total, no chunk mass needed; a
+  // keep-all row under race-v2 draws nothing here, the race kernel takes
+  // its own mass)
+  const bool mass64 = row_ok && nleg > 0 && mode == M_KEEPALL && !A.nodraw;
   uint32_t cnt_i[PER_MAX];
   double m0 = 0.0, m1 = 0.0;
   {
