@@ -24,7 +24,7 @@
 // (uncertified) and it carries the device's winner.
 //
 // Launch: grid (8 C, rows / 8) of RNT-thread workgroups; chunk c of a row covers
-// tokens [c RT, (c + 1) RT), one 32-token word of the kept set per thread.
+// tokens [c RT, (c + 1) RT), 32 tokens RNT apart per thread.
 // Each chunk reduces its kept tokens to a RaceStat; the row's last chunk to
 // arrive (device-scope counter) merges them and writes the row's result.
 #include <hip/hip_runtime.h>
@@ -166,14 +166,29 @@ __device__ __forceinline__ void best_merge(Best& a, double s1, double s2, uint32
   }
 }
 
+// History counts of a chunk's tokens, two 16-bit counts per LDS word (token
+// d of the chunk in half d & 1), so that the table takes 16 KB and eight
+// workgroups share a CU.  A row with at most 65535 history entries cannot
+// carry a count into its neighbour, and plain adds are exact.  A longer
+// history adds with compare-and-swap, saturating at 0xFFFF, and a saturated
+// count is recounted from the history itself.
+__device__ __forceinline__ void cnt_add_sat(uint32_t* p, uint32_t sh) {
+  uint32_t old = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  while (((old >> sh) & 0xFFFFu) != 0xFFFFu) {
+    const uint32_t prev = atomicCAS(p, old, old + (1u << sh));
+    if (prev == old) return;
+    old = prev;
+  }
+}
+
 struct RaceSmem {
-  uint32_t cnt[RT];          // history counts of the chunk's tokens
+  uint32_t cnt[RT / 2];      // history counts of the chunk's tokens (16-bit pairs)
   float redf[RNW], redf2[RNW];
   double redd[RNW];
   double b1[RNW], b2[RNW];
   uint32_t bid[RNW];
   float bl[RNW];
-  float ss[RT];              // f32 screening scores of the chunk's kept tokens
+  uint32_t kw[RNT];          // the chunk's kept-set words
   uint32_t any, last;
 };
 
@@ -192,6 +207,7 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
   const uint32_t w = chunk * (uint32_t)RNT + tid;
   uint32_t word = w < A.nwords ? A.kept[(uint64_t)row * A.nwords + w] : 0u;
   if (tid == 0) S.any = 0u;
+  S.kw[tid] = word;
   __syncthreads();
   if (word) S.any = 1u;
   __syncthreads();
@@ -205,12 +221,16 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     const uint32_t hb = A.hoff[row], he = A.hoff[row + 1];
     const uint32_t bb = A.boff[row], be = A.boff[row + 1];
     const float rep = A.rep[row], pres = A.pres[row], freq = A.freq[row];
+    const bool longh = he - hb > 0xFFFFu;
     if (he > hb) {
-      for (uint32_t i = tid; i < RT; i += RNT) S.cnt[i] = 0u;
+      for (uint32_t i = tid; i < RT / 2u; i += RNT) S.cnt[i] = 0u;
       __syncthreads();
       for (uint32_t h = hb + tid; h < he; h += RNT) {
         const uint32_t d = A.hids[h] - base;
-        if (d < RT) atomicAdd(&S.cnt[d], 1u);
+        if (d < RT) {
+          if (!longh) atomicAdd(&S.cnt[d >> 1], 1u << ((d & 1u) * 16u));
+          else cnt_add_sat(&S.cnt[d >> 1], (d & 1u) * 16u);
+        }
       }
       __syncthreads();
     }
@@ -219,7 +239,15 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     // stage, penalize_logit).
     auto adjusted = [&](uint32_t id) -> float {
       const float l = Quad<In>::one(lrow + id);
-      const uint32_t cnt = he > hb ? S.cnt[id - base] : 0u;
+      uint32_t cnt = 0u;
+      if (he > hb) {
+        const uint32_t d = id - base;
+        cnt = (S.cnt[d >> 1] >> ((d & 1u) * 16u)) & 0xFFFFu;
+        if (cnt == 0xFFFFu) {   // saturated (histories above 65535 entries): recount
+          cnt = 0u;
+          for (uint32_t h = hb; h < he; ++h) cnt += A.hids[h] == id ? 1u : 0u;
+        }
+      }
       uint32_t lo = bb, hi = be;   // bias ids are strictly increasing
       while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
@@ -228,8 +256,13 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
       const bool hasb = lo < be && A.bids[lo] == id;
       return penalize_logit(l, cnt, hasb, hasb ? A.bvals[lo] : 0.0f, rep, pres, freq);
     };
-    const uint32_t id0 = base + 32u * tid;
-    for (uint32_t r = word; r; r &= r - 1u) m = fmaxf(m, adjusted(id0 + (uint32_t)__builtin_ctz(r)));
+    // Thread tid takes the chunk's tokens tid + 256 j (j < 32): a wave's
+    // logit loads are consecutive tokens.  Bit j of `mine` is token
+    // tid + 256 j's kept bit (word tid / 32 + 8 j, bit tid mod 32).
+    uint32_t mine = 0u;
+    for (uint32_t j = 0; j < 32u; ++j) mine |= ((S.kw[(tid >> 5) + 8u * j] >> (tid & 31u)) & 1u) << j;
+    const uint32_t id0 = base + tid;
+    for (uint32_t r = mine; r; r &= r - 1u) m = fmaxf(m, adjusted(id0 + 256u * (uint32_t)__builtin_ctz(r)));
     // chunk maximum
     m = wave_max(m);
     if (lane() == 0) S.redf[wave()] = m;
@@ -241,14 +274,14 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     const float invT32 = (float)(1.0 / T);
     // f32 screening scores and the f64 mass
     float smax = -INFINITY;
-    for (uint32_t r = word; r; r &= r - 1u) {
-      const uint32_t id = id0 + (uint32_t)__builtin_ctz(r);
+    for (uint32_t r = mine; r; r &= r - 1u) {
+      const uint32_t id = id0 + 256u * (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
       mass += exp(((double)l - (double)m) / T);
       const float s32 = (l - m) * invT32 + gumbel32(race_bits(seed, choice, position, id));
-      S.ss[id - base] = s32;
       smax = fmaxf(smax, s32);
     }
+    const float tmax = smax;   // this thread's largest screening score
     smax = wave_max(smax);
     if (lane() == 0) S.redf2[wave()] = smax;
     __syncthreads();
@@ -262,13 +295,22 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     // f64; the finisher has already checked that (l - M) / T is finite.)
     const bool screen = __builtin_isfinite(invT32) && __builtin_isfinite(smax);
     const float cut = smax - err32(smax) - 0x1p-10f;
+    // s + err32(s) rises with s, up to f32 rounding far below err32, so a
+    // thread whose largest score fails the screen by more than err32 holds
+    // no token that passes it; the others recompute their screening scores
+    // (the same operations, so the same values) token by token.
     uint32_t out = 0u;
-    for (uint32_t r = word; r; r &= r - 1u) {
-      const uint32_t id = id0 + (uint32_t)__builtin_ctz(r);
-      const float s32 = S.ss[id - base];
-      if (screen && !(s32 + err32(s32) >= cut)) { ++out; continue; }
+    if (screen && !(tmax + err32(tmax) + err32(tmax) >= cut)) out = __builtin_popcount(mine);
+    else
+    for (uint32_t r = mine; r; r &= r - 1u) {
+      const uint32_t id = id0 + 256u * (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
-      const double s = (double)l / T + gumbel_from_bits(race_bits(seed, choice, position, id));
+      const uint64_t bits = race_bits(seed, choice, position, id);
+      if (screen) {
+        const float s32 = (l - m) * invT32 + gumbel32(bits);
+        if (!(s32 + err32(s32) >= cut)) { ++out; continue; }
+      }
+      const double s = (double)l / T + gumbel_from_bits(bits);
       if (!isfinite(s)) flags |= RF_NONFINITE;
       best_merge(b, s, -INFINITY, id, l);
     }
@@ -412,10 +454,17 @@ extern "C" int mxs_sample_race(mxs_ctx* ctx, const mxs_batch* b, const mxs_race*
   (void)hipGetDevice(&prev);
   if (prev != ctx->device) (void)hipSetDevice(ctx->device);
   const dim3 grid(8u * A.C, (b->rows + 7u) / 8u);
+  // Unused dynamic LDS caps the workgroups per CU at ceil(grid / CUs), so a
+  // compute-bound grid (whole-row races) spreads over every CU instead of
+  // filling some to the occupancy limit; a grid that fits the CUs at that
+  // cap is resident at once either way.
+  const uint32_t per_cu = (grid.x * grid.y + ctx->cus - 1u) / ctx->cus;
+  const uint32_t lds_cu = 160u * 1024u, lds_wg = lds_cu / per_cu - 1024u;
+  const uint32_t pad = lds_wg > sizeof(mxs::RaceSmem) ? lds_wg - (uint32_t)sizeof(mxs::RaceSmem) : 0u;
   if (b->dtype == MXS_F32)
-    hipLaunchKernelGGL(mxs::race_kernel<float>, grid, dim3(mxs::RNT), 0, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::race_kernel<float>, grid, dim3(mxs::RNT), pad, ctx->stream, A);
   else
-    hipLaunchKernelGGL(mxs::race_kernel<uint16_t>, grid, dim3(mxs::RNT), 0, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::race_kernel<uint16_t>, grid, dim3(mxs::RNT), pad, ctx->stream, A);
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "race_kernel launch");

@@ -95,6 +95,7 @@ struct mxs_ctx {
   uint32_t* race_ctr = nullptr;
   void* race_scratch = nullptr;
   uint32_t* race_kept = nullptr;
+  uint32_t cus = 256;     // compute units of the device (race launches spread over them)
   // the uniform of the inverse-CDF draw mxs_sample_race discards (below)
   double* d_race_u = nullptr;
   // grammar-mask staging (mxs_mask_host / mxs_mask_upload, mx_mask.hip):

@@ -167,3 +167,41 @@ def test_race_whole_row_temperature_extremes(torch_mod, sampler, orc, T):
     b.temperature[:] = T
     gpu, _ = check(torch_mod, sampler, orc, b, 13)
     assert (gpu["status"] == 0).all()
+
+
+def test_race_heavy_histories(torch_mod, sampler, orc):
+    """Penalty histories with counts past the race kernel's 16-bit count
+    pairs: 70000 entries with one token repeated 66000 times (saturating
+    counts, recounted from the history), 65535 entries that are all one
+    token, and 40000 entries split between the two tokens of one count
+    word.  Those tokens lead their rows by enough that a wrong count moves
+    the winner or its log probability."""
+    from metallix_amd import synth
+
+    R, V = 8, 20000
+    s = synth.Stream(0x4857)
+    x = s.normal(R * V).reshape(R, V).astype(np.float32)
+    hists = []
+    for r in range(R):
+        if r == 0:
+            h = np.concatenate([np.full(66000, 7), np.full(3000, 8), s.u64(1000) % np.uint64(V)])
+        elif r == 1:
+            h = np.full(65535, 9)
+        elif r == 2:
+            h = np.concatenate([np.full(39000, 10), np.full(1000, 11)])
+        else:
+            h = s.u64(200 * r) % np.uint64(V)
+        hists.append(np.asarray(h, dtype=np.uint32))
+    for r, toks in enumerate(([7, 8], [8, 9], [10, 11])):
+        x[r, toks] = 12.0
+    b = synth.Batch(name="race-heavy-hist", logits=x, temperature=np.ones(R), uniform=np.zeros(R))
+    b.top_k = np.array([0, 0, 0, 0, 50, 0, 1000, 0], dtype=np.uint32)
+    b.top_p = np.array([1.0, 1.0, 1.0, 1.0, 0.9, 1.0, 0.95, 1.0])
+    b.min_p = np.zeros(R)
+    b.repetition = np.full(R, 1.1, dtype=np.float32)
+    b.presence = np.full(R, 0.05, dtype=np.float32)
+    b.frequency = np.full(R, 1.0e-4, dtype=np.float32)
+    b.history_offsets = np.concatenate([[0], np.cumsum([len(h) for h in hists])]).astype(np.uint32)
+    b.history_ids = np.concatenate(hists)
+    gpu, _ = check(torch_mod, sampler, orc, b, 17)
+    assert (gpu["status"] == 0).all(), gpu["status"]
