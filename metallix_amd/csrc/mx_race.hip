@@ -199,13 +199,18 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
   // i runs on XCD i mod 8, so a row's chunks share one XCD's L2.
   const uint32_t tid = threadIdx.x, chunk = blockIdx.x >> 3, row = blockIdx.y * 8u + (blockIdx.x & 7u);
   if (row >= A.rows) return;
+  // Every per-row load goes out at once (the kept words and the row's
+  // parameters are in bounds for every row below A.rows).
   const int32_t st0 = A.status[row];
   const double T = A.temperature[row];
-  // Rows the finisher rejected and greedy rows keep the finisher's result.
-  if (st0 < 0 || T == 0.0) return;
   const uint32_t base = chunk * RT;
   const uint32_t w = chunk * (uint32_t)RNT + tid;
   uint32_t word = w < A.nwords ? A.kept[(uint64_t)row * A.nwords + w] : 0u;
+  const uint32_t hb = A.hoff[row], he = A.hoff[row + 1];
+  const uint32_t bb = A.boff[row], be = A.boff[row + 1];
+  const float rep = A.rep[row], pres = A.pres[row], freq = A.freq[row];
+  // Rows the finisher rejected and greedy rows keep the finisher's result.
+  if (st0 < 0 || T == 0.0) return;
   if (tid == 0) S.any = 0u;
   S.kw[tid] = word;
   __syncthreads();
@@ -218,9 +223,6 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
   double mass = 0.0;
   uint32_t flags = 0u;
   if (any) {
-    const uint32_t hb = A.hoff[row], he = A.hoff[row + 1];
-    const uint32_t bb = A.boff[row], be = A.boff[row + 1];
-    const float rep = A.rep[row], pres = A.pres[row], freq = A.freq[row];
     const bool longh = he - hb > 0xFFFFu;
     if (he > hb) {
       for (uint32_t i = tid; i < RT / 2u; i += RNT) S.cnt[i] = 0u;
@@ -341,12 +343,14 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
       best_merge(t, S.b1[i], S.b2[i], S.bid[i], S.bl[i]);
     }
     RaceStat* p = &A.stat[(uint64_t)row * A.C + chunk];
-    st_dev(&p->best, t.s1);
-    st_dev(&p->second, t.s2);
-    st_dev(&p->mass, ms);
-    st_dev(&p->m, m);
-    st_dev(&p->lbest, t.l);
-    st_dev(&p->id, t.id);
+    if (any) {   // the merge reads only the flags of a chunk that keeps nothing
+      st_dev(&p->best, t.s1);
+      st_dev(&p->second, t.s2);
+      st_dev(&p->mass, ms);
+      st_dev(&p->m, m);
+      st_dev(&p->lbest, t.l);
+      st_dev(&p->id, t.id);
+    }
     st_dev(&p->flags, flags | (any ? RF_ANY : 0u));
     // The chunk's record is this thread's own device-scope stores: they
     // complete before the increment (the ordering argument of arrive_last),
