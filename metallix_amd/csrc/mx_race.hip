@@ -273,13 +273,14 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     for (int i = 1; i < RNW; ++i) m = fmaxf(m, S.redf[i]);
     const uint64_t seed = A.seed[row];
     const uint32_t choice = A.choice[row], position = A.position[row];
-    const float invT32 = (float)(1.0 / T);
+    const double invT = 1.0 / T;
+    const float invT32 = (float)invT;
     // f32 screening scores and the f64 mass
     float smax = -INFINITY;
     for (uint32_t r = mine; r; r &= r - 1u) {
       const uint32_t id = id0 + 256u * (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
-      mass += exp(((double)l - (double)m) / T);
+      mass += exp(((double)l - (double)m) * invT);   // (within an ulp of the quotient: the mass feeds only the logprob)
       const float s32 = (l - m) * invT32 + gumbel32(race_bits(seed, choice, position, id));
       smax = fmaxf(smax, s32);
     }
