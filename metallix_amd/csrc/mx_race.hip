@@ -44,8 +44,8 @@ constexpr uint32_t RT = (uint32_t)RNT * 32u;    // tokens per race chunk
 struct alignas(16) RaceStat {
   double best;      // largest score (-inf when the chunk keeps nothing)
   double second;    // largest score of every other kept token of the chunk
-  double mass;      // sum of exp((l - m) / T) over the chunk's kept tokens
-  float m;          // largest adjusted logit of the chunk's kept tokens
+  double mass;      // sum of exp((l - m) / T) over the chunk's kept tokens (m the row maximum)
+  float m;          // the row's largest adjusted logit (the mass's reference point)
   float lbest;      // the winner's adjusted logit
   uint32_t id;      // the winner's token ID (NONE when empty)
   uint32_t flags;   // RF_* below
@@ -72,6 +72,7 @@ struct RaceArgs {
   const uint32_t* bids;
   const float* bvals;
   const uint32_t* kept;     // rows x nwords, written by the row finisher
+  const float* rowmax;      // rows: the largest adjusted logit (written by the row finisher)
   const uint64_t* seed;
   const uint32_t* choice;
   const uint32_t* position;
@@ -137,7 +138,8 @@ __device__ __forceinline__ float gumbel32(uint64_t bits) {
 }
 
 // Bound on |s32 - (l / T + g - m / T)| for the f32 screening score
-// s32 = (l - m) * (1/T)_f32 + g32 (m the chunk's largest kept logit):
+// s32 = (l - m) * (1/T)_f32 + g32 (m the row's largest adjusted logit, at or
+// above every kept logit):
 // (l - m) / T <= 0 and g <= 45.1 give |(l - m) / T| <= |s32| + 46, whose
 // three f32 roundings cost under 2^-22.4 (|s32| + 46); plus |g32 - g| and
 // the final rounding.  The form below is several times larger than that.
@@ -183,7 +185,7 @@ __device__ __forceinline__ void cnt_add_sat(uint32_t* p, uint32_t sh) {
 
 struct RaceSmem {
   uint32_t cnt[RT / 2];      // history counts of the chunk's tokens (16-bit pairs)
-  float redf[RNW], redf2[RNW];
+  float redf2[RNW];
   double redd[RNW];
   double b1[RNW], b2[RNW];
   uint32_t bid[RNW];
@@ -209,6 +211,7 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
   const uint32_t hb = A.hoff[row], he = A.hoff[row + 1];
   const uint32_t bb = A.boff[row], be = A.boff[row + 1];
   const float rep = A.rep[row], pres = A.pres[row], freq = A.freq[row];
+  const float mrow = A.rowmax[row];
   // Rows the finisher rejected and greedy rows keep the finisher's result.
   if (st0 < 0 || T == 0.0) return;
   if (tid == 0) S.any = 0u;
@@ -264,13 +267,10 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     uint32_t mine = 0u;
     for (uint32_t j = 0; j < 32u; ++j) mine |= ((S.kw[(tid >> 5) + 8u * j] >> (tid & 31u)) & 1u) << j;
     const uint32_t id0 = base + tid;
-    for (uint32_t r = mine; r; r &= r - 1u) m = fmaxf(m, adjusted(id0 + 256u * (uint32_t)__builtin_ctz(r)));
-    // chunk maximum
-    m = wave_max(m);
-    if (lane() == 0) S.redf[wave()] = m;
-    __syncthreads();
-    m = S.redf[0];
-    for (int i = 1; i < RNW; ++i) m = fmaxf(m, S.redf[i]);
+    // The reference point of the scores and the mass: the row's largest
+    // adjusted logit, which the finisher found (the kept set holds it), so
+    // no pass over the chunk's tokens precedes the scoring.
+    m = mrow;
     const uint64_t seed = A.seed[row];
     const uint32_t choice = A.choice[row], position = A.position[row];
     const double invT = 1.0 / T;
@@ -447,6 +447,7 @@ extern "C" int mxs_sample_race(mxs_ctx* ctx, const mxs_batch* b, const mxs_race*
   A.bids = b->bias_ids ? b->bias_ids : ctx->d_zero_u32;
   A.bvals = b->bias_values ? b->bias_values : ctx->d_zero_f32;
   A.kept = o2.kept_bits;
+  A.rowmax = ctx->race_m;
   A.seed = race->seed;
   A.choice = race->choice ? race->choice : ctx->d_zero_u32;
   A.position = race->position;

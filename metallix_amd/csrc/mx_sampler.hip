@@ -102,6 +102,7 @@ struct SampleArgs {
   uint32_t masked;     // a grammar mask was given (else mask_words is an all-ones row)
   uint32_t epoch;      // this call's tag for Work::rowx (never 0; the row's last chunk also clears its word)
   uint32_t nodraw;     // keep-all rows skip the inverse-CDF draw (race-v2 calls)
+  float* race_m;       // race-v2 calls: each row's largest adjusted logit (else null)
   // Step receipts fused into the pick (mxs_step without race-v2): rows whose
   // rx_want entry is not MXS_RECEIPT_NONE also get the log-softmax top rx_n
   // of their logits after suppression, read in the same pass; rx_want null:
@@ -3302,6 +3303,7 @@ __device__ __forceinline__ void finish_row(const SampleArgs& A, FinSmem& F, cons
   const uint32_t flags = F.hdr.flags, nlegal = F.hdr.nlegal, bi = F.hdr.bi;
   const double M = (double)okey_value(F.hdr.Mkey);
   const int32_t err = combine_errors(c, flags, nlegal);
+  if (A.race_m && tid == 0) A.race_m[row] = (float)M;   // the race kernel's reference point
   const uint32_t nwords = (V + 31u) / 32u;
   uint32_t* kbits = A.o.kept_bits ? A.o.kept_bits + (uint64_t)row * nwords : nullptr;
   FinCtx X;
@@ -5684,6 +5686,7 @@ int sample_launch(mxs_ctx* ctx, const mxs_batch* b, const mxs_out* o, bool nodra
   if (++ctx->epoch == 0u) ctx->epoch = 1u;   // 0 is the zeroed scratch's tag
   A.epoch = ctx->epoch;
   A.nodraw = nodraw ? 1u : 0u;
+  A.race_m = nodraw ? ctx->race_m : nullptr;
   A.masked = b->mask_words != nullptr;
   A.rx_want = nullptr;
   if (rx) {
@@ -6144,6 +6147,7 @@ int mxs_finish_tiles(mxs_ctx* ctx, const mxs_batch* b, const void* tile_stats, c
   if (++ctx->epoch == 0u) ctx->epoch = 1u;
   A.epoch = ctx->epoch;
   A.nodraw = 0u;
+  A.race_m = nullptr;
   A.masked = 0u;
   A.rx_want = nullptr;
   A.b.mask_words = ctx->d_mask_ones;
@@ -6259,6 +6263,7 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   e = e ? e : hipMemset(ctx->race_ctr, 0, (size_t)max_rows * mxs::CTR_STRIDE * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->race_scratch, mxs::race_scratch_bytes(max_rows, max_vocab));
   e = e ? e : hipMalloc(&ctx->race_kept, (size_t)max_rows * ((max_vocab + 31u) / 32u) * sizeof(uint32_t));
+  e = e ? e : hipMalloc(&ctx->race_m, (size_t)max_rows * sizeof(float));
   const size_t nr = (size_t)max_rows + 1, nwords = (size_t)max_vocab / 32 + 2;
   e = e ? e : hipMalloc(&ctx->d_zero_u32, nr * sizeof(uint32_t));
   e = e ? e : hipMalloc(&ctx->d_one_f64, nr * sizeof(double));
@@ -6315,6 +6320,7 @@ int mxs_destroy(mxs_ctx* ctx) {
   hipFree(ctx->race_ctr);
   hipFree(ctx->race_scratch);
   hipFree(ctx->race_kept);
+  hipFree(ctx->race_m);
   mxs::mask_release(ctx);
   hipSetDevice(prev);
   delete ctx;
