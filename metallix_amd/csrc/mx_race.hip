@@ -276,15 +276,24 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     const double invT = 1.0 / T;
     const float invT32 = (float)invT;
     // f32 screening scores and the f64 mass
-    float smax = -INFINITY;
+    // This thread's two largest screening scores, and the largest one's
+    // token, logit and noise bits.
+    float t1 = -INFINITY, t2 = -INFINITY, l1 = 0.0f;
+    uint32_t id1 = 0u;
+    uint64_t bits1 = 0ull;
     for (uint32_t r = mine; r; r &= r - 1u) {
       const uint32_t id = id0 + 256u * (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
       mass += exp(((double)l - (double)m) * invT);   // (within an ulp of the quotient: the mass feeds only the logprob)
-      const float s32 = (l - m) * invT32 + gumbel32(race_bits(seed, choice, position, id));
-      smax = fmaxf(smax, s32);
+      const uint64_t bits = race_bits(seed, choice, position, id);
+      const float s32 = (l - m) * invT32 + gumbel32(bits);
+      if (s32 > t1) {
+        t2 = t1; t1 = s32; id1 = id; l1 = l; bits1 = bits;
+      } else {
+        t2 = fmaxf(t2, s32);
+      }
     }
-    const float tmax = smax;   // this thread's largest screening score
+    float smax = t1;
     smax = wave_max(smax);
     if (lane() == 0) S.redf2[wave()] = smax;
     __syncthreads();
@@ -300,11 +309,24 @@ __global__ __launch_bounds__(RNT) void race_kernel(RaceArgs A) {
     const float cut = smax - err32(smax) - 0x1p-10f;
     // s + err32(s) rises with s, up to f32 rounding far below err32, so a
     // thread whose largest score fails the screen by more than err32 holds
-    // no token that passes it; the others recompute their screening scores
-    // (the same operations, so the same values) token by token.
+    // no token that passes it.  When its second largest score fails that
+    // way, only its largest can pass, and that token was kept in registers;
+    // the other threads recompute their screening scores (the same
+    // operations, so the same values) token by token.
     uint32_t out = 0u;
-    if (screen && !(tmax + err32(tmax) + err32(tmax) >= cut)) out = __builtin_popcount(mine);
-    else
+    if (screen && !(t1 + err32(t1) + err32(t1) >= cut)) {
+      out = __builtin_popcount(mine);
+    } else if (screen && !(t2 + err32(t2) + err32(t2) >= cut)) {
+      // only the thread's largest score can pass: its token needs no reload
+      out = __builtin_popcount(mine) - 1u;
+      if (!(t1 + err32(t1) >= cut)) {
+        ++out;
+      } else {
+        const double sc = (double)l1 / T + gumbel_from_bits(bits1);
+        if (!isfinite(sc)) flags |= RF_NONFINITE;
+        best_merge(b, sc, -INFINITY, id1, l1);
+      }
+    } else
     for (uint32_t r = mine; r; r &= r - 1u) {
       const uint32_t id = id0 + 256u * (uint32_t)__builtin_ctz(r);
       const float l = adjusted(id);
