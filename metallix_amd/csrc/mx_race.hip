@@ -482,17 +482,10 @@ extern "C" int mxs_sample_race(mxs_ctx* ctx, const mxs_batch* b, const mxs_race*
   (void)hipGetDevice(&prev);
   if (prev != ctx->device) (void)hipSetDevice(ctx->device);
   const dim3 grid(8u * A.C, (b->rows + 7u) / 8u);
-  // Unused dynamic LDS caps the workgroups per CU at ceil(grid / CUs), so a
-  // compute-bound grid (whole-row races) spreads over every CU instead of
-  // filling some to the occupancy limit; a grid that fits the CUs at that
-  // cap is resident at once either way.
-  const uint32_t per_cu = (grid.x * grid.y + ctx->cus - 1u) / ctx->cus;
-  const uint32_t lds_cu = 160u * 1024u, lds_wg = lds_cu / per_cu - 1024u;
-  const uint32_t pad = lds_wg > sizeof(mxs::RaceSmem) ? lds_wg - (uint32_t)sizeof(mxs::RaceSmem) : 0u;
   if (b->dtype == MXS_F32)
-    hipLaunchKernelGGL(mxs::race_kernel<float>, grid, dim3(mxs::RNT), pad, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::race_kernel<float>, grid, dim3(mxs::RNT), 0, ctx->stream, A);
   else
-    hipLaunchKernelGGL(mxs::race_kernel<uint16_t>, grid, dim3(mxs::RNT), pad, ctx->stream, A);
+    hipLaunchKernelGGL(mxs::race_kernel<uint16_t>, grid, dim3(mxs::RNT), 0, ctx->stream, A);
   hipError_t e = hipGetLastError();
   if (prev != ctx->device) (void)hipSetDevice(prev);
   if (e != hipSuccess) return hip_fail(ctx, e, "race_kernel launch");

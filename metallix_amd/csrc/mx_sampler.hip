@@ -6239,7 +6239,6 @@ int mxs_create(int device, void* stream, uint32_t max_rows, uint32_t max_vocab, 
   ctx->stream = (hipStream_t)stream;
   ctx->max_rows = max_rows;
   ctx->max_vocab = max_vocab;
-  if (prop.multiProcessorCount > 0) ctx->cus = (uint32_t)prop.multiProcessorCount;
   int prev = 0;
   hipGetDevice(&prev);
   hipSetDevice(device);

@@ -96,7 +96,6 @@ struct mxs_ctx {
   void* race_scratch = nullptr;
   uint32_t* race_kept = nullptr;
   float* race_m = nullptr;   // each row's largest adjusted logit, from the finisher to the race kernel
-  uint32_t cus = 256;     // compute units of the device (race launches spread over them)
   // the uniform of the inverse-CDF draw mxs_sample_race discards (below)
   double* d_race_u = nullptr;
   // grammar-mask staging (mxs_mask_host / mxs_mask_upload, mx_mask.hip):
